@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""Benchmark of the KLA scan hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A step is one forward + backward pass of the Moebius precision scan and of the
+affine information scan over one batch of synthetic inputs already resident in
+HBM (BASELINE metric "KLA scan fwd+bwd tokens/s + achieved HBM GB/s, B=8 T=4096
+fp32, 1 GPU"; workload: Moebius + affine, batch 8, 4096 steps, 2048 lanes =
+heads * d_state, fp32). Prints one JSON line with tokens/s (value), the achieved
+HBM bandwidth, a roofline entry for the dominant kernel (HIP-event timing on the
+launch stream) and a CPU baseline: the reference's pure-PyTorch CPU algorithm
+(restated in oracle/torch_ref.py) timed on a bounded sample on this host.
+
+Inputs are drawn on the CPU with torch.Generator(seed 0) in a fixed order and
+copied to the GPU, so the CPU and GPU sides see the same bytes.
+
+``--only KERNEL`` runs just one kernel K times (for rocprofv3 counter runs);
+``--only copy`` runs a 1 GiB device-to-device copy, the calibration kernel for
+the FETCH_SIZE / WRITE_SIZE counters.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "kalman-linear-attention_amd"))
+
+import torch  # noqa: E402
+import torch.nn.functional as F  # noqa: E402
+
+METRIC = "KLA scan fwd+bwd tokens/s + achieved HBM GB/s, B=8 T=4096 fp32, 1 GPU"
+PEAK_HBM_GBPS = 8000.0
+
+WORKLOADS = {
+    # name: (batch, steps, lanes, affine I/O dtype)
+    "mobius_affine_b8_t4096_l2048": (8, 4096, 2048, torch.float32),
+    "mobius_affine_b8_t8192_l2048": (8, 8192, 2048, torch.float32),
+    "mobius_affine_b8_t4096_l2048_bf16affine": (8, 4096, 2048, torch.bfloat16),
+    "small_b2_t1024_l512": (2, 1024, 512, torch.float32),
+}
+DEFAULT_WORKLOAD = "mobius_affine_b8_t4096_l2048"
+
+# Compulsory HBM bytes per element (each input read once, each output written
+# once). Moebius with D == 1: fwd reads A, B, C and writes lam; bwd reads dlam,
+# A, B, C, lam and writes dA, dB, dC. Affine: fwd reads g, u and writes h; bwd
+# reads dh, g, h and writes dg, du. [batch, lanes] state tensors are excluded.
+def alg_bytes_per_elem(kernel: str, affine_dtype: torch.dtype) -> int:
+    e = 2 if affine_dtype == torch.bfloat16 else 4
+    return {"mobius_fwd": 16, "mobius_bwd": 32, "affine_fwd": 3 * e, "affine_bwd": 5 * e}[kernel]
+
+
+# ------------------------------------------------------------------ inputs
+
+
+def mobius_inputs(batch, steps, lanes, seed=0):
+    """A = exp(-softplus(z1)), B = softplus(z2), C = softplus(z3), D = 1 (implicit),
+    lam0 = softplus(N(0,1)), dlam ~ N(0,1); z ~ N(0,1). CPU tensors."""
+    g = torch.Generator().manual_seed(seed)
+    z1 = torch.randn(batch, steps, lanes, generator=g)
+    z2 = torch.randn(batch, steps, lanes, generator=g)
+    z3 = torch.randn(batch, steps, lanes, generator=g)
+    A = torch.exp(-F.softplus(z1))
+    B = F.softplus(z2)
+    C = F.softplus(z3)
+    lam0 = F.softplus(torch.randn(batch, lanes, generator=g))
+    dlam = torch.randn(batch, steps, lanes, generator=g)
+    return A, B, C, lam0, dlam
+
+
+def affine_inputs(batch, steps, lanes, seed=1, dtype=torch.float32):
+    """g = sigmoid(N(0,1)), u ~ N(0,1), h0 = 0, dh ~ N(0,1); bf16 by round-to-nearest-even."""
+    gen = torch.Generator().manual_seed(seed)
+    g = torch.sigmoid(torch.randn(batch, steps, lanes, generator=gen))
+    u = torch.randn(batch, steps, lanes, generator=gen)
+    dh = torch.randn(batch, steps, lanes, generator=gen)
+    return g.to(dtype), u.to(dtype), dh.to(dtype)
+
+
+# --------------------------------------------------------------- CPU baseline
+
+
+def cpu_model_name() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(lanes_full: int, reps: int = 4) -> dict:
+    """The reference's pure-PyTorch CPU scan (oracle.torch_ref: doubling scans of the
+    trace-normalised Moebius combine and the affine combine, backward by autograd),
+    fp32, on a bounded sample: batch 1, 4096 steps, 256 of the lanes."""
+    from oracle import torch_ref
+
+    sb, st, sl = 1, 4096, 256
+    A, B, C, lam0, dlam = mobius_inputs(sb, st, sl, seed=0)
+    g, u, dh = affine_inputs(sb, st, sl, seed=1)
+
+    def one():
+        Ar, Br, Cr, lr = (t.clone().requires_grad_(True) for t in (A, B, C, lam0))
+        lam = torch_ref.mobius_scan(Ar, Br, Cr, None, lr)
+        torch.autograd.backward(lam, dlam)
+        gr, ur = g.clone().requires_grad_(True), u.clone().requires_grad_(True)
+        h = torch_ref.affine_scan(gr, ur)
+        torch.autograd.backward(h, dh)
+
+    one()  # warm-up
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    full_width_tokens = sb * st * sl / lanes_full
+    return {
+        "value": full_width_tokens / med,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle/torch_ref (reference kla_ops.py doubling scans, autograd) Moebius+affine fwd+bwd fp32 "
+                   f"on batch {sb} x {st} steps x {sl} of {lanes_full} lanes; median of {reps} reps = "
+                   f"{med:.3f} s; tokens scaled by {sl}/{lanes_full} lanes"),
+        "host": {"cpu": cpu_model_name(), "affinity_cores": len(os.sched_getaffinity(0)),
+                 "torch_threads": torch.get_num_threads()},
+    }
+
+
+# ----------------------------------------------------------------- GPU side
+
+
+def build_step(batch, steps, lanes, adt, device):
+    from kla.ops.hip import scans as hs
+
+    A, B, C, lam0, dlam = (t.to(device) for t in mobius_inputs(batch, steps, lanes))
+    g, u, dh = (t.to(device) for t in affine_inputs(batch, steps, lanes, dtype=adt))
+    state = {}
+
+    def mobius_fwd():
+        state["lam"] = hs._mobius_scan_op(A, B, C, None, lam0)
+
+    def mobius_bwd():
+        state["dm"] = hs._mobius_scan_bwd_op(dlam, A, B, C, None, lam0, state["lam"])
+
+    def affine_fwd():
+        state["h"] = hs._affine_scan_op(g, u, None)
+
+    def affine_bwd():
+        state["da"] = hs._affine_scan_bwd_op(dh, g, state["h"], None)
+
+    kernels = {"mobius_fwd": mobius_fwd, "mobius_bwd": mobius_bwd, "affine_fwd": affine_fwd,
+               "affine_bwd": affine_bwd}
+
+    def step():
+        mobius_fwd()
+        mobius_bwd()
+        affine_fwd()
+        affine_bwd()
+
+    return step, kernels
+
+
+def time_kernels(kernels, reps, stream):
+    """Average duration of each kernel, HIP events on the launch stream."""
+    out = {}
+    for name, fn in kernels.items():
+        fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for s, e in ev:
+            s.record(stream)
+            fn()
+            e.record(stream)
+        torch.cuda.synchronize()
+        out[name] = statistics.mean(s.elapsed_time(e) for s, e in ev)
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--only", default=None,
+                    choices=["mobius_fwd", "mobius_bwd", "affine_fwd", "affine_bwd", "copy"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the scan on one GPU "
+              "(the multi-GPU sharding of the path is a design note only); use --gpus 1.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+
+    device = torch.device("cuda", 0)
+    stream = torch.cuda.current_stream(device)
+    batch, steps, lanes, adt = WORKLOADS[args.workload]
+    elems = batch * steps * lanes
+
+    if args.only == "copy":
+        a = torch.empty(1 << 28, device=device)
+        b = torch.empty_like(a)
+        for _ in range(args.warmup + args.steps):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "copy", "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
+                          "launches": args.warmup + args.steps}), flush=True)
+        return 0
+
+    print(f"[bench] building inputs for {args.workload} ({batch}x{steps}x{lanes})", file=sys.stderr, flush=True)
+    step, kernels = build_step(batch, steps, lanes, adt, device)
+
+    if args.only:
+        kernels["mobius_fwd"]()
+        kernels["affine_fwd"]()
+        for _ in range(args.warmup + args.steps):
+            kernels[args.only]()
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "launches": args.warmup + args.steps, "workload": args.workload}),
+              flush=True)
+        return 0
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = start.elapsed_time(end) / args.steps
+
+    from kla.ops.hip import _lib
+
+    failures = _lib.workspace_failures(device)
+    per_kernel_ms = time_kernels(kernels, max(args.steps, 10), stream)
+    per_kernel = {}
+    for name, ms in per_kernel_ms.items():
+        nbytes = alg_bytes_per_elem(name, adt if name.startswith("affine") else torch.float32) * elems
+        per_kernel[name] = {"ms": round(ms, 4), "alg_bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    dom = max(per_kernel, key=lambda k: per_kernel[k]["ms"])
+    step_bytes = sum(v["alg_bytes"] for v in per_kernel.values())
+    tokens = batch * steps
+    achieved_step = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    traffic = None
+    tfile = os.path.join(REPO, "profiles", f"traffic_{args.workload}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic = json.load(f).get(dom)
+
+    result = {
+        "metric": METRIC,
+        "value": tokens / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if adt == torch.float32 else "f32 (Moebius), bf16 I/O with f32 state (affine)",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "batch": batch, "steps": steps, "lanes": lanes,
+                   "ops": "Moebius fwd+bwd (D=1) + affine fwd+bwd", "parallelism": "single GPU"},
+        "achieved_GBps": round(achieved_step, 1),
+        "alg_bytes_per_step": step_bytes,
+        "roofline": {
+            "kernel": dom,
+            "bound": "hbm",
+            "achieved": per_kernel[dom]["GBps"],
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(per_kernel[dom]["GBps"] / PEAK_HBM_GBPS, 4),
+            "traffic": traffic,
+        },
+        "kernels": per_kernel,
+        "wall_s": round(wall, 4),
+        "lookback_failures": failures,
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(lanes)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,132 @@
+/*
+ * kla_hip.h -- C ABI of libkla_hip.so, the MI355X (gfx950) scan kernels behind
+ * the "hip" entry of the kla backend registry.
+ *
+ * Every entry point takes caller-owned device buffers (plain pointers), the
+ * problem size and a HIP stream; it validates its arguments on the host,
+ * launches on `stream` and returns without synchronising. Nothing here
+ * allocates device memory. Status codes are the KLA_* values below; after a
+ * non-zero status, kla_hip_last_error() describes it (thread-local string).
+ *
+ * Layout. A "sequence tensor" is a dense row-major [batch, steps, lanes] array:
+ * lanes are contiguous, time stride = lanes, batch stride = steps*lanes. For the
+ * reference's [B, L, M, S] scan operands this is lanes = M*S. A "state tensor"
+ * is dense [batch, lanes].
+ *
+ * Workspace. The single-pass scans publish per-chunk carries to one another
+ * through a caller-owned device workspace of kla_scan_workspace_bytes() bytes.
+ * Zero-fill it ONCE when it is allocated; the kernels keep it consistent from
+ * call to call (an epoch-tagged record scheme resets itself at the end of every
+ * launch), so it must not be zeroed again between calls, and calls that share
+ * one workspace must be ordered on one stream.
+ *
+ * Reference interfaces replaced (file:line in vaisakh-shaj/kalman-linear-attention):
+ *   kla_mobius_scan_fwd  <- TiledMobiusScan.forward / tiled_mobius_lambda
+ *                           (src/kla/ops/kernels/triton/tiled_mobius_scan.py:257-264, :113-151)
+ *   kla_mobius_scan_bwd  <- TiledMobiusScan.backward
+ *                           (src/kla/ops/kernels/triton/tiled_mobius_scan.py:266-279)
+ *   kla_affine_scan_fwd  <- TiledAffineScan.forward / tiled_linear_eta
+ *                           (src/kla/ops/kernels/triton/tiled_mobius_scan.py:282-289, :205-233)
+ *   kla_affine_scan_bwd  <- TiledAffineScan.backward / _reverse_affine
+ *                           (src/kla/ops/kernels/triton/tiled_mobius_scan.py:291-298, :247-254)
+ *   kla_hip_last_error   <- the TORCH_CHECK messages of the CUDA binding
+ *                           (src/kla/ops/kernels/cuda/v2_2/kla_matmul_scan.cu:35-59)
+ */
+#ifndef KLA_HIP_H_
+#define KLA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define KLA_OK 0
+#define KLA_ERR_INVALID_ARG 1 /* null pointer, negative or oversized shape   */
+#define KLA_ERR_WORKSPACE 2   /* workspace null, misaligned or too small     */
+#define KLA_ERR_DTYPE 3       /* unsupported element type                    */
+#define KLA_ERR_ALIGN 4       /* operand pointer not aligned to its element  */
+#define KLA_ERR_HIP 5         /* the HIP runtime refused the launch          */
+
+/* Element types of the affine scan's sequence tensors (state is always fp32). */
+#define KLA_DTYPE_F32 0
+#define KLA_DTYPE_BF16 1
+
+/* Scan kinds, for kla_scan_workspace_bytes(). */
+#define KLA_SCAN_MOBIUS_FWD 0
+#define KLA_SCAN_MOBIUS_BWD 1
+#define KLA_SCAN_AFFINE_FWD 2
+#define KLA_SCAN_AFFINE_BWD 3
+
+/* ABI version of this header; bumped on any signature change. */
+int kla_hip_abi_version(void);
+
+/* Message of the last non-zero status returned on the calling thread. */
+const char *kla_hip_last_error(void);
+
+/* Bytes of workspace a scan of this kind and size needs (0 on bad arguments). */
+size_t kla_scan_workspace_bytes(int kind, int64_t batch, int64_t steps, int64_t lanes);
+
+/* Number of look-back waits that gave up since the workspace was zero-filled
+ * (0 in every correct run). Reads the workspace header: synchronises `stream`. */
+int kla_workspace_failures(const void *workspace, hipStream_t stream, uint32_t *failures);
+
+/*
+ * Moebius (2x2 linear-fractional) precision scan, forward.
+ *   lam[b,t,n] = (A*l + B) / max(C*l + D, 1e-12),  l = lam[b,t-1,n], lam[b,-1,n] = lam0[b,n]
+ * A, B, C, D, lam: sequence tensors (fp32). D may be NULL (D == 1).
+ * lam0: state tensor (fp32) or NULL (lam0 == 1).
+ * Replaces TiledMobiusScan.forward (tiled_mobius_scan.py:257-264).
+ */
+int kla_mobius_scan_fwd(const float *A, const float *B, const float *C, const float *D,
+                        const float *lam0, float *lam, int64_t batch, int64_t steps,
+                        int64_t lanes, void *workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/*
+ * Moebius scan, exact scalar-adjoint backward.
+ *   den_t = max(C_t*l_{t-1} + D_t, 1e-12), gain_t = (A_t*D_t - B_t*C_t) / den_t^2
+ *   nu_t = dlam_t + gain_{t+1}*nu_{t+1}          (reverse scan, nu_T = 0)
+ *   dA = nu*l_{t-1}/den, dB = nu/den, dC = -nu*l_t*l_{t-1}/den, dD = -nu*l_t/den
+ *   dlam0 = nu_0*gain_0
+ * lam: the forward's output. D, dD, lam0, dlam0 may be NULL (dD is written only
+ * when both D and dD are given); dA, dB, dC may be NULL to skip that output.
+ * Replaces TiledMobiusScan.backward (tiled_mobius_scan.py:266-279).
+ */
+int kla_mobius_scan_bwd(const float *dlam, const float *A, const float *B, const float *C,
+                        const float *D, const float *lam0, const float *lam, float *dA,
+                        float *dB, float *dC, float *dD, float *dlam0, int64_t batch,
+                        int64_t steps, int64_t lanes, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Affine (first-order linear) scan, forward: h_t = g_t*h_{t-1} + u_t, h_{-1} = h0.
+ * g, u, h: sequence tensors of `dtype` (KLA_DTYPE_F32 or KLA_DTYPE_BF16; fp32
+ * arithmetic, bf16 stored round-to-nearest-even). h0: fp32 state tensor or NULL (0).
+ * Replaces TiledAffineScan.forward (tiled_mobius_scan.py:282-289).
+ */
+int kla_affine_scan_fwd(int dtype, const void *g, const void *u, const float *h0, void *h,
+                        int64_t batch, int64_t steps, int64_t lanes, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Affine scan, exact backward.
+ *   mu_t = dh_t + g_{t+1}*mu_{t+1} (reverse, mu_T = 0), dg_t = mu_t*h_{t-1}, du_t = mu_t,
+ *   dh0 = g_0*mu_0.
+ * dh, g, h (the forward's output), dg, du: sequence tensors of `dtype`.
+ * h0, dh0: fp32 state tensors or NULL; dg, du may be NULL to skip that output.
+ * Replaces TiledAffineScan.backward (tiled_mobius_scan.py:291-298).
+ */
+int kla_affine_scan_bwd(int dtype, const void *dh, const void *g, const void *h,
+                        const float *h0, void *dg, void *du, float *dh0, int64_t batch,
+                        int64_t steps, int64_t lanes, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KLA_HIP_H_ */

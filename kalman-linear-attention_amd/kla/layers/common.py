@@ -1,0 +1,113 @@
+"""Building blocks around the KLA filter: activations, l2 norm, Delta init,
+RMSNorm, the depthwise causal conv with carried state, and the channel MLP.
+
+Behaviour (including parameter shapes, init distributions and the order in
+which they draw from the torch RNG) matches the reference's
+src/kla/layers/common.py, so seeded layers initialise identically.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+_ACTIVATIONS = {"silu": F.silu, "gelu": F.gelu, "relu": F.relu}
+
+
+def get_activation(name: str):
+    """Activation function by name ("silu", "gelu", "relu")."""
+    if name not in _ACTIVATIONS:
+        raise ValueError(f"Unknown activation {name!r}; expected one of {sorted(_ACTIVATIONS)}")
+    return _ACTIVATIONS[name]
+
+
+def l2_norm(x: torch.Tensor, eps: float = 1e-12) -> torch.Tensor:
+    """x / max(||x||_2, eps) over the last dimension."""
+    return x / x.norm(dim=-1, keepdim=True).clamp_min(eps)
+
+
+def inv_softplus_dt_init(shape, dt_min: float, dt_max: float, dt_init_floor: float) -> torch.Tensor:
+    """Delta drawn log-uniformly in [dt_min, dt_max] (floored), returned pre-softplus.
+
+    softplus(dt + log(1 - exp(-dt))) = dt, so the stored value maps back to dt.
+    """
+    lo, hi = math.log(dt_min), math.log(dt_max)
+    dt = torch.exp(torch.rand(*shape) * (hi - lo) + lo).clamp_min(dt_init_floor)
+    return dt + torch.log(-torch.expm1(-dt))
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) * weight, computed in float32."""
+
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return (xf * self.weight.float()).to(x.dtype)
+
+
+class CausalConv1d(nn.Module):
+    """Depthwise causal conv over time on [B, L, D], with its state carried explicitly.
+
+    The state is the last ``kernel_size - 1`` pre-conv inputs, [B, D, kernel_size - 1].
+    """
+
+    def __init__(self, dim: int, kernel_size: int, activation: str = "silu", bias: bool = True):
+        super().__init__()
+        self.dim = dim
+        self.kernel_size = kernel_size
+        self.act = get_activation(activation)
+        self.weight = nn.Parameter(torch.empty(dim, 1, kernel_size))
+        self.bias = nn.Parameter(torch.empty(dim)) if bias else None
+        self.reset_parameters()
+
+    @torch.no_grad()
+    def reset_parameters(self):
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+        if self.bias is not None:
+            nn.init.zeros_(self.bias)
+
+    def init_state(self, batch: int, device=None, dtype=None) -> torch.Tensor:
+        return torch.zeros(batch, self.dim, self.kernel_size - 1, device=device, dtype=dtype)
+
+    def forward(self, x: torch.Tensor, conv_state: torch.Tensor | None = None):
+        """Returns (y [B, L, D], new_state [B, D, kernel_size - 1])."""
+        xt = x.transpose(1, 2)
+        if conv_state is None:
+            conv_state = self.init_state(x.shape[0], device=x.device, dtype=xt.dtype)
+        padded = torch.cat((conv_state.to(xt.dtype), xt), dim=-1)
+        y = F.conv1d(padded, self.weight, self.bias, groups=self.dim)
+        keep = self.kernel_size - 1
+        new_state = padded[..., padded.shape[-1] - keep:]
+        return self.act(y).transpose(1, 2), new_state
+
+
+class MLP(nn.Module):
+    """Channel mixer: SwiGLU (hidden = 2/3 of dim*ratio) or a GELU MLP."""
+
+    def __init__(self, dim: int, ratio: float = 4.0, kind: str = "swiglu", bias: bool = False):
+        super().__init__()
+        hidden = int(dim * ratio)
+        self.kind = kind
+        if kind == "swiglu":
+            hidden = int(2 * hidden / 3)
+            self.w12 = nn.Linear(dim, 2 * hidden, bias=bias)
+            self.w3 = nn.Linear(hidden, dim, bias=bias)
+        elif kind == "gelu":
+            self.w1 = nn.Linear(dim, hidden, bias=bias)
+            self.w2 = nn.Linear(hidden, dim, bias=bias)
+        else:
+            raise ValueError(f"Unknown MLP kind {kind!r}")
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.kind == "swiglu":
+            gate, up = self.w12(x).chunk(2, dim=-1)
+            return self.w3(F.silu(gate) * up)
+        return self.w2(F.gelu(self.w1(x)))

@@ -1,0 +1,230 @@
+"""The KLA sequence-mixing layer (reference src/kla/layers/kla_layer.py:49-349).
+
+    x [B, L, D] -> in_proj -> (z, gate) [B, L, d_inner]
+    z -> causal conv -> sensor_proj -> v, log sigma^2_v [B, L, M], k, q [B, L, S]
+    static Delta, a, p -> discrete (a_bar, p_bar) [M, S]
+    -> kla_scan (information-form Kalman filter) -> y [B, L, M]
+    -> lambda-skip, gate -> out_proj -> [B, L, D]
+
+Everything is driven by :class:`kla.configs.KLAConfig`; the scan itself is
+:func:`kla.ops.kla_scan` (or :func:`kla.ops.kla_step` for one-token decode),
+dispatched on ``config.backend``. Modules are created and initialised in the
+reference's order, so a seeded layer draws the same parameters.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import NamedTuple, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from kla.configs import KLAConfig
+from kla.layers.common import CausalConv1d, get_activation, inv_softplus_dt_init, l2_norm
+from kla.ops import KLAState, init_state, kla_scan, kla_step
+
+
+class KLALayerState(NamedTuple):
+    """Recurrent state of one layer: the conv window and the filter state."""
+
+    conv: Optional[torch.Tensor]  # [B, d_inner, K - 1]
+    ssm: KLAState  # (lam, eta), each [B, d_inner, d_state]
+
+
+class KLALayer(nn.Module):
+    def __init__(self, d_model: int, config: KLAConfig | None = None):
+        super().__init__()
+        cfg = config if config is not None else KLAConfig()
+        self.config = cfg
+        self.d_model = d_model
+        self.d_inner = cfg.d_inner(d_model)
+        self.d_state = cfg.d_state
+        M, S = self.d_inner, self.d_state
+
+        self.in_proj = nn.Linear(d_model, 2 * M if cfg.use_gating else M, bias=cfg.bias)
+        self.conv = CausalConv1d(M, cfg.conv_kernel_size, cfg.conv_activation) if cfg.use_conv else None
+
+        # One projection emits v (unless v = z), log sigma^2_v (full width or a
+        # low-rank code), k and q.
+        rank = cfg.dt_rank or math.ceil(d_model / 8)
+        self._value_rank = rank if cfg.value_rank == "dt" else cfg.value_rank
+        self._var_rank = rank if cfg.var_rank == "dt" else cfg.var_rank
+        if self._value_rank == "conv":
+            self._w_value = 0
+        elif self._value_rank == "full":
+            self._w_value = M
+        else:
+            self._w_value = int(self._value_rank)
+        self._w_var = M if self._var_rank == "full" else int(self._var_rank)
+        self.sensor_proj = nn.Linear(M, self._w_value + self._w_var + 2 * S, bias=cfg.bias)
+        low_rank_value = self._value_rank not in ("full", "conv")
+        self.value_expand = nn.Linear(int(self._value_rank), M, bias=cfg.bias) if low_rank_value else None
+        self.var_expand = nn.Linear(int(self._var_rank), M, bias=cfg.bias) if self._var_rank != "full" else None
+
+        # Static, time-invariant dynamics: step Delta, continuous rate a = -exp(lambda_log), noise p.
+        self.delta = nn.Parameter(torch.empty(M, S))
+        self.delta._no_weight_decay = True
+        self.lambda_log = nn.Parameter(torch.empty(M, S))
+        self.lambda_log._no_weight_decay = True
+        if cfg.learnable_process_noise and not cfg.zero_process_noise:
+            self.process_noise = nn.Parameter(torch.empty(M, S))
+        else:
+            self.register_buffer("process_noise", torch.empty(M, S))
+
+        if cfg.use_lambda_skip:
+            shape = (M,) if cfg.lambda_skip_mode == "vector" else ()
+            self.lambda_skip = nn.Parameter(torch.empty(shape))
+        else:
+            self.lambda_skip = None
+
+        self.gate_act = get_activation(cfg.gating_activation) if cfg.use_gating else None
+        self.out_proj = nn.Linear(M, d_model, bias=cfg.bias)
+        self.reset_parameters()
+
+    @torch.no_grad()
+    def reset_parameters(self):
+        """(Re-)initialise every parameter (safe after meta-device construction)."""
+        cfg = self.config
+        for mod in self.modules():
+            if isinstance(mod, (nn.Linear, CausalConv1d)):
+                mod.reset_parameters()
+        self.delta.copy_(inv_softplus_dt_init((self.d_inner, self.d_state), cfg.dt_min, cfg.dt_max,
+                                              cfg.dt_init_floor))
+        self.lambda_log.zero_()
+        self.process_noise.fill_(0.0 if cfg.zero_process_noise else cfg.process_noise_scale)
+        if self.lambda_skip is not None:
+            self.lambda_skip.fill_(cfg.lambda_skip_init)
+
+    # ------------------------------------------------------------------ state
+
+    def init_state(self, batch: int, device=None, dtype=None) -> KLALayerState:
+        conv = self.conv.init_state(batch, device=device, dtype=dtype) if self.conv is not None else None
+        return KLALayerState(conv=conv, ssm=init_state(batch, self.d_inner, self.d_state, device=device))
+
+    # ------------------------------------------------------------- dynamics
+
+    def _continuous_params(self):
+        """Continuous transition a (< 0) and process noise p, each [M, S]."""
+        cfg = self.config
+        a = -torch.exp(self.lambda_log.float())
+        p = self.process_noise.float()
+        if cfg.zero_process_noise:
+            p = p + 1e-12
+        else:
+            p = p.clamp_min(1e-7)
+            if cfg.clip_value is not None:
+                p = p.clamp_max(cfg.clip_value)
+        return a, p
+
+    def _discretize(self, delta: torch.Tensor, a: torch.Tensor, p: torch.Tensor):
+        """Delta -> a_bar = exp(Delta a) and p_bar (Ornstein-Uhlenbeck or zero-order hold)."""
+        a_bar = torch.exp(delta * a)
+        if self.config.discretization == "ou":
+            rate = a.abs().clamp_min(1e-8)
+            p_bar = (p / (2.0 * rate)) * (-torch.expm1(-2.0 * rate * delta))
+        else:
+            p_bar = p * delta
+        return a_bar, p_bar
+
+    def _compute_aq(self):
+        """Discrete (a_bar, p_bar), each [M, S]."""
+        a, p = self._continuous_params()
+        delta = F.softplus(self.delta.float()) + 1e-7
+        return self._discretize(delta, a, p)
+
+    # ----------------------------------------------------------- projections
+
+    def _project_sensors(self, z: torch.Tensor):
+        """z [B, L, M] -> (v, lambda_v [B, L, M], k, q [B, L, S]), all float32."""
+        cfg = self.config
+        S = self.d_state
+        v, log_var, k, q = torch.split(self.sensor_proj(z), [self._w_value, self._w_var, S, S], dim=-1)
+        if self._value_rank == "conv":
+            v = z
+        elif self.value_expand is not None:
+            v = self.value_expand(v)
+        if self.var_expand is not None:
+            log_var = self.var_expand(log_var)
+        if cfg.qk_norm:
+            k, q = l2_norm(k), l2_norm(q)
+        if cfg.clip_value is not None:
+            k = k.clamp(-cfg.clip_value, cfg.clip_value)
+            q = q.clamp(-cfg.clip_value, cfg.clip_value)
+        obs_var = F.softplus(log_var.float()) + cfg.obs_var_min
+        if cfg.obs_var_max is not None:
+            obs_var = obs_var.clamp_max(cfg.obs_var_max)
+        return v.float(), 1.0 / obs_var, k.float(), q.float()
+
+    # ---------------------------------------------------------------- compute
+
+    def _run_ssm(self, z: torch.Tensor, ssm_state: KLAState | None):
+        cfg = self.config
+        v, lambda_v, k, q = self._project_sensors(z)
+        a_bar, p_bar = self._compute_aq()
+
+        def scan(v, lambda_v, k, q, lam0, eta0):
+            state = None if lam0 is None else KLAState(lam=lam0, eta=eta0)
+            return kla_scan(v, lambda_v, k, q, a_bar, p_bar, initial_state=state, backend=cfg.backend,
+                            scan_impl=cfg.scan_impl, mobius_impl=cfg.mobius_impl,
+                            decode_from_prior=cfg.decode_from_prior)
+
+        lam0 = ssm_state.lam if ssm_state is not None else None
+        eta0 = ssm_state.eta if ssm_state is not None else None
+        with torch.autocast(device_type=z.device.type, enabled=False):
+            if cfg.checkpoint_ssm and torch.is_grad_enabled() and self.training:
+                return torch.utils.checkpoint.checkpoint(scan, v, lambda_v, k, q, lam0, eta0,
+                                                         use_reentrant=False)
+            return scan(v, lambda_v, k, q, lam0, eta0)
+
+    def _run_ssm_step(self, z: torch.Tensor, ssm_state: KLAState):
+        """One-token decode, z [B, 1, M]."""
+        cfg = self.config
+        v, lambda_v, k, q = self._project_sensors(z)
+        a_bar, p_bar = self._compute_aq()
+        with torch.autocast(device_type=z.device.type, enabled=False):
+            y, y_var, new_state = kla_step(v[:, 0], lambda_v[:, 0], k[:, 0], q[:, 0], a_bar, p_bar, ssm_state,
+                                           decode_from_prior=cfg.decode_from_prior)
+        return y.unsqueeze(1), y_var.unsqueeze(1), new_state
+
+    def forward(self, x: torch.Tensor, state: KLALayerState | None = None, return_state: bool = False):
+        """x [B, L, d_model] -> out, or (out, new_state) when a state is passed or requested.
+
+        ``out`` is y, or (y, y_var) when ``config.return_variance``.
+        """
+        cfg = self.config
+        L = x.shape[1]
+        emit_state = return_state or state is not None
+
+        projected = self.in_proj(x)
+        if cfg.use_gating:
+            z, gate = projected.chunk(2, dim=-1)
+        else:
+            z, gate = projected, None
+
+        conv_state = state.conv if state is not None else None
+        if self.conv is not None:
+            z, conv_state = self.conv(z, conv_state)
+        residual = z
+
+        ssm_state = state.ssm if state is not None else None
+        if state is not None and L == 1:
+            y, y_var, ssm_state = self._run_ssm_step(z, ssm_state)
+        else:
+            y, y_var, ssm_state = self._run_ssm(z, ssm_state)
+        y = y.to(x.dtype)
+        y_var = y_var.to(x.dtype)
+
+        if self.lambda_skip is not None:
+            y = y + self.lambda_skip * residual
+        if gate is not None:
+            g = self.gate_act(gate)
+            y = y * g
+            y_var = y_var * g.pow(2)
+
+        out = self.out_proj(y)
+        result = (out, F.linear(y_var, self.out_proj.weight.pow(2))) if cfg.return_variance else out
+        if emit_state:
+            return result, KLALayerState(conv=conv_state, ssm=ssm_state)
+        return result

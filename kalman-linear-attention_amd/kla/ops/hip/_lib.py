@@ -1,0 +1,134 @@
+"""ctypes binding of libkla_hip.so (the C ABI declared in include/kla_hip.h).
+
+The library is loaded after torch, so it binds to the HIP runtime torch already
+brought into the process (both name it libamdhip64.so.7), and streams and device
+pointers from torch are valid on its side. A missing or stale library is an
+error here, never a silent fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
+                        "lib", "libkla_hip.so")
+ABI_VERSION = 1
+
+KLA_OK = 0
+KLA_ERR_INVALID_ARG = 1
+KLA_ERR_WORKSPACE = 2
+KLA_ERR_DTYPE = 3
+KLA_ERR_ALIGN = 4
+KLA_ERR_HIP = 5
+
+KLA_DTYPE_F32 = 0
+KLA_DTYPE_BF16 = 1
+
+KLA_SCAN_MOBIUS_FWD = 0
+KLA_SCAN_MOBIUS_BWD = 1
+KLA_SCAN_AFFINE_FWD = 2
+KLA_SCAN_AFFINE_BWD = 3
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_SIGNATURES = {
+    "kla_hip_abi_version": (ctypes.c_int, []),
+    "kla_hip_last_error": (ctypes.c_char_p, []),
+    "kla_scan_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, _i64, _i64, _i64]),
+    "kla_workspace_failures": (ctypes.c_int, [_p, _p, ctypes.POINTER(ctypes.c_uint32)]),
+    "kla_mobius_scan_fwd": (ctypes.c_int, [_p] * 6 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
+    "kla_mobius_scan_bwd": (ctypes.c_int, [_p] * 12 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
+    "kla_affine_scan_fwd": (ctypes.c_int, [ctypes.c_int] + [_p] * 4 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
+    "kla_affine_scan_bwd": (ctypes.c_int, [ctypes.c_int] + [_p] * 7 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
+}
+
+
+class KLAHipError(RuntimeError):
+    """A libkla_hip.so entry point returned a non-zero status."""
+
+    def __init__(self, fn: str, status: int, message: str):
+        super().__init__(f"{fn} failed with status {status}: {message}")
+        self.status = status
+
+
+@functools.cache
+def lib() -> ctypes.CDLL:
+    """Load libkla_hip.so (once). Raises RuntimeError if it is missing or stale."""
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} not found: build the MI355X kernels with "
+            "`python kalman-linear-attention_amd/csrc/build.py` (or __graft_entry__.build())."
+        )
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    got = handle.kla_hip_abi_version()
+    if got != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} has ABI version {got}, this package expects {ABI_VERSION}; rebuild it")
+    return handle
+
+
+def last_error() -> str:
+    return lib().kla_hip_last_error().decode(errors="replace")
+
+
+def check(fn: str, status: int) -> None:
+    if status != KLA_OK:
+        raise KLAHipError(fn, status, last_error())
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+# ----------------------------------------------------------------- workspace
+#
+# One zero-filled workspace per (device, stream): the kernels keep it valid from
+# call to call, and calls on one stream are ordered, so reuse needs no reset.
+
+_WORKSPACES: dict = {}
+_WS_LOCK = threading.Lock()
+
+
+def workspace(kind: int, batch: int, steps: int, lanes: int, device: torch.device) -> tuple[torch.Tensor, int]:
+    """(workspace tensor, stream handle) for a scan on the current stream of ``device``."""
+    need = int(lib().kla_scan_workspace_bytes(kind, batch, steps, lanes))
+    if need == 0:
+        raise ValueError(f"kla_scan_workspace_bytes: {last_error()}")
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    with _WS_LOCK:
+        ws = _WORKSPACES.get(key)
+        if ws is None or ws.numel() < need:
+            size = max(need, 2 * ws.numel() if ws is not None else 0)
+            with torch.cuda.stream(stream):
+                ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            if ws.data_ptr() % 256:
+                raise RuntimeError("workspace allocation is not 256-byte aligned")
+            _WORKSPACES[key] = ws
+    return ws, stream.cuda_stream
+
+
+def workspace_failures(device: torch.device) -> int:
+    """Look-back waits that gave up on the current stream's workspace (0 when healthy)."""
+    stream = torch.cuda.current_stream(device)
+    ws = _WORKSPACES.get((device.index, stream.cuda_stream))
+    if ws is None:
+        return 0
+    out = ctypes.c_uint32(0)
+    check("kla_workspace_failures", lib().kla_workspace_failures(ws.data_ptr(), stream.cuda_stream, ctypes.byref(out)))
+    return int(out.value)
+
+
+def reset_workspaces() -> None:
+    """Drop every cached workspace (the next call allocates a fresh zero-filled one)."""
+    with _WS_LOCK:
+        _WORKSPACES.clear()

@@ -1,0 +1,209 @@
+"""GPU parity of the standalone Moebius and affine scans against the CPU oracle.
+
+Every case draws its inputs on the CPU (torch.Generator), runs the HIP kernels
+through the public ops (:func:`kla.ops.hip.mobius_scan`, :func:`affine_scan`)
+and compares with oracle.scans in float64 at the path's tolerance:
+rtol 1e-5, atol 1e-6 for fp32 (outputs, final states and every gradient), and
+rtol 2e-2 for bf16 I/O. Shapes cover a single step, ragged lane tiles (lanes not
+a multiple of 64), ragged chunks (steps not a multiple of the 64-step chunk),
+long sequences (many look-back hops) and the full headline shape (checked on a
+subset of lanes, plus whole-tensor properties).
+"""
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from bench import affine_inputs, mobius_inputs
+from oracle import scans as ref
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+SHAPES = [
+    (1, 1, 1),
+    (2, 7, 3),
+    (1, 64, 64),
+    (2, 65, 63),
+    (3, 130, 65),
+    (2, 257, 130),
+    (1, 1000, 64),
+    (2, 4096, 96),
+    (1, 3001, 1),
+]
+
+
+def _close(name, got, want, rtol=RTOL, atol=ATOL):
+    got = got.detach().double().cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got)
+    want = np.asarray(want, dtype=np.float64).reshape(got.shape)
+    assert np.isfinite(got).all(), f"{name}: non-finite values"
+    ratio = np.abs(got - want) / (atol + rtol * np.abs(want))
+    worst = float(ratio.max()) if ratio.size else 0.0
+    print(f"  {name:8s} worst |d|/(atol+rtol|ref|) = {worst:.3f}", flush=True)
+    assert worst <= 1.0, f"{name}: outside rtol={rtol} atol={atol} (worst ratio {worst:.3f})"
+
+
+def _log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("with_lam0", [True, False])
+def test_mobius_fwd_bwd_matches_oracle(cuda, shape, with_lam0):
+    from kla.ops.hip import mobius_scan
+
+    B, T, N = shape
+    _log(f"[mobius] shape={shape} lam0={with_lam0}")
+    A, Bm, C, lam0, dlam = mobius_inputs(B, T, N, seed=3)
+    if not with_lam0:
+        lam0 = None
+    leaves = [t.to(cuda).requires_grad_(True) for t in (A, Bm, C)]
+    l0 = lam0.to(cuda).requires_grad_(True) if lam0 is not None else None
+    lam = mobius_scan(*leaves, None, l0)
+    torch.autograd.backward(lam, dlam.to(cuda))
+
+    want = ref.mobius_scan_fwd(A, Bm, C, None, lam0)
+    _close("lam", lam, want)
+    dA, dB, dC, _, dl0 = ref.mobius_scan_bwd(dlam, A, Bm, C, None, lam0, want)
+    _close("dA", leaves[0].grad, dA)
+    _close("dB", leaves[1].grad, dB)
+    _close("dC", leaves[2].grad, dC)
+    if l0 is not None:
+        _close("dlam0", l0.grad, dl0)
+
+
+@pytest.mark.parametrize("shape", [(2, 130, 65), (1, 300, 128)])
+def test_mobius_explicit_D(cuda, shape):
+    """A general D tensor (the reference passes ones_like(phi)) and its gradient dD."""
+    from kla.ops.hip import mobius_scan
+
+    B, T, N = shape
+    A, Bm, C, lam0, dlam = mobius_inputs(B, T, N, seed=4)
+    D = torch.rand(B, T, N, generator=torch.Generator().manual_seed(9)) + 0.5
+    xs = [t.to(cuda).requires_grad_(True) for t in (A, Bm, C, D, lam0)]
+    lam = mobius_scan(*xs)
+    torch.autograd.backward(lam, dlam.to(cuda))
+    want = ref.mobius_scan_fwd(A, Bm, C, D, lam0)
+    _close("lam", lam, want)
+    grads = ref.mobius_scan_bwd(dlam, A, Bm, C, D, lam0, want)
+    for name, got, w in zip(("dA", "dB", "dC", "dD", "dlam0"), xs, grads):
+        _close(name, got.grad, w)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("with_h0", [True, False])
+def test_affine_fwd_bwd_matches_oracle(cuda, shape, with_h0):
+    from kla.ops.hip import affine_scan
+
+    B, T, N = shape
+    _log(f"[affine] shape={shape} h0={with_h0}")
+    g, u, dh = affine_inputs(B, T, N, seed=5)
+    h0 = torch.randn(B, N, generator=torch.Generator().manual_seed(6)) if with_h0 else None
+    gg, uu = g.to(cuda).requires_grad_(True), u.to(cuda).requires_grad_(True)
+    hh0 = h0.to(cuda).requires_grad_(True) if h0 is not None else None
+    h = affine_scan(gg, uu, hh0)
+    torch.autograd.backward(h, dh.to(cuda))
+    want = ref.affine_scan_fwd(g, u, h0)
+    _close("h", h, want)
+    dg, du, dh0 = ref.affine_scan_bwd(dh, g, want, h0)
+    _close("dg", gg.grad, dg)
+    _close("du", uu.grad, du)
+    if hh0 is not None:
+        _close("dh0", hh0.grad, dh0)
+
+
+@pytest.mark.parametrize("shape", [(2, 65, 63), (2, 1000, 130), (1, 4096, 64)])
+def test_affine_bf16_io(cuda, shape):
+    """bf16 sequence I/O, fp32 accumulation: within rtol 2e-2 of the fp64 oracle run
+    on the same (bf16-exact) inputs; outputs come back in bf16."""
+    from kla.ops.hip import affine_scan
+
+    B, T, N = shape
+    g, u, dh = affine_inputs(B, T, N, seed=7, dtype=torch.bfloat16)
+    gg, uu = g.to(cuda).requires_grad_(True), u.to(cuda).requires_grad_(True)
+    h = affine_scan(gg, uu)
+    assert h.dtype == torch.bfloat16
+    torch.autograd.backward(h, dh.to(cuda))
+    assert gg.grad.dtype == torch.bfloat16 and uu.grad.dtype == torch.bfloat16
+    want = ref.affine_scan_fwd(g.float(), u.float())
+    _close("h", h, want, rtol=2e-2, atol=1e-2)
+    dg, du, _ = ref.affine_scan_bwd(dh.float(), g.float(), want)
+    _close("dg", gg.grad, dg, rtol=2e-2, atol=1e-2)
+    _close("du", uu.grad, du, rtol=2e-2, atol=1e-2)
+
+
+def test_empty_and_zero_length(cuda):
+    from kla.ops.hip import affine_scan, mobius_scan
+
+    for shape in [(0, 5, 4), (2, 0, 4), (2, 5, 0)]:
+        A = torch.rand(*shape, device=cuda) + 0.1
+        lam = mobius_scan(A, A, A)
+        assert lam.shape == shape
+        h = affine_scan(A, A)
+        assert h.shape == shape
+    # Zero steps with a state: the state gradient is exactly zero.
+    A = (torch.rand(2, 0, 4, device=cuda) + 0.1).requires_grad_(True)
+    l0 = torch.rand(2, 4, device=cuda).requires_grad_(True)
+    lam = mobius_scan(A, A, A, None, l0)
+    lam.sum().backward()
+    assert torch.equal(l0.grad, torch.zeros_like(l0))
+
+
+def test_deterministic_bitwise(cuda):
+    """The look-back composes carries in a fixed order, so repeated runs agree bit for bit."""
+    from kla.ops.hip import affine_scan, mobius_scan
+
+    A, Bm, C, lam0, dlam = (t.to(cuda) for t in mobius_inputs(4, 2048, 512, seed=11))
+    runs = []
+    for _ in range(3):
+        xs = [t.clone().requires_grad_(True) for t in (A, Bm, C, lam0)]
+        lam = mobius_scan(xs[0], xs[1], xs[2], None, xs[3])
+        lam.backward(dlam)
+        runs.append([lam.detach()] + [x.grad for x in xs])
+    for other in runs[1:]:
+        for a, b in zip(runs[0], other):
+            assert torch.equal(a, b)
+    g, u, dh = (t.to(cuda) for t in affine_inputs(4, 2048, 512, seed=12))
+    hs = [affine_scan(g, u) for _ in range(3)]
+    assert torch.equal(hs[0], hs[1]) and torch.equal(hs[0], hs[2])
+
+
+def test_headline_shape_subset_of_lanes(cuda):
+    """Full (8, 4096, 2048) run; every lane finite, a spread of lanes (tile edges
+    included) against the fp64 oracle, no look-back wait gave up."""
+    from kla.ops.hip import _lib, affine_scan, mobius_scan
+
+    B, T, N = 8, 4096, 2048
+    _log("[headline] generating inputs")
+    A, Bm, C, lam0, dlam = mobius_inputs(B, T, N, seed=0)
+    xs = [t.to(cuda).requires_grad_(True) for t in (A, Bm, C, lam0)]
+    lam = mobius_scan(xs[0], xs[1], xs[2], None, xs[3])
+    lam.backward(dlam.to(cuda))
+    g, u, dh = affine_inputs(B, T, N, seed=1)
+    gg, uu = g.to(cuda).requires_grad_(True), u.to(cuda).requires_grad_(True)
+    h = affine_scan(gg, uu)
+    h.backward(dh.to(cuda))
+    torch.cuda.synchronize()
+    assert _lib.workspace_failures(cuda) == 0
+    for t in [lam, xs[0].grad, xs[1].grad, xs[2].grad, xs[3].grad, h, gg.grad, uu.grad]:
+        assert torch.isfinite(t).all()
+
+    lanes = sorted(set(list(range(0, N, 61)) + [63, 64, 127, 128, 1023, 1024, N - 1]))
+    idx = torch.tensor(lanes)
+    sub = lambda t: t[..., idx]  # noqa: E731
+    _log(f"[headline] oracle on {len(lanes)} lanes")
+    want = ref.mobius_scan_fwd(sub(A), sub(Bm), sub(C), None, sub(lam0))
+    _close("lam", sub(lam.cpu()), want)
+    dA, dBm, dC, _, dl0 = ref.mobius_scan_bwd(sub(dlam), sub(A), sub(Bm), sub(C), None, sub(lam0), want)
+    _close("dA", sub(xs[0].grad.cpu()), dA)
+    _close("dB", sub(xs[1].grad.cpu()), dBm)
+    _close("dC", sub(xs[2].grad.cpu()), dC)
+    _close("dlam0", sub(xs[3].grad.cpu()), dl0)
+    hw = ref.affine_scan_fwd(sub(g), sub(u))
+    _close("h", sub(h.cpu()), hw)
+    dg, du, _ = ref.affine_scan_bwd(sub(dh), sub(g), hw)
+    _close("dg", sub(gg.grad.cpu()), dg)
+    _close("du", sub(uu.grad.cpu()), du)
