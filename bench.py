@@ -17,7 +17,8 @@ copied to the GPU, so the CPU and GPU sides see the same bytes.
 
 ``--only KERNEL`` runs just one kernel K times (for rocprofv3 counter runs);
 ``--only copy`` runs a 1 GiB device-to-device copy, the calibration kernel for
-the FETCH_SIZE / WRITE_SIZE counters.
+the FETCH_SIZE / WRITE_SIZE counters; ``--only all`` runs the copy and then every
+scan kernel, so one counter pass covers them all.
 """
 
 from __future__ import annotations
@@ -98,13 +99,14 @@ def cpu_model_name() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(lanes_full: int, reps: int = 4) -> dict:
+def cpu_baseline(lanes_full: int, budget_s: float = 12.0) -> dict:
     """The reference's pure-PyTorch CPU scan (oracle.torch_ref: doubling scans of the
     trace-normalised Moebius combine and the affine combine, backward by autograd),
-    fp32, on a bounded sample: batch 1, 4096 steps, 256 of the lanes."""
+    fp32, on a bounded sample: batch 1, 4096 steps, all lanes; repeated to fill
+    about ``budget_s`` seconds, median reported."""
     from oracle import torch_ref
 
-    sb, st, sl = 1, 4096, 256
+    sb, st, sl = 1, 4096, lanes_full
     A, B, C, lam0, dlam = mobius_inputs(sb, st, sl, seed=0)
     g, u, dh = affine_inputs(sb, st, sl, seed=1)
 
@@ -116,7 +118,9 @@ def cpu_baseline(lanes_full: int, reps: int = 4) -> dict:
         h = torch_ref.affine_scan(gr, ur)
         torch.autograd.backward(h, dh)
 
+    t0 = time.perf_counter()
     one()  # warm-up
+    reps = int(min(20, max(3, budget_s / max(time.perf_counter() - t0, 1e-3))))
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -131,7 +135,7 @@ def cpu_baseline(lanes_full: int, reps: int = 4) -> dict:
         "kind": "port",
         "sample": (f"oracle/torch_ref (reference kla_ops.py doubling scans, autograd) Moebius+affine fwd+bwd fp32 "
                    f"on batch {sb} x {st} steps x {sl} of {lanes_full} lanes; median of {reps} reps = "
-                   f"{med:.3f} s; tokens scaled by {sl}/{lanes_full} lanes"),
+                   f"{med:.3f} s"),
         "host": {"cpu": cpu_model_name(), "affinity_cores": len(os.sched_getaffinity(0)),
                  "torch_threads": torch.get_num_threads()},
     }
@@ -193,7 +197,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--only", default=None,
-                    choices=["mobius_fwd", "mobius_bwd", "affine_fwd", "affine_bwd", "copy"])
+                    choices=["mobius_fwd", "mobius_bwd", "affine_fwd", "affine_bwd", "copy", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args(argv)
 
@@ -210,15 +214,18 @@ def main(argv=None) -> int:
     batch, steps, lanes, adt = WORKLOADS[args.workload]
     elems = batch * steps * lanes
 
-    if args.only == "copy":
-        a = torch.empty(1 << 28, device=device)
+    if args.only in ("copy", "all"):
+        # Calibration kernel for the HBM byte counters: 1 GiB read + 1 GiB written per launch.
+        a = torch.ones(1 << 28, device=device)
         b = torch.empty_like(a)
         for _ in range(args.warmup + args.steps):
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"only": "copy", "bytes_read": a.numel() * 4, "bytes_written": b.numel() * 4,
                           "launches": args.warmup + args.steps}), flush=True)
-        return 0
+        del a, b
+        if args.only == "copy":
+            return 0
 
     print(f"[bench] building inputs for {args.workload} ({batch}x{steps}x{lanes})", file=sys.stderr, flush=True)
     step, kernels = build_step(batch, steps, lanes, adt, device)
@@ -226,8 +233,10 @@ def main(argv=None) -> int:
     if args.only:
         kernels["mobius_fwd"]()
         kernels["affine_fwd"]()
+        names = list(kernels) if args.only == "all" else [args.only]
         for _ in range(args.warmup + args.steps):
-            kernels[args.only]()
+            for name in names:
+                kernels[name]()
         torch.cuda.synchronize()
         print(json.dumps({"only": args.only, "launches": args.warmup + args.steps, "workload": args.workload}),
               flush=True)
