@@ -9,11 +9,14 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+#include <initializer_list>
+
 #pragma GCC visibility push(default)
 #include "kla_hip.h"
 #pragma GCC visibility pop
 
-#include "scan_ops.hpp"
+#include "lookback_scan.hpp"
 
 namespace {
 
@@ -21,25 +24,24 @@ using namespace kla;
 
 constexpr int kAbiVersion = 1;
 
-// Tile shape per scan: W waves x S steps per wave, 64 lanes per workgroup.
-template <int KIND>
-struct Tile;
-template <>
-struct Tile<KLA_SCAN_MOBIUS_FWD> {
-  static constexpr int W = 4, S = 16, AGG = 4;
+// Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
+// thread (tile = 64 V lanes). Chosen by measurement on MI355X at
+// (batch 8, steps 4096, lanes 2048): the forward scans want a short register
+// footprint (occupancy hides the look-back), the backward scans long chunks.
+// A V > 1 shape needs lanes % V == 0 and operands aligned to V elements; the
+// V = 1 shape of the same kind serves every other call.
+template <class P, int W_, int S_, int V_>
+struct Shape3 {
+  using Policy = P;
+  static constexpr int W = W_, S = S_, V = V_;
 };
-template <>
-struct Tile<KLA_SCAN_MOBIUS_BWD> {
-  static constexpr int W = 4, S = 16, AGG = 2;
-};
-template <>
-struct Tile<KLA_SCAN_AFFINE_FWD> {
-  static constexpr int W = 4, S = 16, AGG = 2;
-};
-template <>
-struct Tile<KLA_SCAN_AFFINE_BWD> {
-  static constexpr int W = 4, S = 16, AGG = 2;
-};
+using MobiusFwdTile = Shape3<void, 8, 12, 1>;
+using MobiusBwdTile = Shape3<void, 8, 32, 1>;
+using AffineFwdTile = Shape3<void, 16, 24, 1>;
+using AffineBwdTile = Shape3<void, 12, 32, 1>;
+using AffineFwdBf16Tile = Shape3<void, 8, 24, 2>;
+using AffineBwdBf16Tile = Shape3<void, 16, 8, 4>;
+using AffineBf16Fallback = Shape3<void, 8, 32, 1>;
 
 constexpr uint32_t kMaxSpin = 1u << 20;   // ~1 s of polling before a wait gives up
 
@@ -67,26 +69,60 @@ int check_shape(const char *fn, Shape s) {
   return KLA_OK;
 }
 
-template <int KIND>
-Geom make_geom(Shape s) {
+Geom make_geom(Shape s, int W, int S, int V) {
   Geom g;
   g.batch = s.batch;
   g.steps = s.steps;
   g.lanes = s.lanes;
-  g.tiles_per_batch = (s.lanes + kWave - 1) / kWave;
+  const int64_t tile = static_cast<int64_t>(kWave) * V;
+  g.tiles_per_batch = (s.lanes + tile - 1) / tile;
   g.n_tiles = s.batch * g.tiles_per_batch;
-  const int64_t chunk = Tile<KIND>::W * Tile<KIND>::S;
+  const int64_t chunk = static_cast<int64_t>(W) * S;
   g.n_chunks = (s.steps + chunk - 1) / chunk;
-  g.plane = g.n_tiles * kWave;
+  g.plane = g.n_tiles * tile;
   g.max_spin = kMaxSpin;
   return g;
 }
 
-template <int KIND>
-size_t workspace_bytes_for(Shape s) {
-  const Geom g = make_geom<KIND>(s);
-  const int64_t words = kHeaderWords + (Tile<KIND>::AGG + 1) * g.n_chunks * g.plane;
-  return static_cast<size_t>(words) * sizeof(uint64_t);
+template <class T>
+Geom make_geom(Shape s) {
+  return make_geom(s, T::W, T::S, T::V);
+}
+
+// Workspace words of one tile shape: header, then K aggregate planes and one
+// carry plane, each n_chunks * plane words.
+size_t words_for(Shape s, int W, int S, int V, int K) {
+  const Geom g = make_geom(s, W, S, V);
+  return static_cast<size_t>(kHeaderWords + (K + 1) * g.n_chunks * g.plane);
+}
+
+template <class T>
+size_t words_for(Shape s, int K) {
+  return words_for(s, T::W, T::S, T::V, K);
+}
+
+// Bytes of workspace a scan kind needs: the largest over the shapes it may run.
+size_t workspace_bytes_kind(int kind, Shape s) {
+  size_t w = 0;
+  switch (kind) {
+    case KLA_SCAN_MOBIUS_FWD:
+      w = words_for<MobiusFwdTile>(s, 4);
+      break;
+    case KLA_SCAN_MOBIUS_BWD:
+      w = words_for<MobiusBwdTile>(s, 2);
+      break;
+    case KLA_SCAN_AFFINE_FWD:
+      w = std::max(words_for<AffineFwdTile>(s, 2),
+                   std::max(words_for<AffineFwdBf16Tile>(s, 2), words_for<AffineBf16Fallback>(s, 2)));
+      break;
+    case KLA_SCAN_AFFINE_BWD:
+      w = std::max(words_for<AffineBwdTile>(s, 2),
+                   std::max(words_for<AffineBwdBf16Tile>(s, 2), words_for<AffineBf16Fallback>(s, 2)));
+      break;
+    default:
+      return 0;
+  }
+  return w * sizeof(uint64_t);
 }
 
 bool empty(Shape s) { return s.batch == 0 || s.steps == 0 || s.lanes == 0; }
@@ -97,18 +133,18 @@ bool misaligned(const T *p) {
 }
 bool misaligned_bytes(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) != 0; }
 
-template <int KIND>
-int check_launch(const char *fn, Shape s, void *ws, size_t ws_bytes, int64_t *grid) {
-  const Geom g = make_geom<KIND>(s);
-  const int64_t blocks = g.n_tiles * g.n_chunks;
+int check_launch(const char *fn, int kind, Shape s, void *ws, size_t ws_bytes) {
+  // The largest grid any shape of this kind launches: the V = 1 shapes have
+  // the most tiles, the shortest chunks the most chunks.
+  const Geom g1 = make_geom(s, 8, 8, 1);
+  const int64_t blocks = g1.n_tiles * g1.n_chunks;
   if (blocks >= (1ll << 31))
     return fail(KLA_ERR_INVALID_ARG, "%s: %lld workgroups exceed the grid limit", fn, (long long)blocks);
   if (ws == nullptr) return fail(KLA_ERR_WORKSPACE, "%s: workspace is NULL", fn);
   if (misaligned_bytes(ws, 256)) return fail(KLA_ERR_WORKSPACE, "%s: workspace not 256-byte aligned", fn);
-  const size_t need = workspace_bytes_for<KIND>(s);
+  const size_t need = workspace_bytes_kind(kind, s);
   if (ws_bytes < need)
     return fail(KLA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, ws_bytes, need);
-  *grid = blocks;
   return KLA_OK;
 }
 
@@ -117,14 +153,20 @@ int hip_status(const char *fn, hipError_t e) {
   return KLA_OK;
 }
 
-template <class P, int KIND>
-int launch(const char *fn, const typename P::Params &prm, Shape s, void *ws, int64_t grid,
-           hipStream_t stream) {
-  constexpr int W = Tile<KIND>::W, S = Tile<KIND>::S;
-  const Geom g = make_geom<KIND>(s);
-  hipLaunchKernelGGL((lookback_scan_kernel<P, W, S>), dim3(static_cast<uint32_t>(grid)),
-                     dim3(kWave * W), 0, stream, prm, g, static_cast<uint64_t *>(ws));
+template <class P, class T>
+int launch(const char *fn, const typename P::Params &prm, Shape s, void *ws, hipStream_t stream) {
+  const Geom g = make_geom<T>(s);
+  const int64_t grid = g.n_tiles * g.n_chunks;
+  hipLaunchKernelGGL((lookback_scan_kernel<P, T::W, T::S, T::V>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(kWave * T::W), 0, stream, prm, g, static_cast<uint64_t *>(ws));
   return hip_status(fn, hipGetLastError());
+}
+
+// True when every non-NULL pointer is aligned to `bytes`.
+bool all_aligned(size_t bytes, std::initializer_list<const void *> ptrs) {
+  for (const void *p : ptrs)
+    if (p != nullptr && misaligned_bytes(p, bytes)) return false;
+  return true;
 }
 
 int zero_state(const char *fn, float *p, int64_t count, hipStream_t stream) {
@@ -146,15 +188,9 @@ const char *kla_hip_last_error(void) { return g_last_error; }
 size_t kla_scan_workspace_bytes(int kind, int64_t batch, int64_t steps, int64_t lanes) {
   const Shape s{batch, steps, lanes};
   if (check_shape("kla_scan_workspace_bytes", s) != KLA_OK) return 0;
-  switch (kind) {
-    case KLA_SCAN_MOBIUS_FWD: return workspace_bytes_for<KLA_SCAN_MOBIUS_FWD>(s);
-    case KLA_SCAN_MOBIUS_BWD: return workspace_bytes_for<KLA_SCAN_MOBIUS_BWD>(s);
-    case KLA_SCAN_AFFINE_FWD: return workspace_bytes_for<KLA_SCAN_AFFINE_FWD>(s);
-    case KLA_SCAN_AFFINE_BWD: return workspace_bytes_for<KLA_SCAN_AFFINE_BWD>(s);
-    default:
-      fail(KLA_ERR_INVALID_ARG, "kla_scan_workspace_bytes: unknown scan kind %d", kind);
-      return 0;
-  }
+  const size_t bytes = workspace_bytes_kind(kind, s);
+  if (bytes == 0) fail(KLA_ERR_INVALID_ARG, "kla_scan_workspace_bytes: unknown scan kind %d", kind);
+  return bytes;
 }
 
 int kla_workspace_failures(const void *workspace, hipStream_t stream, uint32_t *failures) {
@@ -183,17 +219,14 @@ int kla_mobius_scan_fwd(const float *A, const float *B, const float *C, const fl
   if (misaligned(A) || misaligned(B) || misaligned(C) || misaligned(D) || misaligned(lam0) ||
       misaligned(lam))
     return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
-  int64_t grid = 0;
-  rc = check_launch<KLA_SCAN_MOBIUS_FWD>(fn, s, workspace, workspace_bytes, &grid);
+  rc = check_launch(fn, KLA_SCAN_MOBIUS_FWD, s, workspace, workspace_bytes);
   if (rc != KLA_OK) return rc;
   if (D) {
     using P = MobiusFwd<true>;
-    const P::Params prm{A, B, C, D, lam0, lam, lanes};
-    return launch<P, KLA_SCAN_MOBIUS_FWD>(fn, prm, s, workspace, grid, stream);
+    return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, D, lam0, lam}, s, workspace, stream);
   }
   using P = MobiusFwd<false>;
-  const P::Params prm{A, B, C, nullptr, lam0, lam, lanes};
-  return launch<P, KLA_SCAN_MOBIUS_FWD>(fn, prm, s, workspace, grid, stream);
+  return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, nullptr, lam0, lam}, s, workspace, stream);
 }
 
 int kla_mobius_scan_bwd(const float *dlam, const float *A, const float *B, const float *C,
@@ -213,17 +246,16 @@ int kla_mobius_scan_bwd(const float *dlam, const float *A, const float *B, const
       misaligned(lam0) || misaligned(lam) || misaligned(dA) || misaligned(dB) || misaligned(dC) ||
       misaligned(dD) || misaligned(dlam0))
     return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
-  int64_t grid = 0;
-  rc = check_launch<KLA_SCAN_MOBIUS_BWD>(fn, s, workspace, workspace_bytes, &grid);
+  rc = check_launch(fn, KLA_SCAN_MOBIUS_BWD, s, workspace, workspace_bytes);
   if (rc != KLA_OK) return rc;
   if (D) {
     using P = MobiusBwd<true>;
-    const P::Params prm{dlam, A, B, C, D, lam0, lam, dA, dB, dC, dD, dlam0, lanes};
-    return launch<P, KLA_SCAN_MOBIUS_BWD>(fn, prm, s, workspace, grid, stream);
+    return launch<P, MobiusBwdTile>(fn, P::Params{dlam, A, B, C, D, lam0, lam, dA, dB, dC, dD, dlam0},
+                                    s, workspace, stream);
   }
   using P = MobiusBwd<false>;
-  const P::Params prm{dlam, A, B, C, nullptr, lam0, lam, dA, dB, dC, nullptr, dlam0, lanes};
-  return launch<P, KLA_SCAN_MOBIUS_BWD>(fn, prm, s, workspace, grid, stream);
+  return launch<P, MobiusBwdTile>(fn, P::Params{dlam, A, B, C, nullptr, lam0, lam, dA, dB, dC, nullptr, dlam0},
+                                  s, workspace, stream);
 }
 
 int kla_affine_scan_fwd(int dtype, const void *g, const void *u, const float *h0, void *h,
@@ -240,19 +272,19 @@ int kla_affine_scan_fwd(int dtype, const void *g, const void *u, const float *h0
   const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
   if (misaligned_bytes(g, el) || misaligned_bytes(u, el) || misaligned_bytes(h, el) || misaligned(h0))
     return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
-  int64_t grid = 0;
-  rc = check_launch<KLA_SCAN_AFFINE_FWD>(fn, s, workspace, workspace_bytes, &grid);
+  rc = check_launch(fn, KLA_SCAN_AFFINE_FWD, s, workspace, workspace_bytes);
   if (rc != KLA_OK) return rc;
   if (dtype == KLA_DTYPE_F32) {
     using P = AffineFwd<float>;
-    const P::Params prm{static_cast<const float *>(g), static_cast<const float *>(u), h0,
-                        static_cast<float *>(h), lanes};
-    return launch<P, KLA_SCAN_AFFINE_FWD>(fn, prm, s, workspace, grid, stream);
+    const P::Params prm{static_cast<const float *>(g), static_cast<const float *>(u), h0, static_cast<float *>(h)};
+    return launch<P, AffineFwdTile>(fn, prm, s, workspace, stream);
   }
   using P = AffineFwd<bf16_t>;
-  const P::Params prm{static_cast<const bf16_t *>(g), static_cast<const bf16_t *>(u), h0,
-                      static_cast<bf16_t *>(h), lanes};
-  return launch<P, KLA_SCAN_AFFINE_FWD>(fn, prm, s, workspace, grid, stream);
+  const P::Params prm{static_cast<const bf16_t *>(g), static_cast<const bf16_t *>(u), h0, static_cast<bf16_t *>(h)};
+  constexpr int V = AffineFwdBf16Tile::V;
+  if (lanes % V == 0 && all_aligned(V * el, {g, u, h}))
+    return launch<P, AffineFwdBf16Tile>(fn, prm, s, workspace, stream);
+  return launch<P, AffineBf16Fallback>(fn, prm, s, workspace, stream);
 }
 
 int kla_affine_scan_bwd(int dtype, const void *dh, const void *g, const void *h,
@@ -272,21 +304,23 @@ int kla_affine_scan_bwd(int dtype, const void *dh, const void *g, const void *h,
   if (misaligned_bytes(dh, el) || misaligned_bytes(g, el) || misaligned_bytes(h, el) ||
       misaligned_bytes(dg, el) || misaligned_bytes(du, el) || misaligned(h0) || misaligned(dh0))
     return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
-  int64_t grid = 0;
-  rc = check_launch<KLA_SCAN_AFFINE_BWD>(fn, s, workspace, workspace_bytes, &grid);
+  rc = check_launch(fn, KLA_SCAN_AFFINE_BWD, s, workspace, workspace_bytes);
   if (rc != KLA_OK) return rc;
   if (dtype == KLA_DTYPE_F32) {
     using P = AffineBwd<float>;
     const P::Params prm{static_cast<const float *>(dh), static_cast<const float *>(g),
                         static_cast<const float *>(h), h0, static_cast<float *>(dg),
-                        static_cast<float *>(du), dh0, lanes};
-    return launch<P, KLA_SCAN_AFFINE_BWD>(fn, prm, s, workspace, grid, stream);
+                        static_cast<float *>(du), dh0};
+    return launch<P, AffineBwdTile>(fn, prm, s, workspace, stream);
   }
   using P = AffineBwd<bf16_t>;
   const P::Params prm{static_cast<const bf16_t *>(dh), static_cast<const bf16_t *>(g),
                       static_cast<const bf16_t *>(h), h0, static_cast<bf16_t *>(dg),
-                      static_cast<bf16_t *>(du), dh0, lanes};
-  return launch<P, KLA_SCAN_AFFINE_BWD>(fn, prm, s, workspace, grid, stream);
+                      static_cast<bf16_t *>(du), dh0};
+  constexpr int V = AffineBwdBf16Tile::V;
+  if (lanes % V == 0 && all_aligned(V * el, {dh, g, h, dg, du}))
+    return launch<P, AffineBwdBf16Tile>(fn, prm, s, workspace, stream);
+  return launch<P, AffineBf16Fallback>(fn, prm, s, workspace, stream);
 }
 
 }  // extern "C"

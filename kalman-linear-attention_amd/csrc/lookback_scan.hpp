@@ -3,9 +3,12 @@
 //
 // Problem shape: `batch * lanes` independent chains, each `steps` long, stored
 // as dense [batch, steps, lanes] (lanes contiguous). One workgroup owns a tile
-// of 64 lanes (one lane per thread, so every wave-wide load or store touches
-// 256 contiguous bytes of one time row) and a chunk of W*S consecutive steps:
-// wave w holds steps [w*S, (w+1)*S) of the chunk in registers.
+// of 64 V lanes (V consecutive lanes per thread, moved by one vector access, so
+// a wave-wide load or store touches 256 V contiguous bytes of one fp32 time
+// row) and a chunk of W*S consecutive steps: wave w holds steps
+// [w*S, (w+1)*S) of the chunk in registers. Workgroups are numbered
+// chunk-major, so the tiles of one time chunk (adjacent pieces of the same
+// rows) are in flight together.
 //
 //   1. every thread loads its S steps and reduces them to a chunk-local
 //      aggregate (an element of the scan's monoid: a 2x2 projective map for the
@@ -40,64 +43,56 @@
 // failure in the workspace header instead of hanging the GPU.
 #pragma once
 
-#include <hip/hip_runtime.h>
-#include <stdint.h>
+#include "scan_ops.hpp"
 
 namespace kla {
 
-constexpr float kEps = 1e-12f;   // EPS = P_MIN of the reference (kla_ops.py:43-44)
-constexpr int kWave = 64;
 constexpr int64_t kHeaderWords = 32;   // 256-byte workspace header
 
 // Header word 0: (epoch << 32) | tickets drawn in the running launch.
 // Header word 1: count of look-back waits that gave up.
-
-struct Geom {
-  int64_t batch, steps, lanes;
-  int64_t tiles_per_batch;   // ceil(lanes / 64)
-  int64_t n_tiles;           // batch * tiles_per_batch
-  int64_t n_chunks;          // ceil(steps / (W * S))
-  int64_t plane;             // record words per (plane, chunk) = n_tiles * 64
-  uint32_t max_spin;
-};
-
-template <int K>
-struct Agg {
-  float v[K];
-};
 
 __device__ __forceinline__ void put_word(uint64_t *p, float v, uint32_t tag) {
   const uint64_t w = (static_cast<uint64_t>(tag) << 32) | static_cast<uint64_t>(__float_as_uint(v));
   __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ bool get_word(uint64_t *p, uint32_t tag, float &v) {
-  const uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  v = __uint_as_float(static_cast<uint32_t>(w));
-  return static_cast<uint32_t>(w >> 32) == tag;
+__device__ __forceinline__ uint64_t load_word(uint64_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ bool word_ok(uint64_t w, uint32_t tag) { return static_cast<uint32_t>(w >> 32) == tag; }
+__device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float(static_cast<uint32_t>(w)); }
+
 // Carry entering `chunk` along one lane chain (see "Determinism" above).
+//
+// Polls the nearest unresolved predecessor's carry word (one load per poll
+// while it waits); when only its aggregate is out, the search passes on to the
+// chunk before. The aggregates between the carry found and `chunk` are then
+// applied one by one in chain order. Each chunk's K aggregate words are read
+// with their loads in flight together.
 template <class P>
 __device__ float look_back(uint64_t *rec, uint64_t *ctl, const Geom &g, int64_t chunk,
                            int64_t slot, uint32_t tag) {
   constexpr int K = P::AGG;
   const int64_t carry_plane = K * g.n_chunks;
   int64_t j = chunk - 1;
-  float base = 0.0f;
   uint32_t spins = 0;
+  float x;
   for (;;) {
-    float v;
-    if (get_word(rec + (carry_plane + j) * g.plane + slot, tag, v)) {
-      base = v;
+    const uint64_t cw = load_word(rec + (carry_plane + j) * g.plane + slot);
+    if (word_ok(cw, tag)) {
+      x = word_val(cw);
       break;
     }
     // Chunk 0 publishes only its carry, never an aggregate.
     bool ready = j > 0;
+    if (ready) {
+      uint64_t aw[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      float t;
-      if (ready) ready = get_word(rec + (k * g.n_chunks + j) * g.plane + slot, tag, t);
+      for (int k = 0; k < K; ++k) aw[k] = load_word(rec + (k * g.n_chunks + j) * g.plane + slot);
+#pragma unroll
+      for (int k = 0; k < K; ++k) ready = ready && word_ok(aw[k], tag);
     }
     if (ready) {
       --j;
@@ -109,37 +104,32 @@ __device__ float look_back(uint64_t *rec, uint64_t *ctl, const Geom &g, int64_t 
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  float x = base;
   for (int64_t i = j + 1; i < chunk; ++i) {
+    uint64_t aw[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) aw[k] = load_word(rec + (k * g.n_chunks + i) * g.plane + slot);
     Agg<K> a;
 #pragma unroll
-    for (int k = 0; k < K; ++k) get_word(rec + (k * g.n_chunks + i) * g.plane + slot, tag, a.v[k]);
+    for (int k = 0; k < K; ++k) a.v[k] = word_val(aw[k]);
     x = P::apply(a, x);
   }
   return x;
 }
 
-// P (a scan policy) provides:
-//   AGG                       floats per aggregate
-//   Params                    operand pointers
-//   Regs<S>                   per-thread register file for S steps
-//   load<S>(prm, g, r, b, n, lane_ok, s0, nvalid)
-//   reduce<S>(r, nvalid) -> Agg        chunk-local aggregate, scan order
-//   compose(later, earlier) -> Agg
-//   apply(agg, x) -> float             act on the carried scalar
-//   initial(prm, b, n) -> float        carry entering scan position 0
-//   walk<S>(prm, g, r, b, n, lane_ok, s0, nvalid, x)   re-walk and store
-template <class P, int W, int S>
+// P is a scan policy (scan_ops.hpp). Grid: n_tiles * n_chunks workgroups of W
+// waves; a workgroup covers 64 V lanes and W * S steps.
+template <class P, int W, int S, int V>
 __global__ void __launch_bounds__(kWave * W)
     lookback_scan_kernel(typename P::Params prm, Geom g, uint64_t *__restrict__ ws) {
   constexpr int K = P::AGG;
+  constexpr int TILE = kWave * V;
   __shared__ uint32_t s_ticket, s_tag;
-  __shared__ float s_agg[K][W][kWave];
-  __shared__ float s_carry[kWave];
+  __shared__ float s_agg[K][W][TILE];
+  __shared__ float s_carry[TILE];
 
   const int tid = static_cast<int>(threadIdx.x);
   const int l = tid & (kWave - 1);
-  const int w = tid / kWave;
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   uint64_t *ctl = ws;
   uint64_t *rec = ws + kHeaderWords;
 
@@ -169,57 +159,84 @@ __global__ void __launch_bounds__(kWave * W)
 
   const int64_t chunk = static_cast<int64_t>(ticket) / g.n_tiles;
   const int64_t tile = static_cast<int64_t>(ticket) % g.n_tiles;
-  const int64_t b = tile / g.tiles_per_batch;
-  const int64_t n = (tile % g.tiles_per_batch) * kWave + l;
-  const bool lane_ok = n < g.lanes;
+  Pos q;
+  q.b = tile / g.tiles_per_batch;
+  q.n0 = (tile % g.tiles_per_batch) * TILE;
+  q.off = static_cast<uint32_t>(l * V);
+  q.ok = q.n0 + q.off < g.lanes;
   const int64_t s0 = chunk * (W * S) + static_cast<int64_t>(w) * S;
-  int64_t rem = g.steps - s0;
+  const int64_t rem = g.steps - s0;
   const int nvalid = rem <= 0 ? 0 : (rem >= S ? S : static_cast<int>(rem));
 
-  typename P::template Regs<S> r;
-  P::template load<S>(prm, g, r, b, n, lane_ok, s0, nvalid);
-  const Agg<K> mine = P::template reduce<S>(r, nvalid);
+  typename P::template Regs<S, V> r;
+  {
+    typename P::template Raw<S, V> raw;
+    P::template fetch<S, V>(prm, g, raw, q, s0, nvalid);
+    P::template prep<S, V>(raw, r);
+  }
+  Agg<K> mine[V];
 #pragma unroll
-  for (int k = 0; k < K; ++k) s_agg[k][w][l] = mine.v[k];
+  for (int v = 0; v < V; ++v) {
+    mine[v] = P::template reduce<S, V>(r, v, nvalid);
+#pragma unroll
+    for (int k = 0; k < K; ++k) s_agg[k][w][l * V + v] = mine[v].v[k];
+  }
   __syncthreads();
 
   if (w == 0) {
-    Agg<K> tot = mine;
 #pragma unroll
-    for (int q = 1; q < W; ++q) {
-      Agg<K> a;
+    for (int v = 0; v < V; ++v) {
+      Agg<K> tot = mine[v];
 #pragma unroll
-      for (int k = 0; k < K; ++k) a.v[k] = s_agg[k][q][l];
-      tot = P::compose(a, tot);
-    }
-    const int64_t slot = tile * kWave + l;
-    float carry = 0.0f;
-    if (lane_ok) {
-      if (chunk == 0) {
-        carry = P::initial(prm, b, n);
-      } else {
+      for (int u = 1; u < W; ++u) {
+        Agg<K> a;
 #pragma unroll
-        for (int k = 0; k < K; ++k) put_word(rec + (k * g.n_chunks + chunk) * g.plane + slot, tot.v[k], tag);
-        carry = look_back<P>(rec, ctl, g, chunk, slot, tag);
+        for (int k = 0; k < K; ++k) a.v[k] = s_agg[k][u][l * V + v];
+        tot = P::compose(a, tot);
       }
-      if (chunk + 1 < g.n_chunks)
-        put_word(rec + (K * g.n_chunks + chunk) * g.plane + slot, P::apply(tot, carry), tag);
+      const int64_t slot = tile * TILE + l * V + v;
+      float carry = 0.0f;
+      if (q.ok) {
+        if (chunk == 0) {
+          carry = P::initial(prm, g, q, v);
+        } else {
+#pragma unroll
+          for (int k = 0; k < K; ++k) put_word(rec + (k * g.n_chunks + chunk) * g.plane + slot, tot.v[k], tag);
+        }
+      }
+      s_carry[l * V + v] = carry;
+      mine[v] = tot;
     }
-    s_carry[l] = carry;
+    if (q.ok && chunk > 0) {
+      // Aggregates of all V lanes are out; now wait for the carries.
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        s_carry[l * V + v] = look_back<P>(rec, ctl, g, chunk, tile * TILE + l * V + v, tag);
+    }
+    if (q.ok && chunk + 1 < g.n_chunks) {
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        put_word(rec + (K * g.n_chunks + chunk) * g.plane + tile * TILE + l * V + v,
+                 P::apply(mine[v], s_carry[l * V + v]), tag);
+    }
   }
   __syncthreads();
 
-  float x = s_carry[l];
+  float x[V];
 #pragma unroll
-  for (int q = 0; q < W - 1; ++q) {
-    if (q < w) {
-      Agg<K> a;
+  for (int v = 0; v < V; ++v) {
+    x[v] = s_carry[l * V + v];
 #pragma unroll
-      for (int k = 0; k < K; ++k) a.v[k] = s_agg[k][q][l];
-      x = P::apply(a, x);
+    for (int u = 0; u < W - 1; ++u) {
+      if (u < w) {
+        Agg<K> a;
+#pragma unroll
+        for (int k = 0; k < K; ++k) a.v[k] = s_agg[k][u][l * V + v];
+        x[v] = P::apply(a, x[v]);
+      }
     }
   }
-  P::template walk<S>(prm, g, r, b, n, lane_ok, s0, nvalid, x);
+  P::template walk<S, V>(prm, g, r, q, s0, nvalid, x);
 }
 
 // Fills a fp32 state tensor with zeros (gradients of an empty sequence).

@@ -1,4 +1,5 @@
-// scan_ops.hpp -- the four scan policies run by lookback_scan_kernel:
+// scan_ops.hpp -- the four scan policies run by the scan kernels
+// (lookback_scan_kernel, stripe_scan_kernel):
 //
 //   MobiusFwd   lam_t = (A lam_{t-1} + B) / max(C lam_{t-1} + D, EPS)
 //   MobiusBwd   exact scalar adjoint of MobiusFwd (reverse in time)
@@ -17,11 +18,47 @@
 // nu_t = dlam_t + gain_{t+1} nu_{t+1} becomes w_t = gain_t (dlam_t + w_{t+1}),
 // an affine map whose coefficients come from step t alone. The carry passed
 // between chunks is w, and dlam0 (dh0) is w_0.
+//
+// Policy interface (P):
+//   AGG                                   floats per aggregate (monoid element)
+//   Params                                operand pointers
+//   Raw<S, V>                             registers filled by fetch (loads only)
+//   Regs<S, V>                            registers after prep (per-step coefficients)
+//   fetch<S, V>(prm, g, raw, pos, s0, nvalid)  issue the loads of scan positions
+//                                         [s0, s0 + nvalid) (nvalid <= S, wave-uniform)
+//   prep<S, V>(raw, regs)                 turn loaded values into coefficients
+//   reduce<S, V>(regs, v, nvalid) -> Agg  chunk-local aggregate of lane v, scan order
+//   compose(later, earlier) -> Agg
+//   apply(agg, x) -> float                act on the carried scalar
+//   initial(prm, g, pos, v) -> float      carry entering scan position 0 (lane v)
+//   walk<S, V>(prm, g, regs, pos, s0, nvalid, x[V])   re-walk and store
+// A thread owns V consecutive lanes (V = 1, 2 or 4) and moves them with one
+// vector load or store per operand and step.
+// fetch only loads, so a kernel can issue the next chunk's fetch before it
+// works on the current one.
 #pragma once
 
-#include "lookback_scan.hpp"
+#include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace kla {
+
+constexpr float kEps = 1e-12f;   // EPS = P_MIN of the reference (kla_ops.py:43-44)
+constexpr int kWave = 64;
+
+struct Geom {
+  int64_t batch, steps, lanes;
+  int64_t tiles_per_batch;   // ceil(lanes / (64 V)): a tile is the 64 V lanes of one workgroup
+  int64_t n_tiles;           // batch * tiles_per_batch
+  int64_t n_chunks;          // look-back kernel: ceil(steps / (W * S))
+  int64_t plane;             // look-back kernel: record words per (plane, chunk) = n_tiles * 64 V
+  uint32_t max_spin;         // look-back kernel: polls before a wait gives up
+};
+
+template <int K>
+struct Agg {
+  float v[K];
+};
 
 // ---------------------------------------------------------------- element I/O
 
@@ -51,13 +88,126 @@ __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
   return bf16_t{static_cast<uint16_t>(u >> 16)};
 }
 
-// Scan position s of a chain maps to time t = s (forward) or steps-1-s (reverse).
-__device__ __forceinline__ int64_t time_of(bool reverse, const Geom &g, int64_t s) {
-  return reverse ? g.steps - 1 - s : s;
+// Where one thread sits: batch b and lane tile [n0, n0 + 64 V) are wave-uniform
+// (so row addresses below live in SGPRs); the thread owns lanes
+// [n0 + off, n0 + off + V) with off = V * (thread index in the wave).
+struct Pos {
+  int64_t b;      // batch
+  int64_t n0;     // first lane of the tile
+  uint32_t off;   // first lane of this thread within the tile
+  bool ok;        // n0 + off < lanes (lanes is a multiple of V, so all V lanes are valid)
+};
+
+// Element index of (b, t, n0): the start of a tile's row at time t (wave-uniform).
+__device__ __forceinline__ int64_t row_index(const Geom &g, const Pos &q, int64_t t) {
+  return (q.b * g.steps + t) * g.lanes + q.n0;
 }
 
-__device__ __forceinline__ int64_t seq_index(const Geom &g, int64_t b, int64_t t, int64_t n) {
-  return (b * g.steps + t) * g.lanes + n;
+// The thread's first element in the row starting at `row`: uniform base plus a
+// 32-bit lane offset, which the compiler turns into SGPR-base addressing.
+template <class T>
+__device__ __forceinline__ T *at(T *p, int64_t row, const Pos &q) {
+  return (p + row) + q.off;
+}
+
+__device__ __forceinline__ int64_t state_index(const Geom &g, const Pos &q) {
+  return q.b * g.lanes + q.n0 + q.off;
+}
+
+// Sequence tensors are streamed: every element is read once and written once,
+// so their loads and stores carry the nontemporal hint (they do not displace
+// reused lines from the caches). One dword / dwordx2 / dwordx4 access per
+// operand and step moves the V lanes of a thread.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// V consecutive sequence elements, widened to fp32.
+template <int V>
+__device__ __forceinline__ void load_v(const float *p, float (&o)[V]) {
+  if constexpr (V == 1) {
+    o[0] = __builtin_nontemporal_load(p);
+  } else if constexpr (V == 2) {
+    const f32x2 t = __builtin_nontemporal_load(reinterpret_cast<const f32x2 *>(p));
+    o[0] = t.x;
+    o[1] = t.y;
+  } else {
+    static_assert(V == 4, "V must be 1, 2 or 4");
+    const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+    o[0] = t.x;
+    o[1] = t.y;
+    o[2] = t.z;
+    o[3] = t.w;
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void load_v(const bf16_t *p, float (&o)[V]) {
+  if constexpr (V == 1) {
+    const uint16_t u = __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
+    o[0] = __uint_as_float(static_cast<uint32_t>(u) << 16);
+  } else if constexpr (V == 2) {
+    const uint32_t u = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+    o[0] = __uint_as_float(u << 16);
+    o[1] = __uint_as_float(u & 0xFFFF0000u);
+  } else {
+    static_assert(V == 4, "V must be 1, 2 or 4");
+    const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+    o[0] = __uint_as_float(u.x << 16);
+    o[1] = __uint_as_float(u.x & 0xFFFF0000u);
+    o[2] = __uint_as_float(u.y << 16);
+    o[3] = __uint_as_float(u.y & 0xFFFF0000u);
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void store_v(float *p, const float (&x)[V]) {
+  if constexpr (V == 1) {
+    __builtin_nontemporal_store(x[0], p);
+  } else if constexpr (V == 2) {
+    const f32x2 t = {x[0], x[1]};
+    __builtin_nontemporal_store(t, reinterpret_cast<f32x2 *>(p));
+  } else {
+    static_assert(V == 4, "V must be 1, 2 or 4");
+    const f32x4 t = {x[0], x[1], x[2], x[3]};
+    __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(p));
+  }
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(from_f32<bf16_t>(lo).bits) | (static_cast<uint32_t>(from_f32<bf16_t>(hi).bits) << 16);
+}
+
+template <int V>
+__device__ __forceinline__ void store_v(bf16_t *p, const float (&x)[V]) {
+  if constexpr (V == 1) {
+    __builtin_nontemporal_store(from_f32<bf16_t>(x[0]).bits, reinterpret_cast<uint16_t *>(p));
+  } else if constexpr (V == 2) {
+    __builtin_nontemporal_store(pack_bf16x2(x[0], x[1]), reinterpret_cast<uint32_t *>(p));
+  } else {
+    static_assert(V == 4, "V must be 1, 2 or 4");
+    const u32x2 u = {pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+    __builtin_nontemporal_store(u, reinterpret_cast<u32x2 *>(p));
+  }
+}
+
+// V consecutive elements of a [batch, lanes] fp32 state tensor (ordinary access).
+template <int V>
+__device__ __forceinline__ void load_state_v(const float *p, float (&o)[V]) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) o[v] = p[v];
+}
+
+template <int V>
+__device__ __forceinline__ void store_state_v(float *p, const float (&x)[V]) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) p[v] = x[v];
+}
+
+template <int V>
+__device__ __forceinline__ void fill_v(float (&o)[V], float x) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) o[v] = x;
 }
 
 // ------------------------------------------------------------ affine monoid
@@ -69,6 +219,20 @@ __device__ __forceinline__ Agg<2> affine_compose(const Agg<2> &L, const Agg<2> &
 }
 
 __device__ __forceinline__ float affine_apply(const Agg<2> &a, float x) { return a.v[0] * x + a.v[1]; }
+
+// Aggregate of the affine steps (m_j, c_j), j < nvalid, in order.
+template <int S, class M, class C>
+__device__ __forceinline__ Agg<2> affine_reduce(M m, C c, int nvalid) {
+  Agg<2> acc{{1.0f, 0.0f}};
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    if (j < nvalid) {
+      const Agg<2> f{{m(j), c(j)}};
+      acc = (j == 0) ? f : affine_compose(f, acc);
+    }
+  }
+  return acc;
+}
 
 // ------------------------------------------------------------ Moebius monoid
 // [[a, b], [c, d]] acts as x -> (a x + b) / (c x + d). Composition is the 2x2
@@ -98,64 +262,80 @@ __device__ __forceinline__ float mobius_apply(const Agg<4> &m, float x) {
 template <bool HAS_D>
 struct MobiusFwd {
   static constexpr int AGG = 4;
+  using IO = float;
   struct Params {
     const float *A, *B, *C, *D, *lam0;
     float *lam;
-    int64_t state_stride;   // lanes: state tensors are [batch, lanes]
   };
-  template <int S>
-  struct Regs {
-    float a[S], b[S], c[S], d[HAS_D ? S : 1];
+  template <int S, int V>
+  struct Raw {
+    float a[S][V], b[S][V], c[S][V], d[HAS_D ? S : 1][V];
   };
+  template <int S, int V>
+  using Regs = Raw<S, V>;
 
-  template <int S>
-  __device__ static void load(const Params &p, const Geom &g, Regs<S> &r, int64_t bb, int64_t n,
-                              bool ok, int64_t s0, int nvalid) {
+  template <int S, int V>
+  __device__ static void fetch(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q, int64_t s0,
+                               int nvalid) {
+    const int64_t row = row_index(g, q, s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-      r.a[j] = 1.0f;
-      r.b[j] = 0.0f;
-      r.c[j] = 0.0f;
-      if (HAS_D) r.d[HAS_D ? j : 0] = 1.0f;
-      if (ok && j < nvalid) {
-        const int64_t i = seq_index(g, bb, s0 + j, n);
-        r.a[j] = p.A[i];
-        r.b[j] = p.B[i];
-        r.c[j] = p.C[i];
-        if (HAS_D) r.d[HAS_D ? j : 0] = p.D[i];
+      fill_v(r.a[j], 1.0f);
+      fill_v(r.b[j], 0.0f);
+      fill_v(r.c[j], 0.0f);
+      if (HAS_D) fill_v(r.d[HAS_D ? j : 0], 1.0f);
+    }
+    if (!q.ok) return;
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      if (j < nvalid) {
+        const int64_t rj = row + j * g.lanes;
+        load_v<V>(at(p.A, rj, q), r.a[j]);
+        load_v<V>(at(p.B, rj, q), r.b[j]);
+        load_v<V>(at(p.C, rj, q), r.c[j]);
+        if (HAS_D) load_v<V>(at(p.D, rj, q), r.d[HAS_D ? j : 0]);
       }
     }
   }
 
-  template <int S>
-  __device__ static Agg<4> leaf(const Regs<S> &r, int j) {
-    return Agg<4>{{r.a[j], r.b[j], r.c[j], HAS_D ? r.d[HAS_D ? j : 0] : 1.0f}};
+  template <int S, int V>
+  __device__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
+    r = raw;
   }
 
-  template <int S>
-  __device__ static Agg<4> reduce(const Regs<S> &r, int nvalid) {
+  template <int S, int V>
+  __device__ static Agg<4> leaf(const Regs<S, V> &r, int j, int v) {
+    return Agg<4>{{r.a[j][v], r.b[j][v], r.c[j][v], HAS_D ? r.d[HAS_D ? j : 0][v] : 1.0f}};
+  }
+
+  template <int S, int V>
+  __device__ static Agg<4> reduce(const Regs<S, V> &r, int v, int nvalid) {
     Agg<4> m{{1.0f, 0.0f, 0.0f, 1.0f}};
 #pragma unroll
     for (int j = 0; j < S; ++j)
-      if (j < nvalid) m = (j == 0) ? leaf<S>(r, 0) : mobius_compose(leaf<S>(r, j), m);
+      if (j < nvalid) m = (j == 0) ? leaf<S, V>(r, 0, v) : mobius_compose(leaf<S, V>(r, j, v), m);
     return m;
   }
 
   __device__ static Agg<4> compose(const Agg<4> &L, const Agg<4> &M) { return mobius_compose(L, M); }
   __device__ static float apply(const Agg<4> &m, float x) { return mobius_apply(m, x); }
-  __device__ static float initial(const Params &p, int64_t bb, int64_t n) {
-    return p.lam0 ? p.lam0[bb * p.state_stride + n] : 1.0f;
+  __device__ static float initial(const Params &p, const Geom &g, const Pos &q, int v) {
+    return p.lam0 ? p.lam0[state_index(g, q) + v] : 1.0f;
   }
 
-  template <int S>
-  __device__ static void walk(const Params &p, const Geom &g, const Regs<S> &r, int64_t bb,
-                              int64_t n, bool ok, int64_t s0, int nvalid, float x) {
+  template <int S, int V>
+  __device__ static void walk(const Params &p, const Geom &g, const Regs<S, V> &r, const Pos &q,
+                              int64_t s0, int nvalid, float (&x)[V]) {
+    const int64_t row = row_index(g, q, s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
-        const float d = HAS_D ? r.d[HAS_D ? j : 0] : 1.0f;
-        x = (r.a[j] * x + r.b[j]) / fmaxf(r.c[j] * x + d, kEps);
-        if (ok) p.lam[seq_index(g, bb, s0 + j, n)] = x;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float d = HAS_D ? r.d[HAS_D ? j : 0][v] : 1.0f;
+          x[v] = (r.a[j][v] * x[v] + r.b[j][v]) / fmaxf(r.c[j][v] * x[v] + d, kEps);
+        }
+        if (q.ok) store_v<V>(at(p.lam, row + j * g.lanes, q), x);
       }
     }
   }
@@ -168,150 +348,194 @@ struct MobiusFwd {
 //   nu_t   = dlam_t + w_{t+1},   w_t = gain_t nu_t,   w_T = 0
 //   q = nu_t / den_t:  dA = q lam_{t-1}, dB = q, dC = -q lam_t lam_{t-1}, dD = -q lam_t
 //   dlam0 = w_0
+// Scan position s0 + j is time t = T-1-s0-j, at row `row - j * lanes`.
 
 template <bool HAS_D>
 struct MobiusBwd {
   static constexpr int AGG = 2;
+  using IO = float;
   struct Params {
     const float *dlam, *A, *B, *C, *D, *lam0, *lam;
     float *dA, *dB, *dC, *dD, *dlam0;
-    int64_t state_stride;   // lanes: state tensors are [batch, lanes]
   };
-  template <int S>
+  template <int S, int V>
+  struct Raw {
+    // lv[j] = lam at step j's time t, lv[j+1] = lam_{t-1} (lam0 before time 0).
+    float dl[S][V], a[S][V], b[S][V], c[S][V], d[HAS_D ? S : 1][V], lv[S + 1][V];
+  };
+  template <int S, int V>
   struct Regs {
-    float dl[S], den[S], gain[S], lv[S + 1];   // lv[j] = lam at step j's time, lv[j+1] = lam_{t-1}
+    float dl[S][V], den[S][V], gain[S][V], lv[S + 1][V];
   };
 
-  template <int S>
-  __device__ static void load(const Params &p, const Geom &g, Regs<S> &r, int64_t bb, int64_t n,
-                              bool ok, int64_t s0, int nvalid) {
-    const float lam_init = (ok && p.lam0) ? p.lam0[bb * p.state_stride + n] : 1.0f;
+  template <int S, int V>
+  __device__ static void fetch(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q, int64_t s0,
+                               int nvalid) {
+    const int64_t row = row_index(g, q, g.steps - 1 - s0);
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      fill_v(r.dl[j], 0.0f);
+      fill_v(r.a[j], 1.0f);
+      fill_v(r.b[j], 0.0f);
+      fill_v(r.c[j], 0.0f);
+      if (HAS_D) fill_v(r.d[HAS_D ? j : 0], 1.0f);
+      fill_v(r.lv[j], 1.0f);
+    }
+    fill_v(r.lv[S], 1.0f);
+    if (!q.ok) return;
 #pragma unroll
     for (int j = 0; j <= S; ++j) {
-      r.lv[j] = 1.0f;
-      // Step j's time is t = T-1-s0-j; lv[j] needs t >= 0, lv[j] for t == -1 is lam0.
-      if (ok && j <= nvalid) {
-        const int64_t t = g.steps - 1 - s0 - j;
-        r.lv[j] = (t >= 0) ? p.lam[seq_index(g, bb, t, n)] : lam_init;
+      if (j < nvalid) {
+        load_v<V>(at(p.lam, row - j * g.lanes, q), r.lv[j]);
+      } else if (j == nvalid) {
+        // Time T-1-s0-nvalid: lam there, or lam0 once the scan has passed time 0.
+        if (s0 + nvalid < g.steps) {
+          load_v<V>(at(p.lam, row - j * g.lanes, q), r.lv[j]);
+        } else if (p.lam0) {
+          load_state_v<V>(p.lam0 + state_index(g, q), r.lv[j]);
+        }
       }
     }
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-      r.dl[j] = 0.0f;
-      r.den[j] = 1.0f;
-      r.gain[j] = 1.0f;
-      if (ok && j < nvalid) {
-        const int64_t i = seq_index(g, bb, g.steps - 1 - s0 - j, n);
-        const float A = p.A[i], B = p.B[i], C = p.C[i];
-        const float D = HAS_D ? p.D[i] : 1.0f;
-        r.dl[j] = p.dlam[i];
-        const float den = fmaxf(C * r.lv[j + 1] + D, kEps);
-        r.den[j] = den;
-        r.gain[j] = (A * D - B * C) / (den * den);
+      if (j < nvalid) {
+        const int64_t rj = row - j * g.lanes;
+        load_v<V>(at(p.dlam, rj, q), r.dl[j]);
+        load_v<V>(at(p.A, rj, q), r.a[j]);
+        load_v<V>(at(p.B, rj, q), r.b[j]);
+        load_v<V>(at(p.C, rj, q), r.c[j]);
+        if (HAS_D) load_v<V>(at(p.D, rj, q), r.d[HAS_D ? j : 0]);
       }
     }
   }
 
-  template <int S>
-  __device__ static Agg<2> reduce(const Regs<S> &r, int nvalid) {
-    Agg<2> m{{1.0f, 0.0f}};
+  template <int S, int V>
+  __device__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
+#pragma unroll
+    for (int j = 0; j <= S; ++j)
+#pragma unroll
+      for (int v = 0; v < V; ++v) r.lv[j][v] = raw.lv[j][v];
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-      if (j < nvalid) {
-        const Agg<2> f{{r.gain[j], r.gain[j] * r.dl[j]}};
-        m = (j == 0) ? f : affine_compose(f, m);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float D = HAS_D ? raw.d[HAS_D ? j : 0][v] : 1.0f;
+        const float den = fmaxf(raw.c[j][v] * raw.lv[j + 1][v] + D, kEps);
+        r.dl[j][v] = raw.dl[j][v];
+        r.den[j][v] = den;
+        r.gain[j][v] = (raw.a[j][v] * D - raw.b[j][v] * raw.c[j][v]) / (den * den);
       }
     }
-    return m;
+  }
+
+  template <int S, int V>
+  __device__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
+    return affine_reduce<S>([&](int j) { return r.gain[j][v]; },
+                            [&](int j) { return r.gain[j][v] * r.dl[j][v]; }, nvalid);
   }
 
   __device__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
   __device__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
-  __device__ static float initial(const Params &, int64_t, int64_t) { return 0.0f; }
+  __device__ static float initial(const Params &, const Geom &, const Pos &, int) { return 0.0f; }
 
-  template <int S>
-  __device__ static void walk(const Params &p, const Geom &g, const Regs<S> &r, int64_t bb,
-                              int64_t n, bool ok, int64_t s0, int nvalid, float x) {
+  template <int S, int V>
+  __device__ static void walk(const Params &p, const Geom &g, const Regs<S, V> &r, const Pos &q,
+                              int64_t s0, int nvalid, float (&x)[V]) {
+    const int64_t row = row_index(g, q, g.steps - 1 - s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
-        const int64_t t = g.steps - 1 - s0 - j;
-        const int64_t i = seq_index(g, bb, t, n);
-        const float nu = r.dl[j] + x;
-        const float q = nu / r.den[j];
-        const float lt = r.lv[j], lp = r.lv[j + 1];
-        if (ok) {
-          if (p.dA) p.dA[i] = q * lp;
-          if (p.dB) p.dB[i] = q;
-          if (p.dC) p.dC[i] = (-q * lt) * lp;
-          if (HAS_D && p.dD) p.dD[i] = -q * lt;
+        const int64_t rj = row - j * g.lanes;
+        float da[V], db[V], dc[V], dd[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          const float nu = r.dl[j][v] + x[v];
+          const float qv = nu / r.den[j][v];
+          const float lt = r.lv[j][v], lp = r.lv[j + 1][v];
+          da[v] = qv * lp;
+          db[v] = qv;
+          dc[v] = (-qv * lt) * lp;
+          dd[v] = -qv * lt;
+          x[v] = r.gain[j][v] * nu;
         }
-        x = r.gain[j] * nu;
-        if (t == 0 && ok && p.dlam0) p.dlam0[bb * p.state_stride + n] = x;
+        if (q.ok) {
+          if (p.dA) store_v<V>(at(p.dA, rj, q), da);
+          if (p.dB) store_v<V>(at(p.dB, rj, q), db);
+          if (p.dC) store_v<V>(at(p.dC, rj, q), dc);
+          if (HAS_D && p.dD) store_v<V>(at(p.dD, rj, q), dd);
+        }
       }
     }
+    // The position that is time 0 closes the chain: dlam0 = w_0.
+    if (s0 + nvalid == g.steps && nvalid > 0 && q.ok && p.dlam0) store_state_v<V>(p.dlam0 + state_index(g, q), x);
   }
 };
 
 // ================================================================ AffineFwd
 // h_t = g_t h_{t-1} + u_t, h_{-1} = h0 (reference tiled_mobius_scan.py:161-203).
 
-template <class IO>
+template <class IOT>
 struct AffineFwd {
   static constexpr int AGG = 2;
+  using IO = IOT;
   struct Params {
     const IO *g, *u;
     const float *h0;
     IO *h;
-    int64_t state_stride;
   };
-  template <int S>
-  struct Regs {
-    float g[S], u[S];
+  template <int S, int V>
+  struct Raw {
+    float g[S][V], u[S][V];
   };
+  template <int S, int V>
+  using Regs = Raw<S, V>;
 
-  template <int S>
-  __device__ static void load(const Params &p, const Geom &gm, Regs<S> &r, int64_t bb, int64_t n,
-                              bool ok, int64_t s0, int nvalid) {
+  template <int S, int V>
+  __device__ static void fetch(const Params &p, const Geom &gm, Raw<S, V> &r, const Pos &q, int64_t s0,
+                               int nvalid) {
+    const int64_t row = row_index(gm, q, s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-      r.g[j] = 1.0f;
-      r.u[j] = 0.0f;
-      if (ok && j < nvalid) {
-        const int64_t i = seq_index(gm, bb, s0 + j, n);
-        r.g[j] = to_f32(p.g[i]);
-        r.u[j] = to_f32(p.u[i]);
+      fill_v(r.g[j], 1.0f);
+      fill_v(r.u[j], 0.0f);
+    }
+    if (!q.ok) return;
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      if (j < nvalid) {
+        const int64_t rj = row + j * gm.lanes;
+        load_v<V>(at(p.g, rj, q), r.g[j]);
+        load_v<V>(at(p.u, rj, q), r.u[j]);
       }
     }
   }
 
-  template <int S>
-  __device__ static Agg<2> reduce(const Regs<S> &r, int nvalid) {
-    Agg<2> m{{1.0f, 0.0f}};
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      if (j < nvalid) {
-        const Agg<2> f{{r.g[j], r.u[j]}};
-        m = (j == 0) ? f : affine_compose(f, m);
-      }
-    }
-    return m;
+  template <int S, int V>
+  __device__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
+    r = raw;
+  }
+
+  template <int S, int V>
+  __device__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
+    return affine_reduce<S>([&](int j) { return r.g[j][v]; }, [&](int j) { return r.u[j][v]; }, nvalid);
   }
 
   __device__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
   __device__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
-  __device__ static float initial(const Params &p, int64_t bb, int64_t n) {
-    return p.h0 ? p.h0[bb * p.state_stride + n] : 0.0f;
+  __device__ static float initial(const Params &p, const Geom &gm, const Pos &q, int v) {
+    return p.h0 ? p.h0[state_index(gm, q) + v] : 0.0f;
   }
 
-  template <int S>
-  __device__ static void walk(const Params &p, const Geom &gm, const Regs<S> &r, int64_t bb,
-                              int64_t n, bool ok, int64_t s0, int nvalid, float x) {
+  template <int S, int V>
+  __device__ static void walk(const Params &p, const Geom &gm, const Regs<S, V> &r, const Pos &q,
+                              int64_t s0, int nvalid, float (&x)[V]) {
+    const int64_t row = row_index(gm, q, s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
-        x = r.g[j] * x + r.u[j];
-        if (ok) p.h[seq_index(gm, bb, s0 + j, n)] = from_f32<IO>(x);
+#pragma unroll
+        for (int v = 0; v < V; ++v) x[v] = r.g[j][v] * x[v] + r.u[j][v];
+        if (q.ok) store_v<V>(at(p.h, row + j * gm.lanes, q), x);
       }
     }
   }
@@ -322,74 +546,85 @@ struct AffineFwd {
 //   mu_t = dh_t + w_{t+1},  w_t = g_t mu_t,  w_T = 0
 //   dg_t = mu_t h_{t-1} (h_{-1} = h0 or 0),  du_t = mu_t,  dh0 = w_0
 
-template <class IO>
+template <class IOT>
 struct AffineBwd {
   static constexpr int AGG = 2;
+  using IO = IOT;
   struct Params {
     const IO *dh, *g, *h;
     const float *h0;
     IO *dg, *du;
     float *dh0;
-    int64_t state_stride;
   };
-  template <int S>
-  struct Regs {
-    float dh[S], g[S], hp[S];
+  template <int S, int V>
+  struct Raw {
+    float dh[S][V], g[S][V], hp[S][V];   // hp[j] = h_{t-1} for step j's time t
   };
+  template <int S, int V>
+  using Regs = Raw<S, V>;
 
-  template <int S>
-  __device__ static void load(const Params &p, const Geom &gm, Regs<S> &r, int64_t bb, int64_t n,
-                              bool ok, int64_t s0, int nvalid) {
-    const float h_init = (ok && p.h0) ? p.h0[bb * p.state_stride + n] : 0.0f;
+  template <int S, int V>
+  __device__ static void fetch(const Params &p, const Geom &gm, Raw<S, V> &r, const Pos &q, int64_t s0,
+                               int nvalid) {
+    const int64_t row = row_index(gm, q, gm.steps - 1 - s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-      r.dh[j] = 0.0f;
-      r.g[j] = 1.0f;
-      r.hp[j] = 0.0f;
-      if (ok && j < nvalid) {
-        const int64_t t = gm.steps - 1 - s0 - j;
-        const int64_t i = seq_index(gm, bb, t, n);
-        r.dh[j] = to_f32(p.dh[i]);
-        r.g[j] = to_f32(p.g[i]);
-        r.hp[j] = (t > 0) ? to_f32(p.h[i - gm.lanes]) : h_init;
+      fill_v(r.dh[j], 0.0f);
+      fill_v(r.g[j], 1.0f);
+      fill_v(r.hp[j], 0.0f);
+    }
+    if (!q.ok) return;
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      if (j < nvalid) {
+        const int64_t rj = row - j * gm.lanes;
+        load_v<V>(at(p.dh, rj, q), r.dh[j]);
+        load_v<V>(at(p.g, rj, q), r.g[j]);
+        if (s0 + j + 1 < gm.steps)
+          load_v<V>(at(p.h, rj - gm.lanes, q), r.hp[j]);
+        else if (p.h0)
+          load_state_v<V>(p.h0 + state_index(gm, q), r.hp[j]);
       }
     }
   }
 
-  template <int S>
-  __device__ static Agg<2> reduce(const Regs<S> &r, int nvalid) {
-    Agg<2> m{{1.0f, 0.0f}};
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      if (j < nvalid) {
-        const Agg<2> f{{r.g[j], r.g[j] * r.dh[j]}};
-        m = (j == 0) ? f : affine_compose(f, m);
-      }
-    }
-    return m;
+  template <int S, int V>
+  __device__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
+    r = raw;
+  }
+
+  template <int S, int V>
+  __device__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
+    return affine_reduce<S>([&](int j) { return r.g[j][v]; },
+                            [&](int j) { return r.g[j][v] * r.dh[j][v]; }, nvalid);
   }
 
   __device__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
   __device__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
-  __device__ static float initial(const Params &, int64_t, int64_t) { return 0.0f; }
+  __device__ static float initial(const Params &, const Geom &, const Pos &, int) { return 0.0f; }
 
-  template <int S>
-  __device__ static void walk(const Params &p, const Geom &gm, const Regs<S> &r, int64_t bb,
-                              int64_t n, bool ok, int64_t s0, int nvalid, float x) {
+  template <int S, int V>
+  __device__ static void walk(const Params &p, const Geom &gm, const Regs<S, V> &r, const Pos &q,
+                              int64_t s0, int nvalid, float (&x)[V]) {
+    const int64_t row = row_index(gm, q, gm.steps - 1 - s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
-        const int64_t t = gm.steps - 1 - s0 - j;
-        const int64_t i = seq_index(gm, bb, t, n);
-        const float mu = r.dh[j] + x;
-        if (ok) {
-          if (p.dg) p.dg[i] = from_f32<IO>(mu * r.hp[j]);
-          if (p.du) p.du[i] = from_f32<IO>(mu);
+        const int64_t rj = row - j * gm.lanes;
+        float dg[V], mu[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          mu[v] = r.dh[j][v] + x[v];
+          dg[v] = mu[v] * r.hp[j][v];
+          x[v] = r.g[j][v] * mu[v];
         }
-        x = r.g[j] * mu;
-        if (t == 0 && ok && p.dh0) p.dh0[bb * p.state_stride + n] = x;
+        if (q.ok) {
+          if (p.dg) store_v<V>(at(p.dg, rj, q), dg);
+          if (p.du) store_v<V>(at(p.du, rj, q), mu);
+        }
       }
     }
+    if (s0 + nvalid == gm.steps && nvalid > 0 && q.ok && p.dh0) store_state_v<V>(p.dh0 + state_index(gm, q), x);
   }
 };
 
