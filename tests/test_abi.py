@@ -1,0 +1,175 @@
+"""The C ABI of libkla_hip.so, exercised on the CPU (no GPU needed).
+
+* the library loads, reports the ABI version the Python binding expects, and
+  exports every function include/kla_hip.h declares (and the binding binds);
+* every argument check returns its documented status and message before any
+  HIP call: NULL operands, negative or oversized shapes, unknown dtype or scan
+  kind, operands not aligned to their element, a missing / misaligned / short
+  workspace. Calls here use fake device addresses that the library rejects
+  before dereferencing or launching anything;
+* empty problems succeed without launching;
+* the last-error message is per thread.
+
+Mirrors the reference binding's TORCH_CHECK validation
+(src/kla/ops/kernels/cuda/v2_2/kla_matmul_scan.cu:35-59).
+"""
+
+import ctypes
+import os
+import re
+import threading
+
+import pytest
+
+from kla.ops.hip import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "kla_hip.h")
+
+# Fake, never-dereferenced device addresses: aligned (ALIGNED) and not (ODD).
+ALIGNED = 0x7F0000000000
+ODD = ALIGNED + 2
+WS = 0x7F0000100000  # 256-byte aligned
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kla_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.lib()
+
+
+def err(lib):
+    return lib.kla_hip_last_error().decode()
+
+
+def test_library_loads_and_reports_abi(lib):
+    assert lib.kla_hip_abi_version() == _lib.ABI_VERSION
+
+
+def test_every_declared_function_is_exported_and_bound(lib):
+    declared = header_functions()
+    assert len(declared) >= 8
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in kla_hip.h but not exported"
+    assert sorted(_lib._SIGNATURES) == declared, "ctypes binding and header disagree"
+
+
+def test_workspace_bytes(lib):
+    for kind in range(4):
+        n = lib.kla_scan_workspace_bytes(kind, 8, 4096, 2048)
+        assert n > 256 and n % 8 == 0
+        # Grows with the problem, never shrinks.
+        assert lib.kla_scan_workspace_bytes(kind, 8, 8192, 2048) >= n
+        assert lib.kla_scan_workspace_bytes(kind, 1, 1, 1) > 0
+    assert lib.kla_scan_workspace_bytes(9, 8, 4096, 2048) == 0
+    assert "unknown scan kind 9" in err(lib)
+    assert lib.kla_scan_workspace_bytes(0, -1, 4, 4) == 0
+    assert "negative size" in err(lib)
+
+
+def _mobius_fwd(lib, A=ALIGNED, B=ALIGNED, C=ALIGNED, D=None, lam0=None, lam=ALIGNED, shape=(2, 3, 4),
+                ws=WS, ws_bytes=1 << 40):
+    return lib.kla_mobius_scan_fwd(A, B, C, D, lam0, lam, *shape, ws, ws_bytes, None)
+
+
+def test_mobius_fwd_validation(lib):
+    assert _mobius_fwd(lib, A=None) == _lib.KLA_ERR_INVALID_ARG
+    assert "must not be NULL" in err(lib)
+    assert _mobius_fwd(lib, shape=(2, -3, 4)) == _lib.KLA_ERR_INVALID_ARG
+    assert "negative size" in err(lib)
+    assert _mobius_fwd(lib, shape=(2, 3, (1 << 31) + 1)) == _lib.KLA_ERR_INVALID_ARG
+    assert "above 2^31" in err(lib)
+    assert _mobius_fwd(lib, C=ODD) == _lib.KLA_ERR_ALIGN
+    assert _mobius_fwd(lib, D=ODD) == _lib.KLA_ERR_ALIGN
+    assert _mobius_fwd(lib, lam0=ODD) == _lib.KLA_ERR_ALIGN
+    assert _mobius_fwd(lib, ws=None) == _lib.KLA_ERR_WORKSPACE
+    assert "workspace is NULL" in err(lib)
+    assert _mobius_fwd(lib, ws=WS + 8) == _lib.KLA_ERR_WORKSPACE
+    assert "256-byte aligned" in err(lib)
+    assert _mobius_fwd(lib, ws_bytes=64) == _lib.KLA_ERR_WORKSPACE
+    assert "needed" in err(lib)
+    # Empty problems succeed without touching any operand.
+    for shape in [(0, 3, 4), (2, 0, 4), (2, 3, 0)]:
+        assert _mobius_fwd(lib, A=None, B=None, C=None, lam=None, ws=None, shape=shape) == _lib.KLA_OK
+
+
+def test_mobius_bwd_validation(lib):
+    def call(**kw):
+        a = dict(dlam=ALIGNED, A=ALIGNED, B=ALIGNED, C=ALIGNED, D=None, lam0=None, lam=ALIGNED, dA=ALIGNED,
+                 dB=ALIGNED, dC=ALIGNED, dD=None, dlam0=None, shape=(2, 3, 4), ws=WS, ws_bytes=1 << 40)
+        a.update(kw)
+        return lib.kla_mobius_scan_bwd(a["dlam"], a["A"], a["B"], a["C"], a["D"], a["lam0"], a["lam"], a["dA"],
+                                       a["dB"], a["dC"], a["dD"], a["dlam0"], *a["shape"], a["ws"], a["ws_bytes"],
+                                       None)
+
+    assert call(lam=None) == _lib.KLA_ERR_INVALID_ARG
+    assert call(dlam=None) == _lib.KLA_ERR_INVALID_ARG
+    assert call(dB=ODD) == _lib.KLA_ERR_ALIGN
+    assert call(dlam0=ODD) == _lib.KLA_ERR_ALIGN
+    assert call(ws=None) == _lib.KLA_ERR_WORKSPACE
+    assert call(ws_bytes=8) == _lib.KLA_ERR_WORKSPACE
+    # Zero steps and no state gradient asked for: nothing to do.
+    assert call(shape=(2, 0, 4), dlam=None, A=None, B=None, C=None, lam=None) == _lib.KLA_OK
+    assert call(shape=(0, 5, 4)) == _lib.KLA_OK
+
+
+def test_affine_validation(lib):
+    def fwd(dtype=_lib.KLA_DTYPE_F32, g=ALIGNED, u=ALIGNED, h0=None, h=ALIGNED, shape=(2, 3, 4), ws=WS,
+            ws_bytes=1 << 40):
+        return lib.kla_affine_scan_fwd(dtype, g, u, h0, h, *shape, ws, ws_bytes, None)
+
+    assert fwd(dtype=7) == _lib.KLA_ERR_DTYPE
+    assert "unsupported dtype code 7" in err(lib)
+    assert fwd(u=None) == _lib.KLA_ERR_INVALID_ARG
+    assert fwd(g=ODD) == _lib.KLA_ERR_ALIGN
+    # bf16 operands need 2-byte alignment only.
+    assert fwd(dtype=_lib.KLA_DTYPE_BF16, g=ALIGNED + 1) == _lib.KLA_ERR_ALIGN
+    assert fwd(dtype=_lib.KLA_DTYPE_BF16, g=ODD, ws=None) == _lib.KLA_ERR_WORKSPACE
+    assert fwd(h0=ODD) == _lib.KLA_ERR_ALIGN
+    assert fwd(ws_bytes=0) == _lib.KLA_ERR_WORKSPACE
+
+    def bwd(dtype=_lib.KLA_DTYPE_F32, dh=ALIGNED, g=ALIGNED, h=ALIGNED, h0=None, dg=ALIGNED, du=ALIGNED,
+            dh0=None, shape=(2, 3, 4), ws=WS, ws_bytes=1 << 40):
+        return lib.kla_affine_scan_bwd(dtype, dh, g, h, h0, dg, du, dh0, *shape, ws, ws_bytes, None)
+
+    assert bwd(dtype=-1) == _lib.KLA_ERR_DTYPE
+    assert bwd(h=None) == _lib.KLA_ERR_INVALID_ARG
+    assert bwd(du=ODD) == _lib.KLA_ERR_ALIGN
+    assert bwd(ws=WS + 64) == _lib.KLA_ERR_WORKSPACE
+    assert bwd(shape=(2, 0, 4), dh=None, g=None, h=None) == _lib.KLA_OK
+
+
+def test_workspace_failures_validation(lib):
+    out = ctypes.c_uint32(0)
+    assert lib.kla_workspace_failures(None, None, ctypes.byref(out)) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_workspace_failures(WS, None, None) == _lib.KLA_ERR_INVALID_ARG
+
+
+def test_last_error_is_per_thread(lib):
+    assert _mobius_fwd(lib, A=None) == _lib.KLA_ERR_INVALID_ARG
+    seen = {}
+
+    def other():
+        seen["before"] = err(lib)
+        lib.kla_affine_scan_fwd(5, None, None, None, None, 1, 1, 1, None, 0, None)
+        seen["after"] = err(lib)
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["before"] == ""
+    assert "unsupported dtype code 5" in seen["after"]
+    assert "must not be NULL" in err(lib)
+
+
+def test_python_errors_carry_the_message():
+    e = _lib.KLAHipError("kla_x", 1, "boom")
+    assert "kla_x failed with status 1: boom" in str(e)
+    with pytest.raises(_lib.KLAHipError, match="must not be NULL"):
+        _mobius_fwd(_lib.lib(), A=None)
+        _lib.check("kla_mobius_scan_fwd", _lib.KLA_ERR_INVALID_ARG)
