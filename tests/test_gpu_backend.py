@@ -1,0 +1,253 @@
+"""The "hip" backend as a drop-in for the reference's kla_scan, on the GPU.
+
+Inputs are drawn on the CPU (torch.Generator) and copied, so both sides see
+the same bytes. Parity anchors: the float64 sequential filter (oracle.kla,
+pinned against the covariance-form filter) for outputs and state, and float64
+torch autograd through oracle.torch_ref for every gradient -- including the
+initial-state gradients the stateful prefill needs. The bar is the path's
+fp32 tolerance, |got - want| <= atol + rtol |want| with rtol 1e-5, atol 1e-6
+taken relative to each tensor's scale (atol * max|want|, as the reference's
+tests/test_backends.py rel_err does), and the layer-level checks reuse the
+reference's golden vectors (tests/golden/layer_golden.npz).
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from kla import KLAConfig, KLALayer, ModelConfig, SequenceModel
+from kla.ops import KLAState, init_state, kla_scan, resolve_backend
+from oracle import kla as okla
+from oracle import torch_ref
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-5, 1e-6
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "layer_golden.npz")
+
+
+def make_inputs(B=2, L=64, M=16, S=8, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (
+        torch.randn(B, L, M, generator=g),
+        torch.rand(B, L, M, generator=g) + 0.5,
+        torch.randn(B, L, S, generator=g) * 0.3,
+        torch.randn(B, L, S, generator=g) * 0.3,
+        torch.rand(M, S, generator=g) * 0.5 + 0.4,
+        torch.rand(M, S, generator=g) * 0.05 + 0.01,
+    )
+
+
+def check(name, got, want, rtol=RTOL, atol=ATOL):
+    got = got.detach().double().cpu().numpy()
+    want = np.asarray(want, dtype=np.float64).reshape(got.shape)
+    assert np.isfinite(got).all(), f"{name}: non-finite values"
+    scale = max(float(np.abs(want).max()), 1e-30)
+    worst = float((np.abs(got - want) / (atol * scale + rtol * np.abs(want))).max())
+    print(f"  {name:10s} worst |d|/(atol*scale + rtol|ref|) = {worst:.3f}", flush=True)
+    assert worst <= 1.0, f"{name}: outside rtol={rtol} atol={atol} (ratio {worst:.3f})"
+
+
+def oracle(inputs, state=None, decode_from_prior=False):
+    np_in = [t.detach().double().cpu().numpy() for t in inputs]
+    lam0 = None if state is None else state.lam.detach().double().cpu().numpy()
+    eta0 = None if state is None else state.eta.detach().double().cpu().numpy()
+    return okla.kla_scan_sequential(*np_in, lam0, eta0, decode_from_prior=decode_from_prior)
+
+
+def random_state(B, M, S, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    return KLAState(lam=torch.rand(B, M, S, generator=g) * 2 + 0.5, eta=torch.randn(B, M, S, generator=g))
+
+
+@pytest.mark.parametrize("backend", ["hip", "hip_composed"])
+@pytest.mark.parametrize("decode_from_prior", [False, True])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_forward_and_state_match_oracle(cuda, backend, decode_from_prior, with_state):
+    ins = make_inputs()
+    st = random_state(2, 16, 8) if with_state else None
+    y, y_var, fin = kla_scan(*(t.to(cuda) for t in ins), backend=backend, decode_from_prior=decode_from_prior,
+                             initial_state=None if st is None else KLAState(st.lam.to(cuda), st.eta.to(cuda)))
+    assert y.dtype == torch.float32 and y.device.type == "cuda"
+    wy, wv, wl, we = oracle(ins, st, decode_from_prior)
+    check("y", y, wy)
+    check("y_var", y_var, wv)
+    check("lam", fin.lam, wl)
+    check("eta", fin.eta, we)
+    assert (y_var >= 0).all()
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 3, 2), (3, 257, 5, 16), (2, 1000, 8, 8)])
+def test_forward_ragged_shapes(cuda, shape):
+    B, L, M, S = shape
+    ins = make_inputs(B, L, M, S, seed=7)
+    y, y_var, fin = kla_scan(*(t.to(cuda) for t in ins), backend="hip")
+    wy, wv, wl, we = oracle(ins)
+    check("y", y, wy)
+    check("y_var", y_var, wv)
+    check("lam", fin.lam, wl)
+    check("eta", fin.eta, we)
+
+
+def test_chunked_state_carry(cuda):
+    """Reference tests/test_backends.py:269-288: two halves with the carried state = one scan."""
+    v, lv, k, q, a, p = (t.to(cuda) for t in make_inputs())
+    y_full, _, s_full = kla_scan(v, lv, k, q, a, p, backend="hip")
+    y1, _, s = kla_scan(v[:, :40], lv[:, :40], k[:, :40], q[:, :40], a, p, backend="hip")
+    y2, _, s2 = kla_scan(v[:, 40:], lv[:, 40:], k[:, 40:], q[:, 40:], a, p, backend="hip", initial_state=s)
+    torch.testing.assert_close(torch.cat([y1, y2], 1), y_full, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(s2.lam, s_full.lam, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(s2.eta, s_full.eta, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("decode_from_prior", [False, True])
+def test_gradients_match_float64_autograd(cuda, decode_from_prior):
+    """Every input gradient, the initial-state gradients, and gradients flowing in
+    through the returned state, against float64 autograd of the reference's
+    torch algorithm (oracle.torch_ref.kla_scan_torch)."""
+    ins = make_inputs(L=48)
+    st = random_state(2, 16, 8)
+    g = torch.Generator().manual_seed(5)
+    wy, wv = torch.randn(2, 48, 16, generator=g), torch.randn(2, 48, 16, generator=g)
+    wl, we = torch.randn(2, 16, 8, generator=g), torch.randn(2, 16, 8, generator=g)
+
+    def loss(y, y_var, lam, eta):
+        w = [t.to(device=y.device, dtype=y.dtype) for t in (wy, wv, wl, we)]
+        return (w[0] * y).sum() + (w[1] * y_var).sum() + (w[2] * lam).sum() + (w[3] * eta).sum()
+
+    xs = [t.double().requires_grad_(True) for t in ins + (st.lam, st.eta)]
+    ref = torch_ref.kla_scan_torch(*xs, decode_from_prior=decode_from_prior)
+    loss(*ref).backward()
+
+    gs = [t.to(cuda).requires_grad_(True) for t in ins + (st.lam, st.eta)]
+    y, y_var, fin = kla_scan(*gs[:6], backend="hip", initial_state=KLAState(gs[6], gs[7]),
+                             decode_from_prior=decode_from_prior)
+    loss(y, y_var, fin.lam, fin.eta).backward()
+    for name, got, want in zip(("v", "lambda_v", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
+        check("d" + name, got.grad, want.grad.numpy())
+
+
+def test_non_positive_noise_and_near_zero_decay_stay_finite(cuda):
+    """Reference tests/test_backends.py:421-493."""
+    v, lv, k, q, a, p = (t.to(cuda) for t in make_inputs())
+    for pp in (torch.zeros_like(p), torch.full_like(p, -0.05)):
+        y, y_var, _ = kla_scan(v, lv, k, q, a, pp, backend="hip")
+        assert torch.isfinite(y).all() and torch.isfinite(y_var).all()
+    y, y_var, _ = kla_scan(v, lv, k, q, torch.full_like(a, 1e-10), p, backend="hip")
+    assert torch.isfinite(y).all() and torch.isfinite(y_var).all()
+
+
+def test_high_information_tokens_are_not_clipped(cuda):
+    """Reference tests/test_backends.py:496-564."""
+    ins = list(make_inputs())
+    ins[1] = ins[1] * 1e4
+    y, y_var, _ = kla_scan(*(t.to(cuda) for t in ins), backend="hip")
+    wy, wv, _, _ = oracle(ins)
+    check("y", y, wy)
+    check("y_var", y_var, wv)
+
+
+def test_gradient_descent_reduces_loss(cuda):
+    """Reference tests/test_backends.py:374-418."""
+    inputs = [t.to(cuda).requires_grad_(True) for t in make_inputs()]
+    _, lv, _, _, a, p = inputs
+    target = torch.randn(2, 64, 16, generator=torch.Generator().manual_seed(1)).to(cuda)
+    opt = torch.optim.Adam(inputs, lr=1e-2)
+    losses = []
+    for _ in range(10):
+        opt.zero_grad()
+        y, _, _ = kla_scan(*inputs, backend="hip")
+        loss = (y - target).pow(2).mean()
+        loss.backward()
+        opt.step()
+        with torch.no_grad():
+            lv.clamp_(min=1e-3)
+            p.clamp_(min=1e-6)
+            a.clamp_(min=1e-3, max=0.999)
+        losses.append(loss.item())
+    assert all(np.isfinite(losses)) and losses[-1] < losses[0]
+
+
+def test_auto_picks_hip_on_the_gpu(cuda):
+    assert resolve_backend("cuda") == "hip"
+
+
+# ------------------------------------------------------------ layer level
+
+GOLDEN_CASES = {
+    "default": (32, dict(d_state=4), (2, 12, 32)),
+    "mamba_zoh": (24, dict(d_state=8, value_rank="conv", var_rank="dt", discretization="zoh",
+                           lambda_skip_mode="vector", bias=True), (2, 10, 24)),
+    "noconv_prior": (16, dict(d_state=4, use_conv=False, decode_from_prior=True, return_variance=True), (1, 9, 16)),
+}
+
+
+def _first(y):
+    return y[0] if isinstance(y, tuple) else y
+
+
+@pytest.mark.parametrize("tag", sorted(GOLDEN_CASES))
+def test_layer_on_hip_reproduces_reference_vectors(cuda, tag):
+    """A seeded KLALayer(backend="hip") on the GPU reproduces the outputs the
+    reference's own layer produced (golden vectors), prefill state included."""
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        gold = {k: z[k] for k in z.files if k.startswith(tag + "/")}
+    d_model, cfg, shape = GOLDEN_CASES[tag]
+    torch.manual_seed(0)
+    layer = KLALayer(d_model, KLAConfig(backend="hip", **cfg)).to(cuda)
+    x = torch.from_numpy(gold[f"{tag}/x"]).to(cuda)
+    with torch.no_grad():
+        check("y", _first(layer(x)), gold[f"{tag}/y"], rtol=1e-4, atol=1e-5)
+        state = layer.init_state(shape[0], device=cuda)
+        _, state = layer(x[:, : shape[1] // 2], state=state)
+        check("lam", state.ssm.lam, gold[f"{tag}/prefill_lam"])
+        check("eta", state.ssm.eta, gold[f"{tag}/prefill_eta"], rtol=1e-4, atol=1e-5)
+        step, _ = layer(x[:, shape[1] // 2: shape[1] // 2 + 1], state=state)
+        check("decode", _first(step), gold[f"{tag}/decode_y"], rtol=1e-4, atol=1e-5)
+
+
+def test_layer_train_step_and_decode_parity(cuda):
+    torch.manual_seed(0)
+    layer = KLALayer(64, KLAConfig(d_state=8, backend="hip")).to(cuda)
+    x = torch.randn(2, 40, 64, generator=torch.Generator().manual_seed(4)).to(cuda)
+    y = layer(x)
+    y.square().mean().backward()
+    assert all(p.grad is None or torch.isfinite(p.grad).all() for p in layer.parameters())
+    layer.eval()
+    with torch.no_grad():
+        full = layer(x)
+        state = layer.init_state(2, device=cuda)
+        outs = []
+        for t in range(40):
+            o, state = layer(x[:, t:t + 1], state=state)
+            outs.append(o)
+    assert (full - torch.cat(outs, 1)).abs().max().item() < 1e-4
+
+
+def test_layer_bf16_autocast(cuda):
+    """Reference tests/test_kla_layer.py:90-97: the scan runs in fp32 under autocast."""
+    torch.manual_seed(0)
+    layer = KLALayer(64, KLAConfig(d_state=8, backend="hip")).to(cuda)
+    x = torch.randn(2, 32, 64, device=cuda)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(x)
+    assert torch.isfinite(y).all()
+    y.float().sum().backward()
+
+
+def test_sequence_model_prefill_and_decode_on_hip(cuda):
+    torch.manual_seed(0)
+    model = SequenceModel(ModelConfig(vocab_size=97, d_model=32, n_layers=2),
+                          KLAConfig(d_state=4, backend="hip")).to(cuda).eval()
+    ids = torch.randint(0, 97, (2, 16), generator=torch.Generator().manual_seed(0)).to(cuda)
+    with torch.no_grad():
+        full = model(ids)
+        state = model.init_state(2)
+        head, state = model(ids[:, :9], state=state)
+        tail = []
+        for t in range(9, 16):
+            o, state = model(ids[:, t:t + 1], state=state)
+            tail.append(o)
+    torch.testing.assert_close(torch.cat([head] + tail, 1), full, rtol=1e-4, atol=1e-4)
