@@ -15,6 +15,13 @@ launch stream) and a CPU baseline: the reference's pure-PyTorch CPU algorithm
 Inputs are drawn on the CPU with torch.Generator(seed 0) in a fixed order and
 copied to the GPU, so the CPU and GPU sides see the same bytes.
 
+``--layer c4|c5`` measures the layer-level BASELINE configs instead of the
+headline (its own JSON line; ``--backend`` picks the kla backend): c4 is a
+KLALayer(1024, d_state=16) training step on x (4, 4096, 1024) under bf16
+autocast, loss = mean(out^2); c5 is SequenceModel(vocab 50304, d_model 512,
+6 layers) stateful prefill of (16, 2048) random ids, then 256 one-token decode
+steps (prefill tokens/s and decode ms/token).
+
 ``--only KERNEL`` runs just one kernel K times (for rocprofv3 counter runs);
 ``--only copy`` runs a 1 GiB device-to-device copy, the calibration kernel for
 the FETCH_SIZE / WRITE_SIZE counters; ``--only all`` runs the copy and then every
@@ -190,6 +197,66 @@ def time_kernels(kernels, reps, stream):
     return out
 
 
+def _timed(fn, steps, warmup, stream):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_layer(args, device, stream) -> dict:
+    """Layer-level BASELINE configs c4 / c5 on the chosen kla backend."""
+    from kla import KLAConfig, KLALayer, ModelConfig, SequenceModel
+
+    torch.manual_seed(0)
+    if args.layer == "c4":
+        layer = KLALayer(1024, KLAConfig(d_state=16, backend=args.backend)).to(device)
+        x = torch.randn(4, 4096, 1024, generator=torch.Generator().manual_seed(0)).to(device)
+
+        def step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = layer(x)
+            y.float().square().mean().backward()
+            layer.zero_grad(set_to_none=True)
+
+        ms = _timed(step, args.steps, args.warmup, stream)
+        return {"metric": "KLALayer(1024, d_state=16) train step tokens/s, x (4,4096,1024), bf16 autocast",
+                "value": 4 * 4096 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": round(ms, 3),
+                "backend": args.backend, "steps": args.steps, "warmup": args.warmup,
+                "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
+    model = SequenceModel(ModelConfig(vocab_size=50304, d_model=512, n_layers=6),
+                          KLAConfig(backend=args.backend)).to(device).eval()
+    ids = torch.randint(0, 50304, (16, 2048), generator=torch.Generator().manual_seed(0)).to(device)
+    state = {}
+
+    @torch.no_grad()
+    def prefill():
+        st = model.init_state(16)
+        logits, st = model(ids, state=st)
+        state["s"], state["tok"] = st, logits[:, -1].argmax(-1, keepdim=True)
+
+    pre_ms = _timed(prefill, max(1, args.steps // 4), 1, stream)
+
+    @torch.no_grad()
+    def decode256():
+        st, tok = state["s"], state["tok"]
+        for _ in range(256):
+            logits, st = model(tok, state=st)
+            tok = logits[:, -1].argmax(-1, keepdim=True)
+
+    dec_ms = _timed(decode256, 1, 1, stream)
+    return {"metric": "SequenceModel(d=512, 6 layers) prefill tokens/s (16x2048) + decode ms/token (256 steps)",
+            "value": 16 * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
+            "decode_ms_per_token": round(dec_ms / 256, 4), "backend": args.backend,
+            "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +266,9 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default=None,
                     choices=["mobius_fwd", "mobius_bwd", "affine_fwd", "affine_bwd", "copy", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--layer", default=None, choices=["c4", "c5"],
+                    help="measure a layer-level config instead of the headline scan step")
+    ap.add_argument("--backend", default="hip", help="kla backend for --layer (hip, hip_composed, torch)")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -211,6 +281,9 @@ def main(argv=None) -> int:
 
     device = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(device)
+    if args.layer:
+        print(json.dumps(bench_layer(args, device, stream)), flush=True)
+        return 0
     batch, steps, lanes, adt = WORKLOADS[args.workload]
     elems = batch * steps * lanes
 
