@@ -125,6 +125,51 @@ int kla_affine_scan_bwd(int dtype, const void *dh, const void *g, const void *h,
                         int64_t steps, int64_t lanes, void *workspace,
                         size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Fused KLA scan: the whole filter of kla_scan_torch in one kernel per direction.
+ * Shapes (reference kla_ops.py:23-28): v, lambda_v, y, y_var [batch, steps, M];
+ * k, q [batch, steps, S]; a, p [M, S]; lam0, eta0, lam_fin, eta_fin [batch, M, S];
+ * all fp32, dense. S <= 64. lam0 / eta0 may be NULL (precision 1, information 0).
+ *   phi = lambda_v k^2, r = (v lambda_v) k, a2 = max(a^2, 1e-12), p' = max(p, 1e-12)
+ *   lam_t = (A lam_{t-1} + phi) / (C lam_{t-1} + 1), A = (1 + p' phi)/a2, C = p'/a2
+ *   eta_t = a / max(a2 + p' lam_{t-1}, 1e-12) * eta_{t-1} + r
+ *   var = 1/max(lam_t, 1e-12), mean = eta_t var (decode_from_prior: mean = a mean,
+ *   var = a2 var + p'); y = sum_s q mean, y_var = sum_s q^2 var.
+ * ck_lam / ck_eta: [batch, kla_fused_checkpoints(steps), M, S] buffers the forward
+ * fills for the backward, or both NULL when no backward will follow.
+ * Replaces kla_scan_torch (src/kla/ops/kla_ops.py:188-290) / the fused kernels
+ * (src/kla/ops/kernels/cuda/v2_2/kla_matmul_fwd_kernel.cuh:89-476,
+ * src/kla/ops/kernels/mps/fused_kla_scan.metal:53-131).
+ */
+int64_t kla_fused_checkpoints(int64_t steps);
+
+int kla_fused_scan_fwd(const float *v, const float *lambda_v, const float *k, const float *q,
+                       const float *a, const float *p, const float *lam0, const float *eta0, float *y,
+                       float *y_var, float *lam_fin, float *eta_fin, float *ck_lam, float *ck_eta,
+                       int decode_from_prior, int64_t batch, int64_t steps, int64_t M, int64_t S,
+                       hipStream_t stream);
+
+/* Bytes of workspace kla_fused_scan_bwd needs (partial sums; no zero-fill needed). */
+size_t kla_fused_workspace_bytes(int64_t batch, int64_t steps, int64_t M, int64_t S);
+
+/*
+ * Exact adjoint of kla_fused_scan_fwd (checkpoint replay). Inputs: the output
+ * gradients dy, dy_var and (optional, NULL = 0) dlam_fin, deta_fin, the forward's
+ * inputs and its checkpoints. Outputs: dv, dlambda_v [batch, steps, M]; dk, dq
+ * [batch, steps, S]; da, dp [M, S]; dlam0, deta0 [batch, M, S] (NULL to skip).
+ * Every output is written (not accumulated); sums over channels and batch run in
+ * a fixed order, so results are deterministic.
+ * Replaces the exact fused backward (src/kla/ops/kernels/mps/fused_kla_scan.metal:135-324)
+ * and the CUDA backward (kla_matmul_bwd_kernel.cuh:156-800), whose adjoint is approximate.
+ */
+int kla_fused_scan_bwd(const float *dy, const float *dy_var, const float *dlam_fin, const float *deta_fin,
+                       const float *v, const float *lambda_v, const float *k, const float *q,
+                       const float *a, const float *p, const float *ck_lam, const float *ck_eta,
+                       float *dv, float *dlambda_v, float *dk, float *dq, float *da, float *dp,
+                       float *dlam0, float *deta0, int decode_from_prior, int64_t batch, int64_t steps,
+                       int64_t M, int64_t S, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,18 +11,20 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <type_traits>
 
 #pragma GCC visibility push(default)
 #include "kla_hip.h"
 #pragma GCC visibility pop
 
+#include "fused_kla.hpp"
 #include "lookback_scan.hpp"
 
 namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X at
@@ -177,6 +179,54 @@ int zero_state(const char *fn, float *p, int64_t count, hipStream_t stream) {
   return hip_status(fn, hipGetLastError());
 }
 
+// ----------------------------------------------------------- fused scan
+
+int sp_of(int64_t S) {
+  int sp = 1;
+  while (sp < S) sp *= 2;
+  return sp;
+}
+
+FusedGeom fused_geom(int64_t batch, int64_t steps, int64_t M, int64_t S) {
+  FusedGeom g;
+  g.batch = batch;
+  g.steps = steps;
+  g.M = M;
+  g.S = S;
+  const int64_t ch = kFusedThreads / sp_of(S);
+  g.groups = (M + ch - 1) / ch;
+  g.n_ck = (steps + kCkpt - 1) / kCkpt;
+  return g;
+}
+
+// Partials of the fused backward: part_k, part_q [B, L, G, S]; part_a, part_p [B, M, S].
+size_t fused_workspace_floats(const FusedGeom &g) {
+  return static_cast<size_t>(2 * g.batch * g.steps * g.groups * g.S + 2 * g.batch * g.M * g.S);
+}
+
+int check_fused_shape(const char *fn, int64_t batch, int64_t steps, int64_t M, int64_t S) {
+  if (batch < 0 || steps < 0 || M < 0 || S < 0)
+    return fail(KLA_ERR_INVALID_ARG, "%s: negative size (batch=%lld steps=%lld M=%lld S=%lld)", fn,
+                (long long)batch, (long long)steps, (long long)M, (long long)S);
+  if (S > 64) return fail(KLA_ERR_INVALID_ARG, "%s: d_state S=%lld above 64", fn, (long long)S);
+  if (batch > (1ll << 31) || steps > (1ll << 31) || M > (1ll << 31))
+    return fail(KLA_ERR_INVALID_ARG, "%s: dimension above 2^31", fn);
+  return KLA_OK;
+}
+
+template <class F>
+int with_sp(int64_t S, F &&f) {
+  switch (sp_of(S)) {
+    case 1: return f(std::integral_constant<int, 1>{});
+    case 2: return f(std::integral_constant<int, 2>{});
+    case 4: return f(std::integral_constant<int, 4>{});
+    case 8: return f(std::integral_constant<int, 8>{});
+    case 16: return f(std::integral_constant<int, 16>{});
+    case 32: return f(std::integral_constant<int, 32>{});
+    default: return f(std::integral_constant<int, 64>{});
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -321,6 +371,110 @@ int kla_affine_scan_bwd(int dtype, const void *dh, const void *g, const void *h,
   if (lanes % V == 0 && all_aligned(V * el, {dh, g, h, dg, du}))
     return launch<P, AffineBwdBf16Tile>(fn, prm, s, workspace, stream);
   return launch<P, AffineBf16Fallback>(fn, prm, s, workspace, stream);
+}
+
+int64_t kla_fused_checkpoints(int64_t steps) { return steps < 0 ? 0 : (steps + kCkpt - 1) / kCkpt; }
+
+size_t kla_fused_workspace_bytes(int64_t batch, int64_t steps, int64_t M, int64_t S) {
+  if (check_fused_shape("kla_fused_workspace_bytes", batch, steps, M, S) != KLA_OK) return 0;
+  return std::max<size_t>(256, fused_workspace_floats(fused_geom(batch, steps, M, S)) * sizeof(float));
+}
+
+int kla_fused_scan_fwd(const float *v, const float *lambda_v, const float *k, const float *q,
+                       const float *a, const float *p, const float *lam0, const float *eta0, float *y,
+                       float *y_var, float *lam_fin, float *eta_fin, float *ck_lam, float *ck_eta,
+                       int decode_from_prior, int64_t batch, int64_t steps, int64_t M, int64_t S,
+                       hipStream_t stream) {
+  const char *fn = "kla_fused_scan_fwd";
+  int rc = check_fused_shape(fn, batch, steps, M, S);
+  if (rc != KLA_OK) return rc;
+  if (batch == 0 || M == 0 || S == 0) return KLA_OK;
+  if (!a || !p || !lam_fin || !eta_fin)
+    return fail(KLA_ERR_INVALID_ARG, "%s: a, p, lam_fin and eta_fin must not be NULL", fn);
+  if (steps > 0 && (!v || !lambda_v || !k || !q || !y || !y_var))
+    return fail(KLA_ERR_INVALID_ARG, "%s: v, lambda_v, k, q, y and y_var must not be NULL", fn);
+  if ((ck_lam == nullptr) != (ck_eta == nullptr))
+    return fail(KLA_ERR_INVALID_ARG, "%s: pass both checkpoint buffers or neither", fn);
+  if (!all_aligned(4, {v, lambda_v, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  const FusedGeom g = fused_geom(batch, steps, M, S);
+  const int64_t grid = batch * g.groups;
+  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+  const FusedFwdParams prm{v, lambda_v, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta};
+  return with_sp(S, [&](auto sp) {
+    constexpr int SP = decltype(sp)::value;
+    if (decode_from_prior)
+      hipLaunchKernelGGL((fused_kla_fwd_kernel<SP, true>), dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads),
+                         0, stream, prm, g);
+    else
+      hipLaunchKernelGGL((fused_kla_fwd_kernel<SP, false>), dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads),
+                         0, stream, prm, g);
+    return hip_status(fn, hipGetLastError());
+  });
+}
+
+int kla_fused_scan_bwd(const float *dy, const float *dy_var, const float *dlam_fin, const float *deta_fin,
+                       const float *v, const float *lambda_v, const float *k, const float *q,
+                       const float *a, const float *p, const float *ck_lam, const float *ck_eta,
+                       float *dv, float *dlambda_v, float *dk, float *dq, float *da, float *dp,
+                       float *dlam0, float *deta0, int decode_from_prior, int64_t batch, int64_t steps,
+                       int64_t M, int64_t S, void *workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+  const char *fn = "kla_fused_scan_bwd";
+  int rc = check_fused_shape(fn, batch, steps, M, S);
+  if (rc != KLA_OK) return rc;
+  if (M == 0 || S == 0) return KLA_OK;
+  if (!a || !p || !da || !dp) return fail(KLA_ERR_INVALID_ARG, "%s: a, p, da and dp must not be NULL", fn);
+  if (steps > 0 && (!dy || !dy_var || !v || !lambda_v || !k || !q || !ck_lam || !ck_eta || !dv ||
+                    !dlambda_v || !dk || !dq))
+    return fail(KLA_ERR_INVALID_ARG,
+                "%s: dy, dy_var, v, lambda_v, k, q, checkpoints, dv, dlambda_v, dk and dq must not be NULL", fn);
+  if (!all_aligned(4, {dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta, dv, dlambda_v,
+                       dk, dq, da, dp, dlam0, deta0}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  const FusedGeom g = fused_geom(batch, steps, M, S);
+  if (workspace == nullptr) return fail(KLA_ERR_WORKSPACE, "%s: workspace is NULL", fn);
+  if (misaligned_bytes(workspace, 256)) return fail(KLA_ERR_WORKSPACE, "%s: workspace not 256-byte aligned", fn);
+  const size_t need = fused_workspace_floats(g) * sizeof(float);
+  if (workspace_bytes < need)
+    return fail(KLA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
+  const int64_t grid = batch * g.groups;
+  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+
+  float *ws = static_cast<float *>(workspace);
+  float *part_k = ws;
+  float *part_q = part_k + batch * steps * g.groups * S;
+  float *part_a = part_q + batch * steps * g.groups * S;
+  float *part_p = part_a + batch * M * S;
+  if (batch > 0) {
+    const FusedBwdParams prm{dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta,
+                             dv, dlambda_v, dlam0, deta0, part_k, part_q, part_a, part_p};
+    rc = with_sp(S, [&](auto sp) {
+      constexpr int SP = decltype(sp)::value;
+      if (decode_from_prior)
+        hipLaunchKernelGGL((fused_kla_bwd_kernel<SP, true>), dim3(static_cast<uint32_t>(grid)),
+                           dim3(kFusedThreads), 0, stream, prm, g);
+      else
+        hipLaunchKernelGGL((fused_kla_bwd_kernel<SP, false>), dim3(static_cast<uint32_t>(grid)),
+                           dim3(kFusedThreads), 0, stream, prm, g);
+      return hip_status(fn, hipGetLastError());
+    });
+    if (rc != KLA_OK) return rc;
+  }
+  // Fixed-order sums of the partials: dk, dq over channel groups; da, dp over batch.
+  auto reduce = [&](const float *in, float *out, int64_t outer, int64_t G, int64_t inner) {
+    const int64_t n = outer * inner;
+    if (n == 0) return KLA_OK;
+    hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream,
+                       in, out, outer, G, inner);
+    return hip_status(fn, hipGetLastError());
+  };
+  if (steps > 0 && batch > 0) {
+    if ((rc = reduce(part_k, dk, batch * steps, g.groups, S)) != KLA_OK) return rc;
+    if ((rc = reduce(part_q, dq, batch * steps, g.groups, S)) != KLA_OK) return rc;
+  }
+  if ((rc = reduce(part_a, da, 1, batch, M * S)) != KLA_OK) return rc;
+  return reduce(part_p, dp, 1, batch, M * S);
 }
 
 }  // extern "C"

@@ -18,6 +18,7 @@ Backend = Literal[
     "auto",
     "torch",
     "hip",
+    "hip_fused",
     "hip_composed",
     "triton",
     "triton_fused",

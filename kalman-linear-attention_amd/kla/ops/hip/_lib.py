@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -45,6 +45,10 @@ _SIGNATURES = {
     "kla_mobius_scan_bwd": (ctypes.c_int, [_p] * 12 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
     "kla_affine_scan_fwd": (ctypes.c_int, [ctypes.c_int] + [_p] * 4 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
     "kla_affine_scan_bwd": (ctypes.c_int, [ctypes.c_int] + [_p] * 7 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
+    "kla_fused_checkpoints": (_i64, [_i64]),
+    "kla_fused_workspace_bytes": (ctypes.c_size_t, [_i64] * 4),
+    "kla_fused_scan_fwd": (ctypes.c_int, [_p] * 14 + [ctypes.c_int] + [_i64] * 4 + [_p]),
+    "kla_fused_scan_bwd": (ctypes.c_int, [_p] * 20 + [ctypes.c_int] + [_i64] * 4 + [_p, ctypes.c_size_t, _p]),
 }
 
 
@@ -117,6 +121,24 @@ def workspace(kind: int, batch: int, steps: int, lanes: int, device: torch.devic
     return ws, stream.cuda_stream
 
 
+_SCRATCH: dict = {}
+
+
+def scratch(nbytes: int, device: torch.device) -> tuple[torch.Tensor, int]:
+    """(uninitialised buffer of at least ``nbytes``, stream handle) for the current
+    stream of ``device``: scratch whose contents no call relies on between calls
+    (the fused backward's partial sums). Reused while large enough."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    with _WS_LOCK:
+        buf = _SCRATCH.get(key)
+        if buf is None or buf.numel() < nbytes:
+            with torch.cuda.stream(stream):
+                buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            _SCRATCH[key] = buf
+    return buf, stream.cuda_stream
+
+
 def workspace_failures(device: torch.device) -> int:
     """Look-back waits that gave up on the current stream's workspace (0 when healthy)."""
     stream = torch.cuda.current_stream(device)
@@ -132,3 +154,4 @@ def reset_workspaces() -> None:
     """Drop every cached workspace (the next call allocates a fresh zero-filled one)."""
     with _WS_LOCK:
         _WORKSPACES.clear()
+        _SCRATCH.clear()

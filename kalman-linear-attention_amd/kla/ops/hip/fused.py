@@ -1,0 +1,157 @@
+"""The fused KLA scan on MI355X: one kernel per direction, no [B, L, M, S] tensors.
+
+:func:`kla_scan_fused` computes what the reference's ``kla_scan_torch``
+(src/kla/ops/kla_ops.py:188-290) computes -- y, y_var [B, L, M] and the final
+state (lam, eta) [B, M, S] -- from v, lambda_v [B, L, M], k, q [B, L, S] and the
+static a, p [M, S], with an optional initial state and ``decode_from_prior``.
+It is a ``torch.library`` custom op (``kla_hip::kla_scan_fused``) whose backward
+is the hand-written exact adjoint kernel (checkpoint replay), giving gradients
+for all six inputs and for the initial state, including gradients that arrive
+through the returned final state.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from kla.ops.hip import _lib
+from kla.ops.hip.scans import _require_device
+
+_F32 = torch.float32
+MAX_STATE = 64
+
+
+def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    return None if t is None else t.to(_F32).contiguous()
+
+
+def _check(v, lambda_v, k, q, a, p, lam0, eta0):
+    if v.dim() != 3 or k.dim() != 3:
+        raise ValueError(f"v must be [B, L, M] and k [B, L, S]; got {tuple(v.shape)} and {tuple(k.shape)}")
+    B, L, M = v.shape
+    S = k.shape[2]
+    if S > MAX_STATE:
+        raise NotImplementedError(f"the fused hip kernel supports d_state <= {MAX_STATE} (got {S}); "
+                                  "use backend='hip_composed'")
+    for name, t, shape in (("lambda_v", lambda_v, (B, L, M)), ("k", k, (B, L, S)), ("q", q, (B, L, S)),
+                           ("a", a, (M, S)), ("p", p, (M, S)), ("lam0", lam0, (B, M, S)),
+                           ("eta0", eta0, (B, M, S))):
+        if t is not None and tuple(t.shape) != shape:
+            raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {shape}")
+    return B, L, M, S
+
+
+@torch.library.custom_op("kla_hip::kla_scan_fused", mutates_args=())
+def _fused_fwd_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
+                  p: torch.Tensor, lam0: Optional[torch.Tensor], eta0: Optional[torch.Tensor],
+                  decode_from_prior: bool, save: bool
+                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns (y, y_var, lam_fin, eta_fin, ck_lam, ck_eta); the checkpoints are
+    empty unless ``save``."""
+    dev = _require_device(v, lambda_v, k, q, a, p, lam0, eta0)
+    B, L, M, S = _check(v, lambda_v, k, q, a, p, lam0, eta0)
+    y = v.new_empty(B, L, M)
+    y_var = v.new_empty(B, L, M)
+    lam_fin = v.new_empty(B, M, S)
+    eta_fin = v.new_empty(B, M, S)
+    n_ck = int(_lib.lib().kla_fused_checkpoints(L))
+    ck_lam = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
+    ck_eta = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
+    if B * M * S == 0:
+        return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    pt = _lib.ptr
+    _lib.check("kla_fused_scan_fwd", _lib.lib().kla_fused_scan_fwd(
+        pt(v), pt(lambda_v), pt(k), pt(q), pt(a), pt(p), pt(lam0), pt(eta0), pt(y), pt(y_var),
+        pt(lam_fin), pt(eta_fin), pt(ck_lam) if save else None, pt(ck_eta) if save else None,
+        int(decode_from_prior), B, L, M, S, stream))
+    return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
+
+
+@_fused_fwd_op.register_fake
+def _(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save):
+    B, L, M = v.shape
+    S = k.shape[2]
+    n_ck = (L + 15) // 16
+    ck = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
+    return (v.new_empty(B, L, M), v.new_empty(B, L, M), v.new_empty(B, M, S), v.new_empty(B, M, S), ck,
+            torch.empty_like(ck))
+
+
+@torch.library.custom_op("kla_hip::kla_scan_fused_backward", mutates_args=())
+def _fused_bwd_op(dy: torch.Tensor, dy_var: torch.Tensor, dlam_fin: torch.Tensor, deta_fin: torch.Tensor,
+                  v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
+                  p: torch.Tensor, ck_lam: torch.Tensor, ck_eta: torch.Tensor, decode_from_prior: bool
+                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                             torch.Tensor, torch.Tensor]:
+    """Returns (dv, dlambda_v, dk, dq, da, dp, dlam0, deta0)."""
+    dev = _require_device(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta)
+    B, L, M, S = _check(v, lambda_v, k, q, a, p, None, None)
+    dv, dlv = torch.empty_like(v), torch.empty_like(lambda_v)
+    dk, dq = torch.empty_like(k), torch.empty_like(q)
+    da, dp = torch.empty_like(a), torch.empty_like(p)
+    dlam0, deta0 = v.new_empty(B, M, S), v.new_empty(B, M, S)
+    if M * S == 0:
+        return dv, dlv, dk, dq, da, dp, dlam0, deta0
+    nbytes = int(_lib.lib().kla_fused_workspace_bytes(B, L, M, S))
+    ws, stream = _lib.scratch(nbytes, dev)
+    pt = _lib.ptr
+    _lib.check("kla_fused_scan_bwd", _lib.lib().kla_fused_scan_bwd(
+        pt(dy), pt(dy_var), pt(dlam_fin), pt(deta_fin), pt(v), pt(lambda_v), pt(k), pt(q), pt(a), pt(p),
+        pt(ck_lam), pt(ck_eta), pt(dv), pt(dlv), pt(dk), pt(dq), pt(da), pt(dp), pt(dlam0), pt(deta0),
+        int(decode_from_prior), B, L, M, S, pt(ws), ws.numel(), stream))
+    return dv, dlv, dk, dq, da, dp, dlam0, deta0
+
+
+@_fused_bwd_op.register_fake
+def _(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta, decode_from_prior):
+    B, L, M = v.shape
+    S = k.shape[2]
+    return (torch.empty_like(v), torch.empty_like(lambda_v), torch.empty_like(k), torch.empty_like(q),
+            torch.empty_like(a), torch.empty_like(p), v.new_empty(B, M, S), v.new_empty(B, M, S))
+
+
+def _setup(ctx, inputs, output):
+    v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save = inputs
+    _, _, _, _, ck_lam, ck_eta = output
+    if not save:
+        raise RuntimeError("kla_scan_fused was run without checkpoints but a gradient is required")
+    ctx.prior = decode_from_prior
+    ctx.has_lam0, ctx.has_eta0 = lam0 is not None, eta0 is not None
+    ctx.save_for_backward(v, lambda_v, k, q, a, p, ck_lam, ck_eta)
+
+
+def _backward(ctx, dy, dy_var, dlam_fin, deta_fin, _dck_lam, _dck_eta):
+    v, lambda_v, k, q, a, p, ck_lam, ck_eta = ctx.saved_tensors
+
+    def g(t, like):
+        return torch.zeros_like(like) if t is None else t.to(_F32).contiguous()
+
+    B, _, M = v.shape
+    S = k.shape[2]
+    state = v.new_empty(B, M, S)
+    dv, dlv, dk, dq, da, dp, dlam0, deta0 = _fused_bwd_op(
+        g(dy, v), g(dy_var, v), g(dlam_fin, state), g(deta_fin, state), v, lambda_v, k, q, a, p, ck_lam, ck_eta,
+        ctx.prior)
+    return (dv, dlv, dk, dq, da, dp, dlam0 if ctx.has_lam0 else None, deta0 if ctx.has_eta0 else None,
+            None, None)
+
+
+_fused_fwd_op.register_autograd(_backward, setup_context=_setup)
+
+
+def kla_scan_fused(v, lambda_v, k, q, a, p, lam0=None, eta0=None, decode_from_prior: bool = False):
+    """(y, y_var, lam_fin, eta_fin) of the KLA scan, computed by the fused kernels.
+
+    All inputs are cast to contiguous float32 (the reference's GPU backends
+    compute in float32 too). Checkpoints for the backward are kept only when a
+    gradient can be required.
+    """
+    v, lambda_v, k, q, a, p, lam0, eta0 = (_f32(t) for t in (v, lambda_v, k, q, a, p, lam0, eta0))
+    save = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (v, lambda_v, k, q, a, p, lam0, eta0))
+    y, y_var, lam_fin, eta_fin, _, _ = _fused_fwd_op(v, lambda_v, k, q, a, p, lam0, eta0,
+                                                     bool(decode_from_prior), save)
+    return y, y_var, lam_fin, eta_fin

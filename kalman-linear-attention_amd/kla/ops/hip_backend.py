@@ -1,4 +1,8 @@
-"""The ``"hip"`` KLA backend: the KLA scan on MI355X scan kernels.
+"""The ``"hip"`` KLA backend: the KLA scan on MI355X kernels.
+
+Fused path (``kernel="fused"``, the default for d_state <= 64): the whole
+filter in one kernel per direction (:mod:`kla.ops.hip.fused`); nothing of shape
+[B, L, M, S] is materialised, and the backward is the exact adjoint.
 
 Composed path (``kernel="composed"``): the per-(b, l, m, s) glue -- sufficient
 statistics, Moebius leaves, the gain alpha, posterior and read-out -- is torch
@@ -36,13 +40,20 @@ def kla_scan_hip(
     decode_from_prior: bool = False,
     kernel: str = "auto",
 ):
-    """KLA scan on the MI355X kernels. ``kernel``: "auto" or "composed"."""
+    """KLA scan on the MI355X kernels. ``kernel``: "auto", "fused" or "composed"."""
     from kla.ops.hip import affine_scan, mobius_scan
+    from kla.ops.hip.fused import MAX_STATE, kla_scan_fused
 
-    if kernel not in ("auto", "composed"):
-        raise ValueError(f"Unknown hip kernel {kernel!r}; expected 'auto' or 'composed'")
+    if kernel not in ("auto", "fused", "composed"):
+        raise ValueError(f"Unknown hip kernel {kernel!r}; expected 'auto', 'fused' or 'composed'")
     if not v.is_cuda:
         raise NotImplementedError("The hip KLA backend requires tensors on a ROCm GPU; use backend='torch'.")
+    if kernel == "fused" or (kernel == "auto" and k.shape[-1] <= MAX_STATE):
+        lam0 = eta0 = None
+        if initial_state is not None:
+            lam0, eta0 = initial_state.lam, initial_state.eta
+        y, y_var, lam, eta = kla_scan_fused(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior)
+        return y, y_var, KLAState(lam=lam, eta=eta)
 
     v, lambda_v, k, q = (t.float() for t in (v, lambda_v, k, q))
     Bn, L, M = v.shape

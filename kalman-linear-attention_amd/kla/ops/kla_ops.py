@@ -17,8 +17,9 @@ leaf A = (1 + p phi)/a^2, B = phi, C = p/a^2, D = 1, scanned as trace-normalised
 
 Backends (``kla_scan(..., backend=...)``):
   torch          this module's pure-torch path (CPU or GPU)
-  hip            MI355X kernels (see :mod:`kla.ops.hip_backend`)
-  hip_composed   the same, pinned to the composed path
+  hip            MI355X kernels (see :mod:`kla.ops.hip_backend`): the fused scan
+  hip_fused      pinned to the fused kernels (d_state <= 64)
+  hip_composed   pinned to the composed path (HIP scans + torch glue)
   triton*, cuda*, mps*  names kept from the reference registry for config
                  compatibility; their kernels are not part of this build and
                  they raise NotImplementedError naming a backend that works.
@@ -275,6 +276,13 @@ def _backend_hip(*args, **kwargs):
     return kla_scan_hip(*args, **kwargs)
 
 
+def _backend_hip_fused(*args, **kwargs):
+    """MI355X kernels, pinned to the fused scan (one kernel per direction)."""
+    from kla.ops.hip_backend import kla_scan_hip
+
+    return kla_scan_hip(*args, kernel="fused", **kwargs)
+
+
 def _backend_hip_composed(*args, **kwargs):
     """MI355X kernels, pinned to the composed path (HIP scans + torch glue)."""
     from kla.ops.hip_backend import kla_scan_hip
@@ -298,6 +306,7 @@ def _not_in_this_build(name: str):
 _BACKENDS = {
     "torch": _backend_torch,
     "hip": _backend_hip,
+    "hip_fused": _backend_hip_fused,
     "hip_composed": _backend_hip_composed,
     "triton": _not_in_this_build("triton"),
     "triton_fused": _not_in_this_build("triton_fused"),

@@ -62,7 +62,10 @@ def random_state(B, M, S, seed=3):
     return KLAState(lam=torch.rand(B, M, S, generator=g) * 2 + 0.5, eta=torch.randn(B, M, S, generator=g))
 
 
-@pytest.mark.parametrize("backend", ["hip", "hip_composed"])
+BACKENDS = ["hip_fused", "hip_composed"]
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("decode_from_prior", [False, True])
 @pytest.mark.parametrize("with_state", [False, True])
 def test_forward_and_state_match_oracle(cuda, backend, decode_from_prior, with_state):
@@ -79,11 +82,13 @@ def test_forward_and_state_match_oracle(cuda, backend, decode_from_prior, with_s
     assert (y_var >= 0).all()
 
 
-@pytest.mark.parametrize("shape", [(1, 1, 3, 2), (3, 257, 5, 16), (2, 1000, 8, 8)])
-def test_forward_ragged_shapes(cuda, shape):
+@pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("shape", [(1, 1, 3, 2), (3, 257, 5, 16), (2, 1000, 8, 8), (1, 40, 70, 3), (2, 33, 9, 64),
+                                   (1, 17, 300, 1), (2, 64, 3, 40)])
+def test_forward_ragged_shapes(cuda, backend, shape):
     B, L, M, S = shape
     ins = make_inputs(B, L, M, S, seed=7)
-    y, y_var, fin = kla_scan(*(t.to(cuda) for t in ins), backend="hip")
+    y, y_var, fin = kla_scan(*(t.to(cuda) for t in ins), backend=backend)
     wy, wv, wl, we = oracle(ins)
     check("y", y, wy)
     check("y_var", y_var, wv)
@@ -91,27 +96,31 @@ def test_forward_ragged_shapes(cuda, shape):
     check("eta", fin.eta, we)
 
 
-def test_chunked_state_carry(cuda):
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_chunked_state_carry(cuda, backend):
     """Reference tests/test_backends.py:269-288: two halves with the carried state = one scan."""
     v, lv, k, q, a, p = (t.to(cuda) for t in make_inputs())
-    y_full, _, s_full = kla_scan(v, lv, k, q, a, p, backend="hip")
-    y1, _, s = kla_scan(v[:, :40], lv[:, :40], k[:, :40], q[:, :40], a, p, backend="hip")
-    y2, _, s2 = kla_scan(v[:, 40:], lv[:, 40:], k[:, 40:], q[:, 40:], a, p, backend="hip", initial_state=s)
+    y_full, _, s_full = kla_scan(v, lv, k, q, a, p, backend=backend)
+    y1, _, s = kla_scan(v[:, :40], lv[:, :40], k[:, :40], q[:, :40], a, p, backend=backend)
+    y2, _, s2 = kla_scan(v[:, 40:], lv[:, 40:], k[:, 40:], q[:, 40:], a, p, backend=backend, initial_state=s)
     torch.testing.assert_close(torch.cat([y1, y2], 1), y_full, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(s2.lam, s_full.lam, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(s2.eta, s_full.eta, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("decode_from_prior", [False, True])
-def test_gradients_match_float64_autograd(cuda, decode_from_prior):
+@pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 20, 3, 3)])
+def test_gradients_match_float64_autograd(cuda, backend, decode_from_prior, shape):
     """Every input gradient, the initial-state gradients, and gradients flowing in
     through the returned state, against float64 autograd of the reference's
     torch algorithm (oracle.torch_ref.kla_scan_torch)."""
-    ins = make_inputs(L=48)
-    st = random_state(2, 16, 8)
+    B, L, M, S = shape
+    ins = make_inputs(B, L, M, S)
+    st = random_state(B, M, S)
     g = torch.Generator().manual_seed(5)
-    wy, wv = torch.randn(2, 48, 16, generator=g), torch.randn(2, 48, 16, generator=g)
-    wl, we = torch.randn(2, 16, 8, generator=g), torch.randn(2, 16, 8, generator=g)
+    wy, wv = torch.randn(B, L, M, generator=g), torch.randn(B, L, M, generator=g)
+    wl, we = torch.randn(B, M, S, generator=g), torch.randn(B, M, S, generator=g)
 
     def loss(y, y_var, lam, eta):
         w = [t.to(device=y.device, dtype=y.dtype) for t in (wy, wv, wl, we)]
@@ -122,34 +131,37 @@ def test_gradients_match_float64_autograd(cuda, decode_from_prior):
     loss(*ref).backward()
 
     gs = [t.to(cuda).requires_grad_(True) for t in ins + (st.lam, st.eta)]
-    y, y_var, fin = kla_scan(*gs[:6], backend="hip", initial_state=KLAState(gs[6], gs[7]),
+    y, y_var, fin = kla_scan(*gs[:6], backend=backend, initial_state=KLAState(gs[6], gs[7]),
                              decode_from_prior=decode_from_prior)
     loss(y, y_var, fin.lam, fin.eta).backward()
     for name, got, want in zip(("v", "lambda_v", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
         check("d" + name, got.grad, want.grad.numpy())
 
 
-def test_non_positive_noise_and_near_zero_decay_stay_finite(cuda):
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_non_positive_noise_and_near_zero_decay_stay_finite(cuda, backend):
     """Reference tests/test_backends.py:421-493."""
     v, lv, k, q, a, p = (t.to(cuda) for t in make_inputs())
     for pp in (torch.zeros_like(p), torch.full_like(p, -0.05)):
-        y, y_var, _ = kla_scan(v, lv, k, q, a, pp, backend="hip")
+        y, y_var, _ = kla_scan(v, lv, k, q, a, pp, backend=backend)
         assert torch.isfinite(y).all() and torch.isfinite(y_var).all()
-    y, y_var, _ = kla_scan(v, lv, k, q, torch.full_like(a, 1e-10), p, backend="hip")
+    y, y_var, _ = kla_scan(v, lv, k, q, torch.full_like(a, 1e-10), p, backend=backend)
     assert torch.isfinite(y).all() and torch.isfinite(y_var).all()
 
 
-def test_high_information_tokens_are_not_clipped(cuda):
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_high_information_tokens_are_not_clipped(cuda, backend):
     """Reference tests/test_backends.py:496-564."""
     ins = list(make_inputs())
     ins[1] = ins[1] * 1e4
-    y, y_var, _ = kla_scan(*(t.to(cuda) for t in ins), backend="hip")
+    y, y_var, _ = kla_scan(*(t.to(cuda) for t in ins), backend=backend)
     wy, wv, _, _ = oracle(ins)
     check("y", y, wy)
     check("y_var", y_var, wv)
 
 
-def test_gradient_descent_reduces_loss(cuda):
+@pytest.mark.parametrize("backend", BACKENDS)
+def test_gradient_descent_reduces_loss(cuda, backend):
     """Reference tests/test_backends.py:374-418."""
     inputs = [t.to(cuda).requires_grad_(True) for t in make_inputs()]
     _, lv, _, _, a, p = inputs
@@ -158,7 +170,7 @@ def test_gradient_descent_reduces_loss(cuda):
     losses = []
     for _ in range(10):
         opt.zero_grad()
-        y, _, _ = kla_scan(*inputs, backend="hip")
+        y, _, _ = kla_scan(*inputs, backend=backend)
         loss = (y - target).pow(2).mean()
         loss.backward()
         opt.step()

@@ -203,7 +203,7 @@ def test_dispatcher_rules():
     with pytest.raises(ValueError, match="Unknown backend"):
         kla_scan(*ins, backend="nope")
     # The MI355X kernels refuse CPU tensors and name a backend that works.
-    for name in ("hip", "hip_composed"):
+    for name in ("hip", "hip_fused", "hip_composed"):
         with pytest.raises(NotImplementedError, match="torch"):
             kla_scan(*ins, backend=name)
     # Families whose kernels are not part of this build say so.
@@ -221,7 +221,8 @@ def test_dispatcher_rules():
 COVERAGE = {
     "torch": "this file and test_oracle_pins.py",
     "hip": "tests/test_gpu_backend.py (GPU)",
-    "hip_composed": "tests/test_gpu_backend.py (GPU); same path as 'hip'",
+    "hip_fused": "tests/test_gpu_backend.py (GPU); the default path of 'hip'",
+    "hip_composed": "tests/test_gpu_backend.py (GPU)",
     "triton": "not in this build: raises NotImplementedError (test_dispatcher_rules)",
     "triton_fused": "not in this build: raises NotImplementedError",
     "triton_composed": "not in this build: raises NotImplementedError",
