@@ -17,9 +17,10 @@
 //
 // Layout. One thread owns one (b, m, s) lane chain and walks time serially; a
 // 256-thread workgroup holds CH = 256/SP channels of SP (= S rounded up to a
-// power of two) state lanes, so the SP lanes of a channel are consecutive and
-// the read-out sum over s is a DPP row reduction (SP <= 16) plus cross-row
-// shuffles (SP = 32, 64). Padding lanes (s >= S, m >= M) carry q = 0, k = 0 and
+// power of two, at least 4) state lanes, so the SP lanes of a channel are
+// consecutive and the read-out sum over s is a DPP row reduction (SP <= 16)
+// plus cross-row shuffles (SP = 32, 64). Inputs and outputs move through LDS
+// in double-buffered blocks of time steps (see "block staging"). Padding lanes (s >= S, m >= M) carry q = 0, k = 0 and
 // take part in every reduction without contributing to it. With 2^17 and more
 // chains (batch * M * S) the lane-serial walk fills the machine; time is not
 // split.
@@ -43,7 +44,7 @@ namespace kla {
 
 constexpr int kFusedThreads = 256;
 constexpr int kCkpt = 16;   // steps per checkpoint block
-constexpr int kFusedTB = 8; // steps per prefetch block in the forward
+constexpr int kFusedTB = 32; // steps per staged block in the forward
 
 struct FusedGeom {
   int64_t batch, steps, M, S;
@@ -111,10 +112,15 @@ __device__ __forceinline__ FusedLane fused_lane(const FusedGeom &g) {
 }
 
 // One step of the filter; returns lam_t and leaves the intermediates the
-// backward needs in the out-parameters.
+// backward needs in the out-parameters. The fused kernels are VALU-bound, so
+// quotients are formed with the hardware reciprocal (v_rcp_f32, 1 ulp) times the
+// numerator instead of the ~10-instruction IEEE division: a relative error of
+// ~2 ulp per step, which the contractive recurrence does not amplify.
 struct StepIO {
-  float phi, r, A, den, Da, alpha;
+  float phi, r, A, den, Da, alpha, inv_den, inv_Da;
 };
+
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
 __device__ __forceinline__ float filter_step(float lam, float &eta, float sig, float vv, float kk, float a_s,
                                              float a2, float pp, float inv_a2, float C, StepIO &io) {
@@ -122,22 +128,86 @@ __device__ __forceinline__ float filter_step(float lam, float &eta, float sig, f
   io.r = (vv * sig) * kk;
   io.A = (1.0f + pp * io.phi) * inv_a2;
   io.den = C * lam + 1.0f;
-  const float lam_t = (io.A * lam + io.phi) / io.den;
+  io.inv_den = rcp(io.den);
+  const float lam_t = (io.A * lam + io.phi) * io.inv_den;
   io.Da = fmaxf(a2 + pp * lam, kEps);
-  io.alpha = a_s / io.Da;
+  io.inv_Da = rcp(io.Da);
+  io.alpha = a_s * io.inv_Da;
   eta = io.alpha * eta + io.r;
   return lam_t;
+}
+
+// ------------------------------------------------------- block staging
+//
+// Per block of TB steps the workgroup moves its [TB, CH] tiles of the
+// [B, L, M] tensors and its [TB, S] rows of the [B, L, S] tensors through LDS:
+// a few coalesced global accesses per thread instead of one (broadcast) access
+// per lane and step. Tiles are stored channel-major ([CH][TB + 4]) so a lane
+// reads its channel's value at step j from one LDS word that all SP lanes of
+// the channel share.
+
+constexpr int kPad = 4;
+
+// Global -> registers: element e = tid + 256 i of the [TB, W] tile whose rows
+// are `row0 + t * ld` (t < rows) and columns c < cols of a row.
+template <int TB, int W>
+struct TileRegs {
+  static constexpr int N = (TB * W + kFusedThreads - 1) / kFusedThreads;
+  float x[N];
+};
+
+template <int TB, int W>
+__device__ __forceinline__ void tile_load(TileRegs<TB, W> &r, const float *__restrict__ base, int64_t ld,
+                                          int64_t rows, int64_t cols) {
+  const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+  for (int i = 0; i < TileRegs<TB, W>::N; ++i) {
+    const int e = tid + i * kFusedThreads;
+    const int t = e / W, c = e % W;
+    r.x[i] = (e < TB * W && t < rows && c < cols) ? __builtin_nontemporal_load(base + t * ld + c) : 0.0f;
+  }
+}
+
+template <int TB, int W>
+__device__ __forceinline__ void tile_to_lds(const TileRegs<TB, W> &r, float (*lds)[TB + kPad]) {
+  const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+  for (int i = 0; i < TileRegs<TB, W>::N; ++i) {
+    const int e = tid + i * kFusedThreads;
+    if (e < TB * W) lds[e % W][e / W] = r.x[i];
+  }
+}
+
+// LDS [W][TB + 4] -> global rows `row0 + t * ld`, columns c < cols.
+template <int TB, int W>
+__device__ __forceinline__ void lds_to_global(const float (*lds)[TB + kPad], float *__restrict__ base, int64_t ld,
+                                              int64_t rows, int64_t cols) {
+  const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+  for (int i = 0; i < TileRegs<TB, W>::N; ++i) {
+    const int e = tid + i * kFusedThreads;
+    const int t = e / W, c = e % W;
+    if (e < TB * W && t < rows && c < cols) __builtin_nontemporal_store(lds[c][t], base + t * ld + c);
+  }
 }
 
 // ================================================================ forward
 
 template <int SP, bool PRIOR>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdParams prm, FusedGeom g) {
+  constexpr int CH = kFusedThreads / SP;
+  constexpr int TB = kFusedTB;
+  __shared__ float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
+  __shared__ float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
+  __shared__ float s_y[2][CH][TB + kPad], s_yv[2][CH][TB + kPad];
+
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
-  const bool mok = ln.m < M, sok = ln.s < S;
+  const int64_t m0 = (static_cast<int64_t>(blockIdx.x) % g.groups) * CH;
+  const int c = static_cast<int>(ln.m - m0);
   const int64_t ms = ln.m * S + ln.s;
   const int64_t bms = ln.b * M * S + ms;
+  const int64_t cols_m = M - m0 < CH ? M - m0 : CH;
 
   const float a_s = ln.active ? prm.a[ms] : 1.0f;
   const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
@@ -147,62 +217,92 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
   float lam = (ln.active && prm.lam0) ? prm.lam0[bms] : 1.0f;
   float eta = (ln.active && prm.eta0) ? prm.eta0[bms] : 0.0f;
 
-  const float *__restrict__ vrow = prm.v + ln.b * L * M + ln.m;
-  const float *__restrict__ lrow = prm.lv + ln.b * L * M + ln.m;
-  const float *__restrict__ krow = prm.k + ln.b * L * S + ln.s;
-  const float *__restrict__ qrow = prm.q + ln.b * L * S + ln.s;
-  float *yrow = prm.y + ln.b * L * M + ln.m;
-  float *vyrow = prm.yvar + ln.b * L * M + ln.m;
+  const float *vbase = prm.v + ln.b * L * M + m0;
+  const float *lbase = prm.lv + ln.b * L * M + m0;
+  const float *kbase = prm.k + ln.b * L * S;
+  const float *qbase = prm.q + ln.b * L * S;
+  float *ybase = prm.y + ln.b * L * M + m0;
+  float *yvbase = prm.yvar + ln.b * L * M + m0;
 
-  float cv[kFusedTB], cl[kFusedTB], ck[kFusedTB], cq[kFusedTB];
-  float nv[kFusedTB], nl[kFusedTB], nk[kFusedTB], nq[kFusedTB];
-  auto fetch = [&](int64_t t0, float (&fv)[kFusedTB], float (&fl)[kFusedTB], float (&fk)[kFusedTB],
-                   float (&fq)[kFusedTB]) {
-#pragma unroll
-    for (int j = 0; j < kFusedTB; ++j) {
-      const int64_t t = t0 + j;
-      const bool tok = t < L;
-      fv[j] = (tok && mok) ? vrow[t * M] : 0.0f;
-      fl[j] = (tok && mok) ? lrow[t * M] : 0.0f;
-      fk[j] = (tok && sok) ? krow[t * S] : 0.0f;
-      fq[j] = (tok && sok) ? qrow[t * S] : 0.0f;
-    }
+  TileRegs<TB, CH> rv, rl;
+  TileRegs<TB, SP> rk, rq;
+  auto load = [&](int64_t t0) {
+    const int64_t rows = L - t0;
+    tile_load<TB, CH>(rv, vbase + t0 * M, M, rows, cols_m);
+    tile_load<TB, CH>(rl, lbase + t0 * M, M, rows, cols_m);
+    tile_load<TB, SP>(rk, kbase + t0 * S, S, rows, S);
+    tile_load<TB, SP>(rq, qbase + t0 * S, S, rows, S);
   };
-  fetch(0, cv, cl, ck, cq);
-  for (int64_t t0 = 0; t0 < L; t0 += kFusedTB) {
-    if (t0 + kFusedTB < L) fetch(t0 + kFusedTB, nv, nl, nk, nq);
+  auto stage = [&](int buf) {
+    tile_to_lds<TB, CH>(rv, s_v[buf]);
+    tile_to_lds<TB, CH>(rl, s_l[buf]);
+    tile_to_lds<TB, SP>(rk, s_k[buf]);
+    tile_to_lds<TB, SP>(rq, s_q[buf]);
+  };
+
+  // Checkpoint of the state entering step t: ck[((b * n_ck + t / kCkpt) * M + m) * S + s].
+  const int64_t ck_off = (ln.b * g.n_ck * M + ln.m) * S + ln.s;
+  const int64_t ck_stride = M * S;
+  static_assert(TB % kCkpt == 0, "checkpoints must fall on half-block boundaries");
+
+  const int64_t nblk = (L + TB - 1) / TB;
+  if (nblk > 0) {
+    load(0);
+    stage(0);
+  }
+  __syncthreads();
+  for (int64_t blk = 0; blk < nblk; ++blk) {
+    const int cur = static_cast<int>(blk & 1);
+    const int64_t t0 = blk * TB;
+    if (blk + 1 < nblk) load(t0 + TB);
+    if (blk > 0) {
+      lds_to_global<TB, CH>(s_y[cur ^ 1], ybase + (t0 - TB) * M, M, TB, cols_m);
+      lds_to_global<TB, CH>(s_yv[cur ^ 1], yvbase + (t0 - TB) * M, M, TB, cols_m);
+    }
+    // One step at block position j; FULL: the whole block lies inside the sequence.
+    auto step = [&](int j) {
+      StepIO io;
+      lam = filter_step(lam, eta, s_l[cur][c][j], s_v[cur][c][j], s_k[cur][ln.s][j], a_s, a2, pp, inv_a2, C, io);
+      const float var = rcp(fmaxf(lam, kEps));
+      float mean = eta * var, vo = var;
+      if (PRIOR) {
+        mean = a_s * mean;
+        vo = a2 * var + pp;
+      }
+      const float qq = s_q[cur][ln.s][j];
+      const float ys = group_sum<SP>(qq * mean);
+      const float vs = group_sum<SP>((qq * qq) * vo);
+      if (ln.s == 0) {
+        s_y[cur][c][j] = ys;
+        s_yv[cur][c][j] = vs;
+      }
+    };
+    // Checkpoints enter every kCkpt-step half of the block (TB is a multiple of kCkpt).
 #pragma unroll
-    for (int j = 0; j < kFusedTB; ++j) {
-      const int64_t t = t0 + j;
-      if (t < L) {
-        if (prm.ck_lam && (t % kCkpt) == 0 && ln.active) {
-          const int64_t ci = ((ln.b * g.n_ck + t / kCkpt) * M + ln.m) * S + ln.s;
-          prm.ck_lam[ci] = lam;
-          prm.ck_eta[ci] = eta;
+    for (int h = 0; h < TB / kCkpt; ++h) {
+      const int64_t th = t0 + h * kCkpt;
+      if (th < L) {
+        if (prm.ck_lam && ln.active) {
+          prm.ck_lam[ck_off + (th / kCkpt) * ck_stride] = lam;
+          prm.ck_eta[ck_off + (th / kCkpt) * ck_stride] = eta;
         }
-        StepIO io;
-        lam = filter_step(lam, eta, cl[j], cv[j], ck[j], a_s, a2, pp, inv_a2, C, io);
-        const float var = 1.0f / fmaxf(lam, kEps);
-        float mean = eta * var, vo = var;
-        if (PRIOR) {
-          mean = a_s * mean;
-          vo = a2 * var + pp;
-        }
-        const float ys = group_sum<SP>(cq[j] * mean);
-        const float vs = group_sum<SP>((cq[j] * cq[j]) * vo);
-        if (ln.s == 0 && mok) {
-          yrow[t * M] = ys;
-          vyrow[t * M] = vs;
+        if (th + kCkpt <= L) {
+#pragma unroll
+          for (int j = 0; j < kCkpt; ++j) step(h * kCkpt + j);
+        } else {
+          for (int j = 0; j < kCkpt; ++j)
+            if (th + j < L) step(h * kCkpt + j);
         }
       }
     }
-#pragma unroll
-    for (int j = 0; j < kFusedTB; ++j) {
-      cv[j] = nv[j];
-      cl[j] = nl[j];
-      ck[j] = nk[j];
-      cq[j] = nq[j];
-    }
+    if (blk + 1 < nblk) stage(cur ^ 1);
+    __syncthreads();
+  }
+  if (nblk > 0) {
+    const int last = static_cast<int>((nblk - 1) & 1);
+    const int64_t t0 = (nblk - 1) * TB;
+    lds_to_global<TB, CH>(s_y[last], ybase + t0 * M, M, L - t0, cols_m);
+    lds_to_global<TB, CH>(s_yv[last], yvbase + t0 * M, M, L - t0, cols_m);
   }
   if (ln.active) {
     prm.lam_fin[bms] = lam;
@@ -214,17 +314,25 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
 
 template <int SP, bool PRIOR>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdParams prm, FusedGeom g) {
+  constexpr int CH = kFusedThreads / SP;
   constexpr int NW = kFusedThreads / kWave;
-  __shared__ float s_red[2][kCkpt][NW][SP];
+  constexpr int TB = kCkpt;
+  __shared__ float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
+  __shared__ float s_dy[2][CH][TB + kPad], s_dyv[2][CH][TB + kPad];
+  __shared__ float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
+  __shared__ float s_dv[2][CH][TB + kPad], s_dl[2][CH][TB + kPad];
+  __shared__ float s_red[2][2][TB][NW][SP];
 
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
-  const bool mok = ln.m < M, sok = ln.s < S;
+  const int64_t grp = static_cast<int64_t>(blockIdx.x) % g.groups;
+  const int64_t m0 = grp * CH;
+  const int c = static_cast<int>(ln.m - m0);
   const int64_t ms = ln.m * S + ln.s;
   const int64_t bms = ln.b * M * S + ms;
+  const int64_t cols_m = M - m0 < CH ? M - m0 : CH;
   const int tid = static_cast<int>(threadIdx.x);
   const int wave = tid / kWave, lane = tid % kWave;
-  const int64_t grp = static_cast<int64_t>(blockIdx.x) % g.groups;
 
   const float a_s = ln.active ? prm.a[ms] : 1.0f;
   const float p_raw = ln.active ? prm.p[ms] : 0.0f;
@@ -237,53 +345,90 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
   float ge = (ln.active && prm.deta_fin) ? prm.deta_fin[bms] : 0.0f;   // adjoint of eta_t
   float acc_a = 0.0f, acc_a2 = 0.0f, acc_p = 0.0f;
 
-  const int64_t bLM = ln.b * L * M + ln.m, bLS = ln.b * L * S + ln.s;
-  const float *__restrict__ V = prm.v;
-  const float *__restrict__ LV = prm.lv;
-  const float *__restrict__ K = prm.k;
-  const float *__restrict__ Q = prm.q;
-  const float *__restrict__ DY = prm.dy;
-  const float *__restrict__ DYV = prm.dyvar;
+  const int64_t offM = ln.b * L * M + m0, offS = ln.b * L * S;
+  TileRegs<TB, CH> rv, rl, rdy, rdyv;
+  TileRegs<TB, SP> rk, rq;
+  auto load = [&](int64_t t0) {
+    const int64_t rows = L - t0;
+    tile_load<TB, CH>(rv, prm.v + offM + t0 * M, M, rows, cols_m);
+    tile_load<TB, CH>(rl, prm.lv + offM + t0 * M, M, rows, cols_m);
+    tile_load<TB, CH>(rdy, prm.dy + offM + t0 * M, M, rows, cols_m);
+    tile_load<TB, CH>(rdyv, prm.dyvar + offM + t0 * M, M, rows, cols_m);
+    tile_load<TB, SP>(rk, prm.k + offS + t0 * S, S, rows, S);
+    tile_load<TB, SP>(rq, prm.q + offS + t0 * S, S, rows, S);
+  };
+  auto stage = [&](int buf) {
+    tile_to_lds<TB, CH>(rv, s_v[buf]);
+    tile_to_lds<TB, CH>(rl, s_l[buf]);
+    tile_to_lds<TB, CH>(rdy, s_dy[buf]);
+    tile_to_lds<TB, CH>(rdyv, s_dyv[buf]);
+    tile_to_lds<TB, SP>(rk, s_k[buf]);
+    tile_to_lds<TB, SP>(rq, s_q[buf]);
+  };
+  // Outputs of block c (buffer `buf`): dv, dLv rows, and the workgroup's
+  // partial sums of dk, dq (the waves' sums added here, in wave order).
+  auto flush = [&](int64_t blk, int buf) {
+    const int64_t t0 = blk * TB;
+    lds_to_global<TB, CH>(s_dv[buf], prm.dv + offM + t0 * M, M, L - t0, cols_m);
+    lds_to_global<TB, CH>(s_dl[buf], prm.dlv + offM + t0 * M, M, L - t0, cols_m);
+    for (int i = tid; i < 2 * TB * SP; i += kFusedThreads) {
+      const int which = i / (TB * SP);
+      const int j = (i / SP) % TB;
+      const int s = i % SP;
+      const int64_t t = t0 + j;
+      if (t < L && s < S) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) sum += s_red[buf][which][j][w][s];
+        float *part = which == 0 ? prm.part_k : prm.part_q;
+        part[((ln.b * L + t) * g.groups + grp) * S + s] = sum;
+      }
+    }
+  };
 
-  for (int64_t c = g.n_ck - 1; c >= 0; --c) {
-    const int64_t t0 = c * kCkpt;
-    float lh[kCkpt], eh[kCkpt];   // lam_{t-1}, eta_{t-1} over the block
+  const int64_t n_ck = g.n_ck;
+  if (n_ck > 0) {
+    load((n_ck - 1) * TB);
+    stage(0);
+  }
+  __syncthreads();
+  for (int64_t i = 0; i < n_ck; ++i) {
+    const int cur = static_cast<int>(i & 1);
+    const int64_t blk = n_ck - 1 - i;
+    const int64_t t0 = blk * TB;
+    if (i + 1 < n_ck) load(t0 - TB);
+    if (i > 0) flush(blk + 1, cur ^ 1);
+
+    float lh[TB], eh[TB];   // lam_{t-1}, eta_{t-1} over the block
     {
-      const int64_t ci = ((ln.b * g.n_ck + c) * M + ln.m) * S + ln.s;
+      const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
       float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
       float eta = ln.active ? prm.ck_eta[ci] : 0.0f;
 #pragma unroll
-      for (int j = 0; j < kCkpt; ++j) {
+      for (int j = 0; j < TB; ++j) {
         lh[j] = lam;
         eh[j] = eta;
-        const int64_t t = t0 + j;
-        if (t < L) {
-          const float vv = mok ? V[bLM + t * M] : 0.0f;
-          const float sig = mok ? LV[bLM + t * M] : 0.0f;
-          const float kk = sok ? K[bLS + t * S] : 0.0f;
+        if (t0 + j < L) {
           StepIO io;
-          lam = filter_step(lam, eta, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
+          lam = filter_step(lam, eta, s_l[cur][c][j], s_v[cur][c][j], s_k[cur][ln.s][j], a_s, a2, pp, inv_a2, C,
+                            io);
         }
       }
     }
 #pragma unroll
-    for (int j = kCkpt - 1; j >= 0; --j) {
+    for (int j = TB - 1; j >= 0; --j) {
       const int64_t t = t0 + j;
       float dk_c = 0.0f, dq_c = 0.0f;
       if (t < L) {
-        const float vv = mok ? V[bLM + t * M] : 0.0f;
-        const float sig = mok ? LV[bLM + t * M] : 0.0f;
-        const float dy = mok ? DY[bLM + t * M] : 0.0f;
-        const float dyv = mok ? DYV[bLM + t * M] : 0.0f;
-        const float kk = sok ? K[bLS + t * S] : 0.0f;
-        const float qq = sok ? Q[bLS + t * S] : 0.0f;
+        const float vv = s_v[cur][c][j], sig = s_l[cur][c][j];
+        const float dy = s_dy[cur][c][j], dyv = s_dyv[cur][c][j];
+        const float kk = s_k[cur][ln.s][j], qq = s_q[cur][ln.s][j];
         const float lp = lh[j], ep = eh[j];
 
         StepIO io;
         float eta_t = ep;
         const float lam_t = filter_step(lp, eta_t, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
-        const float lclamp = fmaxf(lam_t, kEps);
-        const float var = 1.0f / lclamp;
+        const float var = rcp(fmaxf(lam_t, kEps));
         const float mean = eta_t * var;
         const float mean_o = PRIOR ? a_s * mean : mean;
         const float var_o = PRIOR ? a2 * var + pp : var;
@@ -308,15 +453,15 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         const float dr = ge_t;
         ge = ge_t * io.alpha;
         // alpha = a / Da, Da = max(a2 + p' lam', EPS)
-        acc_a += dalpha / io.Da;
-        const float dDa = (a2 + pp * lp >= kEps) ? -dalpha * io.alpha / io.Da : 0.0f;
+        acc_a += dalpha * io.inv_Da;
+        const float dDa = (a2 + pp * lp >= kEps) ? -dalpha * io.alpha * io.inv_Da : 0.0f;
         acc_a2 += dDa;
         acc_p += dDa * lp;
         // lam_t = (A lam' + phi) / den, den = C lam' + 1;  d lam_t / d lam' = 1/(a2 den^2)
-        const float u = gl_t / io.den;
+        const float u = gl_t * io.inv_den;
         const float dA = u * lp;
         const float dC = -u * lam_t * lp;
-        gl = gl_t * (inv_a2 / (io.den * io.den)) + dDa * pp;
+        gl = u * io.inv_den * inv_a2 + dDa * pp;
         // A = (1 + p' phi)/a2, C = p'/a2
         const float dphi = u + dA * pp * inv_a2;
         acc_p += (dA * io.phi + dC) * inv_a2;
@@ -328,36 +473,23 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         dk_c = dphi * 2.0f * sig * kk + dr * (vv * sig);
         const float dv_s = group_sum<SP>(dv_c);
         const float dl_s = group_sum<SP>(dsig_c);
-        if (ln.s == 0 && mok) {
-          prm.dv[bLM + t * M] = dv_s;
-          prm.dlv[bLM + t * M] = dl_s;
+        if (ln.s == 0) {
+          s_dv[cur][c][j] = dv_s;
+          s_dl[cur][c][j] = dl_s;
         }
       }
-      // Partial sums over this workgroup's channels: across the lane groups of
-      // the wave here, across the waves once the block is done.
+      // Sum over this wave's channels now, over the waves at the flush.
       dk_c = cross_group_sum<SP>(dk_c);
       dq_c = cross_group_sum<SP>(dq_c);
       if (lane < SP) {
-        s_red[0][j][wave][lane] = dk_c;
-        s_red[1][j][wave][lane] = dq_c;
+        s_red[cur][0][j][wave][lane] = dk_c;
+        s_red[cur][1][j][wave][lane] = dq_c;
       }
     }
-    __syncthreads();
-    for (int i = tid; i < 2 * kCkpt * SP; i += kFusedThreads) {
-      const int which = i / (kCkpt * SP);
-      const int j = (i / SP) % kCkpt;
-      const int s = i % SP;
-      const int64_t t = t0 + j;
-      if (t < L && s < S) {
-        float sum = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) sum += s_red[which][j][w][s];
-        float *part = which == 0 ? prm.part_k : prm.part_q;
-        part[((ln.b * L + t) * g.groups + grp) * S + s] = sum;
-      }
-    }
+    if (i + 1 < n_ck) stage(cur ^ 1);
     __syncthreads();
   }
+  if (n_ck > 0) flush(0, static_cast<int>((n_ck - 1) & 1));
 
   if (ln.active) {
     if (prm.dlam0) prm.dlam0[bms] = gl;

@@ -181,8 +181,9 @@ int zero_state(const char *fn, float *p, int64_t count, hipStream_t stream) {
 
 // ----------------------------------------------------------- fused scan
 
+// State lanes per channel in the fused kernels: S rounded up to a power of two, at least 4.
 int sp_of(int64_t S) {
-  int sp = 1;
+  int sp = 4;
   while (sp < S) sp *= 2;
   return sp;
 }
@@ -217,8 +218,6 @@ int check_fused_shape(const char *fn, int64_t batch, int64_t steps, int64_t M, i
 template <class F>
 int with_sp(int64_t S, F &&f) {
   switch (sp_of(S)) {
-    case 1: return f(std::integral_constant<int, 1>{});
-    case 2: return f(std::integral_constant<int, 2>{});
     case 4: return f(std::integral_constant<int, 4>{});
     case 8: return f(std::integral_constant<int, 8>{});
     case 16: return f(std::integral_constant<int, 16>{});
