@@ -251,10 +251,23 @@ def bench_layer(args, device, stream) -> dict:
             tok = logits[:, -1].argmax(-1, keepdim=True)
 
     dec_ms = _timed(decode256, 1, 1, stream)
-    return {"metric": "SequenceModel(d=512, 6 layers) prefill tokens/s (16x2048) + decode ms/token (256 steps)",
-            "value": 16 * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
-            "decode_ms_per_token": round(dec_ms / 256, 4), "backend": args.backend,
-            "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
+    out = {"metric": "SequenceModel(d=512, 6 layers) prefill tokens/s (16x2048) + decode ms/token (256 steps)",
+           "value": 16 * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
+           "decode_ms_per_token": round(dec_ms / 256, 4), "backend": args.backend}
+    if args.backend.startswith("hip"):
+        from kla.models.decode_graph import DecodeGraph
+
+        graph = DecodeGraph(model, state["s"])
+
+        @torch.no_grad()
+        def decode256_graph():
+            tok = state["tok"]
+            for _ in range(256):
+                tok = graph.step(tok)[:, -1].argmax(-1, keepdim=True)
+
+        out["decode_graph_ms_per_token"] = round(_timed(decode256_graph, 1, 1, stream) / 256, 4)
+    out["peak_mem_GiB"] = round(torch.cuda.max_memory_allocated(device) / 2**30, 2)
+    return out
 
 
 def main(argv=None) -> int:

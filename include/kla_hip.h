@@ -170,6 +170,16 @@ int kla_fused_scan_bwd(const float *dy, const float *dy_var, const float *dlam_f
                        int64_t M, int64_t S, void *workspace, size_t workspace_bytes,
                        hipStream_t stream);
 
+/*
+ * One O(1) decode step of the filter for every (b, m, s) lane: kla_step
+ * (reference src/kla/ops/kla_ops.py:293-331), phi floored at 1e-12 as there.
+ * v, lambda_v, y, y_var [batch, M]; k, q [batch, S]; a, p [M, S]; lam, eta,
+ * lam_out, eta_out [batch, M, S] (lam_out / eta_out may alias lam / eta). No gradient.
+ */
+int kla_step_fwd(const float *v, const float *lambda_v, const float *k, const float *q, const float *a,
+                 const float *p, const float *lam, const float *eta, float *y, float *y_var, float *lam_out,
+                 float *eta_out, int decode_from_prior, int64_t batch, int64_t M, int64_t S, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

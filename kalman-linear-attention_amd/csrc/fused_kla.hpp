@@ -513,3 +513,64 @@ __global__ void reduce_groups_kernel(const float *__restrict__ in, float *__rest
 }
 
 }  // namespace kla
+
+namespace kla {
+
+// ========================================================== one decode step
+//
+// kla_step (reference src/kla/ops/kla_ops.py:293-331) for every (b, m, s) lane:
+//   phi = max(Lv k^2, EPS)  (the step floors phi, the scan does not)
+//   r = (v Lv) k,  denom = max(a2 + p' lam, EPS)
+//   lam <- lam/denom + phi,  eta <- (a/denom) eta + r
+//   var = 1/max(lam, EPS), mean = eta var (prior: mean = a mean, var = a2 var + p')
+//   y[b, m] = sum_s q mean,  y_var[b, m] = sum_s q^2 var
+// Same lane layout as the fused scan. lam_out / eta_out may alias lam / eta
+// (each lane reads its own element before writing it). IEEE division: the step
+// is tiny and launch-bound, not VALU-bound.
+
+struct StepParams {
+  const float *v, *lv, *k, *q, *a, *p, *lam, *eta;
+  float *y, *yvar, *lam_out, *eta_out;
+};
+
+template <int SP, bool PRIOR>
+__global__ void __launch_bounds__(kFusedThreads) kla_step_kernel(StepParams prm, FusedGeom g) {
+  const FusedLane ln = fused_lane<SP>(g);
+  const int64_t M = g.M, S = g.S;
+  const bool mok = ln.m < M, sok = ln.s < S;
+  const int64_t ms = ln.m * S + ln.s;
+  const int64_t bms = ln.b * M * S + ms;
+  const float a_s = ln.active ? prm.a[ms] : 1.0f;
+  const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
+  const float a2 = fmaxf(a_s * a_s, kEps);
+  const float vv = mok ? prm.v[ln.b * M + ln.m] : 0.0f;
+  const float sig = mok ? prm.lv[ln.b * M + ln.m] : 0.0f;
+  const float kk = sok ? prm.k[ln.b * S + ln.s] : 0.0f;
+  const float qq = sok ? prm.q[ln.b * S + ln.s] : 0.0f;
+  float lam = ln.active ? prm.lam[bms] : 1.0f;
+  float eta = ln.active ? prm.eta[bms] : 0.0f;
+
+  const float phi = fmaxf(sig * (kk * kk), kEps);
+  const float r = (vv * sig) * kk;
+  const float denom = fmaxf(a2 + pp * lam, kEps);
+  lam = lam / denom + phi;
+  eta = (a_s / denom) * eta + r;
+  const float var = 1.0f / fmaxf(lam, kEps);
+  float mean = eta * var, vo = var;
+  if (PRIOR) {
+    mean = a_s * mean;
+    vo = a2 * var + pp;
+  }
+  const float ys = group_sum<SP>(mean * qq);
+  const float vs = group_sum<SP>(vo * (qq * qq));
+  if (ln.s == 0 && mok) {
+    prm.y[ln.b * M + ln.m] = ys;
+    prm.yvar[ln.b * M + ln.m] = vs;
+  }
+  if (ln.active) {
+    prm.lam_out[bms] = lam;
+    prm.eta_out[bms] = eta;
+  }
+}
+
+}  // namespace kla

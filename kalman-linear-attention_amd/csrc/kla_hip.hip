@@ -476,4 +476,31 @@ int kla_fused_scan_bwd(const float *dy, const float *dy_var, const float *dlam_f
   return reduce(part_p, dp, 1, batch, M * S);
 }
 
+int kla_step_fwd(const float *v, const float *lambda_v, const float *k, const float *q, const float *a,
+                 const float *p, const float *lam, const float *eta, float *y, float *y_var, float *lam_out,
+                 float *eta_out, int decode_from_prior, int64_t batch, int64_t M, int64_t S, hipStream_t stream) {
+  const char *fn = "kla_step_fwd";
+  int rc = check_fused_shape(fn, batch, 1, M, S);
+  if (rc != KLA_OK) return rc;
+  if (batch == 0 || M == 0 || S == 0) return KLA_OK;
+  if (!v || !lambda_v || !k || !q || !a || !p || !lam || !eta || !y || !y_var || !lam_out || !eta_out)
+    return fail(KLA_ERR_INVALID_ARG, "%s: NULL operand", fn);
+  if (!all_aligned(4, {v, lambda_v, k, q, a, p, lam, eta, y, y_var, lam_out, eta_out}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  const FusedGeom g = fused_geom(batch, 1, M, S);
+  const int64_t grid = batch * g.groups;
+  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+  const StepParams prm{v, lambda_v, k, q, a, p, lam, eta, y, y_var, lam_out, eta_out};
+  return with_sp(S, [&](auto sp) {
+    constexpr int SP = decltype(sp)::value;
+    if (decode_from_prior)
+      hipLaunchKernelGGL((kla_step_kernel<SP, true>), dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0,
+                         stream, prm, g);
+    else
+      hipLaunchKernelGGL((kla_step_kernel<SP, false>), dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0,
+                         stream, prm, g);
+    return hip_status(fn, hipGetLastError());
+  });
+}
+
 }  // extern "C"

@@ -83,7 +83,14 @@ class CausalConv1d(nn.Module):
         if conv_state is None:
             conv_state = self.init_state(x.shape[0], device=x.device, dtype=xt.dtype)
         padded = torch.cat((conv_state.to(xt.dtype), xt), dim=-1)
-        y = F.conv1d(padded, self.weight, self.bias, groups=self.dim)
+        if xt.shape[-1] == 1:
+            # One decode token: the depthwise conv is a kernel_size-tap weighted sum
+            # per channel (no convolution library call, so it replays in a HIP graph).
+            y = (padded * self.weight[:, 0, :].to(padded.dtype)).sum(-1, keepdim=True)
+            if self.bias is not None:
+                y = y + self.bias.to(y.dtype).unsqueeze(-1)
+        else:
+            y = F.conv1d(padded, self.weight, self.bias, groups=self.dim)
         keep = self.kernel_size - 1
         new_state = padded[..., padded.shape[-1] - keep:]
         return self.act(y).transpose(1, 2), new_state

@@ -185,7 +185,7 @@ class KLALayer(nn.Module):
         a_bar, p_bar = self._compute_aq()
         with torch.autocast(device_type=z.device.type, enabled=False):
             y, y_var, new_state = kla_step(v[:, 0], lambda_v[:, 0], k[:, 0], q[:, 0], a_bar, p_bar, ssm_state,
-                                           decode_from_prior=cfg.decode_from_prior)
+                                           decode_from_prior=cfg.decode_from_prior, backend=cfg.backend)
         return y.unsqueeze(1), y_var.unsqueeze(1), new_state
 
     def forward(self, x: torch.Tensor, state: KLALayerState | None = None, return_state: bool = False):

@@ -152,16 +152,28 @@ class SequenceModel(MarginalReadout, nn.Module):
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, temperature: float = 1.0,
-                 top_k: Optional[int] = None) -> torch.Tensor:
-        """Sample with recurrent state: one prefill, then O(1) work per new token."""
+                 top_k: Optional[int] = None, cuda_graph: bool = False) -> torch.Tensor:
+        """Sample with recurrent state: one prefill, then O(1) work per new token.
+
+        ``cuda_graph`` replays the one-token step as a HIP graph
+        (:class:`kla.models.decode_graph.DecodeGraph`); same tokens, fewer launches.
+        """
         self.eval()
         state = self.init_state(input_ids.shape[0])
         logits, state = self.forward(input_ids, state=state)
         out = [input_ids]
         token = self._sample(logits[:, -1], temperature, top_k)
+        graph = None
+        if cuda_graph and max_new_tokens > 1:
+            from kla.models.decode_graph import DecodeGraph
+
+            graph = DecodeGraph(self, state)
         for _ in range(max_new_tokens - 1):
             out.append(token)
-            logits, state = self.forward(token, state=state)
+            if graph is not None:
+                logits = graph.step(token)
+            else:
+                logits, state = self.forward(token, state=state)
             token = self._sample(logits[:, -1], temperature, top_k)
         out.append(token)
         return torch.cat(out, dim=1)

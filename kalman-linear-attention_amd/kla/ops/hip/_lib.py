@@ -49,6 +49,7 @@ _SIGNATURES = {
     "kla_fused_workspace_bytes": (ctypes.c_size_t, [_i64] * 4),
     "kla_fused_scan_fwd": (ctypes.c_int, [_p] * 14 + [ctypes.c_int] + [_i64] * 4 + [_p]),
     "kla_fused_scan_bwd": (ctypes.c_int, [_p] * 20 + [ctypes.c_int] + [_i64] * 4 + [_p, ctypes.c_size_t, _p]),
+    "kla_step_fwd": (ctypes.c_int, [_p] * 12 + [ctypes.c_int] + [_i64] * 3 + [_p]),
 }
 
 

@@ -221,11 +221,23 @@ def kla_step(
     p: torch.Tensor,  # [M, S]
     state: KLAState,
     decode_from_prior: bool = False,
+    *,
+    backend: str = "torch",
 ):
     """One filter step for O(1) decode. Returns (y [B, M], y_var [B, M], new_state).
 
     Reference kla_ops.py:293-331; phi is floored at EPS here, as there.
+    ``backend`` names the family the caller runs on (the layer passes its
+    config's): the "hip" family (and "auto" on a ROCm GPU) uses the one-kernel
+    MI355X step when no gradient is required; every other case is the torch
+    formula below.
     """
+    if backend != "torch" and _step_on_hip(backend, v) and not (
+            torch.is_grad_enabled() and any(t.requires_grad for t in (v, lambda_v, k, q, a, p, *state))):
+        from kla.ops.hip.step import kla_step_hip
+
+        y, y_var, lam, eta = kla_step_hip(v, lambda_v, k, q, a, p, state.lam, state.eta, decode_from_prior)
+        return y, y_var, KLAState(lam=lam, eta=eta)
     v, lambda_v, k, q = _compute_dtype(v, lambda_v, k, q)
     dtype = v.dtype
     phi = (lambda_v.unsqueeze(-1) * (k * k).unsqueeze(-2)).clamp_min(EPS)
@@ -245,6 +257,15 @@ def kla_step(
     y = torch.einsum("bms,bs->bm", mean, q)
     y_var = torch.einsum("bms,bs->bm", var, q * q)
     return y, y_var, KLAState(lam=lam, eta=eta)
+
+
+def _step_on_hip(backend: str, x: torch.Tensor) -> bool:
+    """Whether ``kla_step`` for ``backend`` runs on the MI355X step kernel."""
+    if not x.is_cuda or x.dtype == torch.float64:
+        return False
+    if backend == "auto":
+        backend = _resolve_auto(x)
+    return backend.split("_", 1)[0] == "hip" and _hip_available()
 
 
 def kla_scan_reference(v, lambda_v, k, q, a, p, initial_state: Optional[KLAState] = None,

@@ -173,3 +173,25 @@ def test_python_errors_carry_the_message():
     with pytest.raises(_lib.KLAHipError, match="must not be NULL"):
         _mobius_fwd(_lib.lib(), A=None)
         _lib.check("kla_mobius_scan_fwd", _lib.KLA_ERR_INVALID_ARG)
+
+
+def test_fused_and_step_validation(lib):
+    p = [ALIGNED] * 14
+    shape = (2, 5, 6, 16)
+    assert lib.kla_fused_scan_fwd(*p[:12], None, None, 0, 2, 5, 6, 65, None) == _lib.KLA_ERR_INVALID_ARG
+    assert "above 64" in err(lib)
+    assert lib.kla_fused_scan_fwd(*p[:12], ALIGNED, None, 0, *shape, None) == _lib.KLA_ERR_INVALID_ARG
+    assert "both checkpoint buffers" in err(lib)
+    assert lib.kla_fused_scan_fwd(None, *p[1:12], None, None, 0, *shape, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_fused_scan_fwd(ODD, *p[1:12], None, None, 0, *shape, None) == _lib.KLA_ERR_ALIGN
+    assert lib.kla_fused_scan_fwd(*p[:12], None, None, 0, 0, 5, 6, 16, None) == _lib.KLA_OK
+    assert lib.kla_fused_checkpoints(33) == 3 and lib.kla_fused_checkpoints(0) == 0
+    n = lib.kla_fused_workspace_bytes(*shape)
+    assert n >= 4 * (2 * 2 * 5 * 16 + 2 * 2 * 6 * 16)
+    q = [ALIGNED] * 20
+    assert lib.kla_fused_scan_bwd(*q, 0, *shape, None, n, None) == _lib.KLA_ERR_WORKSPACE
+    assert lib.kla_fused_scan_bwd(*q, 0, *shape, WS, n - 4, None) == _lib.KLA_ERR_WORKSPACE
+    assert lib.kla_fused_scan_bwd(*q[:4], None, *q[5:], 0, *shape, WS, n, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_step_fwd(*[ALIGNED] * 11, None, 0, 2, 6, 16, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_step_fwd(*[ALIGNED] * 11, ODD, 0, 2, 6, 16, None) == _lib.KLA_ERR_ALIGN
+    assert lib.kla_step_fwd(*[ALIGNED] * 12, 0, 2, 6, 100, None) == _lib.KLA_ERR_INVALID_ARG

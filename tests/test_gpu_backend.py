@@ -263,3 +263,58 @@ def test_sequence_model_prefill_and_decode_on_hip(cuda):
             o, state = model(ids[:, t:t + 1], state=state)
             tail.append(o)
     torch.testing.assert_close(torch.cat([head] + tail, 1), full, rtol=1e-4, atol=1e-4)
+
+
+# ------------------------------------------------------------ decode step
+
+
+@pytest.mark.parametrize("decode_from_prior", [False, True])
+@pytest.mark.parametrize("shape", [(2, 16, 8), (3, 70, 5), (1, 9, 64), (4, 33, 1)])
+def test_step_kernel_matches_reference_step(cuda, decode_from_prior, shape):
+    """kla_step(backend="hip") (one HIP kernel) against the reference's step
+    formula evaluated in float64 (kla_ops.py:293-331, phi floored)."""
+    from kla.ops import kla_step
+
+    B, M, S = shape
+    v, lv, k, q, a, p = make_inputs(B, 1, M, S, seed=9)
+    st = random_state(B, M, S)
+    ins = (v[:, 0], lv[:, 0], k[:, 0], q[:, 0], a, p)
+    want = kla_step(*(t.double() for t in ins), KLAState(st.lam.double(), st.eta.double()),
+                    decode_from_prior=decode_from_prior)
+    with torch.no_grad():
+        got = kla_step(*(t.to(cuda) for t in ins), KLAState(st.lam.to(cuda), st.eta.to(cuda)),
+                       decode_from_prior=decode_from_prior, backend="hip")
+    for name, g, w in (("y", got[0], want[0]), ("y_var", got[1], want[1]), ("lam", got[2].lam, want[2].lam),
+                       ("eta", got[2].eta, want[2].eta)):
+        check(name, g, w.numpy())
+
+
+def test_decode_graph_replays_match_eager(cuda):
+    """The one-token step replayed as a HIP graph gives the eager step's logits and
+    state at every replay, with eager work and synchronisations between replays;
+    greedy generation is token-identical with and without the graph."""
+    from kla.models.decode_graph import DecodeGraph
+
+    torch.manual_seed(0)
+    model = SequenceModel(ModelConfig(vocab_size=97, d_model=32, n_layers=2),
+                          KLAConfig(d_state=4, backend="hip")).to(cuda).eval()
+    ids = torch.randint(0, 97, (3, 12), generator=torch.Generator().manual_seed(1)).to(cuda)
+    toks = torch.randint(0, 97, (3, 6), generator=torch.Generator().manual_seed(2)).to(cuda)
+    with torch.no_grad():
+        _, state = model(ids, state=model.init_state(3))
+        graph = DecodeGraph(model, state)
+        eager_state = state
+        for i in range(6):
+            tok = toks[:, i:i + 1]
+            want, eager_state = model(tok, state=eager_state)      # eager work between replays
+            torch.cuda.synchronize()
+            got = graph.step(tok)
+            torch.cuda.synchronize()
+            torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+            for layer_g, layer_e in zip(graph.state, eager_state):
+                torch.testing.assert_close(layer_g.ssm.lam, layer_e.ssm.lam, rtol=1e-6, atol=0)
+                torch.testing.assert_close(layer_g.ssm.eta, layer_e.ssm.eta, rtol=1e-6, atol=1e-7)
+                torch.testing.assert_close(layer_g.conv, layer_e.conv, rtol=0, atol=0)
+        a = model.generate(ids, 10, temperature=0.0)
+        b = model.generate(ids, 10, temperature=0.0, cuda_graph=True)
+    assert torch.equal(a, b)
