@@ -41,6 +41,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace kla {
 
 constexpr float kEps = 1e-12f;   // EPS = P_MIN of the reference (kla_ops.py:43-44)
@@ -209,6 +211,48 @@ __device__ __forceinline__ void fill_v(float (&o)[V], float x) {
 #pragma unroll
   for (int v = 0; v < V; ++v) o[v] = x;
 }
+
+// V consecutive sequence elements as held in registers: fp32 as V floats, bf16
+// packed two to a 32-bit register and widened on read, so a bf16 tile costs
+// half the VGPRs of the same tile in fp32.
+template <class IO, int V>
+struct Lanes;
+
+template <int V>
+struct Lanes<float, V> {
+  float w[V];
+  __device__ __forceinline__ float operator[](int v) const { return w[v]; }
+  __device__ __forceinline__ void fill(float x) { fill_v(w, x); }
+  __device__ __forceinline__ void load(const float *p) { load_v<V>(p, w); }
+};
+
+template <int V>
+struct Lanes<bf16_t, V> {
+  static constexpr int N = (V + 1) / 2;
+  uint32_t w[N];
+  __device__ __forceinline__ float operator[](int v) const {
+    const uint32_t x = w[v >> 1];
+    return __uint_as_float((v & 1) ? (x & 0xFFFF0000u) : (x << 16));
+  }
+  // x must be exact in bf16 (the fills are 0 and 1).
+  __device__ __forceinline__ void fill(float x) {
+    const uint32_t b = __float_as_uint(x) >> 16;
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = b | (b << 16);
+  }
+  __device__ __forceinline__ void load(const bf16_t *p) {
+    if constexpr (V == 1) {
+      w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
+    } else if constexpr (V == 2) {
+      w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+    } else {
+      static_assert(V == 4, "V must be 1, 2 or 4");
+      const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(p));
+      w[0] = u.x;
+      w[1] = u.y;
+    }
+  }
+};
 
 // ------------------------------------------------------------ affine monoid
 // (m, c) is the map x -> m*x + c; composing later (L) after earlier (M) gives
@@ -485,7 +529,7 @@ struct AffineFwd {
   };
   template <int S, int V>
   struct Raw {
-    float g[S][V], u[S][V];
+    Lanes<IO, V> g[S], u[S];
   };
   template <int S, int V>
   using Regs = Raw<S, V>;
@@ -496,16 +540,16 @@ struct AffineFwd {
     const int64_t row = row_index(gm, q, s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-      fill_v(r.g[j], 1.0f);
-      fill_v(r.u[j], 0.0f);
+      r.g[j].fill(1.0f);
+      r.u[j].fill(0.0f);
     }
     if (!q.ok) return;
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
         const int64_t rj = row + j * gm.lanes;
-        load_v<V>(at(p.g, rj, q), r.g[j]);
-        load_v<V>(at(p.u, rj, q), r.u[j]);
+        r.g[j].load(at(p.g, rj, q));
+        r.u[j].load(at(p.u, rj, q));
       }
     }
   }
@@ -556,9 +600,13 @@ struct AffineBwd {
     IO *dg, *du;
     float *dh0;
   };
+  // bf16 registers hold h_{-1} = h0 (fp32 state) apart, so it is not rounded;
+  // in fp32 it simply takes the place of h_{t-1} at time 0.
+  static constexpr bool SPLIT_H0 = !std::is_same<IO, float>::value;
   template <int S, int V>
   struct Raw {
-    float dh[S][V], g[S][V], hp[S][V];   // hp[j] = h_{t-1} for step j's time t
+    Lanes<IO, V> dh[S], g[S], hp[S];   // hp[j] = h_{t-1} for step j's time t
+    float h_init[SPLIT_H0 ? V : 1];    // h0, for the position at time 0 (bf16 only)
   };
   template <int S, int V>
   using Regs = Raw<S, V>;
@@ -569,21 +617,26 @@ struct AffineBwd {
     const int64_t row = row_index(gm, q, gm.steps - 1 - s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
-      fill_v(r.dh[j], 0.0f);
-      fill_v(r.g[j], 1.0f);
-      fill_v(r.hp[j], 0.0f);
+      r.dh[j].fill(0.0f);
+      r.g[j].fill(1.0f);
+      r.hp[j].fill(0.0f);
     }
+    fill_v(r.h_init, 0.0f);
     if (!q.ok) return;
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
         const int64_t rj = row - j * gm.lanes;
-        load_v<V>(at(p.dh, rj, q), r.dh[j]);
-        load_v<V>(at(p.g, rj, q), r.g[j]);
-        if (s0 + j + 1 < gm.steps)
-          load_v<V>(at(p.h, rj - gm.lanes, q), r.hp[j]);
-        else if (p.h0)
-          load_state_v<V>(p.h0 + state_index(gm, q), r.hp[j]);
+        r.dh[j].load(at(p.dh, rj, q));
+        r.g[j].load(at(p.g, rj, q));
+        if (s0 + j + 1 < gm.steps) {
+          r.hp[j].load(at(p.h, rj - gm.lanes, q));
+        } else if (p.h0) {
+          if constexpr (SPLIT_H0)
+            load_state_v<V>(p.h0 + state_index(gm, q), r.h_init);
+          else
+            load_state_v<V>(p.h0 + state_index(gm, q), r.hp[j].w);
+        }
       }
     }
   }
@@ -611,11 +664,12 @@ struct AffineBwd {
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
         const int64_t rj = row - j * gm.lanes;
+        const bool first = SPLIT_H0 && s0 + j + 1 >= gm.steps;   // bf16: time 0 takes h0 apart
         float dg[V], mu[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           mu[v] = r.dh[j][v] + x[v];
-          dg[v] = mu[v] * r.hp[j][v];
+          dg[v] = mu[v] * (first ? r.h_init[SPLIT_H0 ? v : 0] : r.hp[j][v]);
           x[v] = r.g[j][v] * mu[v];
         }
         if (q.ok) {
