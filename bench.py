@@ -106,7 +106,7 @@ def cpu_model_name() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(lanes_full: int, budget_s: float = 12.0) -> dict:
+def cpu_baseline(lanes_full: int, budget_s: float = 15.0) -> dict:
     """The reference's pure-PyTorch CPU scan (oracle.torch_ref: doubling scans of the
     trace-normalised Moebius combine and the affine combine, backward by autograd),
     fp32, on a bounded sample: batch 1, 4096 steps, all lanes; repeated to fill
@@ -127,7 +127,7 @@ def cpu_baseline(lanes_full: int, budget_s: float = 12.0) -> dict:
 
     t0 = time.perf_counter()
     one()  # warm-up
-    reps = int(min(20, max(3, budget_s / max(time.perf_counter() - t0, 1e-3))))
+    reps = int(min(60, max(3, budget_s / max(time.perf_counter() - t0, 1e-3))))
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()

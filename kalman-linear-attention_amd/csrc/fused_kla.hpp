@@ -400,6 +400,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     if (i > 0) flush(blk + 1, cur ^ 1);
 
     float lh[TB], eh[TB];   // lam_{t-1}, eta_{t-1} over the block
+    // da, dp sum over all steps: accumulate each block apart and add the block
+    // totals (two-level summation keeps fp32 rounding at ~(TB + L/TB) ulp).
+    float blk_a = 0.0f, blk_a2 = 0.0f, blk_p = 0.0f;
     {
       const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
       float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
@@ -440,9 +443,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         if (PRIOR) {
           dmean = dmo * a_s;
           dvar = dvo * a2;
-          acc_a += dmo * mean;
-          acc_a2 += dvo * var;
-          acc_p += dvo;
+          blk_a += dmo * mean;
+          blk_a2 += dvo * var;
+          blk_p += dvo;
         }
         // mean = eta var, var = 1/max(lam, EPS)
         const float ge_t = ge + dmean * var;
@@ -453,10 +456,10 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         const float dr = ge_t;
         ge = ge_t * io.alpha;
         // alpha = a / Da, Da = max(a2 + p' lam', EPS)
-        acc_a += dalpha * io.inv_Da;
+        blk_a += dalpha * io.inv_Da;
         const float dDa = (a2 + pp * lp >= kEps) ? -dalpha * io.alpha * io.inv_Da : 0.0f;
-        acc_a2 += dDa;
-        acc_p += dDa * lp;
+        blk_a2 += dDa;
+        blk_p += dDa * lp;
         // lam_t = (A lam' + phi) / den, den = C lam' + 1;  d lam_t / d lam' = 1/(a2 den^2)
         const float u = gl_t * io.inv_den;
         const float dA = u * lp;
@@ -464,8 +467,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         gl = u * io.inv_den * inv_a2 + dDa * pp;
         // A = (1 + p' phi)/a2, C = p'/a2
         const float dphi = u + dA * pp * inv_a2;
-        acc_p += (dA * io.phi + dC) * inv_a2;
-        acc_a2 -= (dA * io.A + dC * C) * inv_a2;
+        blk_p += (dA * io.phi + dC) * inv_a2;
+        blk_a2 -= (dA * io.A + dC * C) * inv_a2;
         // phi = Lv k^2, r = (v Lv) k
         const float dmsi = dr * kk;
         const float dsig_c = dphi * (kk * kk) + dmsi * vv;
@@ -486,6 +489,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         s_red[cur][1][j][wave][lane] = dq_c;
       }
     }
+    acc_a += blk_a;
+    acc_a2 += blk_a2;
+    acc_p += blk_p;
     if (i + 1 < n_ck) stage(cur ^ 1);
     __syncthreads();
   }

@@ -318,3 +318,83 @@ def test_decode_graph_replays_match_eager(cuda):
         a = model.generate(ids, 10, temperature=0.0)
         b = model.generate(ids, 10, temperature=0.0, cuda_graph=True)
     assert torch.equal(a, b)
+
+
+# ------------------------------------------------------- full BASELINE sizes
+
+
+def test_fused_at_c4_size(cuda):
+    """C4's scan shape (B=4, L=4096, M=2048, S=16), forward + backward on the fused
+    kernels. A channel's outputs, dv, dLv, da and dp depend only on that channel,
+    so a spread of channels is checked exactly against the float64 oracle
+    (forward) / float64 autograd (backward) run on those channels alone; dk and dq
+    contract over every channel and are checked against the independent composed
+    path (HIP Moebius + affine scans, torch glue) on the same inputs."""
+    B, L, M, S = 4, 4096, 2048, 16
+    g = torch.Generator().manual_seed(21)
+    v = torch.randn(B, L, M, generator=g)
+    lv = torch.rand(B, L, M, generator=g) + 0.5
+    k = torch.randn(B, L, S, generator=g) * 0.3
+    q = torch.randn(B, L, S, generator=g) * 0.3
+    a = torch.rand(M, S, generator=g) * 0.5 + 0.45
+    p = torch.rand(M, S, generator=g) * 0.05 + 0.01
+    dy = torch.randn(B, L, M, generator=g)
+    dyv = torch.randn(B, L, M, generator=g)
+    outs = {}
+    for backend in ("hip_fused", "hip_composed"):
+        xs = [t.to(cuda).requires_grad_(True) for t in (v, lv, k, q, a, p)]
+        y, y_var, _ = kla_scan(*xs, backend=backend)
+        ((dy.to(cuda) * y).sum() + (dyv.to(cuda) * y_var).sum()).backward()
+        outs[backend] = [y.detach(), y_var.detach()] + [x.grad for x in xs]
+        del xs, y, y_var
+    fused, comp = outs["hip_fused"], outs["hip_composed"]
+    for t in fused:
+        assert torch.isfinite(t).all()
+    for name, i in (("dk", 4), ("dq", 5)):
+        check(name, fused[i], comp[i].double().cpu().numpy(), rtol=1e-4, atol=1e-5)
+
+    chans = torch.tensor([0, 1, 15, 16, 17, 255, 256, 1023, 1024, 2047])
+    sub = [v[..., chans], lv[..., chans], k, q, a[chans], p[chans]]
+    wy, wv, _, _ = okla.kla_scan_sequential(*(t.double().numpy() for t in sub))
+    check("y", fused[0][..., chans.to(cuda)], wy)
+    check("y_var", fused[1][..., chans.to(cuda)], wv)
+    xs = [t.double().requires_grad_(True) for t in sub]
+    yr, yvr, _, _ = torch_ref.kla_scan_torch(*xs)
+    ((dy[..., chans].double() * yr).sum() + (dyv[..., chans].double() * yvr).sum()).backward()
+    for name, i, idx in (("dv", 0, (Ellipsis, chans)), ("dlambda_v", 1, (Ellipsis, chans)), ("da", 4, chans),
+                         ("dp", 5, chans)):
+        check(name, fused[2 + i][tuple(c.to(cuda) if isinstance(c, torch.Tensor) else c for c in
+                                       (idx if isinstance(idx, tuple) else (idx,)))], xs[i].grad.numpy())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_affine_scan_at_c3_size(cuda, dtype):
+    """C3 (B=8, T=8192, L=2048), fp32 and bf16 I/O: a spread of lanes against the
+    float64 oracle on the same (dtype-exact) inputs, every value finite, and the
+    forward's state chained in two halves equals one pass."""
+    from kla.ops.hip import affine_scan
+    from oracle import scans as ref
+
+    B, T, N = 8, 8192, 2048
+    gen = torch.Generator().manual_seed(31)
+    g = torch.sigmoid(torch.randn(B, T, N, generator=gen)).to(dtype)
+    u = torch.randn(B, T, N, generator=gen).to(dtype)
+    dh = torch.randn(B, T, N, generator=gen).to(dtype)
+    gg, uu = g.to(cuda).requires_grad_(True), u.to(cuda).requires_grad_(True)
+    h = affine_scan(gg, uu)
+    h.backward(dh.to(cuda))
+    for t in (h, gg.grad, uu.grad):
+        assert torch.isfinite(t.float()).all()
+    lanes = torch.tensor([0, 1, 63, 64, 127, 128, 255, 256, 1000, 1023, 1024, 2046, 2047])
+    sub = lambda t: t[..., lanes]  # noqa: E731
+    tol = dict(rtol=1e-5, atol=1e-6) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
+    hw = ref.affine_scan_fwd(sub(g).float(), sub(u).float())
+    check("h", sub(h.cpu()), hw, **tol)
+    dg, du, _ = ref.affine_scan_bwd(sub(dh).float(), sub(g).float(), hw)
+    check("dg", sub(gg.grad.cpu()), dg, **tol)
+    check("du", sub(uu.grad.cpu()), du, **tol)
+    with torch.no_grad():
+        h1 = affine_scan(gg[:, :4000].detach(), uu[:, :4000].detach())
+        h2 = affine_scan(gg[:, 4000:].detach(), uu[:, 4000:].detach(), h1[:, -1].float())
+        torch.testing.assert_close(torch.cat([h1, h2], 1).float(), h.detach().float(),
+                                   rtol=tol["rtol"], atol=tol["atol"])
