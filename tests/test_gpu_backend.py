@@ -186,6 +186,20 @@ def test_auto_picks_hip_on_the_gpu(cuda):
     assert resolve_backend("cuda") == "hip"
 
 
+def test_cli_self_test_passes_on_hip(cuda):
+    """``python -m kla --check-backends`` marks hip as auto; ``--test-backends hip`` passes every row."""
+    import io
+
+    from kla import __main__ as cli
+
+    out = io.StringIO()
+    assert cli.main(["--check-backends"], out=out) == 0
+    assert "  [X] hip" in out.getvalue()
+    out = io.StringIO()
+    assert cli.main(["--test-backends", "hip"], out=out) == 0, out.getvalue()
+    assert out.getvalue().count(" ok ") == 6  # hip, hip_fused, hip_composed x forward, gradients
+
+
 # ------------------------------------------------------------ layer level
 
 GOLDEN_CASES = {
