@@ -15,12 +15,17 @@ launch stream) and a CPU baseline: the reference's pure-PyTorch CPU algorithm
 Inputs are drawn on the CPU with torch.Generator(seed 0) in a fixed order and
 copied to the GPU, so the CPU and GPU sides see the same bytes.
 
-``--layer c4|c5`` measures the layer-level BASELINE configs instead of the
-headline (its own JSON line; ``--backend`` picks the kla backend): c4 is a
+``--layer c1|c4|c5`` measures the layer-level BASELINE configs instead of the
+headline (its own JSON line; ``--backend`` picks the kla backend): c1 is a
+KLALayer(512, d_state=16) forward on x (2, 1024, 512), timed on the GPU and, on
+backend "torch", on this host's CPU; c4 is a
 KLALayer(1024, d_state=16) training step on x (4, 4096, 1024) under bf16
 autocast, loss = mean(out^2); c5 is SequenceModel(vocab 50304, d_model 512,
 6 layers) stateful prefill of (16, 2048) random ids, then 256 one-token decode
 steps (prefill tokens/s and decode ms/token).
+
+``--workload affine_b8_t8192_l2048[_bf16]`` is BASELINE config 3: the standalone
+affine scan alone, fp32 or bf16 I/O.
 
 ``--only KERNEL`` runs just one kernel K times (for rocprofv3 counter runs);
 ``--only copy`` runs a 1 GiB device-to-device copy, the calibration kernel for
@@ -48,11 +53,14 @@ METRIC = "KLA scan fwd+bwd tokens/s + achieved HBM GB/s, B=8 T=4096 fp32, 1 GPU"
 PEAK_HBM_GBPS = 8000.0
 
 WORKLOADS = {
-    # name: (batch, steps, lanes, affine I/O dtype)
-    "mobius_affine_b8_t4096_l2048": (8, 4096, 2048, torch.float32),
-    "mobius_affine_b8_t8192_l2048": (8, 8192, 2048, torch.float32),
-    "mobius_affine_b8_t4096_l2048_bf16affine": (8, 4096, 2048, torch.bfloat16),
-    "small_b2_t1024_l512": (2, 1024, 512, torch.float32),
+    # name: (batch, steps, lanes, affine I/O dtype, scans in a step)
+    "mobius_affine_b8_t4096_l2048": (8, 4096, 2048, torch.float32, "mobius+affine"),
+    "mobius_affine_b8_t8192_l2048": (8, 8192, 2048, torch.float32, "mobius+affine"),
+    "mobius_affine_b8_t4096_l2048_bf16affine": (8, 4096, 2048, torch.bfloat16, "mobius+affine"),
+    "small_b2_t1024_l512": (2, 1024, 512, torch.float32, "mobius+affine"),
+    # the standalone affine scan, fp32 and bf16 I/O.
+    "affine_b8_t8192_l2048": (8, 8192, 2048, torch.float32, "affine"),
+    "affine_b8_t8192_l2048_bf16": (8, 8192, 2048, torch.bfloat16, "affine"),
 }
 DEFAULT_WORKLOAD = "mobius_affine_b8_t4096_l2048"
 
@@ -106,43 +114,75 @@ def cpu_model_name() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(lanes_full: int, budget_s: float = 15.0) -> dict:
+def _median_time(fn, budget_s: float, max_reps: int = 60):
+    """Warm up once, then repeat ``fn`` to fill about ``budget_s`` seconds; (median s, reps)."""
+    t0 = time.perf_counter()
+    fn()
+    reps = int(min(max_reps, max(3, budget_s / max(time.perf_counter() - t0, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), reps
+
+
+def cpu_baseline(lanes_full: int, ops: str = "mobius+affine", budget_s: float = 15.0,
+                 seq_budget_s: float = 5.0) -> dict:
     """The reference's pure-PyTorch CPU scan (oracle.torch_ref: doubling scans of the
     trace-normalised Moebius combine and the affine combine, backward by autograd),
     fp32, on a bounded sample: batch 1, 4096 steps, all lanes; repeated to fill
-    about ``budget_s`` seconds, median reported."""
+    about ``budget_s`` seconds, median reported. The reference widens bf16 to fp32
+    (kla_ops.py:126-137), so the CPU side is fp32 for every workload.
+
+    Beside it, ``sequential``: the step-by-step form (oracle.scans, the per-step
+    recurrences of lane_mobius_scan.metal / tiled_mobius_scan.py's backward, the
+    shape of kla_scan_reference) in numpy fp32 on one thread, same sample."""
+    import numpy as np
+
+    from oracle import scans as oscans
     from oracle import torch_ref
 
+    with_mobius = ops == "mobius+affine"
     sb, st, sl = 1, 4096, lanes_full
     A, B, C, lam0, dlam = mobius_inputs(sb, st, sl, seed=0)
     g, u, dh = affine_inputs(sb, st, sl, seed=1)
 
     def one():
-        Ar, Br, Cr, lr = (t.clone().requires_grad_(True) for t in (A, B, C, lam0))
-        lam = torch_ref.mobius_scan(Ar, Br, Cr, None, lr)
-        torch.autograd.backward(lam, dlam)
+        if with_mobius:
+            Ar, Br, Cr, lr = (t.clone().requires_grad_(True) for t in (A, B, C, lam0))
+            lam = torch_ref.mobius_scan(Ar, Br, Cr, None, lr)
+            torch.autograd.backward(lam, dlam)
         gr, ur = g.clone().requires_grad_(True), u.clone().requires_grad_(True)
         h = torch_ref.affine_scan(gr, ur)
         torch.autograd.backward(h, dh)
 
-    t0 = time.perf_counter()
-    one()  # warm-up
-    reps = int(min(60, max(3, budget_s / max(time.perf_counter() - t0, 1e-3))))
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        one()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    med, reps = _median_time(one, budget_s)
+
+    na = [t.numpy() for t in (A, B, C, lam0, dlam, g, u, dh)]
+
+    def one_seq():
+        An, Bn, Cn, l0, dl, gn, un, dhn = na
+        if with_mobius:
+            lam = oscans.mobius_scan_fwd(An, Bn, Cn, None, l0, dtype=np.float32)
+            oscans.mobius_scan_bwd(dl, An, Bn, Cn, None, l0, lam, dtype=np.float32)
+        h = oscans.affine_scan_fwd(gn, un, dtype=np.float32)
+        oscans.affine_scan_bwd(dhn, gn, h, dtype=np.float32)
+
+    seq_med, seq_reps = _median_time(one_seq, seq_budget_s)
     full_width_tokens = sb * st * sl / lanes_full
+    what = "Moebius+affine" if with_mobius else "affine"
     return {
         "value": full_width_tokens / med,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"oracle/torch_ref (reference kla_ops.py doubling scans, autograd) Moebius+affine fwd+bwd fp32 "
+        "sample": (f"oracle/torch_ref (reference kla_ops.py doubling scans, autograd) {what} fwd+bwd fp32 "
                    f"on batch {sb} x {st} steps x {sl} of {lanes_full} lanes; median of {reps} reps = "
                    f"{med:.3f} s"),
+        "sequential": {"value": full_width_tokens / seq_med, "unit": "tokens/s", "cores": 1, "kind": "port",
+                       "sample": (f"oracle/scans per-step recurrences, numpy fp32, {what} fwd+bwd, same sample; "
+                                  f"median of {seq_reps} reps = {seq_med:.3f} s")},
         "host": {"cpu": cpu_model_name(), "affinity_cores": len(os.sched_getaffinity(0)),
                  "torch_threads": torch.get_num_threads()},
     }
@@ -151,10 +191,11 @@ def cpu_baseline(lanes_full: int, budget_s: float = 15.0) -> dict:
 # ----------------------------------------------------------------- GPU side
 
 
-def build_step(batch, steps, lanes, adt, device):
+def build_step(batch, steps, lanes, adt, device, ops="mobius+affine"):
     from kla.ops.hip import scans as hs
 
-    A, B, C, lam0, dlam = (t.to(device) for t in mobius_inputs(batch, steps, lanes))
+    if ops == "mobius+affine":
+        A, B, C, lam0, dlam = (t.to(device) for t in mobius_inputs(batch, steps, lanes))
     g, u, dh = (t.to(device) for t in affine_inputs(batch, steps, lanes, dtype=adt))
     state = {}
 
@@ -172,29 +213,35 @@ def build_step(batch, steps, lanes, adt, device):
 
     kernels = {"mobius_fwd": mobius_fwd, "mobius_bwd": mobius_bwd, "affine_fwd": affine_fwd,
                "affine_bwd": affine_bwd}
+    if ops == "affine":
+        del kernels["mobius_fwd"], kernels["mobius_bwd"]
+    order = list(kernels.values())
 
     def step():
-        mobius_fwd()
-        mobius_bwd()
-        affine_fwd()
-        affine_bwd()
+        for fn in order:
+            fn()
 
     return step, kernels
 
 
-def time_kernels(kernels, reps, stream):
-    """Average duration of each kernel, HIP events on the launch stream."""
-    out = {}
-    for name, fn in kernels.items():
-        fn()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for s, e in ev:
+def time_kernels_in_step(kernels, steps, stream):
+    """Average duration of each kernel where it runs in the step: ``steps`` more steps,
+    each kernel bracketed by HIP events on the launch stream.
+
+    Timing a kernel inside the step, not repeated on its own, matters here: run
+    back to back on the same inputs a backward scan is 6-12% faster than after
+    the other kernels of the step (the caches and the DRAM write queue hold what
+    the previous kernel left behind)."""
+    ev = {name: [] for name in kernels}
+    for _ in range(steps):
+        for name, fn in kernels.items():
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record(stream)
             fn()
             e.record(stream)
-        torch.cuda.synchronize()
-        out[name] = statistics.mean(s.elapsed_time(e) for s, e in ev)
-    return out
+            ev[name].append((s, e))
+    torch.cuda.synchronize()
+    return {name: statistics.mean(s.elapsed_time(e) for s, e in pairs) for name, pairs in ev.items()}
 
 
 def _timed(fn, steps, warmup, stream):
@@ -211,10 +258,33 @@ def _timed(fn, steps, warmup, stream):
 
 
 def bench_layer(args, device, stream) -> dict:
-    """Layer-level BASELINE configs c4 / c5 on the chosen kla backend."""
+    """Layer-level BASELINE configs c1 / c4 / c5 on the chosen kla backend."""
     from kla import KLAConfig, KLALayer, ModelConfig, SequenceModel
 
     torch.manual_seed(0)
+    if args.layer == "c1":
+        # BASELINE config 1: the reference's CPU-runnable case, forward only.
+        layer = KLALayer(512, KLAConfig(d_state=16, backend=args.backend))
+        x_cpu = torch.randn(2, 1024, 512, generator=torch.Generator().manual_seed(0))
+        with torch.no_grad():
+            layer.config.backend = "torch"
+            cpu_s, cpu_reps = _median_time(lambda: layer(x_cpu), 10.0, max_reps=30)
+            y_cpu = layer(x_cpu)
+            layer.config.backend = args.backend
+            layer.to(device)
+            x = x_cpu.to(device)
+            ms = _timed(lambda: layer(x), args.steps, args.warmup, stream)
+            y = layer(x).float().cpu()
+        err = ((y - y_cpu).abs().max() / (y_cpu.abs().max() + 1e-12)).item()
+        return {"metric": "KLALayer(512, d_state=16) forward tokens/s, x (2,1024,512) fp32",
+                "value": 2 * 1024 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+                "backend": args.backend, "steps": args.steps, "warmup": args.warmup,
+                "max_rel_err_vs_cpu": err,
+                "cpu_baseline": {"value": 2 * 1024 / cpu_s, "unit": "tokens/s", "cores": torch.get_num_threads(),
+                                 "kind": "port",
+                                 "sample": (f"the same layer and input on backend='torch' (reference kla_scan_torch, "
+                                            f"doubling scan under no_grad), median of {cpu_reps} reps = "
+                                            f"{cpu_s * 1e3:.1f} ms")}}
     if args.layer == "c4":
         layer = KLALayer(1024, KLAConfig(d_state=16, backend=args.backend)).to(device)
         x = torch.randn(4, 4096, 1024, generator=torch.Generator().manual_seed(0)).to(device)
@@ -274,12 +344,12 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--only", default=None,
                     choices=["mobius_fwd", "mobius_bwd", "affine_fwd", "affine_bwd", "copy", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--layer", default=None, choices=["c4", "c5"],
+    ap.add_argument("--layer", default=None, choices=["c1", "c4", "c5"],
                     help="measure a layer-level config instead of the headline scan step")
     ap.add_argument("--backend", default="hip", help="kla backend for --layer (hip, hip_composed, torch)")
     args = ap.parse_args(argv)
@@ -297,7 +367,7 @@ def main(argv=None) -> int:
     if args.layer:
         print(json.dumps(bench_layer(args, device, stream)), flush=True)
         return 0
-    batch, steps, lanes, adt = WORKLOADS[args.workload]
+    batch, steps, lanes, adt, ops = WORKLOADS[args.workload]
     elems = batch * steps * lanes
 
     if args.only in ("copy", "all"):
@@ -314,12 +384,16 @@ def main(argv=None) -> int:
             return 0
 
     print(f"[bench] building inputs for {args.workload} ({batch}x{steps}x{lanes})", file=sys.stderr, flush=True)
-    step, kernels = build_step(batch, steps, lanes, adt, device)
+    step, kernels = build_step(batch, steps, lanes, adt, device, ops)
 
     if args.only:
-        kernels["mobius_fwd"]()
-        kernels["affine_fwd"]()
         names = list(kernels) if args.only == "all" else [args.only]
+        if any(n not in kernels for n in names):
+            print(f"bench.py: workload {args.workload} has no {args.only} kernel", file=sys.stderr)
+            return 2
+        for name in ("mobius_fwd", "affine_fwd"):  # the backward kernels read the forward outputs
+            if name in kernels:
+                kernels[name]()
         for _ in range(args.warmup + args.steps):
             for name in names:
                 kernels[name]()
@@ -344,7 +418,7 @@ def main(argv=None) -> int:
     from kla.ops.hip import _lib
 
     failures = _lib.workspace_failures(device)
-    per_kernel_ms = time_kernels(kernels, max(args.steps, 10), stream)
+    per_kernel_ms = time_kernels_in_step(kernels, args.steps, stream)
     per_kernel = {}
     for name, ms in per_kernel_ms.items():
         nbytes = alg_bytes_per_elem(name, adt if name.startswith("affine") else torch.float32) * elems
@@ -360,8 +434,17 @@ def main(argv=None) -> int:
         with open(tfile) as f:
             traffic = json.load(f).get(dom)
 
+    if ops == "affine":
+        metric = (f"Affine scan fwd+bwd tokens/s + achieved HBM GB/s, B={batch} T={steps} "
+                  f"{'bf16 I/O' if adt == torch.bfloat16 else 'fp32'}, 1 GPU")
+        ops_desc = "affine fwd+bwd" + (" (bf16 I/O, f32 state)" if adt == torch.bfloat16 else "")
+        dtype = "f32" if adt == torch.float32 else "bf16 I/O, f32 arithmetic"
+    else:
+        metric = METRIC
+        ops_desc = "Moebius fwd+bwd (D=1) + affine fwd+bwd"
+        dtype = "f32" if adt == torch.float32 else "f32 (Moebius), bf16 I/O with f32 state (affine)"
     result = {
-        "metric": METRIC,
+        "metric": metric,
         "value": tokens / (ms_per_step * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -371,10 +454,10 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if adt == torch.float32 else "f32 (Moebius), bf16 I/O with f32 state (affine)",
+        "dtype": dtype,
         "data": "synthetic",
         "config": {"workload": args.workload, "batch": batch, "steps": steps, "lanes": lanes,
-                   "ops": "Moebius fwd+bwd (D=1) + affine fwd+bwd", "parallelism": "single GPU"},
+                   "ops": ops_desc, "parallelism": "single GPU"},
         "achieved_GBps": round(achieved_step, 1),
         "alg_bytes_per_step": step_bytes,
         "roofline": {
@@ -392,7 +475,7 @@ def main(argv=None) -> int:
     }
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(lanes)
+        result["cpu_baseline"] = cpu_baseline(lanes, ops)
     print(json.dumps(result), flush=True)
     return 0
 
