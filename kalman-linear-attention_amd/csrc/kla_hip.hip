@@ -27,9 +27,12 @@ using namespace kla;
 constexpr int kAbiVersion = 2;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
-// thread (tile = 64 V lanes). Chosen by measurement on MI355X at
-// (batch 8, steps 4096, lanes 2048): the forward scans want a short register
-// footprint (occupancy hides the look-back), the backward scans long chunks.
+// thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
+// timed inside the fwd+bwd step: fp32 at (batch 8, steps 4096, lanes 2048),
+// bf16 at (8, 8192, 2048). The forward scans want a short register footprint
+// (occupancy hides the look-back), the backward scans long chunks; bf16 holds
+// two elements per register, so its tiles run wider (V = 2, 4) for the same
+// footprint.
 // A V > 1 shape needs lanes % V == 0 and operands aligned to V elements; the
 // V = 1 shape of the same kind serves every other call.
 template <class P, int W_, int S_, int V_>
@@ -42,7 +45,7 @@ using MobiusBwdTile = Shape3<void, 8, 32, 1>;
 using AffineFwdTile = Shape3<void, 16, 24, 1>;
 using AffineBwdTile = Shape3<void, 12, 32, 1>;
 using AffineFwdBf16Tile = Shape3<void, 8, 24, 2>;
-using AffineBwdBf16Tile = Shape3<void, 16, 8, 4>;
+using AffineBwdBf16Tile = Shape3<void, 16, 16, 4>;
 using AffineBf16Fallback = Shape3<void, 8, 32, 1>;
 
 constexpr uint32_t kMaxSpin = 1u << 20;   // ~1 s of polling before a wait gives up

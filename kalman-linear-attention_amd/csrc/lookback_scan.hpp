@@ -72,7 +72,7 @@ __device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float(s
 // applied one by one in chain order. Each chunk's K aggregate words are read
 // with their loads in flight together.
 template <class P>
-__device__ float look_back(uint64_t *rec, uint64_t *ctl, const Geom &g, int64_t chunk,
+__device__ __forceinline__ float look_back(uint64_t *rec, uint64_t *ctl, const Geom &g, int64_t chunk,
                            int64_t slot, uint32_t tag) {
   constexpr int K = P::AGG;
   const int64_t carry_plane = K * g.n_chunks;

@@ -226,13 +226,29 @@ struct Lanes<float, V> {
   __device__ __forceinline__ void load(const float *p) { load_v<V>(p, w); }
 };
 
+// The widening is one VALU op, issued as volatile asm at every read: the
+// compiler can neither hoist it nor keep the widened copies alive between the
+// reduce and the walk over the same registers, which would double the tile's
+// register footprint.
+__device__ __forceinline__ float bf16_lo_to_f32(uint32_t x) {
+  float r;
+  asm volatile("v_lshlrev_b32 %0, 16, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
+__device__ __forceinline__ float bf16_hi_to_f32(uint32_t x) {
+  float r;
+  asm volatile("v_and_b32 %0, 0xffff0000, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 template <int V>
 struct Lanes<bf16_t, V> {
   static constexpr int N = (V + 1) / 2;
   uint32_t w[N];
   __device__ __forceinline__ float operator[](int v) const {
     const uint32_t x = w[v >> 1];
-    return __uint_as_float((v & 1) ? (x & 0xFFFF0000u) : (x << 16));
+    return (v & 1) ? bf16_hi_to_f32(x) : bf16_lo_to_f32(x);
   }
   // x must be exact in bf16 (the fills are 0 and 1).
   __device__ __forceinline__ void fill(float x) {
@@ -319,7 +335,7 @@ struct MobiusFwd {
   using Regs = Raw<S, V>;
 
   template <int S, int V>
-  __device__ static void fetch(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q, int64_t s0,
+  __device__ __forceinline__ static void fetch(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q, int64_t s0,
                                int nvalid) {
     const int64_t row = row_index(g, q, s0);
 #pragma unroll
@@ -343,17 +359,17 @@ struct MobiusFwd {
   }
 
   template <int S, int V>
-  __device__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
+  __device__ __forceinline__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
     r = raw;
   }
 
   template <int S, int V>
-  __device__ static Agg<4> leaf(const Regs<S, V> &r, int j, int v) {
+  __device__ __forceinline__ static Agg<4> leaf(const Regs<S, V> &r, int j, int v) {
     return Agg<4>{{r.a[j][v], r.b[j][v], r.c[j][v], HAS_D ? r.d[HAS_D ? j : 0][v] : 1.0f}};
   }
 
   template <int S, int V>
-  __device__ static Agg<4> reduce(const Regs<S, V> &r, int v, int nvalid) {
+  __device__ __forceinline__ static Agg<4> reduce(const Regs<S, V> &r, int v, int nvalid) {
     Agg<4> m{{1.0f, 0.0f, 0.0f, 1.0f}};
 #pragma unroll
     for (int j = 0; j < S; ++j)
@@ -361,14 +377,14 @@ struct MobiusFwd {
     return m;
   }
 
-  __device__ static Agg<4> compose(const Agg<4> &L, const Agg<4> &M) { return mobius_compose(L, M); }
-  __device__ static float apply(const Agg<4> &m, float x) { return mobius_apply(m, x); }
-  __device__ static float initial(const Params &p, const Geom &g, const Pos &q, int v) {
+  __device__ __forceinline__ static Agg<4> compose(const Agg<4> &L, const Agg<4> &M) { return mobius_compose(L, M); }
+  __device__ __forceinline__ static float apply(const Agg<4> &m, float x) { return mobius_apply(m, x); }
+  __device__ __forceinline__ static float initial(const Params &p, const Geom &g, const Pos &q, int v) {
     return p.lam0 ? p.lam0[state_index(g, q) + v] : 1.0f;
   }
 
   template <int S, int V>
-  __device__ static void walk(const Params &p, const Geom &g, const Regs<S, V> &r, const Pos &q,
+  __device__ __forceinline__ static void walk(const Params &p, const Geom &g, const Regs<S, V> &r, const Pos &q,
                               int64_t s0, int nvalid, float (&x)[V]) {
     const int64_t row = row_index(g, q, s0);
 #pragma unroll
@@ -413,7 +429,7 @@ struct MobiusBwd {
   };
 
   template <int S, int V>
-  __device__ static void fetch(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q, int64_t s0,
+  __device__ __forceinline__ static void fetch(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q, int64_t s0,
                                int nvalid) {
     const int64_t row = row_index(g, q, g.steps - 1 - s0);
 #pragma unroll
@@ -454,7 +470,7 @@ struct MobiusBwd {
   }
 
   template <int S, int V>
-  __device__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
+  __device__ __forceinline__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
 #pragma unroll
     for (int j = 0; j <= S; ++j)
 #pragma unroll
@@ -473,17 +489,17 @@ struct MobiusBwd {
   }
 
   template <int S, int V>
-  __device__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
+  __device__ __forceinline__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
     return affine_reduce<S>([&](int j) { return r.gain[j][v]; },
                             [&](int j) { return r.gain[j][v] * r.dl[j][v]; }, nvalid);
   }
 
-  __device__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
-  __device__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
-  __device__ static float initial(const Params &, const Geom &, const Pos &, int) { return 0.0f; }
+  __device__ __forceinline__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
+  __device__ __forceinline__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
+  __device__ __forceinline__ static float initial(const Params &, const Geom &, const Pos &, int) { return 0.0f; }
 
   template <int S, int V>
-  __device__ static void walk(const Params &p, const Geom &g, const Regs<S, V> &r, const Pos &q,
+  __device__ __forceinline__ static void walk(const Params &p, const Geom &g, const Regs<S, V> &r, const Pos &q,
                               int64_t s0, int nvalid, float (&x)[V]) {
     const int64_t row = row_index(g, q, g.steps - 1 - s0);
 #pragma unroll
@@ -535,7 +551,7 @@ struct AffineFwd {
   using Regs = Raw<S, V>;
 
   template <int S, int V>
-  __device__ static void fetch(const Params &p, const Geom &gm, Raw<S, V> &r, const Pos &q, int64_t s0,
+  __device__ __forceinline__ static void fetch(const Params &p, const Geom &gm, Raw<S, V> &r, const Pos &q, int64_t s0,
                                int nvalid) {
     const int64_t row = row_index(gm, q, s0);
 #pragma unroll
@@ -555,23 +571,23 @@ struct AffineFwd {
   }
 
   template <int S, int V>
-  __device__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
+  __device__ __forceinline__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
     r = raw;
   }
 
   template <int S, int V>
-  __device__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
+  __device__ __forceinline__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
     return affine_reduce<S>([&](int j) { return r.g[j][v]; }, [&](int j) { return r.u[j][v]; }, nvalid);
   }
 
-  __device__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
-  __device__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
-  __device__ static float initial(const Params &p, const Geom &gm, const Pos &q, int v) {
+  __device__ __forceinline__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
+  __device__ __forceinline__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
+  __device__ __forceinline__ static float initial(const Params &p, const Geom &gm, const Pos &q, int v) {
     return p.h0 ? p.h0[state_index(gm, q) + v] : 0.0f;
   }
 
   template <int S, int V>
-  __device__ static void walk(const Params &p, const Geom &gm, const Regs<S, V> &r, const Pos &q,
+  __device__ __forceinline__ static void walk(const Params &p, const Geom &gm, const Regs<S, V> &r, const Pos &q,
                               int64_t s0, int nvalid, float (&x)[V]) {
     const int64_t row = row_index(gm, q, s0);
 #pragma unroll
@@ -612,7 +628,7 @@ struct AffineBwd {
   using Regs = Raw<S, V>;
 
   template <int S, int V>
-  __device__ static void fetch(const Params &p, const Geom &gm, Raw<S, V> &r, const Pos &q, int64_t s0,
+  __device__ __forceinline__ static void fetch(const Params &p, const Geom &gm, Raw<S, V> &r, const Pos &q, int64_t s0,
                                int nvalid) {
     const int64_t row = row_index(gm, q, gm.steps - 1 - s0);
 #pragma unroll
@@ -642,22 +658,22 @@ struct AffineBwd {
   }
 
   template <int S, int V>
-  __device__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
+  __device__ __forceinline__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
     r = raw;
   }
 
   template <int S, int V>
-  __device__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
+  __device__ __forceinline__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
     return affine_reduce<S>([&](int j) { return r.g[j][v]; },
                             [&](int j) { return r.g[j][v] * r.dh[j][v]; }, nvalid);
   }
 
-  __device__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
-  __device__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
-  __device__ static float initial(const Params &, const Geom &, const Pos &, int) { return 0.0f; }
+  __device__ __forceinline__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
+  __device__ __forceinline__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
+  __device__ __forceinline__ static float initial(const Params &, const Geom &, const Pos &, int) { return 0.0f; }
 
   template <int S, int V>
-  __device__ static void walk(const Params &p, const Geom &gm, const Regs<S, V> &r, const Pos &q,
+  __device__ __forceinline__ static void walk(const Params &p, const Geom &gm, const Regs<S, V> &r, const Pos &q,
                               int64_t s0, int nvalid, float (&x)[V]) {
     const int64_t row = row_index(gm, q, gm.steps - 1 - s0);
 #pragma unroll
