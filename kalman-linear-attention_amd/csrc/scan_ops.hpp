@@ -81,13 +81,19 @@ __device__ __forceinline__ float from_f32<float>(float x) {
   return x;
 }
 
-// Round to nearest, ties to even; NaN stays a (quiet) NaN.
+typedef float f32x2_cvt __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
+
+// Two fp32 values rounded to bf16 (to nearest, ties to even; a NaN stays a
+// quiet NaN) and packed lo | hi << 16: one v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2_cvt b = __builtin_convertvector(f32x2_cvt{lo, hi}, bf16x2_cvt);
+  return __builtin_bit_cast(uint32_t, b);
+}
+
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return bf16_t{static_cast<uint16_t>((u >> 16) | 0x0040u)};
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return bf16_t{static_cast<uint16_t>(u >> 16)};
+  return bf16_t{static_cast<uint16_t>(pack_bf16x2(x, 0.0f))};
 }
 
 // Where one thread sits: batch b and lane tile [n0, n0 + 64 V) are wave-uniform
@@ -174,10 +180,6 @@ __device__ __forceinline__ void store_v(float *p, const float (&x)[V]) {
     const f32x4 t = {x[0], x[1], x[2], x[3]};
     __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(p));
   }
-}
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(from_f32<bf16_t>(lo).bits) | (static_cast<uint32_t>(from_f32<bf16_t>(hi).bits) << 16);
 }
 
 template <int V>

@@ -135,6 +135,42 @@ def test_affine_bf16_io(cuda, shape):
     _close("du", uu.grad, du, rtol=2e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("lanes", [64, 130, 2048])
+def test_affine_bf16_outputs_round_to_nearest_even(cuda, lanes):
+    """The kernels' fp32 -> bf16 stores round exactly as torch does (to nearest, ties
+    to even), bit for bit. One step with g = 1, u = -0 stores h = round(h0) of an fp32
+    h0 (1 * h0 + (-0) = h0 exactly); h0 holds random values over all binades, exact
+    ties on even and odd bf16 mantissas, values one fp32 ulp either side of a tie,
+    signed zeros, fp32 subnormals and the largest finite value."""
+    from kla.ops.hip import affine_scan
+
+    gen = torch.Generator().manual_seed(11)
+    B = 4
+    n = B * lanes
+    mant = torch.randint(0, 1 << 23, (n,), generator=gen, dtype=torch.int64)
+    expo = torch.randint(1, 255, (n,), generator=gen, dtype=torch.int64)
+    sign = torch.randint(0, 2, (n,), generator=gen, dtype=torch.int64)
+    bits = (sign << 31) | (expo << 23) | mant
+    # Every 4th value an exact tie (low 16 bits 0x8000), every 4th + 1 one ulp
+    # either side of it, the first few special.
+    bits[0::4] = (bits[0::4] & ~0xFFFF) | 0x8000
+    bits[1::4] = (bits[1::4] & ~0xFFFF) | 0x7FFF
+    bits[2::4] = (bits[2::4] & ~0xFFFF) | 0x8001
+    special = torch.tensor([0x00000000, 0x80000000, 0x00000001, 0x007FFFFF, 0x00408000, 0x80018000,
+                            0x7F7FFFFF, 0x3F808000, 0x3F818000], dtype=torch.int64)
+    bits[:len(special)] = special
+    h0 = bits.to(torch.int32).view(torch.float32).reshape(B, lanes)
+    g = torch.ones(B, 1, lanes, dtype=torch.bfloat16)
+    u = torch.full((B, 1, lanes), -0.0, dtype=torch.bfloat16)   # x + (-0) = x, signed zeros included
+    h = affine_scan(g.to(cuda), u.to(cuda), h0.to(cuda))
+    want = h0.to(torch.bfloat16).reshape(B, 1, lanes)
+    got = h.cpu()
+    mismatch = (got.view(torch.int16) != want.view(torch.int16)).nonzero()
+    assert mismatch.numel() == 0, (
+        f"{mismatch.shape[0]} values rounded differently, e.g. h0 bits "
+        f"{int(bits.reshape(B, 1, lanes)[tuple(mismatch[0])]) & 0xFFFFFFFF:#010x}")
+
+
 def test_empty_and_zero_length(cuda):
     from kla.ops.hip import affine_scan, mobius_scan
 
