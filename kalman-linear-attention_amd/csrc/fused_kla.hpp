@@ -68,9 +68,12 @@ struct FusedBwdParams {
 
 // ------------------------------------------------------------ lane sums
 
+// Every control used here reads a lane of the same row, so no lane's source is
+// out of range and the move needs no "old" value: with none given, the
+// compiler folds the move into the add that consumes it (one v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp_shift(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
 // Sum over aligned groups of SP consecutive lanes (every lane gets its group's sum).
