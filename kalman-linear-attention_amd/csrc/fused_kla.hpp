@@ -88,12 +88,61 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// Sum over the lanes of a wave that share the lane index modulo SP.
+// x of this lane plus x of the same lane position in the paired row (rows
+// 0-1, 2-3): v_permlane16_swap with both operands x leaves x(row 0) in the
+// first result and x(row 1) in the second on both rows of a pair.
+__device__ __forceinline__ float row_pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// x of this lane plus x of the lane 32 away (v_permlane32_swap, as above).
+__device__ __forceinline__ float half_pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over the lanes of a wave that share the lane index modulo SP (every lane
+// gets its sum): rotations by SP within a 16-lane row, then the row pairs and
+// the two wave halves.
 template <int SP>
 __device__ __forceinline__ float cross_group_sum(float x) {
-#pragma unroll
-  for (int off = SP; off < kWave; off *= 2) x += __shfl_xor(x, off);
+  if constexpr (SP <= 4) x += dpp_shift<0x124>(x);   // row_ror:4
+  if constexpr (SP <= 8) x += dpp_shift<0x128>(x);   // row_ror:8
+  if constexpr (SP <= 16) x = row_pair_sum(x);
+  if constexpr (SP <= 32) x = half_pair_sum(x);
   return x;
+}
+
+// One butterfly stage of transpose_sum: lanes whose bit BIT is 0 keep the lower
+// half of w[0, n) and send the upper half to their partner (the lane CTRL reads,
+// whose bit BIT is 1 and which does the opposite); w[0, n/2) becomes kept + received.
+template <int CTRL, int BIT, int n, int N>
+__device__ __forceinline__ void transpose_stage(float (&w)[N], int lane) {
+  const bool hi = (lane >> BIT) & 1;
+#pragma unroll
+  for (int i = 0; i < n / 2; ++i) {
+    const float keep = hi ? w[i + n / 2] : w[i];
+    const float send = hi ? w[i] : w[i + n / 2];
+    w[i] = keep + dpp_shift<CTRL>(send);
+  }
+}
+
+// Group sums of N values at once (SP = 4, 8 or 16 lanes per group, N a multiple
+// of SP): on return lane s of a group holds in w[r], r < N / SP, the sum over the
+// group's lanes of their w[(N / SP) s + r]. The butterfly halves the values at
+// each stage, 3 (N - N / SP) VALU ops in all, where N separate group_sum calls
+// take N log2(SP) DPP adds plus their hazard waits, and every lane ends with
+// distinct results to store. Partners per stage: lane ^ 8 (row_ror:8), the
+// mirror within 8 lanes (row_half_mirror, lane ^ 7), lane ^ 2, lane ^ 1.
+template <int SP, int N>
+__device__ __forceinline__ void transpose_sum(float (&w)[N], int lane) {
+  static_assert(SP == 4 || SP == 8 || SP == 16, "transpose_sum serves 4, 8 or 16 lanes per group");
+  static_assert(N % SP == 0, "N must be a multiple of SP");
+  if constexpr (SP == 16) transpose_stage<0x128, 3, N>(w, lane);
+  if constexpr (SP >= 8) transpose_stage<0x141, 2, N * 8 / SP>(w, lane);
+  transpose_stage<0x4E, 1, N * 4 / SP>(w, lane);
+  transpose_stage<0xB1, 0, N * 2 / SP>(w, lane);
 }
 
 struct FusedLane {
@@ -211,6 +260,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
   const int64_t ms = ln.m * S + ln.s;
   const int64_t bms = ln.b * M * S + ms;
   const int64_t cols_m = M - m0 < CH ? M - m0 : CH;
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
 
   const float a_s = ln.active ? prm.a[ms] : 1.0f;
   const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
@@ -262,8 +312,12 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
       lds_to_global<TB, CH>(s_y[cur ^ 1], ybase + (t0 - TB) * M, M, TB, cols_m);
       lds_to_global<TB, CH>(s_yv[cur ^ 1], yvbase + (t0 - TB) * M, M, TB, cols_m);
     }
-    // One step at block position j; FULL: the whole block lies inside the sequence.
-    auto step = [&](int j) {
+    // The read-out terms of a kCkpt-step half of the block, summed over s after
+    // the half (transpose_sum) when a channel's lanes fit one 16-lane row.
+    constexpr bool kTr = SP <= 16;
+    float yw[kTr ? kCkpt : 1], vw[kTr ? kCkpt : 1];
+    // One step at block position j (position jj within its half).
+    auto step = [&](int j, int jj) {
       StepIO io;
       lam = filter_step(lam, eta, s_l[cur][c][j], s_v[cur][c][j], s_k[cur][ln.s][j], a_s, a2, pp, inv_a2, C, io);
       const float var = rcp(fmaxf(lam, kEps));
@@ -273,11 +327,16 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
         vo = a2 * var + pp;
       }
       const float qq = s_q[cur][ln.s][j];
-      const float ys = group_sum<SP>(qq * mean);
-      const float vs = group_sum<SP>((qq * qq) * vo);
-      if (ln.s == 0) {
-        s_y[cur][c][j] = ys;
-        s_yv[cur][c][j] = vs;
+      if constexpr (kTr) {
+        yw[jj] = qq * mean;
+        vw[jj] = (qq * qq) * vo;
+      } else {
+        const float ys = group_sum<SP>(qq * mean);
+        const float vs = group_sum<SP>((qq * qq) * vo);
+        if (ln.s == 0) {
+          s_y[cur][c][j] = ys;
+          s_yv[cur][c][j] = vs;
+        }
       }
     };
     // Checkpoints enter every kCkpt-step half of the block (TB is a multiple of kCkpt).
@@ -290,11 +349,32 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
           prm.ck_eta[ck_off + (th / kCkpt) * ck_stride] = eta;
         }
         if (th + kCkpt <= L) {
+          // The whole half lies inside the sequence: no per-step bound.
 #pragma unroll
-          for (int j = 0; j < kCkpt; ++j) step(h * kCkpt + j);
+          for (int j = 0; j < kCkpt; ++j) step(h * kCkpt + j, j);
+        } else if constexpr (kTr) {
+          // Unrolled: the terms live in registers indexed by j.
+#pragma unroll
+          for (int j = 0; j < kCkpt; ++j) {
+            if (th + j < L) {
+              step(h * kCkpt + j, j);
+            } else {
+              yw[j] = 0.0f;
+              vw[j] = 0.0f;
+            }
+          }
         } else {
           for (int j = 0; j < kCkpt; ++j)
-            if (th + j < L) step(h * kCkpt + j);
+            if (th + j < L) step(h * kCkpt + j, j);
+        }
+        if constexpr (kTr) {
+          transpose_sum<SP, kCkpt>(yw, lane);
+          transpose_sum<SP, kCkpt>(vw, lane);
+#pragma unroll
+          for (int r = 0; r < kCkpt / SP; ++r) {
+            s_y[cur][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = yw[r];
+            s_yv[cur][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = vw[r];
+          }
         }
       }
     }
@@ -421,10 +501,18 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         }
       }
     }
+    // dv, dLv contributions of the block's steps, summed over s after the walk
+    // (transpose_sum) when a channel's lanes fit one 16-lane row.
+    constexpr bool kTr = SP <= 16;
+    float dv_w[kTr ? TB : 1], dl_w[kTr ? TB : 1];
 #pragma unroll
     for (int j = TB - 1; j >= 0; --j) {
       const int64_t t = t0 + j;
       float dk_c = 0.0f, dq_c = 0.0f;
+      if constexpr (kTr) {
+        dv_w[j] = 0.0f;
+        dl_w[j] = 0.0f;
+      }
       if (t < L) {
         const float vv = s_v[cur][c][j], sig = s_l[cur][c][j];
         const float dy = s_dy[cur][c][j], dyv = s_dyv[cur][c][j];
@@ -477,11 +565,16 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         const float dsig_c = dphi * (kk * kk) + dmsi * vv;
         const float dv_c = dmsi * sig;
         dk_c = dphi * 2.0f * sig * kk + dr * (vv * sig);
-        const float dv_s = group_sum<SP>(dv_c);
-        const float dl_s = group_sum<SP>(dsig_c);
-        if (ln.s == 0) {
-          s_dv[cur][c][j] = dv_s;
-          s_dl[cur][c][j] = dl_s;
+        if constexpr (kTr) {
+          dv_w[j] = dv_c;
+          dl_w[j] = dsig_c;
+        } else {
+          const float dv_s = group_sum<SP>(dv_c);
+          const float dl_s = group_sum<SP>(dsig_c);
+          if (ln.s == 0) {
+            s_dv[cur][c][j] = dv_s;
+            s_dl[cur][c][j] = dl_s;
+          }
         }
       }
       // Sum over this wave's channels now, over the waves at the flush.
@@ -490,6 +583,15 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       if (lane < SP) {
         s_red[cur][0][j][wave][lane] = dk_c;
         s_red[cur][1][j][wave][lane] = dq_c;
+      }
+    }
+    if constexpr (kTr) {
+      transpose_sum<SP, TB>(dv_w, lane);
+      transpose_sum<SP, TB>(dl_w, lane);
+#pragma unroll
+      for (int r = 0; r < TB / SP; ++r) {
+        s_dv[cur][c][(TB / SP) * ln.s + r] = dv_w[r];
+        s_dl[cur][c][(TB / SP) * ln.s + r] = dl_w[r];
       }
     }
     acc_a += blk_a;

@@ -84,7 +84,7 @@ def test_forward_and_state_match_oracle(cuda, backend, decode_from_prior, with_s
 
 @pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("shape", [(1, 1, 3, 2), (3, 257, 5, 16), (2, 1000, 8, 8), (1, 40, 70, 3), (2, 33, 9, 64),
-                                   (1, 17, 300, 1), (2, 64, 3, 40)])
+                                   (1, 17, 300, 1), (2, 64, 3, 40), (2, 50, 7, 24), (1, 45, 20, 12)])
 def test_forward_ragged_shapes(cuda, backend, shape):
     B, L, M, S = shape
     ins = make_inputs(B, L, M, S, seed=7)
@@ -110,7 +110,7 @@ def test_chunked_state_carry(cuda, backend):
 
 @pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("decode_from_prior", [False, True])
-@pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 20, 3, 3)])
+@pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 20, 3, 3), (1, 33, 6, 12), (1, 21, 4, 20)])
 def test_gradients_match_float64_autograd(cuda, backend, decode_from_prior, shape):
     """Every input gradient, the initial-state gradients, and gradients flowing in
     through the returned state, against float64 autograd of the reference's
