@@ -114,6 +114,28 @@ __device__ __forceinline__ float cross_group_sum(float x) {
   return x;
 }
 
+// Sums over the four 16-lane rows of a wave, for N values at once (N a multiple
+// of 4): on return a lane of row r holds in w[i], i < N / 4, the sum over the
+// rows of w[(N / 2)(r >> 1) + (N / 4)(r & 1) + i] at its position in the row.
+// v_permlane32_swap on the pair (w[i], w[i + N/2]) leaves the low half of the
+// wave both halves of w[i] and the high half both halves of w[i + N/2]; then
+// v_permlane16_swap does the same for row pairs. 3 N / 4 swaps and adds in all,
+// against 4 N for N separate cross_group_sum<16> calls.
+template <int N>
+__device__ __forceinline__ void cross_row_transpose_sum(float (&w)[N]) {
+  static_assert(N % 4 == 0, "N must be a multiple of 4");
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(w[i]), __float_as_uint(w[i + N / 2]), false, false);
+    w[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[i]), __float_as_uint(w[i + N / 4]), false, false);
+    w[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
 // One butterfly stage of transpose_sum: lanes whose bit BIT is 0 keep the lower
 // half of w[0, n) and send the upper half to their partner (the lane CTRL reads,
 // whose bit BIT is 1 and which does the opposite); w[0, n/2) becomes kept + received.
@@ -169,8 +191,17 @@ __device__ __forceinline__ FusedLane fused_lane(const FusedGeom &g) {
 // numerator instead of the ~10-instruction IEEE division: a relative error of
 // ~2 ulp per step, which the contractive recurrence does not amplify.
 struct StepIO {
-  float phi, r, A, den, Da, alpha, inv_den, inv_Da;
+  float phi, r, A, inv_den, alpha, inv_Da;
 };
+
+constexpr float kInvEps = 1.0f / kEps;
+
+// 1 / max(a2 + p' lam, EPS) from 1 / den: den = C lam + 1 with C = p'/a2, so
+// a2 + p' lam = a2 den, and its reciprocal is inv_den / a2 (one multiply where
+// a second v_rcp would be). `ok` is the unclamped case a2 + p' lam >= EPS.
+__device__ __forceinline__ float inv_Da_of(float inv_den, float inv_a2, bool ok) {
+  return ok ? inv_den * inv_a2 : kInvEps;
+}
 
 __device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
@@ -179,11 +210,9 @@ __device__ __forceinline__ float filter_step(float lam, float &eta, float sig, f
   io.phi = sig * (kk * kk);
   io.r = (vv * sig) * kk;
   io.A = (1.0f + pp * io.phi) * inv_a2;
-  io.den = C * lam + 1.0f;
-  io.inv_den = rcp(io.den);
+  io.inv_den = rcp(C * lam + 1.0f);
   const float lam_t = (io.A * lam + io.phi) * io.inv_den;
-  io.Da = fmaxf(a2 + pp * lam, kEps);
-  io.inv_Da = rcp(io.Da);
+  io.inv_Da = inv_Da_of(io.inv_den, inv_a2, a2 + pp * lam >= kEps);
   io.alpha = a_s * io.inv_Da;
   eta = io.alpha * eta + io.r;
   return lam_t;
@@ -482,7 +511,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     if (i + 1 < n_ck) load(t0 - TB);
     if (i > 0) flush(blk + 1, cur ^ 1);
 
-    float lh[TB], eh[TB];   // lam_{t-1}, eta_{t-1} over the block
+    // Over the block: lam_{t-1}, eta_{t-1} (lh[TB], eh[TB]: the state after the
+    // block), and each step's 1/den and posterior variance, kept from the replay.
+    float lh[TB + 1], eh[TB + 1], idn[TB], vr[TB];
     // da, dp sum over all steps: accumulate each block apart and add the block
     // totals (two-level summation keeps fp32 rounding at ~(TB + L/TB) ulp).
     float blk_a = 0.0f, blk_a2 = 0.0f, blk_p = 0.0f;
@@ -494,17 +525,27 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       for (int j = 0; j < TB; ++j) {
         lh[j] = lam;
         eh[j] = eta;
+        idn[j] = 0.0f;
+        vr[j] = 0.0f;
         if (t0 + j < L) {
           StepIO io;
           lam = filter_step(lam, eta, s_l[cur][c][j], s_v[cur][c][j], s_k[cur][ln.s][j], a_s, a2, pp, inv_a2, C,
                             io);
+          idn[j] = io.inv_den;
+          vr[j] = rcp(fmaxf(lam, kEps));
         }
       }
+      lh[TB] = lam;
+      eh[TB] = eta;
     }
     // dv, dLv contributions of the block's steps, summed over s after the walk
     // (transpose_sum) when a channel's lanes fit one 16-lane row.
     constexpr bool kTr = SP <= 16;
     float dv_w[kTr ? TB : 1], dl_w[kTr ? TB : 1];
+    // dk, dq contributions, summed over the wave's four channel rows after the
+    // walk (cross_row_transpose_sum) when SP = 16.
+    constexpr bool kRows = SP == 16;
+    float dk_w[kRows ? TB : 1], dq_w[kRows ? TB : 1];
 #pragma unroll
     for (int j = TB - 1; j >= 0; --j) {
       const int64_t t = t0 + j;
@@ -518,11 +559,14 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         const float dy = s_dy[cur][c][j], dyv = s_dyv[cur][c][j];
         const float kk = s_k[cur][ln.s][j], qq = s_q[cur][ln.s][j];
         const float lp = lh[j], ep = eh[j];
-
-        StepIO io;
-        float eta_t = ep;
-        const float lam_t = filter_step(lp, eta_t, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
-        const float var = rcp(fmaxf(lam_t, kEps));
+        const float lam_t = lh[j + 1], eta_t = eh[j + 1];
+        const float inv_den = idn[j], var = vr[j];
+        // The step's intermediates (filter_step) from the kept 1/den.
+        const float phi = sig * (kk * kk);
+        const float A = (1.0f + pp * phi) * inv_a2;
+        const bool da_ok = a2 + pp * lp >= kEps;
+        const float inv_Da = inv_Da_of(inv_den, inv_a2, da_ok);
+        const float alpha = a_s * inv_Da;
         const float mean = eta_t * var;
         const float mean_o = PRIOR ? a_s * mean : mean;
         const float var_o = PRIOR ? a2 * var + pp : var;
@@ -545,21 +589,21 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         // eta_t = alpha eta' + r
         const float dalpha = ge_t * ep;
         const float dr = ge_t;
-        ge = ge_t * io.alpha;
+        ge = ge_t * alpha;
         // alpha = a / Da, Da = max(a2 + p' lam', EPS)
-        blk_a += dalpha * io.inv_Da;
-        const float dDa = (a2 + pp * lp >= kEps) ? -dalpha * io.alpha * io.inv_Da : 0.0f;
+        blk_a += dalpha * inv_Da;
+        const float dDa = da_ok ? -dalpha * alpha * inv_Da : 0.0f;
         blk_a2 += dDa;
         blk_p += dDa * lp;
         // lam_t = (A lam' + phi) / den, den = C lam' + 1;  d lam_t / d lam' = 1/(a2 den^2)
-        const float u = gl_t * io.inv_den;
+        const float u = gl_t * inv_den;
         const float dA = u * lp;
         const float dC = -u * lam_t * lp;
-        gl = u * io.inv_den * inv_a2 + dDa * pp;
+        gl = u * inv_den * inv_a2 + dDa * pp;
         // A = (1 + p' phi)/a2, C = p'/a2
         const float dphi = u + dA * pp * inv_a2;
-        blk_p += (dA * io.phi + dC) * inv_a2;
-        blk_a2 -= (dA * io.A + dC * C) * inv_a2;
+        blk_p += (dA * phi + dC) * inv_a2;
+        blk_a2 -= (dA * A + dC * C) * inv_a2;
         // phi = Lv k^2, r = (v Lv) k
         const float dmsi = dr * kk;
         const float dsig_c = dphi * (kk * kk) + dmsi * vv;
@@ -577,12 +621,29 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
           }
         }
       }
-      // Sum over this wave's channels now, over the waves at the flush.
-      dk_c = cross_group_sum<SP>(dk_c);
-      dq_c = cross_group_sum<SP>(dq_c);
-      if (lane < SP) {
-        s_red[cur][0][j][wave][lane] = dk_c;
-        s_red[cur][1][j][wave][lane] = dq_c;
+      // Sum over this wave's channels (now, or after the walk), over the waves
+      // at the flush.
+      if constexpr (kRows) {
+        dk_w[j] = dk_c;
+        dq_w[j] = dq_c;
+      } else {
+        dk_c = cross_group_sum<SP>(dk_c);
+        dq_c = cross_group_sum<SP>(dq_c);
+        if (lane < SP) {
+          s_red[cur][0][j][wave][lane] = dk_c;
+          s_red[cur][1][j][wave][lane] = dq_c;
+        }
+      }
+    }
+    if constexpr (kRows) {
+      cross_row_transpose_sum<TB>(dk_w);
+      cross_row_transpose_sum<TB>(dq_w);
+      const int row = lane / 16;
+#pragma unroll
+      for (int i = 0; i < TB / 4; ++i) {
+        const int j = (TB / 2) * (row >> 1) + (TB / 4) * (row & 1) + i;
+        s_red[cur][0][j][wave][ln.s] = dk_w[i];
+        s_red[cur][1][j][wave][ln.s] = dq_w[i];
       }
     }
     if constexpr (kTr) {
