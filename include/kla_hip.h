@@ -180,6 +180,56 @@ int kla_step_fwd(const float *v, const float *lambda_v, const float *k, const fl
                  const float *p, const float *lam, const float *eta, float *y, float *y_var, float *lam_out,
                  float *eta_out, int decode_from_prior, int64_t batch, int64_t M, int64_t S, hipStream_t stream);
 
+/*
+ * Options of the layer decode step, from KLAConfig (reference configs.py:45-222).
+ */
+typedef struct kla_decode_config {
+  int discretization;     /* 0 = "ou", 1 = "zoh" (kla_layer.py:172-181)                         */
+  int zero_process_noise; /* p + 1e-12 instead of max(p, 1e-7) (kla_layer.py:164-170)           */
+  int qk_norm;            /* k, q divided by max(||.||_2, 1e-12) over the S states             */
+  int has_clip;           /* clip_value set: p <= clip, k and q clamped to [-clip, clip]       */
+  float clip_value;
+  float obs_var_min;      /* obs_var = softplus(log_var) + obs_var_min                         */
+  float obs_var_max;      /* obs_var clamped above by it; +inf when unset                      */
+  int decode_from_prior;  /* read out the one-step prior (kla_ops.py:325-328)                   */
+  int gate_activation;    /* with a gate: 1 silu, 2 gelu, 3 relu                                */
+  int skip_vector;        /* lambda_skip is [M] (1) or a scalar (0)                             */
+} kla_decode_config;
+
+/*
+ * The whole one-token SSM step of a KLALayer, for inference (fp32, no gradient):
+ * replaces KLALayer._run_ssm_step with _compute_aq / _continuous_params /
+ * _discretize, the tail of _project_sensors and the lambda-skip and gating lines
+ * of forward (reference src/kla/layers/kla_layer.py:164-190, :194-231, :277-293,
+ * :295-349), i.e. ~30 torch kernels per layer and token, as one kernel.
+ *   (a_bar, p_bar) from delta, lambda_log, process_noise [M, S] (recomputed per call);
+ *   k, q [batch, S] rows (stride ld_kq), l2-normalised / clipped per cfg;
+ *   Lambda^v = 1 / min(softplus(log_var) + obs_var_min, obs_var_max), log_var and v
+ *   [batch, M] rows (strides ld_log_var, ld_v);
+ *   the kla_step update of lam, eta [batch, M, S] into lam_out, eta_out (may alias);
+ *   y = sum_s q mean (+ lambda_skip * residual), y_var = sum_s q^2 var, both times
+ *   act(gate) resp. act(gate)^2 when gate is given. residual and lambda_skip come
+ *   together or not at all. y, y_var are dense [batch, M].
+ */
+int kla_decode_step_fwd(const float *v, int64_t ld_v, const float *log_var, int64_t ld_log_var, const float *k,
+                        const float *q, int64_t ld_kq, const float *residual, int64_t ld_residual,
+                        const float *lambda_skip, const float *gate, int64_t ld_gate, const float *delta,
+                        const float *lambda_log, const float *process_noise, const float *lam, const float *eta,
+                        float *lam_out, float *eta_out, float *y, float *y_var, const kla_decode_config *cfg,
+                        int64_t batch, int64_t M, int64_t S, hipStream_t stream);
+
+/*
+ * One token of the depthwise causal conv with its window state: replaces the
+ * one-token path of CausalConv1d.forward (reference src/kla/layers/common.py:70-96).
+ *   window = [state[b, c, 0 : K-1], x[b, c]] (x rows of stride ld_x),
+ *   y[b, c] = act(sum_j weight[c, j] window[j] + bias[c]), state_out = window[1 : K];
+ *   weight [channels, K], bias [channels] or NULL, state / state_out [batch, channels, K-1]
+ *   (may alias), activation 0 none, 1 silu, 2 gelu, 3 relu. fp32.
+ */
+int kla_conv_step_fwd(const float *x, int64_t ld_x, const float *state, float *state_out, const float *weight,
+                      const float *bias, int activation, float *y, int64_t batch, int64_t channels,
+                      int64_t kernel_size, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -745,4 +745,147 @@ __global__ void __launch_bounds__(kFusedThreads) kla_step_kernel(StepParams prm,
   }
 }
 
+// ----------------------------------------------------- layer decode step
+//
+// The whole one-token SSM step of a KLALayer in one kernel, for inference
+// (fp32, no gradient): the discretisation of the static parameters
+// (_continuous_params / _discretize / _compute_aq, reference kla_layer.py:164-190),
+// the sensor read-out of the projection (_project_sensors after the linear maps,
+// :194-231), the filter step (kla_step, kla_ops.py:293-331), the lambda skip and
+// the gating of the layer's forward (:295-349). Each (b, m, s) lane recomputes
+// its (a_bar, p_bar) from the [M, S] parameters, which costs a few exp / log1p
+// per lane instead of ~17 separate elementwise launches per token. Operations
+// follow torch's order and formulas (softplus with threshold 20, silu
+// x / (1 + exp(-x)), gelu 0.5 x (1 + erf(x / sqrt 2))), so results agree with
+// the torch path to a few ulp.
+
+enum DecodeAct { kActNone = 0, kActSilu = 1, kActGelu = 2, kActRelu = 3 };
+
+struct DecodeParams {
+  const float *v, *lv, *k, *q;          // rows of the sensor projection
+  const float *z, *skip, *gate;         // residual z, lambda_skip, raw gate (NULL: absent)
+  int64_t ld_v, ld_lv, ld_kq, ld_z, ld_gate;
+  const float *delta, *lambda_log, *pnoise;   // [M, S]
+  const float *lam, *eta;               // [B, M, S] in
+  float *lam_out, *eta_out, *y, *yvar;  // [B, M, S], [B, M] out
+  int ou, zero_pn, qk_norm, has_clip, skip_vector, gate_act;
+  float clip, ov_min, ov_max;
+};
+
+__device__ __forceinline__ float softplus_t(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+__device__ __forceinline__ float activation(int act, float x) {
+  if (act == kActSilu) return x / (1.0f + expf(-x));
+  if (act == kActGelu) return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+  if (act == kActRelu) return x > 0.0f ? x : 0.0f;
+  return x;
+}
+
+template <int SP, bool PRIOR>
+__global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodeParams prm, FusedGeom g) {
+  const FusedLane ln = fused_lane<SP>(g);
+  const int64_t M = g.M, S = g.S;
+  const bool mok = ln.m < M, sok = ln.s < S;
+  const int64_t ms = ln.m * S + ln.s;
+  const int64_t bms = ln.b * M * S + ms;
+
+  // (a_bar, p_bar) of this (m, s).
+  float a_bar = 1.0f, p_bar = 0.0f;
+  if (ln.active) {
+    const float a = -expf(prm.lambda_log[ms]);
+    float p = prm.pnoise[ms];
+    if (prm.zero_pn) {
+      p = p + 1e-12f;
+    } else {
+      p = fmaxf(p, 1e-7f);
+      if (prm.has_clip) p = fminf(p, prm.clip);
+    }
+    const float delta = softplus_t(prm.delta[ms]) + 1e-7f;
+    a_bar = expf(delta * a);
+    if (prm.ou) {
+      const float rate = fmaxf(fabsf(a), 1e-8f);
+      p_bar = (p / (2.0f * rate)) * (-expm1f((-2.0f * rate) * delta));
+    } else {
+      p_bar = p * delta;
+    }
+  }
+
+  // Sensors: k, q (l2-normalised over the S states, clipped), Lambda^v = 1 / obs_var.
+  float kk = sok ? prm.k[ln.b * prm.ld_kq + ln.s] : 0.0f;
+  float qq = sok ? prm.q[ln.b * prm.ld_kq + ln.s] : 0.0f;
+  if (prm.qk_norm) {
+    kk = kk / fmaxf(sqrtf(group_sum<SP>(kk * kk)), 1e-12f);
+    qq = qq / fmaxf(sqrtf(group_sum<SP>(qq * qq)), 1e-12f);
+  }
+  if (prm.has_clip) {
+    kk = fminf(fmaxf(kk, -prm.clip), prm.clip);
+    qq = fminf(fmaxf(qq, -prm.clip), prm.clip);
+  }
+  const float vv = mok ? prm.v[ln.b * prm.ld_v + ln.m] : 0.0f;
+  float ov = (mok ? softplus_t(prm.lv[ln.b * prm.ld_lv + ln.m]) : 1.0f) + prm.ov_min;
+  ov = fminf(ov, prm.ov_max);
+  const float sig = 1.0f / ov;
+
+  // The filter step (as kla_step_kernel).
+  const float a_s = a_bar;
+  const float pp = fmaxf(p_bar, kEps);
+  const float a2 = fmaxf(a_s * a_s, kEps);
+  float lam = ln.active ? prm.lam[bms] : 1.0f;
+  float eta = ln.active ? prm.eta[bms] : 0.0f;
+  const float phi = fmaxf(sig * (kk * kk), kEps);
+  const float r = (vv * sig) * kk;
+  const float denom = fmaxf(a2 + pp * lam, kEps);
+  lam = lam / denom + phi;
+  eta = (a_s / denom) * eta + r;
+  const float var = 1.0f / fmaxf(lam, kEps);
+  float mean = eta * var, vo = var;
+  if (PRIOR) {
+    mean = a_s * mean;
+    vo = a2 * var + pp;
+  }
+  const float ys = group_sum<SP>(mean * qq);
+  const float vs = group_sum<SP>(vo * (qq * qq));
+  if (ln.s == 0 && mok) {
+    float yo = ys, vo2 = vs;
+    if (prm.z) {
+      const float lsk = prm.skip_vector ? prm.skip[ln.m] : prm.skip[0];
+      yo = yo + lsk * prm.z[ln.b * prm.ld_z + ln.m];
+    }
+    if (prm.gate) {
+      const float gg = activation(prm.gate_act, prm.gate[ln.b * prm.ld_gate + ln.m]);
+      yo = yo * gg;
+      vo2 = vo2 * (gg * gg);
+    }
+    prm.y[ln.b * M + ln.m] = yo;
+    prm.yvar[ln.b * M + ln.m] = vo2;
+  }
+  if (ln.active) {
+    prm.lam_out[bms] = lam;
+    prm.eta_out[bms] = eta;
+  }
+}
+
+// One token of the depthwise causal conv (CausalConv1d, reference common.py:70-96):
+// window = [state[b, d, :], x[b, d]], y = act(sum_j w[d, j] window[j] + bias[d]),
+// new state = window[1:]. One thread per (b, d).
+__global__ void conv_step_kernel(const float *__restrict__ x, int64_t ld_x, const float *__restrict__ state,
+                                 float *__restrict__ state_out, const float *__restrict__ w,
+                                 const float *__restrict__ bias, int act, float *__restrict__ y, int64_t batch,
+                                 int64_t D, int K) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= batch * D) return;
+  const int64_t b = i / D, d = i % D;
+  const float *st = state + i * (K - 1);
+  float *so = state_out + i * (K - 1);
+  const float *wd = w + d * K;
+  const float xt = x[b * ld_x + d];
+  float acc = 0.0f;
+  for (int j = 0; j < K - 1; ++j) acc += st[j] * wd[j];
+  acc += xt * wd[K - 1];
+  if (bias) acc = acc + bias[d];
+  y[i] = activation(act, acc);
+  for (int j = 0; j + 1 < K - 1; ++j) so[j] = st[j + 1];
+  if (K > 1) so[K - 2] = xt;
+}
+
 }  // namespace kla

@@ -24,7 +24,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -504,6 +504,101 @@ int kla_step_fwd(const float *v, const float *lambda_v, const float *k, const fl
                          stream, prm, g);
     return hip_status(fn, hipGetLastError());
   });
+}
+
+int kla_decode_step_fwd(const float *v, int64_t ld_v, const float *log_var, int64_t ld_log_var, const float *k,
+                        const float *q, int64_t ld_kq, const float *residual, int64_t ld_residual,
+                        const float *lambda_skip, const float *gate, int64_t ld_gate, const float *delta,
+                        const float *lambda_log, const float *process_noise, const float *lam, const float *eta,
+                        float *lam_out, float *eta_out, float *y, float *y_var, const kla_decode_config *cfg,
+                        int64_t batch, int64_t M, int64_t S, hipStream_t stream) {
+  const char *fn = "kla_decode_step_fwd";
+  if (!cfg) return fail(KLA_ERR_INVALID_ARG, "%s: cfg must not be NULL", fn);
+  int rc = check_fused_shape(fn, batch, 1, M, S);
+  if (rc != KLA_OK) return rc;
+  if (batch == 0 || M == 0 || S == 0) return KLA_OK;
+  if (!v || !log_var || !k || !q || !delta || !lambda_log || !process_noise || !lam || !eta || !lam_out ||
+      !eta_out || !y || !y_var)
+    return fail(KLA_ERR_INVALID_ARG, "%s: NULL operand", fn);
+  if ((residual == nullptr) != (lambda_skip == nullptr))
+    return fail(KLA_ERR_INVALID_ARG, "%s: pass both residual and lambda_skip or neither", fn);
+  if (ld_v < M || ld_log_var < M || ld_kq < S || (residual && ld_residual < M) || (gate && ld_gate < M))
+    return fail(KLA_ERR_INVALID_ARG, "%s: row stride below the row length", fn);
+  if (cfg->discretization != 0 && cfg->discretization != 1)
+    return fail(KLA_ERR_INVALID_ARG, "%s: discretization must be 0 (ou) or 1 (zoh)", fn);
+  if (gate && (cfg->gate_activation < kActSilu || cfg->gate_activation > kActRelu))
+    return fail(KLA_ERR_INVALID_ARG, "%s: gate_activation must be 1 (silu), 2 (gelu) or 3 (relu)", fn);
+  if (!all_aligned(4, {v, log_var, k, q, residual, lambda_skip, gate, delta, lambda_log, process_noise, lam, eta,
+                       lam_out, eta_out, y, y_var}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  const FusedGeom g = fused_geom(batch, 1, M, S);
+  const int64_t grid = batch * g.groups;
+  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+  DecodeParams prm{};
+  prm.v = v;
+  prm.lv = log_var;
+  prm.k = k;
+  prm.q = q;
+  prm.z = residual;
+  prm.skip = lambda_skip;
+  prm.gate = gate;
+  prm.ld_v = ld_v;
+  prm.ld_lv = ld_log_var;
+  prm.ld_kq = ld_kq;
+  prm.ld_z = ld_residual;
+  prm.ld_gate = ld_gate;
+  prm.delta = delta;
+  prm.lambda_log = lambda_log;
+  prm.pnoise = process_noise;
+  prm.lam = lam;
+  prm.eta = eta;
+  prm.lam_out = lam_out;
+  prm.eta_out = eta_out;
+  prm.y = y;
+  prm.yvar = y_var;
+  prm.ou = cfg->discretization == 0;
+  prm.zero_pn = cfg->zero_process_noise != 0;
+  prm.qk_norm = cfg->qk_norm != 0;
+  prm.has_clip = cfg->has_clip != 0;
+  prm.skip_vector = cfg->skip_vector != 0;
+  prm.gate_act = gate ? cfg->gate_activation : kActNone;
+  prm.clip = cfg->clip_value;
+  prm.ov_min = cfg->obs_var_min;
+  prm.ov_max = cfg->obs_var_max;
+  return with_sp(S, [&](auto sp) {
+    constexpr int SP = decltype(sp)::value;
+    if (cfg->decode_from_prior)
+      hipLaunchKernelGGL((kla_decode_step_kernel<SP, true>), dim3(static_cast<uint32_t>(grid)),
+                         dim3(kFusedThreads), 0, stream, prm, g);
+    else
+      hipLaunchKernelGGL((kla_decode_step_kernel<SP, false>), dim3(static_cast<uint32_t>(grid)),
+                         dim3(kFusedThreads), 0, stream, prm, g);
+    return hip_status(fn, hipGetLastError());
+  });
+}
+
+int kla_conv_step_fwd(const float *x, int64_t ld_x, const float *state, float *state_out, const float *weight,
+                      const float *bias, int activation, float *y, int64_t batch, int64_t channels,
+                      int64_t kernel_size, hipStream_t stream) {
+  const char *fn = "kla_conv_step_fwd";
+  if (batch < 0 || channels < 0 || kernel_size < 1 || kernel_size > 64)
+    return fail(KLA_ERR_INVALID_ARG, "%s: bad size (batch=%lld channels=%lld kernel_size=%lld)", fn,
+                (long long)batch, (long long)channels, (long long)kernel_size);
+  if (batch * channels >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: batch * channels above 2^31", fn);
+  if (activation < kActNone || activation > kActRelu)
+    return fail(KLA_ERR_INVALID_ARG, "%s: activation must be 0 (none), 1 (silu), 2 (gelu) or 3 (relu)", fn);
+  if (batch == 0 || channels == 0) return KLA_OK;
+  if (!x || !weight || !y || (kernel_size > 1 && (!state || !state_out)))
+    return fail(KLA_ERR_INVALID_ARG, "%s: NULL operand", fn);
+  if (ld_x < channels) return fail(KLA_ERR_INVALID_ARG, "%s: row stride below the row length", fn);
+  if (!all_aligned(4, {x, state, state_out, weight, bias, y}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  const int64_t n = batch * channels;
+  const int threads = 256;
+  hipLaunchKernelGGL(conv_step_kernel, dim3(static_cast<uint32_t>((n + threads - 1) / threads)), dim3(threads), 0,
+                     stream, x, ld_x, state, state_out, weight, bias, activation, y, batch, channels,
+                     static_cast<int>(kernel_size));
+  return hip_status(fn, hipGetLastError());
 }
 
 }  // extern "C"

@@ -188,6 +188,39 @@ class KLALayer(nn.Module):
                                            decode_from_prior=cfg.decode_from_prior, backend=cfg.backend)
         return y.unsqueeze(1), y_var.unsqueeze(1), new_state
 
+    def _decode_on_hip(self, projected: torch.Tensor) -> bool:
+        """Whether a one-token step runs on the MI355X decode kernels: inference
+        (no gradient), fp32 activations on a ROCm GPU, a hip-family backend."""
+        from kla.ops.kla_ops import _step_on_hip
+
+        return (not torch.is_grad_enabled() and projected.dtype == torch.float32 and self.d_state <= 64
+                and _step_on_hip(self.config.backend, projected))
+
+    def _decode_step_hip(self, z, gate, residual, ssm_state):
+        """The one-token SSM step with the lambda skip and the gate, as one HIP kernel
+        (kla.ops.hip.decode); the same values as _run_ssm_step plus the tail of forward."""
+        from kla.ops.hip.decode import decode_step_hip
+
+        cfg = self.config
+        S = self.d_state
+        proj = self.sensor_proj(z)[:, 0]
+        v, log_var, k, q = torch.split(proj, [self._w_value, self._w_var, S, S], dim=-1)
+        if self._value_rank == "conv":
+            v = z[:, 0]
+        elif self.value_expand is not None:
+            v = self.value_expand(v)
+        if self.var_expand is not None:
+            log_var = self.var_expand(log_var)
+        skip = self.lambda_skip.float() if self.lambda_skip is not None else None
+        y, y_var, lam, eta = decode_step_hip(
+            v, log_var, k, q, self.delta.float(), self.lambda_log.float(), self.process_noise.float(),
+            ssm_state.lam.contiguous(), ssm_state.eta.contiguous(), residual=residual[:, 0] if skip is not None else None, lambda_skip=skip,
+            gate=gate[:, 0] if gate is not None else None, gate_activation=cfg.gating_activation,
+            discretization=cfg.discretization, zero_process_noise=cfg.zero_process_noise, qk_norm=cfg.qk_norm,
+            clip_value=cfg.clip_value, obs_var_min=cfg.obs_var_min, obs_var_max=cfg.obs_var_max,
+            decode_from_prior=cfg.decode_from_prior)
+        return y.unsqueeze(1), y_var.unsqueeze(1), KLAState(lam=lam, eta=eta)
+
     def forward(self, x: torch.Tensor, state: KLALayerState | None = None, return_state: bool = False):
         """x [B, L, d_model] -> out, or (out, new_state) when a state is passed or requested.
 
@@ -202,26 +235,41 @@ class KLALayer(nn.Module):
             z, gate = projected.chunk(2, dim=-1)
         else:
             z, gate = projected, None
+        # One-token inference step on the GPU: the conv step and the SSM step
+        # (with skip and gate) run as two HIP kernels (kla.ops.hip.decode).
+        hip_decode = (state is not None and L == 1 and state.ssm.lam.dtype == torch.float32
+                      and self._decode_on_hip(projected))
 
         conv_state = state.conv if state is not None else None
         if self.conv is not None:
-            z, conv_state = self.conv(z, conv_state)
+            if hip_decode:
+                from kla.ops.hip.decode import conv_step_hip
+
+                # A torch prefill leaves the window as a view of its padded input.
+                zc, conv_state = conv_step_hip(z[:, 0], conv_state.to(z.dtype).contiguous(),
+                                               self.conv.weight[:, 0, :], self.conv.bias, cfg.conv_activation)
+                z = zc.unsqueeze(1)
+            else:
+                z, conv_state = self.conv(z, conv_state)
         residual = z
 
         ssm_state = state.ssm if state is not None else None
-        if state is not None and L == 1:
-            y, y_var, ssm_state = self._run_ssm_step(z, ssm_state)
+        if hip_decode:
+            y, y_var, ssm_state = self._decode_step_hip(z, gate, residual, ssm_state)
         else:
-            y, y_var, ssm_state = self._run_ssm(z, ssm_state)
-        y = y.to(x.dtype)
-        y_var = y_var.to(x.dtype)
+            if state is not None and L == 1:
+                y, y_var, ssm_state = self._run_ssm_step(z, ssm_state)
+            else:
+                y, y_var, ssm_state = self._run_ssm(z, ssm_state)
+            y = y.to(x.dtype)
+            y_var = y_var.to(x.dtype)
 
-        if self.lambda_skip is not None:
-            y = y + self.lambda_skip * residual
-        if gate is not None:
-            g = self.gate_act(gate)
-            y = y * g
-            y_var = y_var * g.pow(2)
+            if self.lambda_skip is not None:
+                y = y + self.lambda_skip * residual
+            if gate is not None:
+                g = self.gate_act(gate)
+                y = y * g
+                y_var = y_var * g.pow(2)
 
         out = self.out_proj(y)
         result = (out, F.linear(y_var, self.out_proj.weight.pow(2))) if cfg.return_variance else out

@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -50,7 +50,27 @@ _SIGNATURES = {
     "kla_fused_scan_fwd": (ctypes.c_int, [_p] * 14 + [ctypes.c_int] + [_i64] * 4 + [_p]),
     "kla_fused_scan_bwd": (ctypes.c_int, [_p] * 20 + [ctypes.c_int] + [_i64] * 4 + [_p, ctypes.c_size_t, _p]),
     "kla_step_fwd": (ctypes.c_int, [_p] * 12 + [ctypes.c_int] + [_i64] * 3 + [_p]),
+    "kla_decode_step_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _p, _p, _i64] + [_p] * 10
+                            + [_i64] * 3 + [_p]),
+    "kla_conv_step_fwd": (ctypes.c_int, [_p, _i64, _p, _p, _p, _p, ctypes.c_int, _p] + [_i64] * 3 + [_p]),
 }
+
+
+class DecodeConfig(ctypes.Structure):
+    """kla_decode_config of include/kla_hip.h."""
+
+    _fields_ = [
+        ("discretization", ctypes.c_int),
+        ("zero_process_noise", ctypes.c_int),
+        ("qk_norm", ctypes.c_int),
+        ("has_clip", ctypes.c_int),
+        ("clip_value", ctypes.c_float),
+        ("obs_var_min", ctypes.c_float),
+        ("obs_var_max", ctypes.c_float),
+        ("decode_from_prior", ctypes.c_int),
+        ("gate_activation", ctypes.c_int),
+        ("skip_vector", ctypes.c_int),
+    ]
 
 
 class KLAHipError(RuntimeError):

@@ -195,3 +195,39 @@ def test_fused_and_step_validation(lib):
     assert lib.kla_step_fwd(*[ALIGNED] * 11, None, 0, 2, 6, 16, None) == _lib.KLA_ERR_INVALID_ARG
     assert lib.kla_step_fwd(*[ALIGNED] * 11, ODD, 0, 2, 6, 16, None) == _lib.KLA_ERR_ALIGN
     assert lib.kla_step_fwd(*[ALIGNED] * 12, 0, 2, 6, 100, None) == _lib.KLA_ERR_INVALID_ARG
+
+
+def test_decode_and_conv_step_validation(lib):
+    cfg = _lib.DecodeConfig(discretization=0, obs_var_min=1e-4, obs_var_max=float("inf"), gate_activation=1)
+    P = ALIGNED
+
+    def dec(v=P, ld_v=8, lv=P, ld_lv=8, k=P, q=P, ld_kq=4, z=None, ld_z=0, skip=None, gate=None, ld_g=0,
+            delta=P, ll=P, pn=P, lam=P, eta=P, lo=P, eo=P, y=P, yv=P, c=cfg, shape=(2, 8, 4)):
+        return lib.kla_decode_step_fwd(v, ld_v, lv, ld_lv, k, q, ld_kq, z, ld_z, skip, gate, ld_g, delta, ll, pn,
+                                       lam, eta, lo, eo, y, yv, ctypes.byref(c) if c is not None else None,
+                                       *shape, None)
+
+    assert dec(c=None) == _lib.KLA_ERR_INVALID_ARG
+    assert "cfg must not be NULL" in err(lib)
+    assert dec(shape=(2, 8, 65)) == _lib.KLA_ERR_INVALID_ARG
+    assert dec(v=None) == _lib.KLA_ERR_INVALID_ARG
+    assert dec(z=P, ld_z=8) == _lib.KLA_ERR_INVALID_ARG
+    assert "residual and lambda_skip" in err(lib)
+    assert dec(ld_v=7) == _lib.KLA_ERR_INVALID_ARG
+    assert "row stride" in err(lib)
+    bad = _lib.DecodeConfig(discretization=2)
+    assert dec(c=bad) == _lib.KLA_ERR_INVALID_ARG
+    bad = _lib.DecodeConfig(gate_activation=7)
+    assert dec(c=bad, gate=P, ld_g=8) == _lib.KLA_ERR_INVALID_ARG
+    assert dec(k=ODD) == _lib.KLA_ERR_ALIGN
+    assert dec(shape=(0, 8, 4), v=None) == _lib.KLA_OK
+
+    def conv(x=P, ld_x=8, st=P, so=P, w=P, b=None, act=1, y=P, shape=(2, 8, 4)):
+        return lib.kla_conv_step_fwd(x, ld_x, st, so, w, b, act, y, *shape, None)
+
+    assert conv(shape=(2, 8, 0)) == _lib.KLA_ERR_INVALID_ARG
+    assert conv(act=5) == _lib.KLA_ERR_INVALID_ARG
+    assert conv(ld_x=4) == _lib.KLA_ERR_INVALID_ARG
+    assert conv(st=None) == _lib.KLA_ERR_INVALID_ARG
+    assert conv(w=ODD) == _lib.KLA_ERR_ALIGN
+    assert conv(shape=(0, 8, 4), x=None) == _lib.KLA_OK

@@ -412,3 +412,103 @@ def test_affine_scan_at_c3_size(cuda, dtype):
         h2 = affine_scan(gg[:, 4000:].detach(), uu[:, 4000:].detach(), h1[:, -1].float())
         torch.testing.assert_close(torch.cat([h1, h2], 1).float(), h.detach().float(),
                                    rtol=tol["rtol"], atol=tol["atol"])
+
+
+# ------------------------------------------------------- one-token decode kernels
+
+DECODE_CASES = {
+    "default": (48, dict(d_state=16)),
+    "zoh_conv_value": (40, dict(d_state=8, value_rank="conv", var_rank="dt", discretization="zoh",
+                                lambda_skip_mode="vector", bias=True)),
+    "prior_noconv_var": (32, dict(d_state=5, use_conv=False, decode_from_prior=True, return_variance=True)),
+    "clip_obsmax_zero_noise": (32, dict(d_state=16, clip_value=0.5, obs_var_max=2.0, zero_process_noise=True,
+                                        qk_norm=False)),
+    "gelu_relu_no_skip": (24, dict(d_state=3, gating_activation="gelu", conv_activation="relu",
+                                   use_lambda_skip=False)),
+    "relu_gate_lowrank": (40, dict(d_state=12, gating_activation="relu", conv_activation="gelu",
+                                   value_rank=6, var_rank=5)),
+    "no_gate_k2": (32, dict(d_state=16, use_gating=False, conv_kernel_size=2)),
+}
+
+
+@pytest.mark.parametrize("tag", sorted(DECODE_CASES))
+def test_decode_kernels_match_torch_path(cuda, tag):
+    """A one-token inference step through the decode kernels (conv step + fused SSM
+    step with skip and gate) equals the torch path of the same layer: outputs and
+    both states, over several decode steps after a prefill, for each config."""
+    import copy
+
+    d_model, cfg = DECODE_CASES[tag]
+    torch.manual_seed(0)
+    hip = KLALayer(d_model, KLAConfig(backend="hip", **cfg)).to(cuda).eval()
+    ref = copy.deepcopy(hip)
+    ref.config = KLAConfig(backend="torch", **cfg)
+    with torch.no_grad():
+        # Non-default parameters, so every term of the discretisation matters.
+        for layer in (hip, ref):
+            g = torch.Generator().manual_seed(1)
+            layer.lambda_log.copy_((torch.rand(layer.lambda_log.shape, generator=g) - 0.5).to(cuda))
+            if not cfg.get("zero_process_noise"):
+                layer.process_noise.copy_((torch.rand(layer.process_noise.shape, generator=g) * 0.05).to(cuda))
+        x = torch.randn(3, 9, d_model, generator=torch.Generator().manual_seed(2)).to(cuda)
+        sh, sr = hip.init_state(3, device=cuda), ref.init_state(3, device=cuda)
+        _, sh = hip(x[:, :6], state=sh)
+        _, sr = ref(x[:, :6], state=sr)
+        assert hip._decode_on_hip(hip.in_proj(x[:, :1]))
+        for t in range(6, 9):
+            oh, sh = hip(x[:, t:t + 1], state=sh)
+            orf, sr = ref(x[:, t:t + 1], state=sr)
+            for name, a, b in (("out", oh, orf), ("lam", sh.ssm.lam, sr.ssm.lam), ("eta", sh.ssm.eta, sr.ssm.eta)):
+                a = a if isinstance(a, torch.Tensor) else torch.cat([u.flatten() for u in a])
+                b = b if isinstance(b, torch.Tensor) else torch.cat([u.flatten() for u in b])
+                check(f"{name}@{t}", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
+            if sh.conv is not None:
+                torch.testing.assert_close(sh.conv, sr.conv, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("K", [1, 2, 4, 7])
+@pytest.mark.parametrize("act", ["silu", "gelu", "relu"])
+def test_conv_step_kernel_matches_causal_conv(cuda, K, act):
+    """kla_conv_step_fwd against CausalConv1d's torch one-token path (strided x rows)."""
+    from kla.layers.common import CausalConv1d
+    from kla.ops.hip.decode import conv_step_hip
+
+    torch.manual_seed(0)
+    conv = CausalConv1d(37, K, act).to(cuda)
+    g = torch.Generator().manual_seed(3)
+    rows = torch.randn(5, 1, 2 * 37, generator=g).to(cuda)
+    x = rows[..., :37]                       # a chunk view, row stride 74
+    state = torch.randn(5, 37, K - 1, generator=g).to(cuda)
+    with torch.no_grad():
+        want, want_state = conv(x, state)
+        got, got_state = conv_step_hip(x[:, 0], state, conv.weight[:, 0, :], conv.bias, act)
+    torch.testing.assert_close(got, want[:, 0], rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(got_state, want_state, rtol=0, atol=0)
+
+
+def test_decode_graph_with_decode_kernels_matches_torch_decode(cuda):
+    """SequenceModel decode through DecodeGraph (which now captures the decode
+    kernels) against eager torch-backend decode of the same seeded model."""
+    import copy
+
+    from kla.models.decode_graph import DecodeGraph
+
+    torch.manual_seed(0)
+    model = SequenceModel(ModelConfig(vocab_size=97, d_model=32, n_layers=2), KLAConfig(backend="hip")).to(cuda).eval()
+    ref = copy.deepcopy(model)
+    for layer in ref.modules():
+        if isinstance(layer, KLALayer):
+            layer.config = KLAConfig(backend="torch")
+    ids = torch.randint(0, 97, (2, 12), generator=torch.Generator().manual_seed(1)).to(cuda)
+    with torch.no_grad():
+        st_h = model.init_state(2)
+        st_r = ref.init_state(2)
+        lh, st_h = model(ids, state=st_h)
+        lr, st_r = ref(ids, state=st_r)
+        graph = DecodeGraph(model, st_h)
+        tok = lh[:, -1:].argmax(-1)
+        for _ in range(4):
+            out_g = graph.step(tok)
+            out_r, st_r = ref(tok, state=st_r)
+            torch.testing.assert_close(out_g, out_r, rtol=1e-4, atol=1e-5)
+            tok = out_r[:, -1:].argmax(-1)
