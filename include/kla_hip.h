@@ -230,6 +230,40 @@ int kla_conv_step_fwd(const float *x, int64_t ld_x, const float *state, float *s
                       const float *bias, int activation, float *y, int64_t batch, int64_t channels,
                       int64_t kernel_size, hipStream_t stream);
 
+/*
+ * The layer's short depthwise causal conv over a sequence, with autograd's
+ * backward: replaces CausalConv1d.forward for L >= 1 (reference
+ * src/kla/layers/common.py:58-96: transpose, torch.cat of the state in front,
+ * F.conv1d(groups=D), activation) and its backward through autograd.
+ *   xpad = [state (K-1), x (steps)] per (b, c); y[b, t, c] = act(bias[c] + sum_j w[c, j] xpad[t + j]);
+ *   state_out = xpad[steps : steps + K - 1].
+ * x [batch, steps, channels] with element strides ld_t (time) and ld_b (batch),
+ * channels contiguous; y dense [batch, steps, channels]; state, state_out
+ * [batch, channels, K-1] (state NULL = zeros, state_out NULL = not wanted);
+ * weight [channels, K] fp32, bias [channels] fp32 or NULL; K <= 8; activation
+ * 0 none, 1 silu, 2 gelu, 3 relu. dtype KLA_DTYPE_F32 or KLA_DTYPE_BF16 for x,
+ * y and the states; with bf16 the weight and bias are rounded to bf16 and the
+ * conv output is rounded before the activation (torch autocast's numerics).
+ */
+int kla_causal_conv_fwd(int dtype, const void *x, int64_t ld_t, int64_t ld_b, const void *state, const float *weight,
+                        const float *bias, int activation, void *y, void *state_out, int64_t batch, int64_t steps,
+                        int64_t channels, int64_t kernel_size, hipStream_t stream);
+
+/* Bytes of workspace kla_causal_conv_bwd needs (partial sums; no zero-fill needed). */
+size_t kla_causal_conv_workspace_bytes(int64_t batch, int64_t steps, int64_t channels, int64_t kernel_size);
+
+/*
+ * Exact adjoint of kla_causal_conv_fwd given dy (gradient of y, dense) and
+ * optionally dstate_out (gradient of state_out, NULL = 0): dx (dense
+ * [batch, steps, channels]), dstate (NULL to skip), dweight [channels, K] and
+ * dbias [channels] (fp32; dbias may be NULL when bias is). Weight and bias
+ * gradients are summed in a fixed order (deterministic).
+ */
+int kla_causal_conv_bwd(int dtype, const void *dy, const void *x, int64_t ld_t, int64_t ld_b, const void *state,
+                        const float *weight, const float *bias, int activation, const void *dstate_out, void *dx,
+                        void *dstate, float *dweight, float *dbias, int64_t batch, int64_t steps, int64_t channels,
+                        int64_t kernel_size, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

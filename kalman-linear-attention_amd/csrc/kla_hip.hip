@@ -17,6 +17,7 @@
 #include "kla_hip.h"
 #pragma GCC visibility pop
 
+#include "causal_conv.hpp"
 #include "fused_kla.hpp"
 #include "lookback_scan.hpp"
 
@@ -228,6 +229,33 @@ int with_sp(int64_t S, F &&f) {
     default: return f(std::integral_constant<int, 64>{});
   }
 }
+
+template <class F>
+int with_k(int64_t K, F &&f) {
+  switch (K) {
+    case 1: return f(std::integral_constant<int, 1>{});
+    case 2: return f(std::integral_constant<int, 2>{});
+    case 3: return f(std::integral_constant<int, 3>{});
+    case 4: return f(std::integral_constant<int, 4>{});
+    case 5: return f(std::integral_constant<int, 5>{});
+    case 6: return f(std::integral_constant<int, 6>{});
+    case 7: return f(std::integral_constant<int, 7>{});
+    default: return f(std::integral_constant<int, 8>{});
+  }
+}
+
+int check_conv_shape(const char *fn, int dtype, int64_t B, int64_t L, int64_t D, int64_t K, int act) {
+  if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16) return fail(KLA_ERR_DTYPE, "%s: unsupported dtype code %d", fn, dtype);
+  if (B < 0 || L < 0 || D < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  if (K < 1 || K > kConvMaxK) return fail(KLA_ERR_INVALID_ARG, "%s: kernel_size %lld outside [1, %d]", fn, (long long)K, kConvMaxK);
+  if (B > 65535 || (L + kConvT - 1) / kConvT > 65535 || D > (1ll << 31))
+    return fail(KLA_ERR_INVALID_ARG, "%s: batch, steps / %d or channels out of range", fn, kConvT);
+  if (act < kActNone || act > kActRelu)
+    return fail(KLA_ERR_INVALID_ARG, "%s: activation must be 0 (none), 1 (silu), 2 (gelu) or 3 (relu)", fn);
+  return KLA_OK;
+}
+
+int64_t conv_chunks(int64_t L) { return (L + kConvT - 1) / kConvT; }
 
 }  // namespace
 
@@ -599,6 +627,114 @@ int kla_conv_step_fwd(const float *x, int64_t ld_x, const float *state, float *s
                      stream, x, ld_x, state, state_out, weight, bias, activation, y, batch, channels,
                      static_cast<int>(kernel_size));
   return hip_status(fn, hipGetLastError());
+}
+
+int kla_causal_conv_fwd(int dtype, const void *x, int64_t ld_t, int64_t ld_b, const void *state, const float *weight,
+                        const float *bias, int activation, void *y, void *state_out, int64_t batch, int64_t steps,
+                        int64_t channels, int64_t kernel_size, hipStream_t stream) {
+  const char *fn = "kla_causal_conv_fwd";
+  int rc = check_conv_shape(fn, dtype, batch, steps, channels, kernel_size, activation);
+  if (rc != KLA_OK) return rc;
+  if (batch == 0 || channels == 0) return KLA_OK;
+  if (!weight || (steps > 0 && (!x || !y)))
+    return fail(KLA_ERR_INVALID_ARG, "%s: NULL operand", fn);
+  if (steps > 0 && (ld_t < channels || ld_b < (steps - 1) * ld_t + channels))
+    return fail(KLA_ERR_INVALID_ARG, "%s: strides below the row length", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (misaligned_bytes(x, el) || misaligned_bytes(state, el) || misaligned_bytes(y, el) ||
+      misaligned_bytes(state_out, el) || !all_aligned(4, {weight, bias}))
+    return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
+  const int64_t n_state = batch * channels * (kernel_size - 1);
+  auto run = [&](auto io) {
+    using IO = decltype(io);
+    if (steps == 0) {
+      if (state_out && n_state > 0)
+        hipLaunchKernelGGL(copy_or_zero_kernel<IO>, dim3(static_cast<uint32_t>((n_state + 255) / 256)), dim3(256), 0,
+                           stream, static_cast<const IO *>(state), static_cast<IO *>(state_out), n_state);
+      return hip_status(fn, hipGetLastError());
+    }
+    ConvFwdParams<IO> p{static_cast<const IO *>(x), ld_t, ld_b, static_cast<const IO *>(state), weight, bias,
+                        static_cast<IO *>(y), static_cast<IO *>(state_out), batch, steps, channels, activation};
+    const dim3 grid(static_cast<uint32_t>((channels + kConvThreads - 1) / kConvThreads),
+                    static_cast<uint32_t>(conv_chunks(steps)), static_cast<uint32_t>(batch));
+    return with_k(kernel_size, [&](auto kc) {
+      constexpr int K = decltype(kc)::value;
+      hipLaunchKernelGGL((causal_conv_fwd_kernel<IO, K>), grid, dim3(kConvThreads), 0, stream, p);
+      return hip_status(fn, hipGetLastError());
+    });
+  };
+  return dtype == KLA_DTYPE_F32 ? run(float{}) : run(bf16_t{});
+}
+
+size_t kla_causal_conv_workspace_bytes(int64_t batch, int64_t steps, int64_t channels, int64_t kernel_size) {
+  if (batch < 0 || steps < 0 || channels < 0 || kernel_size < 1 || kernel_size > kConvMaxK) {
+    fail(KLA_ERR_INVALID_ARG, "kla_causal_conv_workspace_bytes: bad size");
+    return 0;
+  }
+  return std::max<size_t>(256, static_cast<size_t>(batch * conv_chunks(steps) * channels * (kernel_size + 1)) * 4);
+}
+
+int kla_causal_conv_bwd(int dtype, const void *dy, const void *x, int64_t ld_t, int64_t ld_b, const void *state,
+                        const float *weight, const float *bias, int activation, const void *dstate_out, void *dx,
+                        void *dstate, float *dweight, float *dbias, int64_t batch, int64_t steps, int64_t channels,
+                        int64_t kernel_size, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  const char *fn = "kla_causal_conv_bwd";
+  int rc = check_conv_shape(fn, dtype, batch, steps, channels, kernel_size, activation);
+  if (rc != KLA_OK) return rc;
+  if (batch == 0 || channels == 0) return KLA_OK;
+  if (!weight || !dweight || (steps > 0 && (!dy || !x || !dx)) || (bias && !dbias))
+    return fail(KLA_ERR_INVALID_ARG, "%s: NULL operand", fn);
+  if (steps > 0 && (ld_t < channels || ld_b < (steps - 1) * ld_t + channels))
+    return fail(KLA_ERR_INVALID_ARG, "%s: strides below the row length", fn);
+  const size_t need = kla_causal_conv_workspace_bytes(batch, steps, channels, kernel_size);
+  if (steps > 0 && (!workspace || workspace_bytes < need))
+    return fail(KLA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (misaligned_bytes(dy, el) || misaligned_bytes(x, el) || misaligned_bytes(state, el) ||
+      misaligned_bytes(dstate_out, el) || misaligned_bytes(dx, el) || misaligned_bytes(dstate, el) ||
+      !all_aligned(4, {weight, bias, dweight, dbias, workspace}))
+    return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
+  const int64_t n_state = batch * channels * (kernel_size - 1);
+  auto run = [&](auto io) {
+    using IO = decltype(io);
+    if (steps == 0) {
+      // Empty sequence: d state = d new_state, no weight gradient.
+      if (dstate && n_state > 0)
+        hipLaunchKernelGGL(copy_or_zero_kernel<IO>, dim3(static_cast<uint32_t>((n_state + 255) / 256)), dim3(256), 0,
+                           stream, static_cast<const IO *>(dstate_out), static_cast<IO *>(dstate), n_state);
+      const int64_t nw = channels * kernel_size;
+      hipLaunchKernelGGL(copy_or_zero_kernel<float>, dim3(static_cast<uint32_t>((nw + 255) / 256)), dim3(256), 0,
+                         stream, nullptr, dweight, nw);
+      if (dbias)
+        hipLaunchKernelGGL(copy_or_zero_kernel<float>, dim3(static_cast<uint32_t>((channels + 255) / 256)), dim3(256),
+                           0, stream, nullptr, dbias, channels);
+      return hip_status(fn, hipGetLastError());
+    }
+    const int64_t rows = batch * conv_chunks(steps);
+    float *part_w = static_cast<float *>(workspace);
+    float *part_b = part_w + rows * channels * kernel_size;
+    ConvBwdParams<IO> p{static_cast<const IO *>(dy), static_cast<const IO *>(x), ld_t, ld_b,
+                        static_cast<const IO *>(state), weight, bias, static_cast<const IO *>(dstate_out),
+                        static_cast<IO *>(dx), static_cast<IO *>(dstate), part_w, part_b, batch, steps, channels,
+                        activation};
+    const dim3 grid(static_cast<uint32_t>((channels + kConvThreads - 1) / kConvThreads),
+                    static_cast<uint32_t>(conv_chunks(steps)), static_cast<uint32_t>(batch));
+    rc = with_k(kernel_size, [&](auto kc) {
+      constexpr int K = decltype(kc)::value;
+      hipLaunchKernelGGL((causal_conv_bwd_kernel<IO, K>), grid, dim3(kConvThreads), 0, stream, p);
+      return hip_status(fn, hipGetLastError());
+    });
+    if (rc != KLA_OK) return rc;
+    // Sums over the (batch, chunk) rows in a fixed order.
+    const int64_t nw = channels * kernel_size;
+    hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((nw + 255) / 256)), dim3(256), 0, stream,
+                       part_w, dweight, int64_t{1}, rows, nw);
+    if (dbias)
+      hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((channels + 255) / 256)), dim3(256), 0,
+                         stream, part_b, dbias, int64_t{1}, rows, channels);
+    return hip_status(fn, hipGetLastError());
+  };
+  return dtype == KLA_DTYPE_F32 ? run(float{}) : run(bf16_t{});
 }
 
 }  // extern "C"

@@ -63,6 +63,7 @@ class CausalConv1d(nn.Module):
         super().__init__()
         self.dim = dim
         self.kernel_size = kernel_size
+        self.activation = activation
         self.act = get_activation(activation)
         self.weight = nn.Parameter(torch.empty(dim, 1, kernel_size))
         self.bias = nn.Parameter(torch.empty(dim)) if bias else None
@@ -77,8 +78,16 @@ class CausalConv1d(nn.Module):
     def init_state(self, batch: int, device=None, dtype=None) -> torch.Tensor:
         return torch.zeros(batch, self.dim, self.kernel_size - 1, device=device, dtype=dtype)
 
-    def forward(self, x: torch.Tensor, conv_state: torch.Tensor | None = None):
-        """Returns (y [B, L, D], new_state [B, D, kernel_size - 1])."""
+    def forward(self, x: torch.Tensor, conv_state: torch.Tensor | None = None, hip: bool = False):
+        """Returns (y [B, L, D], new_state [B, D, kernel_size - 1]).
+
+        ``hip``: run the MI355X kernels (kla.ops.hip.conv; x on a ROCm GPU, fp32 or
+        bf16), which stream over x once instead of concatenating and calling a
+        library conv."""
+        if hip:
+            from kla.ops.hip.conv import causal_conv_hip
+
+            return causal_conv_hip(x, conv_state, self.weight[:, 0, :], self.bias, self.activation)
         xt = x.transpose(1, 2)
         if conv_state is None:
             conv_state = self.init_state(x.shape[0], device=x.device, dtype=xt.dtype)

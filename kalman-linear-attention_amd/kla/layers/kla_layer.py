@@ -196,6 +196,13 @@ class KLALayer(nn.Module):
         return (not torch.is_grad_enabled() and projected.dtype == torch.float32 and self.d_state <= 64
                 and _step_on_hip(self.config.backend, projected))
 
+    def _conv_on_hip(self, z: torch.Tensor) -> bool:
+        """Whether the causal conv runs on the MI355X kernels (with autograd)."""
+        from kla.ops.kla_ops import _step_on_hip
+
+        return (z.dtype in (torch.float32, torch.bfloat16) and self.conv.kernel_size <= 8
+                and _step_on_hip(self.config.backend, z))
+
     def _decode_step_hip(self, z, gate, residual, ssm_state):
         """The one-token SSM step with the lambda skip and the gate, as one HIP kernel
         (kla.ops.hip.decode); the same values as _run_ssm_step plus the tail of forward."""
@@ -250,7 +257,7 @@ class KLALayer(nn.Module):
                                                self.conv.weight[:, 0, :], self.conv.bias, cfg.conv_activation)
                 z = zc.unsqueeze(1)
             else:
-                z, conv_state = self.conv(z, conv_state)
+                z, conv_state = self.conv(z, conv_state, hip=self._conv_on_hip(z))
         residual = z
 
         ssm_state = state.ssm if state is not None else None

@@ -53,6 +53,11 @@ _SIGNATURES = {
     "kla_decode_step_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _p, _p, _i64] + [_p] * 10
                             + [_i64] * 3 + [_p]),
     "kla_conv_step_fwd": (ctypes.c_int, [_p, _i64, _p, _p, _p, _p, ctypes.c_int, _p] + [_i64] * 3 + [_p]),
+    "kla_causal_conv_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _i64, _p, _p, _p, ctypes.c_int, _p, _p]
+                            + [_i64] * 4 + [_p]),
+    "kla_causal_conv_workspace_bytes": (ctypes.c_size_t, [_i64] * 4),
+    "kla_causal_conv_bwd": (ctypes.c_int, [ctypes.c_int, _p, _p, _i64, _i64, _p, _p, _p, ctypes.c_int, _p, _p, _p,
+                                           _p, _p] + [_i64] * 4 + [_p, ctypes.c_size_t, _p]),
 }
 
 

@@ -512,3 +512,93 @@ def test_decode_graph_with_decode_kernels_matches_torch_decode(cuda):
             out_r, st_r = ref(tok, state=st_r)
             torch.testing.assert_close(out_g, out_r, rtol=1e-4, atol=1e-5)
             tok = out_r[:, -1:].argmax(-1)
+
+
+# ------------------------------------------------------------- causal conv kernels
+
+def _conv_reference(x, state, weight, bias, act):
+    """float64 CPU CausalConv1d (reference common.py:86-96) for autograd."""
+    import torch.nn.functional as F
+
+    from kla.layers.common import get_activation
+
+    xt = x.transpose(1, 2)
+    pad = torch.cat((state, xt), dim=-1)
+    y = F.conv1d(pad, weight.unsqueeze(1), bias, groups=weight.shape[0])
+    K = weight.shape[1]
+    return get_activation(act)(y).transpose(1, 2), pad[..., pad.shape[-1] - (K - 1):]
+
+
+@pytest.mark.parametrize("K", [1, 2, 4, 7])
+@pytest.mark.parametrize("L", [1, 3, 64, 65, 200])
+@pytest.mark.parametrize("act", ["silu", "gelu", "relu"])
+def test_causal_conv_matches_float64_autograd(cuda, K, L, act):
+    from kla.ops.hip.conv import causal_conv_hip
+
+    B, D = 2, 37
+    g = torch.Generator().manual_seed(K * 1000 + L)
+    rows = torch.randn(B, L, 2 * D + 3, generator=g, dtype=torch.float64)
+    state = torch.randn(B, D, K - 1, generator=g, dtype=torch.float64)
+    weight = torch.randn(D, K, generator=g, dtype=torch.float64) * 0.5
+    bias = torch.randn(D, generator=g, dtype=torch.float64) * 0.1
+    wy = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    ws = torch.randn(B, D, K - 1, generator=g, dtype=torch.float64)
+
+    xs = [t.clone().requires_grad_(True) for t in (rows, state, weight, bias)]
+    y_ref, s_ref = _conv_reference(xs[0][..., 1:D + 1], xs[1], xs[2], xs[3], act)
+    ((y_ref * wy).sum() + (s_ref * ws).sum()).backward()
+
+    gs = [t.float().to(cuda).requires_grad_(True) for t in (rows, state, weight, bias)]
+    y, s_new = causal_conv_hip(gs[0][..., 1:D + 1], gs[1], gs[2], gs[3], act)   # strided channel view
+    ((y * wy.float().to(cuda)).sum() + (s_new * ws.float().to(cuda)).sum()).backward()
+    check("y", y, y_ref.detach().numpy())
+    assert s_new.shape == s_ref.shape
+    if s_ref.numel():
+        check("new_state", s_new, s_ref.detach().numpy())
+    for name, got, want in zip(("dx", "dstate", "dweight", "dbias"), gs, xs):
+        if want.grad.numel():
+            check(name, got.grad, want.grad.numpy())
+
+
+def test_causal_conv_without_state_or_bias_and_bf16(cuda):
+    from kla.ops.hip.conv import causal_conv_hip
+
+    B, L, D, K = 3, 130, 64, 4
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(B, L, D, generator=g)
+    weight = torch.randn(D, K, generator=g) * 0.5
+    y_ref, s_ref = _conv_reference(x.double(), torch.zeros(B, D, K - 1, dtype=torch.float64), weight.double(), None,
+                                   "silu")
+    y, s_new = causal_conv_hip(x.to(cuda), None, weight.to(cuda), None, "silu")
+    check("y", y, y_ref.numpy())
+    check("new_state", s_new, s_ref.numpy())
+    # bf16 I/O against the float64 reference of the same (bf16-exact) inputs: rtol 2e-2.
+    xb = x.to(torch.bfloat16)
+    wb = weight.to(torch.bfloat16).float()
+    y_ref, _ = _conv_reference(xb.double(), torch.zeros(B, D, K - 1, dtype=torch.float64), wb.double(), None, "silu")
+    xg = xb.to(cuda).requires_grad_(True)
+    y, _ = causal_conv_hip(xg, None, wb.to(cuda), None, "silu")
+    assert y.dtype == torch.bfloat16
+    check("y_bf16", y, y_ref.numpy(), rtol=2e-2, atol=1e-2)
+    y.float().sum().backward()
+    assert xg.grad.dtype == torch.bfloat16 and torch.isfinite(xg.grad.float()).all()
+
+
+def test_layer_conv_on_hip_matches_torch_conv(cuda):
+    """A KLALayer training step with its conv on the HIP kernels equals the same
+    layer with the torch conv (fp32): output and every parameter gradient."""
+    import copy
+
+    torch.manual_seed(0)
+    layer = KLALayer(48, KLAConfig(d_state=8, backend="hip")).to(cuda)
+    other = copy.deepcopy(layer)
+    other._conv_on_hip = lambda z: False
+    x = torch.randn(2, 70, 48, generator=torch.Generator().manual_seed(1)).to(cuda)
+    outs = []
+    for m in (layer, other):
+        y = m(x)
+        (y.square().mean()).backward()
+        outs.append((y.detach(), {n: p.grad.detach().clone() for n, p in m.named_parameters()}))
+    check("y", outs[0][0], outs[1][0].cpu().numpy(), rtol=2e-5, atol=2e-6)
+    for n in outs[0][1]:
+        check("d" + n, outs[0][1][n], outs[1][1][n].cpu().numpy(), rtol=5e-5, atol=5e-6)
