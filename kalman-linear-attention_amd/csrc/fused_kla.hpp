@@ -673,6 +673,57 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
 }
 
 // out[o * inner + i] = sum_{j < G} in[(o * G + j) * inner + i], for o < outer, i < inner.
+// out[o, i] = sum_j in[o, j, i] over G rows for INNER columns (a power of two
+// dividing 256): one 256-thread block per o reads the row block [G, INNER]
+// with consecutive threads on consecutive floats, each thread sums every
+// (256 / INNER)-th row of its column, and a fixed-order LDS tree adds those
+// partials -- deterministic, and at streaming speed where reduce_groups_kernel's
+// one-thread-per-output loop is latency-bound.
+template <int INNER>
+__global__ void __launch_bounds__(256) reduce_rows_kernel(const float *__restrict__ in, float *__restrict__ out,
+                                                          int64_t G) {
+  static_assert(INNER >= 1 && INNER <= 256 && 256 % INNER == 0, "INNER must divide 256");
+  constexpr int R = 256 / INNER;
+  __shared__ float sm[256];
+  const int t = static_cast<int>(threadIdx.x);
+  const int i = t % INNER, r = t / INNER;
+  const float *src = in + static_cast<int64_t>(blockIdx.x) * G * INNER + i;
+  float acc = 0.0f;
+  for (int64_t j = r; j < G; j += R) acc += src[j * INNER];
+  sm[t] = acc;
+  __syncthreads();
+#pragma unroll
+  for (int step = R / 2; step > 0; step /= 2) {
+    if (r < step) sm[t] += sm[t + step * INNER];
+    __syncthreads();
+  }
+  if (r == 0) out[static_cast<int64_t>(blockIdx.x) * INNER + i] = sm[i];
+}
+
+// out[i] = sum_j in[j, i] over G rows (outer = 1): a 1024-thread block covers 64
+// columns with 16 row phases, each thread summing every 16th row of its column
+// (coalesced across the 64 columns), then a fixed-order LDS tree adds the 16
+// phase sums. Deterministic; parallel over rows as well as columns.
+__global__ void __launch_bounds__(1024) reduce_cols_kernel(const float *__restrict__ in, float *__restrict__ out,
+                                                           int64_t G, int64_t inner) {
+  constexpr int COLS = 64, PH = 16;
+  __shared__ float sm[PH][COLS];
+  const int t = static_cast<int>(threadIdx.x);
+  const int c = t % COLS, ph = t / COLS;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * COLS + c;
+  float acc = 0.0f;
+  if (col < inner)
+    for (int64_t j = ph; j < G; j += PH) acc += in[j * inner + col];
+  sm[ph][c] = acc;
+  __syncthreads();
+#pragma unroll
+  for (int step = PH / 2; step > 0; step /= 2) {
+    if (ph < step) sm[ph][c] += sm[ph + step][c];
+    __syncthreads();
+  }
+  if (ph == 0 && col < inner) out[col] = sm[0][c];
+}
+
 __global__ void reduce_groups_kernel(const float *__restrict__ in, float *__restrict__ out, int64_t outer,
                                      int64_t G, int64_t inner) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;

@@ -257,6 +257,29 @@ int check_conv_shape(const char *fn, int dtype, int64_t B, int64_t L, int64_t D,
 
 int64_t conv_chunks(int64_t L) { return (L + kConvT - 1) / kConvT; }
 
+// The row-block reduce for many short rows (outer large, inner a power of two up
+// to 64); false when the shape does not suit it.
+bool launch_reduce_rows(const float *in, float *out, int64_t outer, int64_t G, int64_t inner, hipStream_t stream) {
+  if (outer == 1 && G >= 4 && inner < (1ll << 37)) {
+    // One output row: split the rows across phases as well as the columns.
+    hipLaunchKernelGGL(reduce_cols_kernel, dim3(static_cast<uint32_t>((inner + 63) / 64)), dim3(1024), 0, stream, in,
+                       out, G, inner);
+    return true;
+  }
+  if (outer < 256 || outer >= (1ll << 31)) return false;
+  const dim3 grid(static_cast<uint32_t>(outer));
+  switch (inner) {
+    case 1: hipLaunchKernelGGL(reduce_rows_kernel<1>, grid, dim3(256), 0, stream, in, out, G); return true;
+    case 2: hipLaunchKernelGGL(reduce_rows_kernel<2>, grid, dim3(256), 0, stream, in, out, G); return true;
+    case 4: hipLaunchKernelGGL(reduce_rows_kernel<4>, grid, dim3(256), 0, stream, in, out, G); return true;
+    case 8: hipLaunchKernelGGL(reduce_rows_kernel<8>, grid, dim3(256), 0, stream, in, out, G); return true;
+    case 16: hipLaunchKernelGGL(reduce_rows_kernel<16>, grid, dim3(256), 0, stream, in, out, G); return true;
+    case 32: hipLaunchKernelGGL(reduce_rows_kernel<32>, grid, dim3(256), 0, stream, in, out, G); return true;
+    case 64: hipLaunchKernelGGL(reduce_rows_kernel<64>, grid, dim3(256), 0, stream, in, out, G); return true;
+    default: return false;
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -495,6 +518,7 @@ int kla_fused_scan_bwd(const float *dy, const float *dy_var, const float *dlam_f
   auto reduce = [&](const float *in, float *out, int64_t outer, int64_t G, int64_t inner) {
     const int64_t n = outer * inner;
     if (n == 0) return KLA_OK;
+    if (launch_reduce_rows(in, out, outer, G, inner, stream)) return hip_status(fn, hipGetLastError());
     hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream,
                        in, out, outer, G, inner);
     return hip_status(fn, hipGetLastError());
@@ -727,9 +751,10 @@ int kla_causal_conv_bwd(int dtype, const void *dy, const void *x, int64_t ld_t, 
     if (rc != KLA_OK) return rc;
     // Sums over the (batch, chunk) rows in a fixed order.
     const int64_t nw = channels * kernel_size;
-    hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((nw + 255) / 256)), dim3(256), 0, stream,
-                       part_w, dweight, int64_t{1}, rows, nw);
-    if (dbias)
+    if (!launch_reduce_rows(part_w, dweight, 1, rows, nw, stream))
+      hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((nw + 255) / 256)), dim3(256), 0, stream,
+                         part_w, dweight, int64_t{1}, rows, nw);
+    if (dbias && !launch_reduce_rows(part_b, dbias, 1, rows, channels, stream))
       hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((channels + 255) / 256)), dim3(256), 0,
                          stream, part_b, dbias, int64_t{1}, rows, channels);
     return hip_status(fn, hipGetLastError());

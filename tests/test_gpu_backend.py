@@ -110,7 +110,8 @@ def test_chunked_state_carry(cuda, backend):
 
 @pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("decode_from_prior", [False, True])
-@pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 20, 3, 3), (1, 33, 6, 12), (1, 21, 4, 20)])
+@pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 20, 3, 3), (1, 33, 6, 12), (1, 21, 4, 20),
+                                   (2, 150, 20, 16), (1, 260, 6, 4)])
 def test_gradients_match_float64_autograd(cuda, backend, decode_from_prior, shape):
     """Every input gradient, the initial-state gradients, and gradients flowing in
     through the returned state, against float64 autograd of the reference's
