@@ -90,6 +90,15 @@ Geom make_geom(Shape s, int W, int S, int V) {
   return g;
 }
 
+// A forward scan's output is stored cached (for the backward that follows) when
+// the whole [batch, steps, lanes] output fits MI355X's 256 MiB memory-side
+// cache; larger outputs stream. Measured in the fwd + bwd step with the output
+// cached: 256 MiB outputs (8 x 4096 x 2048 fp32, 8 x 8192 x 2048 bf16) gain
+// 1.5-3%, a 512 MiB output (8 x 8192 x 2048 fp32) loses 2-3%.
+constexpr int64_t kCachedOutputBytes = 256ll << 20;
+
+bool output_fits_cache(Shape s, int64_t elem) { return s.batch * s.steps * s.lanes * elem <= kCachedOutputBytes; }
+
 template <class T>
 Geom make_geom(Shape s) {
   return make_geom(s, T::W, T::S, T::V);
@@ -324,12 +333,15 @@ int kla_mobius_scan_fwd(const float *A, const float *B, const float *C, const fl
     return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
   rc = check_launch(fn, KLA_SCAN_MOBIUS_FWD, s, workspace, workspace_bytes);
   if (rc != KLA_OK) return rc;
-  if (D) {
-    using P = MobiusFwd<true>;
-    return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, D, lam0, lam}, s, workspace, stream);
-  }
-  using P = MobiusFwd<false>;
-  return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, nullptr, lam0, lam}, s, workspace, stream);
+  auto run = [&](auto has_d, auto cached) {
+    using P = MobiusFwd<decltype(has_d)::value, decltype(cached)::value>;
+    return launch<P, MobiusFwdTile>(fn, typename P::Params{A, B, C, D, lam0, lam}, s, workspace, stream);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  const bool cached = output_fits_cache(s, 4);
+  if (D) return cached ? run(T{}, T{}) : run(T{}, F{});
+  return cached ? run(F{}, T{}) : run(F{}, F{});
 }
 
 int kla_mobius_scan_bwd(const float *dlam, const float *A, const float *B, const float *C,
@@ -377,17 +389,24 @@ int kla_affine_scan_fwd(int dtype, const void *g, const void *u, const float *h0
     return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
   rc = check_launch(fn, KLA_SCAN_AFFINE_FWD, s, workspace, workspace_bytes);
   if (rc != KLA_OK) return rc;
-  if (dtype == KLA_DTYPE_F32) {
-    using P = AffineFwd<float>;
-    const P::Params prm{static_cast<const float *>(g), static_cast<const float *>(u), h0, static_cast<float *>(h)};
-    return launch<P, AffineFwdTile>(fn, prm, s, workspace, stream);
-  }
-  using P = AffineFwd<bf16_t>;
-  const P::Params prm{static_cast<const bf16_t *>(g), static_cast<const bf16_t *>(u), h0, static_cast<bf16_t *>(h)};
-  constexpr int V = AffineFwdBf16Tile::V;
-  if (lanes % V == 0 && all_aligned(V * el, {g, u, h}))
-    return launch<P, AffineFwdBf16Tile>(fn, prm, s, workspace, stream);
-  return launch<P, AffineBf16Fallback>(fn, prm, s, workspace, stream);
+  const bool cached = output_fits_cache(s, static_cast<int64_t>(el));
+  auto run = [&](auto cached_c) {
+    constexpr bool CACHED = decltype(cached_c)::value;
+    if (dtype == KLA_DTYPE_F32) {
+      using P = AffineFwd<float, CACHED>;
+      const typename P::Params prm{static_cast<const float *>(g), static_cast<const float *>(u), h0,
+                                   static_cast<float *>(h)};
+      return launch<P, AffineFwdTile>(fn, prm, s, workspace, stream);
+    }
+    using P = AffineFwd<bf16_t, CACHED>;
+    const typename P::Params prm{static_cast<const bf16_t *>(g), static_cast<const bf16_t *>(u), h0,
+                                 static_cast<bf16_t *>(h)};
+    constexpr int V = AffineFwdBf16Tile::V;
+    if (lanes % V == 0 && all_aligned(V * el, {g, u, h}))
+      return launch<P, AffineFwdBf16Tile>(fn, prm, s, workspace, stream);
+    return launch<P, AffineBf16Fallback>(fn, prm, s, workspace, stream);
+  };
+  return cached ? run(std::true_type{}) : run(std::false_type{});
 }
 
 int kla_affine_scan_bwd(int dtype, const void *dh, const void *g, const void *h,

@@ -195,6 +195,37 @@ __device__ __forceinline__ void store_v(bf16_t *p, const float (&x)[V]) {
   }
 }
 
+// The forward scans' outputs (lam, h) are read again by the backward scans, in
+// reverse time order and usually right away. With CACHED (chosen per launch: the
+// output fits the memory-side cache) they are stored with ordinary (cached)
+// stores instead of nontemporal ones, so the backward finds the end of the
+// sequence still in L2 and the memory-side cache. The choice is a template
+// parameter, not a branch: the compiler merges the two stores of a branch into
+// one and drops the nontemporal hint.
+template <int V>
+__device__ __forceinline__ void store_v_cached(float *p, const float (&x)[V]) {
+  if constexpr (V == 1) {
+    p[0] = x[0];
+  } else if constexpr (V == 2) {
+    *reinterpret_cast<f32x2 *>(p) = f32x2{x[0], x[1]};
+  } else {
+    static_assert(V == 4, "V must be 1, 2 or 4");
+    *reinterpret_cast<f32x4 *>(p) = f32x4{x[0], x[1], x[2], x[3]};
+  }
+}
+
+template <int V>
+__device__ __forceinline__ void store_v_cached(bf16_t *p, const float (&x)[V]) {
+  if constexpr (V == 1) {
+    *reinterpret_cast<uint16_t *>(p) = from_f32<bf16_t>(x[0]).bits;
+  } else if constexpr (V == 2) {
+    *reinterpret_cast<uint32_t *>(p) = pack_bf16x2(x[0], x[1]);
+  } else {
+    static_assert(V == 4, "V must be 1, 2 or 4");
+    *reinterpret_cast<u32x2 *>(p) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+  }
+}
+
 // V consecutive elements of a [batch, lanes] fp32 state tensor (ordinary access).
 template <int V>
 __device__ __forceinline__ void load_state_v(const float *p, float (&o)[V]) {
@@ -321,7 +352,7 @@ __device__ __forceinline__ float mobius_apply(const Agg<4> &m, float x) {
 
 // ================================================================ MobiusFwd
 
-template <bool HAS_D>
+template <bool HAS_D, bool CACHED = false>
 struct MobiusFwd {
   static constexpr int AGG = 4;
   using IO = float;
@@ -397,7 +428,12 @@ struct MobiusFwd {
           const float d = HAS_D ? r.d[HAS_D ? j : 0][v] : 1.0f;
           x[v] = (r.a[j][v] * x[v] + r.b[j][v]) / fmaxf(r.c[j][v] * x[v] + d, kEps);
         }
-        if (q.ok) store_v<V>(at(p.lam, row + j * g.lanes, q), x);
+        if (q.ok) {
+          if constexpr (CACHED)
+            store_v_cached<V>(at(p.lam, row + j * g.lanes, q), x);
+          else
+            store_v<V>(at(p.lam, row + j * g.lanes, q), x);
+        }
       }
     }
   }
@@ -536,7 +572,7 @@ struct MobiusBwd {
 // ================================================================ AffineFwd
 // h_t = g_t h_{t-1} + u_t, h_{-1} = h0 (reference tiled_mobius_scan.py:161-203).
 
-template <class IOT>
+template <class IOT, bool CACHED = false>
 struct AffineFwd {
   static constexpr int AGG = 2;
   using IO = IOT;
@@ -597,7 +633,12 @@ struct AffineFwd {
       if (j < nvalid) {
 #pragma unroll
         for (int v = 0; v < V; ++v) x[v] = r.g[j][v] * x[v] + r.u[j][v];
-        if (q.ok) store_v<V>(at(p.h, row + j * gm.lanes, q), x);
+        if (q.ok) {
+          if constexpr (CACHED)
+            store_v_cached<V>(at(p.h, row + j * gm.lanes, q), x);
+          else
+            store_v<V>(at(p.h, row + j * gm.lanes, q), x);
+        }
       }
     }
   }
