@@ -171,6 +171,56 @@ int kla_fused_scan_bwd(const float *dy, const float *dy_var, const float *dlam_f
                        hipStream_t stream);
 
 /*
+ * The fused scan's sensor inputs as a KLALayer holds them. v and the precision
+ * operand `obs` are [batch, steps, M] with rows ld_v / ld_obs elements apart:
+ * element (b, t, m) at (b * steps + t) * ld + m, so they may be column slices of
+ * the sensor projection. dtype is KLA_DTYPE_F32 or KLA_DTYPE_BF16 (both operands).
+ * With log_var = 1, obs holds log sigma^2 and the kernels form
+ *   lambda_v = 1 / min(softplus(log sigma^2) + obs_var_min, obs_var_max)
+ * (softplus with torch's threshold 20; obs_var_max = +inf for none), which is the
+ * tail of KLALayer._project_sensors (reference src/kla/layers/kla_layer.py:224-230).
+ * With log_var = 0, obs is lambda_v itself.
+ */
+typedef struct kla_sensors {
+  const void *v;
+  int64_t ld_v;
+  const void *obs;
+  int64_t ld_obs;
+  int dtype;
+  int log_var;
+  float obs_var_min;
+  float obs_var_max;
+} kla_sensors;
+
+/*
+ * kla_fused_scan_fwd with the sensors read as described by `sensors` (the
+ * projection read-out and lambda_v formed in the kernel, never stored).
+ * Replaces _project_sensors' v / lambda_v tail plus kla_scan_torch
+ * (reference src/kla/layers/kla_layer.py:194-231, src/kla/ops/kla_ops.py:188-290).
+ */
+int kla_fused_scan_sensors_fwd(const kla_sensors *sensors, const float *k, const float *q, const float *a,
+                               const float *p, const float *lam0, const float *eta0, float *y, float *y_var,
+                               float *lam_fin, float *eta_fin, float *ck_lam, float *ck_eta,
+                               int decode_from_prior, int64_t batch, int64_t steps, int64_t M, int64_t S,
+                               hipStream_t stream);
+
+/*
+ * Exact adjoint of kla_fused_scan_sensors_fwd. dv and dobs are dense
+ * [batch, steps, M] of the sensors' dtype (bf16: rounded to nearest even, as
+ * autograd's cast back to the projection's dtype rounds); dobs is the gradient
+ * of log sigma^2 (log_var, through the reciprocal, the clamp and softplus as torch
+ * differentiates them) or of lambda_v. Everything else as kla_fused_scan_bwd;
+ * the workspace is kla_fused_workspace_bytes.
+ */
+int kla_fused_scan_sensors_bwd(const float *dy, const float *dy_var, const float *dlam_fin,
+                               const float *deta_fin, const kla_sensors *sensors, const float *k,
+                               const float *q, const float *a, const float *p, const float *ck_lam,
+                               const float *ck_eta, void *dv, void *dobs, float *dk, float *dq, float *da,
+                               float *dp, float *dlam0, float *deta0, int decode_from_prior, int64_t batch,
+                               int64_t steps, int64_t M, int64_t S, void *workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+
+/*
  * One O(1) decode step of the filter for every (b, m, s) lane: kla_step
  * (reference src/kla/ops/kla_ops.py:293-331), phi floored at 1e-12 as there.
  * v, lambda_v, y, y_var [batch, M]; k, q [batch, S]; a, p [M, S]; lam, eta,

@@ -52,16 +52,33 @@ struct FusedGeom {
   int64_t n_ck;     // ceil(steps / kCkpt)
 };
 
+// The [B, L, M] sensor inputs v and the precision operand: rows of stride ld
+// (element (b, t, m) at (b * L + t) * ld + m, so they can be column slices of
+// the layer's projection), fp32 or bf16. The precision operand is Lambda^v, or
+// with log_var the projection's log sigma^2, from which the kernels form
+// Lambda^v = 1 / min(softplus(log sigma^2) + ov_min, ov_max) while staging (the
+// layer's _project_sensors tail, reference kla_layer.py:224-230).
+struct SensorIn {
+  const void *v, *lv;
+  int64_t ld_v, ld_lv;
+  int bf16;       // v, lv -- and the gradients dv, dlv the backward writes -- are bf16
+  int log_var;
+  float ov_min, ov_max;
+};
+
 struct FusedFwdParams {
-  const float *v, *lv, *k, *q, *a, *p, *lam0, *eta0;
+  SensorIn sn;
+  const float *k, *q, *a, *p, *lam0, *eta0;
   float *y, *yvar, *lam_fin, *eta_fin;
   float *ck_lam, *ck_eta;   // [B, n_ck, M, S] or NULL (no backward will follow)
 };
 
 struct FusedBwdParams {
   const float *dy, *dyvar, *dlam_fin, *deta_fin;   // dlam_fin, deta_fin may be NULL
-  const float *v, *lv, *k, *q, *a, *p, *ck_lam, *ck_eta;
-  float *dv, *dlv, *dlam0, *deta0;                 // dlam0, deta0 may be NULL
+  SensorIn sn;
+  const float *k, *q, *a, *p, *ck_lam, *ck_eta;
+  void *dv, *dlv;                                  // dense [B, L, M] of the sensor dtype
+  float *dlam0, *deta0;                            // may be NULL
   float *part_k, *part_q;                          // [B, L, G, S]
   float *part_a, *part_p;                          // [B, M, S]
 };
@@ -274,7 +291,110 @@ __device__ __forceinline__ void lds_to_global(const float (*lds)[TB + kPad], flo
 
 // ================================================================ forward
 
-template <int SP, bool PRIOR>
+// torch's softplus (threshold 20), for the one-token decode step.
+__device__ __forceinline__ float softplus_t(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+// softplus(x) = max(x, 0) + log1p(e), e = exp(-|x|) in (0, 1], with log1p(e) =
+// log(w) e / (w - 1), w = 1 + e rounded (and e itself where w rounds to 1): the
+// log1p identity of Goldberg, "What every computer scientist should know about
+// floating-point arithmetic" (1991), Theorem 4, accurate to a few ulp with the
+// hardware exp2 / log2. Equals torch's x for x > 20 (the correction is below half
+// an ulp of x there). Also returns e, from which sigmoid(x) follows.
+__device__ __forceinline__ float softplus_fast(float x, float &e) {
+  constexpr float kLog2e = 1.44269504088896340736f, kLn2 = 0.69314718055994530942f;
+  e = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
+  const float w = 1.0f + e;
+  const float l = w == 1.0f ? e : (__builtin_amdgcn_logf(w) * kLn2) * (e * __builtin_amdgcn_rcpf(w - 1.0f));
+  return fmaxf(x, 0.0f) + l;
+}
+
+// Lambda^v = 1 / min(softplus(x) + ov_min, ov_max) and the factor f with
+// d log sigma^2 = g Lambda^2 f for the gradient g of Lambda^v: f = -sigmoid(x),
+// or 0 where the clamp is active -- torch's derivatives of the reciprocal
+// (-g r^2), of clamp_max (g where not above the maximum) and of softplus
+// (g sigmoid(x), or g for x > 20, where sigmoid(x) rounds to 1 within 3e-9).
+__device__ __forceinline__ float sensor_precision(float x, float ov_min, float ov_max, float *f = nullptr) {
+  float e;
+  const float obs = softplus_fast(x, e) + ov_min;
+  if (f) {
+    const float sig = (x >= 0.0f ? 1.0f : e) * __builtin_amdgcn_rcpf(1.0f + e);
+    *f = obs > ov_max ? 0.0f : -sig;
+  }
+  return __builtin_amdgcn_rcpf(fminf(obs, ov_max));
+}
+
+// Sensor tile [TB, W] at `base` (row stride ld elements). bf16 elements are kept
+// as raw bits in the low half of each register until widen_sensor, so no load
+// has to complete before the tile is staged.
+template <int TB, int W, bool BF16>
+__device__ __forceinline__ void tile_load_sensor(TileRegs<TB, W> &r, const void *base, int64_t ld, int64_t rows,
+                                                 int64_t cols) {
+  if constexpr (!BF16) {
+    tile_load<TB, W>(r, static_cast<const float *>(base), ld, rows, cols);
+  } else {
+    const uint16_t *p = static_cast<const uint16_t *>(base);
+    const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+    for (int i = 0; i < TileRegs<TB, W>::N; ++i) {
+      const int e = tid + i * kFusedThreads;
+      const int t = e / W, c = e % W;
+      r.x[i] = __uint_as_float((e < TB * W && t < rows && c < cols)
+                                   ? static_cast<uint32_t>(__builtin_nontemporal_load(p + t * ld + c))
+                                   : 0u);
+    }
+  }
+}
+
+template <int TB, int W, bool BF16>
+__device__ __forceinline__ void widen_sensor(TileRegs<TB, W> &r) {
+  if constexpr (BF16) {
+#pragma unroll
+    for (int i = 0; i < TileRegs<TB, W>::N; ++i) r.x[i] = __uint_as_float(__float_as_uint(r.x[i]) << 16);
+  }
+}
+
+// Element (row, column m0) of a sensor tensor.
+template <bool BF16>
+__device__ __forceinline__ const void *sensor_at(const void *base, int64_t row, int64_t m0, int64_t ld) {
+  return static_cast<const char *>(base) + (row * ld + m0) * (BF16 ? 2 : 4);
+}
+
+// LDS [W][TB + 4] -> dense rows of a tensor of the sensor dtype; with F, each
+// value times lam^2 f (the log sigma^2 gradient from that of Lambda^v).
+template <int TB, int W, bool BF16, bool F>
+__device__ __forceinline__ void lds_to_global_sensor(const float (*lds)[TB + kPad], const float (*lam)[TB + kPad],
+                                                     const float (*f)[TB + kPad], void *base, int64_t ld,
+                                                     int64_t rows, int64_t cols) {
+  const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+  for (int i = 0; i < (TB * W + kFusedThreads - 1) / kFusedThreads; ++i) {
+    const int e = tid + i * kFusedThreads;
+    const int t = e / W, c = e % W;
+    if (e < TB * W && t < rows && c < cols) {
+      float d = lds[c][t];
+      if constexpr (F) {
+        const float l = lam[c][t];
+        d = d * (l * l) * f[c][t];
+      }
+      if constexpr (BF16)
+        __builtin_nontemporal_store(from_f32<bf16_t>(d).bits, static_cast<uint16_t *>(base) + t * ld + c);
+      else
+        __builtin_nontemporal_store(d, static_cast<float *>(base) + t * ld + c);
+    }
+  }
+}
+
+// The precision tile as Lambda^v (formed in place when it holds log sigma^2);
+// with f, also each element's log sigma^2 gradient factor, into f.
+template <int TB, int W>
+__device__ __forceinline__ void to_precision(TileRegs<TB, W> &r, const SensorIn &sn, TileRegs<TB, W> *f = nullptr) {
+  if (!sn.log_var) return;
+#pragma unroll
+  for (int i = 0; i < TileRegs<TB, W>::N; ++i)
+    r.x[i] = sensor_precision(r.x[i], sn.ov_min, sn.ov_max, f ? &f->x[i] : nullptr);
+}
+
+template <int SP, bool PRIOR, bool BF16>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int TB = kFusedTB;
@@ -299,8 +419,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
   float lam = (ln.active && prm.lam0) ? prm.lam0[bms] : 1.0f;
   float eta = (ln.active && prm.eta0) ? prm.eta0[bms] : 0.0f;
 
-  const float *vbase = prm.v + ln.b * L * M + m0;
-  const float *lbase = prm.lv + ln.b * L * M + m0;
+  const SensorIn &sn = prm.sn;
   const float *kbase = prm.k + ln.b * L * S;
   const float *qbase = prm.q + ln.b * L * S;
   float *ybase = prm.y + ln.b * L * M + m0;
@@ -310,13 +429,16 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
   TileRegs<TB, SP> rk, rq;
   auto load = [&](int64_t t0) {
     const int64_t rows = L - t0;
-    tile_load<TB, CH>(rv, vbase + t0 * M, M, rows, cols_m);
-    tile_load<TB, CH>(rl, lbase + t0 * M, M, rows, cols_m);
+    tile_load_sensor<TB, CH, BF16>(rv, sensor_at<BF16>(sn.v, ln.b * L + t0, m0, sn.ld_v), sn.ld_v, rows, cols_m);
+    tile_load_sensor<TB, CH, BF16>(rl, sensor_at<BF16>(sn.lv, ln.b * L + t0, m0, sn.ld_lv), sn.ld_lv, rows, cols_m);
     tile_load<TB, SP>(rk, kbase + t0 * S, S, rows, S);
     tile_load<TB, SP>(rq, qbase + t0 * S, S, rows, S);
   };
   auto stage = [&](int buf) {
+    widen_sensor<TB, CH, BF16>(rv);
+    widen_sensor<TB, CH, BF16>(rl);
     tile_to_lds<TB, CH>(rv, s_v[buf]);
+    to_precision<TB, CH>(rl, sn);
     tile_to_lds<TB, CH>(rl, s_l[buf]);
     tile_to_lds<TB, SP>(rk, s_k[buf]);
     tile_to_lds<TB, SP>(rq, s_q[buf]);
@@ -424,7 +546,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
 
 // ================================================================ backward
 
-template <int SP, bool PRIOR>
+template <int SP, bool PRIOR, bool BF16>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int NW = kFusedThreads / kWave;
@@ -433,6 +555,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
   __shared__ float s_dy[2][CH][TB + kPad], s_dyv[2][CH][TB + kPad];
   __shared__ float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
   __shared__ float s_dv[2][CH][TB + kPad], s_dl[2][CH][TB + kPad];
+  __shared__ float s_lf[2][CH][TB + kPad];   // log sigma^2 gradient factors (log_var sensors)
   __shared__ float s_red[2][2][TB][NW][SP];
 
   const FusedLane ln = fused_lane<SP>(g);
@@ -458,19 +581,27 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
   float acc_a = 0.0f, acc_a2 = 0.0f, acc_p = 0.0f;
 
   const int64_t offM = ln.b * L * M + m0, offS = ln.b * L * S;
+  const SensorIn &sn = prm.sn;
   TileRegs<TB, CH> rv, rl, rdy, rdyv;
   TileRegs<TB, SP> rk, rq;
   auto load = [&](int64_t t0) {
     const int64_t rows = L - t0;
-    tile_load<TB, CH>(rv, prm.v + offM + t0 * M, M, rows, cols_m);
-    tile_load<TB, CH>(rl, prm.lv + offM + t0 * M, M, rows, cols_m);
+    tile_load_sensor<TB, CH, BF16>(rv, sensor_at<BF16>(sn.v, ln.b * L + t0, m0, sn.ld_v), sn.ld_v, rows, cols_m);
+    tile_load_sensor<TB, CH, BF16>(rl, sensor_at<BF16>(sn.lv, ln.b * L + t0, m0, sn.ld_lv), sn.ld_lv, rows, cols_m);
     tile_load<TB, CH>(rdy, prm.dy + offM + t0 * M, M, rows, cols_m);
     tile_load<TB, CH>(rdyv, prm.dyvar + offM + t0 * M, M, rows, cols_m);
     tile_load<TB, SP>(rk, prm.k + offS + t0 * S, S, rows, S);
     tile_load<TB, SP>(rq, prm.q + offS + t0 * S, S, rows, S);
   };
   auto stage = [&](int buf) {
+    widen_sensor<TB, CH, BF16>(rv);
+    widen_sensor<TB, CH, BF16>(rl);
     tile_to_lds<TB, CH>(rv, s_v[buf]);
+    if (sn.log_var) {
+      TileRegs<TB, CH> rf;
+      to_precision<TB, CH>(rl, sn, &rf);
+      tile_to_lds<TB, CH>(rf, s_lf[buf]);
+    }
     tile_to_lds<TB, CH>(rl, s_l[buf]);
     tile_to_lds<TB, CH>(rdy, s_dy[buf]);
     tile_to_lds<TB, CH>(rdyv, s_dyv[buf]);
@@ -481,8 +612,14 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
   // partial sums of dk, dq (the waves' sums added here, in wave order).
   auto flush = [&](int64_t blk, int buf) {
     const int64_t t0 = blk * TB;
-    lds_to_global<TB, CH>(s_dv[buf], prm.dv + offM + t0 * M, M, L - t0, cols_m);
-    lds_to_global<TB, CH>(s_dl[buf], prm.dlv + offM + t0 * M, M, L - t0, cols_m);
+    constexpr int64_t el = BF16 ? 2 : 4;
+    void *dvb = static_cast<char *>(prm.dv) + (offM + t0 * M) * el;
+    void *dlb = static_cast<char *>(prm.dlv) + (offM + t0 * M) * el;
+    lds_to_global_sensor<TB, CH, BF16, false>(s_dv[buf], nullptr, nullptr, dvb, M, L - t0, cols_m);
+    if (sn.log_var)
+      lds_to_global_sensor<TB, CH, BF16, true>(s_dl[buf], s_l[buf], s_lf[buf], dlb, M, L - t0, cols_m);
+    else
+      lds_to_global_sensor<TB, CH, BF16, false>(s_dl[buf], nullptr, nullptr, dlb, M, L - t0, cols_m);
     for (int i = tid; i < 2 * TB * SP; i += kFusedThreads) {
       const int which = i / (TB * SP);
       const int j = (i / SP) % TB;
@@ -822,8 +959,6 @@ struct DecodeParams {
   int ou, zero_pn, qk_norm, has_clip, skip_vector, gate_act;
   float clip, ov_min, ov_max;
 };
-
-__device__ __forceinline__ float softplus_t(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
 
 __device__ __forceinline__ float activation(int act, float x) {
   if (act == kActSilu) return x / (1.0f + expf(-x));

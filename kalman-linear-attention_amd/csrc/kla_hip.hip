@@ -25,7 +25,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -289,6 +289,133 @@ bool launch_reduce_rows(const float *in, float *out, int64_t outer, int64_t G, i
   }
 }
 
+// f(std::bool_constant<a>, std::bool_constant<b>) for runtime flags a, b.
+template <class F>
+void with_flags(bool a, bool b, F &&f) {
+  if (a) {
+    if (b) f(std::true_type{}, std::true_type{});
+    else f(std::true_type{}, std::false_type{});
+  } else {
+    if (b) f(std::false_type{}, std::true_type{});
+    else f(std::false_type{}, std::false_type{});
+  }
+}
+
+// SensorIn of dense fp32 v, lambda_v [batch, steps, M].
+SensorIn dense_sensors(const float *v, const float *lambda_v, int64_t M) {
+  return SensorIn{v, lambda_v, M, M, 0, 0, 0.0f, 0.0f};
+}
+
+// Checks a kla_sensors descriptor and turns it into the kernels' SensorIn.
+int sensors_from(const char *fn, const kla_sensors *in, int64_t M, SensorIn *out) {
+  if (!in) return fail(KLA_ERR_INVALID_ARG, "%s: sensors is NULL", fn);
+  if (in->dtype != KLA_DTYPE_F32 && in->dtype != KLA_DTYPE_BF16)
+    return fail(KLA_ERR_DTYPE, "%s: unsupported sensor dtype %d", fn, in->dtype);
+  if (in->ld_v < M || in->ld_obs < M)
+    return fail(KLA_ERR_INVALID_ARG, "%s: row strides (%lld, %lld) below M = %lld", fn,
+                static_cast<long long>(in->ld_v), static_cast<long long>(in->ld_obs), static_cast<long long>(M));
+  if (in->log_var && !(in->obs_var_max > 0.0f))
+    return fail(KLA_ERR_INVALID_ARG, "%s: obs_var_max must be positive (+inf for none)", fn);
+  const size_t el = in->dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (misaligned_bytes(in->v, el) || misaligned_bytes(in->obs, el))
+    return fail(KLA_ERR_ALIGN, "%s: sensor operand not aligned to its element size", fn);
+  *out = SensorIn{in->v, in->obs, in->ld_v, in->ld_obs, in->dtype == KLA_DTYPE_BF16 ? 1 : 0,
+                  in->log_var ? 1 : 0, in->obs_var_min, in->obs_var_max};
+  return KLA_OK;
+}
+
+int fused_fwd(const char *fn, const SensorIn &sn, const float *k, const float *q, const float *a, const float *p,
+              const float *lam0, const float *eta0, float *y, float *y_var, float *lam_fin, float *eta_fin,
+              float *ck_lam, float *ck_eta, int decode_from_prior, int64_t batch, int64_t steps, int64_t M,
+              int64_t S, hipStream_t stream) {
+  int rc = check_fused_shape(fn, batch, steps, M, S);
+  if (rc != KLA_OK) return rc;
+  if (batch == 0 || M == 0 || S == 0) return KLA_OK;
+  if (!a || !p || !lam_fin || !eta_fin)
+    return fail(KLA_ERR_INVALID_ARG, "%s: a, p, lam_fin and eta_fin must not be NULL", fn);
+  if (steps > 0 && (!sn.v || !sn.lv || !k || !q || !y || !y_var))
+    return fail(KLA_ERR_INVALID_ARG, "%s: v, lambda_v, k, q, y and y_var must not be NULL", fn);
+  if ((ck_lam == nullptr) != (ck_eta == nullptr))
+    return fail(KLA_ERR_INVALID_ARG, "%s: pass both checkpoint buffers or neither", fn);
+  if (!all_aligned(4, {k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  const FusedGeom g = fused_geom(batch, steps, M, S);
+  const int64_t grid = batch * g.groups;
+  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+  const FusedFwdParams prm{sn, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta};
+  return with_sp(S, [&](auto sp) {
+    constexpr int SP = decltype(sp)::value;
+    auto run = [&](auto prior, auto bf16) {
+      hipLaunchKernelGGL((fused_kla_fwd_kernel<SP, decltype(prior)::value, decltype(bf16)::value>),
+                         dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0, stream, prm, g);
+    };
+    with_flags(decode_from_prior != 0, sn.bf16 != 0, run);
+    return hip_status(fn, hipGetLastError());
+  });
+}
+
+int fused_bwd(const char *fn, const float *dy, const float *dy_var, const float *dlam_fin, const float *deta_fin,
+              const SensorIn &sn, const float *k, const float *q, const float *a, const float *p,
+              const float *ck_lam, const float *ck_eta, void *dv, void *dlambda_v, float *dk, float *dq, float *da,
+              float *dp, float *dlam0, float *deta0, int decode_from_prior, int64_t batch, int64_t steps, int64_t M,
+              int64_t S, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+  int rc = check_fused_shape(fn, batch, steps, M, S);
+  if (rc != KLA_OK) return rc;
+  if (M == 0 || S == 0) return KLA_OK;
+  if (!a || !p || !da || !dp) return fail(KLA_ERR_INVALID_ARG, "%s: a, p, da and dp must not be NULL", fn);
+  if (steps > 0 && (!dy || !dy_var || !sn.v || !sn.lv || !k || !q || !ck_lam || !ck_eta || !dv ||
+                    !dlambda_v || !dk || !dq))
+    return fail(KLA_ERR_INVALID_ARG,
+                "%s: dy, dy_var, v, lambda_v, k, q, checkpoints, dv, dlambda_v, dk and dq must not be NULL", fn);
+  if (!all_aligned(4, {dy, dy_var, dlam_fin, deta_fin, k, q, a, p, ck_lam, ck_eta, dk, dq, da, dp, dlam0, deta0}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if (misaligned_bytes(dv, sn.bf16 ? 2 : 4) || misaligned_bytes(dlambda_v, sn.bf16 ? 2 : 4))
+    return fail(KLA_ERR_ALIGN, "%s: sensor gradient not aligned to its element size", fn);
+  const FusedGeom g = fused_geom(batch, steps, M, S);
+  if (workspace == nullptr) return fail(KLA_ERR_WORKSPACE, "%s: workspace is NULL", fn);
+  if (misaligned_bytes(workspace, 256)) return fail(KLA_ERR_WORKSPACE, "%s: workspace not 256-byte aligned", fn);
+  const size_t need = fused_workspace_floats(g) * sizeof(float);
+  if (workspace_bytes < need)
+    return fail(KLA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
+  const int64_t grid = batch * g.groups;
+  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+
+  float *ws = static_cast<float *>(workspace);
+  float *part_k = ws;
+  float *part_q = part_k + batch * steps * g.groups * S;
+  float *part_a = part_q + batch * steps * g.groups * S;
+  float *part_p = part_a + batch * M * S;
+  if (batch > 0) {
+    const FusedBwdParams prm{dy, dy_var, dlam_fin, deta_fin, sn, k, q, a, p, ck_lam, ck_eta,
+                             dv, dlambda_v, dlam0, deta0, part_k, part_q, part_a, part_p};
+    rc = with_sp(S, [&](auto sp) {
+      constexpr int SP = decltype(sp)::value;
+      auto run = [&](auto prior, auto bf16) {
+        hipLaunchKernelGGL((fused_kla_bwd_kernel<SP, decltype(prior)::value, decltype(bf16)::value>),
+                           dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0, stream, prm, g);
+      };
+      with_flags(decode_from_prior != 0, sn.bf16 != 0, run);
+      return hip_status(fn, hipGetLastError());
+    });
+    if (rc != KLA_OK) return rc;
+  }
+  // Fixed-order sums of the partials: dk, dq over channel groups; da, dp over batch.
+  auto reduce = [&](const float *in, float *out, int64_t outer, int64_t G, int64_t inner) {
+    const int64_t n = outer * inner;
+    if (n == 0) return KLA_OK;
+    if (launch_reduce_rows(in, out, outer, G, inner, stream)) return hip_status(fn, hipGetLastError());
+    hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream,
+                       in, out, outer, G, inner);
+    return hip_status(fn, hipGetLastError());
+  };
+  if (steps > 0 && batch > 0) {
+    if ((rc = reduce(part_k, dk, batch * steps, g.groups, S)) != KLA_OK) return rc;
+    if ((rc = reduce(part_q, dq, batch * steps, g.groups, S)) != KLA_OK) return rc;
+  }
+  if ((rc = reduce(part_a, da, 1, batch, M * S)) != KLA_OK) return rc;
+  return reduce(part_p, dp, 1, batch, M * S);
+}
+
 }  // namespace
 
 extern "C" {
@@ -458,31 +585,22 @@ int kla_fused_scan_fwd(const float *v, const float *lambda_v, const float *k, co
                        int decode_from_prior, int64_t batch, int64_t steps, int64_t M, int64_t S,
                        hipStream_t stream) {
   const char *fn = "kla_fused_scan_fwd";
-  int rc = check_fused_shape(fn, batch, steps, M, S);
+  if (!all_aligned(4, {v, lambda_v})) return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  return fused_fwd(fn, dense_sensors(v, lambda_v, M), k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin,
+                   ck_lam, ck_eta, decode_from_prior, batch, steps, M, S, stream);
+}
+
+int kla_fused_scan_sensors_fwd(const kla_sensors *sensors, const float *k, const float *q, const float *a,
+                               const float *p, const float *lam0, const float *eta0, float *y, float *y_var,
+                               float *lam_fin, float *eta_fin, float *ck_lam, float *ck_eta,
+                               int decode_from_prior, int64_t batch, int64_t steps, int64_t M, int64_t S,
+                               hipStream_t stream) {
+  const char *fn = "kla_fused_scan_sensors_fwd";
+  SensorIn sn;
+  const int rc = sensors_from(fn, sensors, M, &sn);
   if (rc != KLA_OK) return rc;
-  if (batch == 0 || M == 0 || S == 0) return KLA_OK;
-  if (!a || !p || !lam_fin || !eta_fin)
-    return fail(KLA_ERR_INVALID_ARG, "%s: a, p, lam_fin and eta_fin must not be NULL", fn);
-  if (steps > 0 && (!v || !lambda_v || !k || !q || !y || !y_var))
-    return fail(KLA_ERR_INVALID_ARG, "%s: v, lambda_v, k, q, y and y_var must not be NULL", fn);
-  if ((ck_lam == nullptr) != (ck_eta == nullptr))
-    return fail(KLA_ERR_INVALID_ARG, "%s: pass both checkpoint buffers or neither", fn);
-  if (!all_aligned(4, {v, lambda_v, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta}))
-    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
-  const FusedGeom g = fused_geom(batch, steps, M, S);
-  const int64_t grid = batch * g.groups;
-  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
-  const FusedFwdParams prm{v, lambda_v, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta};
-  return with_sp(S, [&](auto sp) {
-    constexpr int SP = decltype(sp)::value;
-    if (decode_from_prior)
-      hipLaunchKernelGGL((fused_kla_fwd_kernel<SP, true>), dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads),
-                         0, stream, prm, g);
-    else
-      hipLaunchKernelGGL((fused_kla_fwd_kernel<SP, false>), dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads),
-                         0, stream, prm, g);
-    return hip_status(fn, hipGetLastError());
-  });
+  return fused_fwd(fn, sn, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta,
+                   decode_from_prior, batch, steps, M, S, stream);
 }
 
 int kla_fused_scan_bwd(const float *dy, const float *dy_var, const float *dlam_fin, const float *deta_fin,
@@ -493,61 +611,25 @@ int kla_fused_scan_bwd(const float *dy, const float *dy_var, const float *dlam_f
                        int64_t M, int64_t S, void *workspace, size_t workspace_bytes,
                        hipStream_t stream) {
   const char *fn = "kla_fused_scan_bwd";
-  int rc = check_fused_shape(fn, batch, steps, M, S);
-  if (rc != KLA_OK) return rc;
-  if (M == 0 || S == 0) return KLA_OK;
-  if (!a || !p || !da || !dp) return fail(KLA_ERR_INVALID_ARG, "%s: a, p, da and dp must not be NULL", fn);
-  if (steps > 0 && (!dy || !dy_var || !v || !lambda_v || !k || !q || !ck_lam || !ck_eta || !dv ||
-                    !dlambda_v || !dk || !dq))
-    return fail(KLA_ERR_INVALID_ARG,
-                "%s: dy, dy_var, v, lambda_v, k, q, checkpoints, dv, dlambda_v, dk and dq must not be NULL", fn);
-  if (!all_aligned(4, {dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta, dv, dlambda_v,
-                       dk, dq, da, dp, dlam0, deta0}))
-    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
-  const FusedGeom g = fused_geom(batch, steps, M, S);
-  if (workspace == nullptr) return fail(KLA_ERR_WORKSPACE, "%s: workspace is NULL", fn);
-  if (misaligned_bytes(workspace, 256)) return fail(KLA_ERR_WORKSPACE, "%s: workspace not 256-byte aligned", fn);
-  const size_t need = fused_workspace_floats(g) * sizeof(float);
-  if (workspace_bytes < need)
-    return fail(KLA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
-  const int64_t grid = batch * g.groups;
-  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+  if (!all_aligned(4, {v, lambda_v})) return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  return fused_bwd(fn, dy, dy_var, dlam_fin, deta_fin, dense_sensors(v, lambda_v, M), k, q, a, p, ck_lam, ck_eta,
+                   dv, dlambda_v, dk, dq, da, dp, dlam0, deta0, decode_from_prior, batch, steps, M, S, workspace,
+                   workspace_bytes, stream);
+}
 
-  float *ws = static_cast<float *>(workspace);
-  float *part_k = ws;
-  float *part_q = part_k + batch * steps * g.groups * S;
-  float *part_a = part_q + batch * steps * g.groups * S;
-  float *part_p = part_a + batch * M * S;
-  if (batch > 0) {
-    const FusedBwdParams prm{dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta,
-                             dv, dlambda_v, dlam0, deta0, part_k, part_q, part_a, part_p};
-    rc = with_sp(S, [&](auto sp) {
-      constexpr int SP = decltype(sp)::value;
-      if (decode_from_prior)
-        hipLaunchKernelGGL((fused_kla_bwd_kernel<SP, true>), dim3(static_cast<uint32_t>(grid)),
-                           dim3(kFusedThreads), 0, stream, prm, g);
-      else
-        hipLaunchKernelGGL((fused_kla_bwd_kernel<SP, false>), dim3(static_cast<uint32_t>(grid)),
-                           dim3(kFusedThreads), 0, stream, prm, g);
-      return hip_status(fn, hipGetLastError());
-    });
-    if (rc != KLA_OK) return rc;
-  }
-  // Fixed-order sums of the partials: dk, dq over channel groups; da, dp over batch.
-  auto reduce = [&](const float *in, float *out, int64_t outer, int64_t G, int64_t inner) {
-    const int64_t n = outer * inner;
-    if (n == 0) return KLA_OK;
-    if (launch_reduce_rows(in, out, outer, G, inner, stream)) return hip_status(fn, hipGetLastError());
-    hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream,
-                       in, out, outer, G, inner);
-    return hip_status(fn, hipGetLastError());
-  };
-  if (steps > 0 && batch > 0) {
-    if ((rc = reduce(part_k, dk, batch * steps, g.groups, S)) != KLA_OK) return rc;
-    if ((rc = reduce(part_q, dq, batch * steps, g.groups, S)) != KLA_OK) return rc;
-  }
-  if ((rc = reduce(part_a, da, 1, batch, M * S)) != KLA_OK) return rc;
-  return reduce(part_p, dp, 1, batch, M * S);
+int kla_fused_scan_sensors_bwd(const float *dy, const float *dy_var, const float *dlam_fin,
+                               const float *deta_fin, const kla_sensors *sensors, const float *k,
+                               const float *q, const float *a, const float *p, const float *ck_lam,
+                               const float *ck_eta, void *dv, void *dobs, float *dk, float *dq, float *da,
+                               float *dp, float *dlam0, float *deta0, int decode_from_prior, int64_t batch,
+                               int64_t steps, int64_t M, int64_t S, void *workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+  const char *fn = "kla_fused_scan_sensors_bwd";
+  SensorIn sn;
+  const int rc = sensors_from(fn, sensors, M, &sn);
+  if (rc != KLA_OK) return rc;
+  return fused_bwd(fn, dy, dy_var, dlam_fin, deta_fin, sn, k, q, a, p, ck_lam, ck_eta, dv, dobs, dk, dq, da, dp,
+                   dlam0, deta0, decode_from_prior, batch, steps, M, S, workspace, workspace_bytes, stream);
 }
 
 int kla_step_fwd(const float *v, const float *lambda_v, const float *k, const float *q, const float *a,

@@ -136,8 +136,9 @@ class KLALayer(nn.Module):
 
     # ----------------------------------------------------------- projections
 
-    def _project_sensors(self, z: torch.Tensor):
-        """z [B, L, M] -> (v, lambda_v [B, L, M], k, q [B, L, S]), all float32."""
+    def _project_sensors_raw(self, z: torch.Tensor):
+        """z [B, L, M] -> (v, log sigma^2 [B, L, M] in the projection's dtype, k, q
+        [B, L, S] float32 after the norm and the clip)."""
         cfg = self.config
         S = self.d_state
         v, log_var, k, q = torch.split(self.sensor_proj(z), [self._w_value, self._w_var, S, S], dim=-1)
@@ -152,31 +153,49 @@ class KLALayer(nn.Module):
         if cfg.clip_value is not None:
             k = k.clamp(-cfg.clip_value, cfg.clip_value)
             q = q.clamp(-cfg.clip_value, cfg.clip_value)
+        return v, log_var, k.float(), q.float()
+
+    def _project_sensors(self, z: torch.Tensor):
+        """z [B, L, M] -> (v, lambda_v [B, L, M], k, q [B, L, S]), all float32."""
+        cfg = self.config
+        v, log_var, k, q = self._project_sensors_raw(z)
         obs_var = F.softplus(log_var.float()) + cfg.obs_var_min
         if cfg.obs_var_max is not None:
             obs_var = obs_var.clamp_max(cfg.obs_var_max)
-        return v.float(), 1.0 / obs_var, k.float(), q.float()
+        return v.float(), 1.0 / obs_var, k, q
 
     # ---------------------------------------------------------------- compute
 
     def _run_ssm(self, z: torch.Tensor, ssm_state: KLAState | None):
         cfg = self.config
-        v, lambda_v, k, q = self._project_sensors(z)
         a_bar, p_bar = self._compute_aq()
+        if self._sensors_on_hip(z):
+            # The fused hip scan reads v and log sigma^2 straight from the projection
+            # and forms lambda_v itself (the values _project_sensors would give).
+            from kla.ops.hip.fused import kla_scan_fused_sensors
 
-        def scan(v, lambda_v, k, q, lam0, eta0):
-            state = None if lam0 is None else KLAState(lam=lam0, eta=eta0)
-            return kla_scan(v, lambda_v, k, q, a_bar, p_bar, initial_state=state, backend=cfg.backend,
-                            scan_impl=cfg.scan_impl, mobius_impl=cfg.mobius_impl,
-                            decode_from_prior=cfg.decode_from_prior)
+            v, obs, k, q = self._project_sensors_raw(z)
+
+            def scan(v, log_var, k, q, lam0, eta0):
+                y, y_var, lam, eta = kla_scan_fused_sensors(
+                    v, log_var, k, q, a_bar, p_bar, lam0, eta0, log_var=True, obs_var_min=cfg.obs_var_min,
+                    obs_var_max=cfg.obs_var_max, decode_from_prior=cfg.decode_from_prior)
+                return y, y_var, KLAState(lam=lam, eta=eta)
+        else:
+            v, obs, k, q = self._project_sensors(z)
+
+            def scan(v, lambda_v, k, q, lam0, eta0):
+                state = None if lam0 is None else KLAState(lam=lam0, eta=eta0)
+                return kla_scan(v, lambda_v, k, q, a_bar, p_bar, initial_state=state, backend=cfg.backend,
+                                scan_impl=cfg.scan_impl, mobius_impl=cfg.mobius_impl,
+                                decode_from_prior=cfg.decode_from_prior)
 
         lam0 = ssm_state.lam if ssm_state is not None else None
         eta0 = ssm_state.eta if ssm_state is not None else None
         with torch.autocast(device_type=z.device.type, enabled=False):
             if cfg.checkpoint_ssm and torch.is_grad_enabled() and self.training:
-                return torch.utils.checkpoint.checkpoint(scan, v, lambda_v, k, q, lam0, eta0,
-                                                         use_reentrant=False)
-            return scan(v, lambda_v, k, q, lam0, eta0)
+                return torch.utils.checkpoint.checkpoint(scan, v, obs, k, q, lam0, eta0, use_reentrant=False)
+            return scan(v, obs, k, q, lam0, eta0)
 
     def _run_ssm_step(self, z: torch.Tensor, ssm_state: KLAState):
         """One-token decode, z [B, 1, M]."""
@@ -187,6 +206,18 @@ class KLALayer(nn.Module):
             y, y_var, new_state = kla_step(v[:, 0], lambda_v[:, 0], k[:, 0], q[:, 0], a_bar, p_bar, ssm_state,
                                            decode_from_prior=cfg.decode_from_prior, backend=cfg.backend)
         return y.unsqueeze(1), y_var.unsqueeze(1), new_state
+
+    def _sensors_on_hip(self, z: torch.Tensor) -> bool:
+        """Whether the sequence scan runs on the fused hip kernel with the sensor
+        read-out inside it: a backend that picks the fused scan ("hip", "hip_fused"
+        or "auto" on a ROCm GPU), d_state <= 64, a ROCm GPU."""
+        from kla.ops.kla_ops import _resolve_auto, _step_on_hip
+
+        backend = self.config.backend
+        if backend == "auto":
+            backend = _resolve_auto(z)
+        return (backend in ("hip", "hip_fused") and self.d_state <= 64 and z.dtype != torch.float64
+                and _step_on_hip(backend, z))
 
     def _decode_on_hip(self, projected: torch.Tensor) -> bool:
         """Whether a one-token step runs on the MI355X decode kernels: inference

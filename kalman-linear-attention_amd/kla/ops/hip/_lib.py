@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -49,6 +49,9 @@ _SIGNATURES = {
     "kla_fused_workspace_bytes": (ctypes.c_size_t, [_i64] * 4),
     "kla_fused_scan_fwd": (ctypes.c_int, [_p] * 14 + [ctypes.c_int] + [_i64] * 4 + [_p]),
     "kla_fused_scan_bwd": (ctypes.c_int, [_p] * 20 + [ctypes.c_int] + [_i64] * 4 + [_p, ctypes.c_size_t, _p]),
+    "kla_fused_scan_sensors_fwd": (ctypes.c_int, [_p] * 13 + [ctypes.c_int] + [_i64] * 4 + [_p]),
+    "kla_fused_scan_sensors_bwd": (ctypes.c_int, [_p] * 19 + [ctypes.c_int] + [_i64] * 4
+                                   + [_p, ctypes.c_size_t, _p]),
     "kla_step_fwd": (ctypes.c_int, [_p] * 12 + [ctypes.c_int] + [_i64] * 3 + [_p]),
     "kla_decode_step_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _p, _p, _i64] + [_p] * 10
                             + [_i64] * 3 + [_p]),
@@ -75,6 +78,21 @@ class DecodeConfig(ctypes.Structure):
         ("decode_from_prior", ctypes.c_int),
         ("gate_activation", ctypes.c_int),
         ("skip_vector", ctypes.c_int),
+    ]
+
+
+class Sensors(ctypes.Structure):
+    """kla_sensors of include/kla_hip.h."""
+
+    _fields_ = [
+        ("v", ctypes.c_void_p),
+        ("ld_v", ctypes.c_int64),
+        ("obs", ctypes.c_void_p),
+        ("ld_obs", ctypes.c_int64),
+        ("dtype", ctypes.c_int),
+        ("log_var", ctypes.c_int),
+        ("obs_var_min", ctypes.c_float),
+        ("obs_var_max", ctypes.c_float),
     ]
 
 

@@ -8,10 +8,17 @@ It is a ``torch.library`` custom op (``kla_hip::kla_scan_fused``) whose backward
 is the hand-written exact adjoint kernel (checkpoint replay), giving gradients
 for all six inputs and for the initial state, including gradients that arrive
 through the returned final state.
+
+:func:`kla_scan_fused_sensors` is the same scan fed by the layer's sensor
+projection directly (``kla_hip::kla_scan_fused_sensors``): v and log sigma^2 are
+read as the projection's strided bf16 or fp32 columns, and the precision
+lambda_v is formed inside the kernels.
 """
 
 from __future__ import annotations
 
+import ctypes
+import math
 from typing import Optional
 
 import torch
@@ -154,4 +161,178 @@ def kla_scan_fused(v, lambda_v, k, q, a, p, lam0=None, eta0=None, decode_from_pr
         t is not None and t.requires_grad for t in (v, lambda_v, k, q, a, p, lam0, eta0))
     y, y_var, lam_fin, eta_fin, _, _ = _fused_fwd_op(v, lambda_v, k, q, a, p, lam0, eta0,
                                                      bool(decode_from_prior), save)
+    return y, y_var, lam_fin, eta_fin
+
+
+# ------------------------------------------------------- sensors from the projection
+#
+# The layer's sensor read-out (reference src/kla/layers/kla_layer.py:194-231) ends
+# in v.float() and lambda_v = 1 / min(softplus(log sigma^2) + obs_var_min,
+# obs_var_max), each an elementwise pass over [B, L, M] with its own backward.
+# kla_scan_fused_sensors hands the projection's v and log sigma^2 columns to the
+# kernels as they are (bf16 or fp32, strided rows); the kernels form lambda_v
+# while staging and write dv, d log sigma^2 in the projection's dtype.
+
+
+def _sensor_rows(t: torch.Tensor) -> Optional[int]:
+    """Row stride ld of a [B, L, M] view whose element (b, t, m) sits at
+    (b * L + t) * ld + m, or None if the view is not laid out that way."""
+    B, L, M = t.shape
+    if M > 1 and t.stride(2) != 1:
+        return None
+    if L == 1:
+        ld = t.stride(0) if B > 1 else M
+    else:
+        ld = t.stride(1)
+        if B > 1 and t.stride(0) != L * ld:
+            return None
+    return ld if ld >= M else None
+
+
+def _sensor_desc(v: torch.Tensor, obs: torch.Tensor, log_var: bool, obs_var_min: float,
+                 obs_var_max: float) -> "_lib.Sensors":
+    return _lib.Sensors(v=_lib.ptr(v), ld_v=_sensor_rows(v), obs=_lib.ptr(obs), ld_obs=_sensor_rows(obs),
+                        dtype=_lib.KLA_DTYPE_BF16 if v.dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32,
+                        log_var=int(log_var), obs_var_min=obs_var_min, obs_var_max=obs_var_max)
+
+
+def _check_sensors(v, obs):
+    if v.dtype != obs.dtype or v.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"v and the precision operand must both be float32 or both bfloat16; "
+                        f"got {v.dtype} and {obs.dtype}")
+    if _sensor_rows(v) is None or _sensor_rows(obs) is None:
+        raise ValueError("sensor operands must be [B, L, M] rows with a contiguous last dimension")
+
+
+@torch.library.custom_op("kla_hip::kla_scan_fused_sensors", mutates_args=())
+def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
+                    p: torch.Tensor, lam0: Optional[torch.Tensor], eta0: Optional[torch.Tensor], log_var: bool,
+                    obs_var_min: float, obs_var_max: float, decode_from_prior: bool, save: bool
+                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(y, y_var, lam_fin, eta_fin, ck_lam, ck_eta) from strided v and log sigma^2
+    (or lambda_v) of one dtype; the checkpoints are empty unless ``save``."""
+    dev = _require_device(v, obs, k, q, a, p, lam0, eta0)
+    B, L, M, S = _check(v, obs, k, q, a, p, lam0, eta0)
+    _check_sensors(v, obs)
+    f32 = dict(dtype=_F32, device=dev)
+    y, y_var = torch.empty(B, L, M, **f32), torch.empty(B, L, M, **f32)
+    lam_fin, eta_fin = torch.empty(B, M, S, **f32), torch.empty(B, M, S, **f32)
+    n_ck = int(_lib.lib().kla_fused_checkpoints(L))
+    ck_lam = torch.empty(B, n_ck, M, S, **f32) if save else torch.empty(0, **f32)
+    ck_eta = torch.empty(B, n_ck, M, S, **f32) if save else torch.empty(0, **f32)
+    if B * M * S == 0:
+        return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
+    sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
+    pt = _lib.ptr
+    _lib.check("kla_fused_scan_sensors_fwd", _lib.lib().kla_fused_scan_sensors_fwd(
+        ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam0), pt(eta0), pt(y), pt(y_var), pt(lam_fin),
+        pt(eta_fin), pt(ck_lam) if save else None, pt(ck_eta) if save else None, int(decode_from_prior),
+        B, L, M, S, torch.cuda.current_stream(dev).cuda_stream))
+    return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
+
+
+@_sensors_fwd_op.register_fake
+def _(v, obs, k, q, a, p, lam0, eta0, log_var, obs_var_min, obs_var_max, decode_from_prior, save):
+    B, L, M = v.shape
+    S = k.shape[2]
+    n_ck = (L + 15) // 16
+    f = dict(dtype=_F32)
+    ck = k.new_empty(B, n_ck, M, S, **f) if save else k.new_empty(0, **f)
+    return (k.new_empty(B, L, M, **f), k.new_empty(B, L, M, **f), k.new_empty(B, M, S, **f),
+            k.new_empty(B, M, S, **f), ck, torch.empty_like(ck))
+
+
+@torch.library.custom_op("kla_hip::kla_scan_fused_sensors_backward", mutates_args=())
+def _sensors_bwd_op(dy: torch.Tensor, dy_var: torch.Tensor, dlam_fin: torch.Tensor, deta_fin: torch.Tensor,
+                    v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
+                    p: torch.Tensor, ck_lam: torch.Tensor, ck_eta: torch.Tensor, log_var: bool,
+                    obs_var_min: float, obs_var_max: float, decode_from_prior: bool
+                    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                               torch.Tensor, torch.Tensor]:
+    """(dv, dobs, dk, dq, da, dp, dlam0, deta0); dv and dobs dense in the sensors' dtype."""
+    dev = _require_device(dy, dy_var, dlam_fin, deta_fin, v, obs, k, q, a, p, ck_lam, ck_eta)
+    B, L, M, S = _check(v, obs, k, q, a, p, None, None)
+    _check_sensors(v, obs)
+    dv = torch.empty(B, L, M, dtype=v.dtype, device=dev)
+    dobs = torch.empty(B, L, M, dtype=v.dtype, device=dev)
+    dk, dq = torch.empty_like(k), torch.empty_like(q)
+    da, dp = torch.empty_like(a), torch.empty_like(p)
+    dlam0, deta0 = k.new_empty(B, M, S), k.new_empty(B, M, S)
+    if M * S == 0:
+        return dv, dobs, dk, dq, da, dp, dlam0, deta0
+    nbytes = int(_lib.lib().kla_fused_workspace_bytes(B, L, M, S))
+    ws, stream = _lib.scratch(nbytes, dev)
+    sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
+    pt = _lib.ptr
+    _lib.check("kla_fused_scan_sensors_bwd", _lib.lib().kla_fused_scan_sensors_bwd(
+        pt(dy), pt(dy_var), pt(dlam_fin), pt(deta_fin), ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p),
+        pt(ck_lam), pt(ck_eta), pt(dv), pt(dobs), pt(dk), pt(dq), pt(da), pt(dp), pt(dlam0), pt(deta0),
+        int(decode_from_prior), B, L, M, S, pt(ws), ws.numel(), stream))
+    return dv, dobs, dk, dq, da, dp, dlam0, deta0
+
+
+@_sensors_bwd_op.register_fake
+def _(dy, dy_var, dlam_fin, deta_fin, v, obs, k, q, a, p, ck_lam, ck_eta, log_var, obs_var_min, obs_var_max,
+      decode_from_prior):
+    B, L, M = v.shape
+    S = k.shape[2]
+    return (v.new_empty(B, L, M), v.new_empty(B, L, M), torch.empty_like(k), torch.empty_like(q),
+            torch.empty_like(a), torch.empty_like(p), k.new_empty(B, M, S), k.new_empty(B, M, S))
+
+
+def _sensors_setup(ctx, inputs, output):
+    v, obs, k, q, a, p, lam0, eta0, log_var, obs_var_min, obs_var_max, decode_from_prior, save = inputs
+    _, _, _, _, ck_lam, ck_eta = output
+    if not save:
+        raise RuntimeError("kla_scan_fused_sensors was run without checkpoints but a gradient is required")
+    ctx.opts = (log_var, obs_var_min, obs_var_max, decode_from_prior)
+    ctx.has_lam0, ctx.has_eta0 = lam0 is not None, eta0 is not None
+    ctx.save_for_backward(v, obs, k, q, a, p, ck_lam, ck_eta)
+
+
+def _sensors_backward(ctx, dy, dy_var, dlam_fin, deta_fin, _dck_lam, _dck_eta):
+    v, obs, k, q, a, p, ck_lam, ck_eta = ctx.saved_tensors
+
+    def g(t, like):
+        return torch.zeros_like(like) if t is None else t.to(_F32).contiguous()
+
+    B, L, M = v.shape
+    S = k.shape[2]
+    out = k.new_empty(B, L, M)
+    state = k.new_empty(B, M, S)
+    dv, dobs, dk, dq, da, dp, dlam0, deta0 = _sensors_bwd_op(
+        g(dy, out), g(dy_var, out), g(dlam_fin, state), g(deta_fin, state), v, obs, k, q, a, p, ck_lam, ck_eta,
+        *ctx.opts)
+    return (dv, dobs, dk, dq, da, dp, dlam0 if ctx.has_lam0 else None, deta0 if ctx.has_eta0 else None,
+            None, None, None, None, None)
+
+
+_sensors_fwd_op.register_autograd(_sensors_backward, setup_context=_sensors_setup)
+
+
+def kla_scan_fused_sensors(v, obs, k, q, a, p, lam0=None, eta0=None, *, log_var: bool = True,
+                           obs_var_min: float = 1e-4, obs_var_max: Optional[float] = None,
+                           decode_from_prior: bool = False):
+    """(y, y_var, lam_fin, eta_fin) of the KLA scan with the layer's sensor read-out fused in.
+
+    v and obs are [B, L, M] -- views such as column slices of the sensor
+    projection are read in place. With ``log_var`` obs is log sigma^2 and
+    lambda_v = 1 / min(softplus(obs) + obs_var_min, obs_var_max) is formed in
+    the kernel, as KLALayer._project_sensors forms it (reference
+    kla_layer.py:224-230); otherwise obs is lambda_v. bf16 sensors stay bf16 and
+    their gradients come back in bf16; fp32 otherwise. k, q, a, p and the state
+    are computed in fp32.
+    """
+    if v.dtype != obs.dtype or v.dtype not in (torch.float32, torch.bfloat16):
+        v, obs = v.float(), obs.float()
+    if _sensor_rows(v) is None:
+        v = v.contiguous()
+    if _sensor_rows(obs) is None:
+        obs = obs.contiguous()
+    k, q, a, p, lam0, eta0 = (_f32(t) for t in (k, q, a, p, lam0, eta0))
+    save = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (v, obs, k, q, a, p, lam0, eta0))
+    ov_max = math.inf if obs_var_max is None else float(obs_var_max)
+    y, y_var, lam_fin, eta_fin, _, _ = _sensors_fwd_op(v, obs, k, q, a, p, lam0, eta0, bool(log_var),
+                                                       float(obs_var_min), ov_max, bool(decode_from_prior), save)
     return y, y_var, lam_fin, eta_fin

@@ -231,3 +231,65 @@ def test_decode_and_conv_step_validation(lib):
     assert conv(st=None) == _lib.KLA_ERR_INVALID_ARG
     assert conv(w=ODD) == _lib.KLA_ERR_ALIGN
     assert conv(shape=(0, 8, 4), x=None) == _lib.KLA_OK
+
+
+def test_fused_sensors_validation(lib):
+    P = ALIGNED
+    shape = (2, 5, 6, 16)
+
+    def sensors(**kw):
+        a = dict(v=P, ld_v=10, obs=P, ld_obs=10, dtype=_lib.KLA_DTYPE_BF16, log_var=1, obs_var_min=1e-4,
+                 obs_var_max=float("inf"))
+        a.update(kw)
+        return _lib.Sensors(**a)
+
+    def fwd(sn, k=P, shape=shape):
+        return lib.kla_fused_scan_sensors_fwd(ctypes.byref(sn) if sn is not None else None, k, P, P, P, None, None,
+                                              P, P, P, P, None, None, 0, *shape, None)
+
+    assert fwd(None) == _lib.KLA_ERR_INVALID_ARG
+    assert "sensors is NULL" in err(lib)
+    assert fwd(sensors(dtype=7)) == _lib.KLA_ERR_DTYPE
+    assert fwd(sensors(ld_v=5)) == _lib.KLA_ERR_INVALID_ARG
+    assert "row strides" in err(lib)
+    assert fwd(sensors(obs_var_max=0.0)) == _lib.KLA_ERR_INVALID_ARG
+    assert fwd(sensors(v=P + 1)) == _lib.KLA_ERR_ALIGN
+    assert fwd(sensors(v=ODD, dtype=_lib.KLA_DTYPE_F32)) == _lib.KLA_ERR_ALIGN
+    assert fwd(sensors(v=None)) == _lib.KLA_ERR_INVALID_ARG
+    assert fwd(sensors(), k=ODD) == _lib.KLA_ERR_ALIGN
+    assert fwd(sensors(), shape=(2, 5, 6, 65)) == _lib.KLA_ERR_INVALID_ARG
+    assert fwd(sensors(), shape=(0, 5, 6, 16)) == _lib.KLA_OK
+
+    n = lib.kla_fused_workspace_bytes(*shape)
+
+    def bwd(sn, dv=P, ws=WS, nbytes=n):
+        return lib.kla_fused_scan_sensors_bwd(P, P, None, None, ctypes.byref(sn) if sn is not None else None,
+                                              P, P, P, P, P, P, dv, P, P, P, P, P, None, None, 0, *shape, ws,
+                                              nbytes, None)
+
+    assert bwd(None) == _lib.KLA_ERR_INVALID_ARG
+    assert bwd(sensors(), dv=P + 1) == _lib.KLA_ERR_ALIGN
+    assert "sensor gradient" in err(lib)
+    assert bwd(sensors(dtype=_lib.KLA_DTYPE_F32), dv=ODD) == _lib.KLA_ERR_ALIGN
+    assert bwd(sensors(), dv=None) == _lib.KLA_ERR_INVALID_ARG
+    assert bwd(sensors(), ws=None) == _lib.KLA_ERR_WORKSPACE
+    assert bwd(sensors(), nbytes=n - 4) == _lib.KLA_ERR_WORKSPACE
+
+
+def test_sensor_row_layouts():
+    """Which [B, L, M] views the fused-sensor kernels read in place: rows of one
+    stride ld >= M with element (b, t, m) at (b * L + t) * ld + m."""
+    import torch
+
+    from kla.ops.hip.fused import _sensor_rows
+
+    proj = torch.zeros(3, 7, 20)
+    assert _sensor_rows(proj[..., :6]) == 20
+    assert _sensor_rows(proj[..., 7:13]) == 20
+    assert _sensor_rows(torch.zeros(3, 7, 6)) == 6
+    assert _sensor_rows(proj[:, :1, :6]) == 140          # one step: the batch stride is the row stride
+    assert _sensor_rows(proj[:1, :, :6]) == 20
+    assert _sensor_rows(proj[:1, :1, :6]) == 6
+    assert _sensor_rows(proj[:, :5, :6]) is None          # batch stride 140 != 5 * 20
+    assert _sensor_rows(proj[..., :6].transpose(0, 1).contiguous().transpose(0, 1)) is None
+    assert _sensor_rows(proj.transpose(1, 2)[..., :6]) is None

@@ -603,3 +603,160 @@ def test_layer_conv_on_hip_matches_torch_conv(cuda):
     check("y", outs[0][0], outs[1][0].cpu().numpy(), rtol=2e-5, atol=2e-6)
     for n in outs[0][1]:
         check("d" + n, outs[0][1][n], outs[1][1][n].cpu().numpy(), rtol=5e-5, atol=5e-6)
+
+
+# ------------------------------------------- sensor read-out fused into the scan
+
+
+def _projection(B, L, M, S, seed, dtype=torch.float32, extra=3):
+    """A [B, L, P] projection with v and log sigma^2 as strided column slices."""
+    g = torch.Generator().manual_seed(seed)
+    proj = torch.randn(B, L, 2 * M + extra, generator=g)
+    proj[..., M + 1:2 * M + 1] *= 2.0   # log sigma^2 spread over the clamp
+    return proj.to(dtype)
+
+
+def _views(proj, M):
+    return proj[..., :M], proj[..., M + 1:2 * M + 1]
+
+
+@pytest.mark.parametrize("obs_var_max", [None, 1.5])
+@pytest.mark.parametrize("decode_from_prior", [False, True])
+@pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 150, 20, 16), (3, 1, 7, 4), (1, 70, 9, 32)])
+def test_fused_sensors_match_float64_autograd(cuda, shape, decode_from_prior, obs_var_max):
+    """kla_scan_fused_sensors on strided fp32 column slices of a projection: outputs
+    and every gradient (through the projection, so the untouched columns must get
+    zeros) against float64 autograd of the layer's read-out tail, softplus, clamp
+    and reciprocal (reference kla_layer.py:224-230), feeding oracle.torch_ref's
+    filter."""
+    from kla.ops.hip.fused import kla_scan_fused_sensors
+    import torch.nn.functional as F
+
+    B, L, M, S = shape
+    ov_min = 1e-4
+    _, _, k, q, a, p = make_inputs(B, L, M, S, seed=7)
+    st = random_state(B, M, S)
+    proj = _projection(B, L, M, S, seed=8)
+    g = torch.Generator().manual_seed(5)
+    wy, wv = torch.randn(B, L, M, generator=g), torch.randn(B, L, M, generator=g)
+    wl, we = torch.randn(B, M, S, generator=g), torch.randn(B, M, S, generator=g)
+
+    def loss(y, y_var, lam, eta):
+        w = [t.to(device=y.device, dtype=y.dtype) for t in (wy, wv, wl, we)]
+        return (w[0] * y).sum() + (w[1] * y_var).sum() + (w[2] * lam).sum() + (w[3] * eta).sum()
+
+    xs = [t.double().requires_grad_(True) for t in (proj, k, q, a, p, st.lam, st.eta)]
+    v64, lv64 = _views(xs[0], M)
+    obs = F.softplus(lv64) + ov_min
+    if obs_var_max is not None:
+        obs = obs.clamp_max(obs_var_max)
+    ref = torch_ref.kla_scan_torch(v64, 1.0 / obs, *xs[1:], decode_from_prior=decode_from_prior)
+    loss(*ref).backward()
+
+    gs = [t.to(cuda).requires_grad_(True) for t in (proj, k, q, a, p, st.lam, st.eta)]
+    v, lv = _views(gs[0], M)
+    out = kla_scan_fused_sensors(v, lv, *gs[1:], log_var=True, obs_var_min=ov_min, obs_var_max=obs_var_max,
+                                 decode_from_prior=decode_from_prior)
+    for name, got, want in zip(("y", "y_var", "lam", "eta"), out, ref):
+        check(name, got, want.detach().numpy())
+    loss(*out).backward()
+    for name, got, want in zip(("proj", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
+        check("d" + name, got.grad, want.grad.numpy())
+    assert not gs[0].grad[..., M].any() and not gs[0].grad[..., 2 * M + 1:].any()
+
+
+@pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 33, 12, 64)])
+def test_fused_sensors_bf16_equal_fp32_of_the_same_values(cuda, shape):
+    """bf16 sensors are widened exactly and the arithmetic is the fp32 path's, so
+    every fp32 output and gradient equals the fp32 run on the widened values bit
+    for bit, and dv, d log sigma^2 are those of the fp32 run rounded to nearest
+    even (what autograd's cast back to bf16 gives)."""
+    from kla.ops.hip.fused import kla_scan_fused_sensors
+
+    B, L, M, S = shape
+    _, _, k, q, a, p = make_inputs(B, L, M, S, seed=9)
+    proj16 = _projection(B, L, M, S, seed=10, dtype=torch.bfloat16).to(cuda)
+    proj32 = proj16.float()
+    runs = []
+    for proj in (proj16, proj32):
+        pj = proj.clone().requires_grad_(True)
+        xs = [t.to(cuda).requires_grad_(True) for t in (k, q, a, p)]
+        v, lv = _views(pj, M)
+        y, y_var, lam, eta = kla_scan_fused_sensors(v, lv, *xs, obs_var_min=1e-3, obs_var_max=3.0)
+        g = torch.Generator().manual_seed(11)
+        w = [torch.randn(t.shape, generator=g).to(cuda) for t in (y, y_var, lam, eta)]
+        sum((wi * o).sum() for wi, o in zip(w, (y, y_var, lam, eta))).backward()
+        runs.append(((y, y_var, lam, eta), pj.grad, [t.grad for t in xs]))
+    for got, want in zip(runs[0][0], runs[1][0]):
+        assert torch.equal(got, want)
+    for got, want in zip(runs[0][2], runs[1][2]):
+        assert torch.equal(got, want)
+    assert runs[0][1].dtype == torch.bfloat16
+    assert torch.equal(runs[0][1], runs[1][1].to(torch.bfloat16))
+
+
+def test_fused_sensors_without_log_var_equal_the_fused_scan(cuda):
+    """log_var=False takes lambda_v itself: the same numbers as kla_scan_fused."""
+    from kla.ops.hip.fused import kla_scan_fused, kla_scan_fused_sensors
+
+    ins = [t.to(cuda) for t in make_inputs(2, 45, 10, 8, seed=12)]
+    got = kla_scan_fused_sensors(*ins, log_var=False)
+    want = kla_scan_fused(*ins)
+    for a_, b_ in zip(got, want):
+        assert torch.equal(a_, b_)
+
+
+def test_fused_sensors_reject_bad_layouts(cuda):
+    from kla.ops.hip import _lib
+    from kla.ops.hip.fused import _sensors_fwd_op
+
+    B, L, M, S = 2, 8, 4, 4
+    ins = [t.to(cuda) for t in make_inputs(B, L, M, S)]
+    with pytest.raises(TypeError):
+        _sensors_fwd_op(ins[0], ins[1].to(torch.bfloat16), *ins[2:], None, None, True, 1e-4, float("inf"), False,
+                        False)
+    with pytest.raises(ValueError):
+        _sensors_fwd_op(ins[0].transpose(1, 2).contiguous().transpose(1, 2), ins[1], *ins[2:], None, None, True,
+                        1e-4, float("inf"), False, False)
+    with pytest.raises(_lib.KLAHipError):
+        _sensors_fwd_op(ins[0], ins[1], *ins[2:], None, None, True, 1e-4, 0.0, False, False)
+
+
+LAYER_SENSOR_CASES = {
+    "default": (48, dict(d_state=8)),
+    "conv_value_dt_var": (40, dict(d_state=16, value_rank="conv", var_rank="dt", obs_var_max=2.0)),
+    "lowrank_clip_prior": (32, dict(d_state=12, value_rank=6, var_rank=5, clip_value=0.5, decode_from_prior=True,
+                                    qk_norm=False)),
+    "checkpointed": (48, dict(d_state=8, checkpoint_ssm=True)),
+}
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+@pytest.mark.parametrize("tag", sorted(LAYER_SENSOR_CASES))
+def test_layer_sensors_on_hip_match_torch_readout(cuda, tag, autocast):
+    """A KLALayer training step whose scan reads the projection directly equals the
+    same layer with the torch read-out in front of the fused scan: output, the
+    final state and every parameter gradient, in fp32 and under bf16 autocast."""
+    import copy
+
+    d_model, cfg = LAYER_SENSOR_CASES[tag]
+    torch.manual_seed(0)
+    layer = KLALayer(d_model, KLAConfig(backend="hip", **cfg)).to(cuda).train()
+    other = copy.deepcopy(layer)
+    other._sensors_on_hip = lambda z: False
+    assert layer._sensors_on_hip(torch.empty(1, device=cuda))
+    x = torch.randn(2, 70, d_model, generator=torch.Generator().manual_seed(1)).to(cuda)
+    outs = []
+    for m in (layer, other):
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            y, st = m(x, state=m.init_state(2, device=cuda))
+        y = y[0] if isinstance(y, tuple) else y
+        (y.float().square().mean() + st.ssm.lam.mean() + st.ssm.eta.square().mean()).backward()
+        outs.append((y.detach().float(), st.ssm.lam.detach(), st.ssm.eta.detach(),
+                     {n: p.grad.detach().clone() for n, p in m.named_parameters() if p.grad is not None}))
+    tol = dict(rtol=1e-2, atol=1e-3) if autocast else dict(rtol=5e-5, atol=5e-6)
+    for name, i in (("y", 0), ("lam", 1), ("eta", 2)):
+        check(name, outs[0][i], outs[1][i].cpu().numpy(), **tol)
+    assert outs[0][3].keys() == outs[1][3].keys()
+    for n in outs[0][3]:
+        check("d" + n, outs[0][3][n], outs[1][3][n].cpu().numpy(), **tol)
