@@ -137,6 +137,7 @@ int kla_affine_scan_bwd(int dtype, const void *dh, const void *g, const void *h,
  *   var = a2 var + p'); y = sum_s q mean, y_var = sum_s q^2 var.
  * ck_lam / ck_eta: [batch, kla_fused_checkpoints(steps), M, S] buffers the forward
  * fills for the backward, or both NULL when no backward will follow.
+ * y_var may be NULL: the variance read-out is then skipped (a cheaper kernel).
  * Replaces kla_scan_torch (src/kla/ops/kla_ops.py:188-290) / the fused kernels
  * (src/kla/ops/kernels/cuda/v2_2/kla_matmul_fwd_kernel.cuh:89-476,
  * src/kla/ops/kernels/mps/fused_kla_scan.metal:53-131).
@@ -154,7 +155,7 @@ size_t kla_fused_workspace_bytes(int64_t batch, int64_t steps, int64_t M, int64_
 
 /*
  * Exact adjoint of kla_fused_scan_fwd (checkpoint replay). Inputs: the output
- * gradients dy, dy_var and (optional, NULL = 0) dlam_fin, deta_fin, the forward's
+ * gradients dy and (optional, NULL = 0) dy_var, dlam_fin, deta_fin, the forward's
  * inputs and its checkpoints. Outputs: dv, dlambda_v [batch, steps, M]; dk, dq
  * [batch, steps, S]; da, dp [M, S]; dlam0, deta0 [batch, M, S] (NULL to skip).
  * Every output is written (not accumulated); sums over channels and batch run in

@@ -394,7 +394,9 @@ __device__ __forceinline__ void to_precision(TileRegs<TB, W> &r, const SensorIn 
     r.x[i] = sensor_precision(r.x[i], sn.ov_min, sn.ov_max, f ? &f->x[i] : nullptr);
 }
 
-template <int SP, bool PRIOR, bool BF16>
+// VAR: y_var is produced (prm.yvar non-NULL); without it the variance read-out
+// is skipped altogether.
+template <int SP, bool PRIOR, bool BF16, bool VAR>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int TB = kFusedTB;
@@ -423,7 +425,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
   const float *kbase = prm.k + ln.b * L * S;
   const float *qbase = prm.q + ln.b * L * S;
   float *ybase = prm.y + ln.b * L * M + m0;
-  float *yvbase = prm.yvar + ln.b * L * M + m0;
+  float *yvbase = VAR ? prm.yvar + ln.b * L * M + m0 : nullptr;
 
   TileRegs<TB, CH> rv, rl;
   TileRegs<TB, SP> rk, rq;
@@ -461,7 +463,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
     if (blk + 1 < nblk) load(t0 + TB);
     if (blk > 0) {
       lds_to_global<TB, CH>(s_y[cur ^ 1], ybase + (t0 - TB) * M, M, TB, cols_m);
-      lds_to_global<TB, CH>(s_yv[cur ^ 1], yvbase + (t0 - TB) * M, M, TB, cols_m);
+      if constexpr (VAR) lds_to_global<TB, CH>(s_yv[cur ^ 1], yvbase + (t0 - TB) * M, M, TB, cols_m);
     }
     // The read-out terms of a kCkpt-step half of the block, summed over s after
     // the half (transpose_sum) when a channel's lanes fit one 16-lane row.
@@ -480,13 +482,13 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
       const float qq = s_q[cur][ln.s][j];
       if constexpr (kTr) {
         yw[jj] = qq * mean;
-        vw[jj] = (qq * qq) * vo;
+        if constexpr (VAR) vw[jj] = (qq * qq) * vo;
       } else {
         const float ys = group_sum<SP>(qq * mean);
-        const float vs = group_sum<SP>((qq * qq) * vo);
-        if (ln.s == 0) {
-          s_y[cur][c][j] = ys;
-          s_yv[cur][c][j] = vs;
+        if (ln.s == 0) s_y[cur][c][j] = ys;
+        if constexpr (VAR) {
+          const float vs = group_sum<SP>((qq * qq) * vo);
+          if (ln.s == 0) s_yv[cur][c][j] = vs;
         }
       }
     };
@@ -511,7 +513,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
               step(h * kCkpt + j, j);
             } else {
               yw[j] = 0.0f;
-              vw[j] = 0.0f;
+              if constexpr (VAR) vw[j] = 0.0f;
             }
           }
         } else {
@@ -520,11 +522,11 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
         }
         if constexpr (kTr) {
           transpose_sum<SP, kCkpt>(yw, lane);
-          transpose_sum<SP, kCkpt>(vw, lane);
+          if constexpr (VAR) transpose_sum<SP, kCkpt>(vw, lane);
 #pragma unroll
           for (int r = 0; r < kCkpt / SP; ++r) {
             s_y[cur][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = yw[r];
-            s_yv[cur][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = vw[r];
+            if constexpr (VAR) s_yv[cur][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = vw[r];
           }
         }
       }
@@ -536,7 +538,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
     const int last = static_cast<int>((nblk - 1) & 1);
     const int64_t t0 = (nblk - 1) * TB;
     lds_to_global<TB, CH>(s_y[last], ybase + t0 * M, M, L - t0, cols_m);
-    lds_to_global<TB, CH>(s_yv[last], yvbase + t0 * M, M, L - t0, cols_m);
+    if constexpr (VAR) lds_to_global<TB, CH>(s_yv[last], yvbase + t0 * M, M, L - t0, cols_m);
   }
   if (ln.active) {
     prm.lam_fin[bms] = lam;
@@ -546,7 +548,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
 
 // ================================================================ backward
 
-template <int SP, bool PRIOR, bool BF16>
+// VAR: a y_var gradient is given (prm.dyvar non-NULL); without it the
+// variance read-out's adjoint is skipped (a zero gradient).
+template <int SP, bool PRIOR, bool BF16, bool VAR>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int NW = kFusedThreads / kWave;
@@ -589,7 +593,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     tile_load_sensor<TB, CH, BF16>(rv, sensor_at<BF16>(sn.v, ln.b * L + t0, m0, sn.ld_v), sn.ld_v, rows, cols_m);
     tile_load_sensor<TB, CH, BF16>(rl, sensor_at<BF16>(sn.lv, ln.b * L + t0, m0, sn.ld_lv), sn.ld_lv, rows, cols_m);
     tile_load<TB, CH>(rdy, prm.dy + offM + t0 * M, M, rows, cols_m);
-    tile_load<TB, CH>(rdyv, prm.dyvar + offM + t0 * M, M, rows, cols_m);
+    if constexpr (VAR) tile_load<TB, CH>(rdyv, prm.dyvar + offM + t0 * M, M, rows, cols_m);
     tile_load<TB, SP>(rk, prm.k + offS + t0 * S, S, rows, S);
     tile_load<TB, SP>(rq, prm.q + offS + t0 * S, S, rows, S);
   };
@@ -604,7 +608,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     }
     tile_to_lds<TB, CH>(rl, s_l[buf]);
     tile_to_lds<TB, CH>(rdy, s_dy[buf]);
-    tile_to_lds<TB, CH>(rdyv, s_dyv[buf]);
+    if constexpr (VAR) tile_to_lds<TB, CH>(rdyv, s_dyv[buf]);
     tile_to_lds<TB, SP>(rk, s_k[buf]);
     tile_to_lds<TB, SP>(rq, s_q[buf]);
   };
@@ -693,7 +697,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       }
       if (t < L) {
         const float vv = s_v[cur][c][j], sig = s_l[cur][c][j];
-        const float dy = s_dy[cur][c][j], dyv = s_dyv[cur][c][j];
+        const float dy = s_dy[cur][c][j];
         const float kk = s_k[cur][ln.s][j], qq = s_q[cur][ln.s][j];
         const float lp = lh[j], ep = eh[j];
         const float lam_t = lh[j + 1], eta_t = eh[j + 1];
@@ -709,19 +713,30 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         const float var_o = PRIOR ? a2 * var + pp : var;
 
         // read-out
-        const float dmo = dy * qq, dvo = dyv * (qq * qq);
-        dq_c = dy * mean_o + dyv * 2.0f * qq * var_o;
-        float dmean = dmo, dvar = dvo;
+        const float dmo = dy * qq;
+        float dmean = dmo;
         if (PRIOR) {
           dmean = dmo * a_s;
-          dvar = dvo * a2;
           blk_a += dmo * mean;
-          blk_a2 += dvo * var;
-          blk_p += dvo;
+        }
+        float dvar_tot;
+        if constexpr (VAR) {
+          const float dyv = s_dyv[cur][c][j];
+          const float dvo = dyv * (qq * qq);
+          dq_c = dy * mean_o + dyv * 2.0f * qq * var_o;
+          float dvar = dvo;
+          if (PRIOR) {
+            dvar = dvo * a2;
+            blk_a2 += dvo * var;
+            blk_p += dvo;
+          }
+          dvar_tot = dvar + dmean * eta_t;
+        } else {
+          dq_c = dy * mean_o;
+          dvar_tot = dmean * eta_t;
         }
         // mean = eta var, var = 1/max(lam, EPS)
         const float ge_t = ge + dmean * var;
-        const float dvar_tot = dvar + dmean * eta_t;
         const float gl_t = gl + ((lam_t >= kEps) ? -dvar_tot * var * var : 0.0f);
         // eta_t = alpha eta' + r
         const float dalpha = ge_t * ep;

@@ -25,7 +25,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 4;
+constexpr int kAbiVersion = 5;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -289,16 +289,18 @@ bool launch_reduce_rows(const float *in, float *out, int64_t outer, int64_t G, i
   }
 }
 
-// f(std::bool_constant<a>, std::bool_constant<b>) for runtime flags a, b.
+// f(std::bool_constant<b>...) for runtime flags b...: one instantiation per combination.
 template <class F>
-void with_flags(bool a, bool b, F &&f) {
-  if (a) {
-    if (b) f(std::true_type{}, std::true_type{});
-    else f(std::true_type{}, std::false_type{});
-  } else {
-    if (b) f(std::false_type{}, std::true_type{});
-    else f(std::false_type{}, std::false_type{});
-  }
+void with_flags(F &&f) {
+  f();
+}
+
+template <class F, class... Bs>
+void with_flags(F &&f, bool b, Bs... rest) {
+  if (b)
+    with_flags([&](auto... c) { f(std::true_type{}, c...); }, rest...);
+  else
+    with_flags([&](auto... c) { f(std::false_type{}, c...); }, rest...);
 }
 
 // SensorIn of dense fp32 v, lambda_v [batch, steps, M].
@@ -333,8 +335,8 @@ int fused_fwd(const char *fn, const SensorIn &sn, const float *k, const float *q
   if (batch == 0 || M == 0 || S == 0) return KLA_OK;
   if (!a || !p || !lam_fin || !eta_fin)
     return fail(KLA_ERR_INVALID_ARG, "%s: a, p, lam_fin and eta_fin must not be NULL", fn);
-  if (steps > 0 && (!sn.v || !sn.lv || !k || !q || !y || !y_var))
-    return fail(KLA_ERR_INVALID_ARG, "%s: v, lambda_v, k, q, y and y_var must not be NULL", fn);
+  if (steps > 0 && (!sn.v || !sn.lv || !k || !q || !y))
+    return fail(KLA_ERR_INVALID_ARG, "%s: v, lambda_v, k, q and y must not be NULL", fn);
   if ((ck_lam == nullptr) != (ck_eta == nullptr))
     return fail(KLA_ERR_INVALID_ARG, "%s: pass both checkpoint buffers or neither", fn);
   if (!all_aligned(4, {k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta}))
@@ -345,11 +347,12 @@ int fused_fwd(const char *fn, const SensorIn &sn, const float *k, const float *q
   const FusedFwdParams prm{sn, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta};
   return with_sp(S, [&](auto sp) {
     constexpr int SP = decltype(sp)::value;
-    auto run = [&](auto prior, auto bf16) {
-      hipLaunchKernelGGL((fused_kla_fwd_kernel<SP, decltype(prior)::value, decltype(bf16)::value>),
-                         dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0, stream, prm, g);
+    auto run = [&](auto prior, auto bf16, auto var) {
+      hipLaunchKernelGGL(
+          (fused_kla_fwd_kernel<SP, decltype(prior)::value, decltype(bf16)::value, decltype(var)::value>),
+          dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0, stream, prm, g);
     };
-    with_flags(decode_from_prior != 0, sn.bf16 != 0, run);
+    with_flags(run, decode_from_prior != 0, sn.bf16 != 0, y_var != nullptr);
     return hip_status(fn, hipGetLastError());
   });
 }
@@ -363,10 +366,9 @@ int fused_bwd(const char *fn, const float *dy, const float *dy_var, const float 
   if (rc != KLA_OK) return rc;
   if (M == 0 || S == 0) return KLA_OK;
   if (!a || !p || !da || !dp) return fail(KLA_ERR_INVALID_ARG, "%s: a, p, da and dp must not be NULL", fn);
-  if (steps > 0 && (!dy || !dy_var || !sn.v || !sn.lv || !k || !q || !ck_lam || !ck_eta || !dv ||
-                    !dlambda_v || !dk || !dq))
+  if (steps > 0 && (!dy || !sn.v || !sn.lv || !k || !q || !ck_lam || !ck_eta || !dv || !dlambda_v || !dk || !dq))
     return fail(KLA_ERR_INVALID_ARG,
-                "%s: dy, dy_var, v, lambda_v, k, q, checkpoints, dv, dlambda_v, dk and dq must not be NULL", fn);
+                "%s: dy, v, lambda_v, k, q, checkpoints, dv, dlambda_v, dk and dq must not be NULL", fn);
   if (!all_aligned(4, {dy, dy_var, dlam_fin, deta_fin, k, q, a, p, ck_lam, ck_eta, dk, dq, da, dp, dlam0, deta0}))
     return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
   if (misaligned_bytes(dv, sn.bf16 ? 2 : 4) || misaligned_bytes(dlambda_v, sn.bf16 ? 2 : 4))
@@ -390,11 +392,12 @@ int fused_bwd(const char *fn, const float *dy, const float *dy_var, const float 
                              dv, dlambda_v, dlam0, deta0, part_k, part_q, part_a, part_p};
     rc = with_sp(S, [&](auto sp) {
       constexpr int SP = decltype(sp)::value;
-      auto run = [&](auto prior, auto bf16) {
-        hipLaunchKernelGGL((fused_kla_bwd_kernel<SP, decltype(prior)::value, decltype(bf16)::value>),
-                           dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0, stream, prm, g);
+      auto run = [&](auto prior, auto bf16, auto var) {
+        hipLaunchKernelGGL(
+            (fused_kla_bwd_kernel<SP, decltype(prior)::value, decltype(bf16)::value, decltype(var)::value>),
+            dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0, stream, prm, g);
       };
-      with_flags(decode_from_prior != 0, sn.bf16 != 0, run);
+      with_flags(run, decode_from_prior != 0, sn.bf16 != 0, dy_var != nullptr);
       return hip_status(fn, hipGetLastError());
     });
     if (rc != KLA_OK) return rc;

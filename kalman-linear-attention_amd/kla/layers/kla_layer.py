@@ -179,7 +179,8 @@ class KLALayer(nn.Module):
             def scan(v, log_var, k, q, lam0, eta0):
                 y, y_var, lam, eta = kla_scan_fused_sensors(
                     v, log_var, k, q, a_bar, p_bar, lam0, eta0, log_var=True, obs_var_min=cfg.obs_var_min,
-                    obs_var_max=cfg.obs_var_max, decode_from_prior=cfg.decode_from_prior)
+                    obs_var_max=cfg.obs_var_max, decode_from_prior=cfg.decode_from_prior,
+                    with_var=cfg.return_variance)
                 return y, y_var, KLAState(lam=lam, eta=eta)
         else:
             v, obs, k, q = self._project_sensors(z)
@@ -299,15 +300,18 @@ class KLALayer(nn.Module):
                 y, y_var, ssm_state = self._run_ssm_step(z, ssm_state)
             else:
                 y, y_var, ssm_state = self._run_ssm(z, ssm_state)
+            # y_var only reaches the output with return_variance; otherwise its
+            # tail is skipped (the fused hip scan does not even compute it).
             y = y.to(x.dtype)
-            y_var = y_var.to(x.dtype)
+            y_var = y_var.to(x.dtype) if cfg.return_variance else None
 
             if self.lambda_skip is not None:
                 y = y + self.lambda_skip * residual
             if gate is not None:
                 g = self.gate_act(gate)
                 y = y * g
-                y_var = y_var * g.pow(2)
+                if y_var is not None:
+                    y_var = y_var * g.pow(2)
 
         out = self.out_proj(y)
         result = (out, F.linear(y_var, self.out_proj.weight.pow(2))) if cfg.return_variance else out

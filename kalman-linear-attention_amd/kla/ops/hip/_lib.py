@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1

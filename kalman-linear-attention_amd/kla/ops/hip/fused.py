@@ -88,12 +88,15 @@ def _(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save):
 
 
 @torch.library.custom_op("kla_hip::kla_scan_fused_backward", mutates_args=())
-def _fused_bwd_op(dy: torch.Tensor, dy_var: torch.Tensor, dlam_fin: torch.Tensor, deta_fin: torch.Tensor,
+def _fused_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: Optional[torch.Tensor],
+                  deta_fin: Optional[torch.Tensor],
                   v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
                   p: torch.Tensor, ck_lam: torch.Tensor, ck_eta: torch.Tensor, decode_from_prior: bool
                   ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                              torch.Tensor, torch.Tensor]:
-    """Returns (dv, dlambda_v, dk, dq, da, dp, dlam0, deta0)."""
+    """Returns (dv, dlambda_v, dk, dq, da, dp, dlam0, deta0). dy_var, dlam_fin,
+    deta_fin None: zero (without dy_var the kernel skips the variance read-out's
+    adjoint)."""
     dev = _require_device(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta)
     B, L, M, S = _check(v, lambda_v, k, q, a, p, None, None)
     dv, dlv = torch.empty_like(v), torch.empty_like(lambda_v)
@@ -128,20 +131,20 @@ def _setup(ctx, inputs, output):
     ctx.prior = decode_from_prior
     ctx.has_lam0, ctx.has_eta0 = lam0 is not None, eta0 is not None
     ctx.save_for_backward(v, lambda_v, k, q, a, p, ck_lam, ck_eta)
+    # Unused outputs arrive as None, not zeros: an unused y_var selects the
+    # kernel without the variance adjoint, an unused final state reads nothing.
+    ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, dy, dy_var, dlam_fin, deta_fin, _dck_lam, _dck_eta):
     v, lambda_v, k, q, a, p, ck_lam, ck_eta = ctx.saved_tensors
 
-    def g(t, like):
-        return torch.zeros_like(like) if t is None else t.to(_F32).contiguous()
+    def f32(t):
+        return None if t is None else t.to(_F32).contiguous()
 
-    B, _, M = v.shape
-    S = k.shape[2]
-    state = v.new_empty(B, M, S)
     dv, dlv, dk, dq, da, dp, dlam0, deta0 = _fused_bwd_op(
-        g(dy, v), g(dy_var, v), g(dlam_fin, state), g(deta_fin, state), v, lambda_v, k, q, a, p, ck_lam, ck_eta,
-        ctx.prior)
+        torch.zeros_like(v) if dy is None else f32(dy), f32(dy_var), f32(dlam_fin), f32(deta_fin), v, lambda_v,
+        k, q, a, p, ck_lam, ck_eta, ctx.prior)
     return (dv, dlv, dk, dq, da, dp, dlam0 if ctx.has_lam0 else None, deta0 if ctx.has_eta0 else None,
             None, None)
 
@@ -207,15 +210,17 @@ def _check_sensors(v, obs):
 @torch.library.custom_op("kla_hip::kla_scan_fused_sensors", mutates_args=())
 def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
                     p: torch.Tensor, lam0: Optional[torch.Tensor], eta0: Optional[torch.Tensor], log_var: bool,
-                    obs_var_min: float, obs_var_max: float, decode_from_prior: bool, save: bool
+                    obs_var_min: float, obs_var_max: float, decode_from_prior: bool, save: bool, with_var: bool
                     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """(y, y_var, lam_fin, eta_fin, ck_lam, ck_eta) from strided v and log sigma^2
-    (or lambda_v) of one dtype; the checkpoints are empty unless ``save``."""
+    (or lambda_v) of one dtype; the checkpoints are empty unless ``save``, and
+    y_var is empty (and not computed) unless ``with_var``."""
     dev = _require_device(v, obs, k, q, a, p, lam0, eta0)
     B, L, M, S = _check(v, obs, k, q, a, p, lam0, eta0)
     _check_sensors(v, obs)
     f32 = dict(dtype=_F32, device=dev)
-    y, y_var = torch.empty(B, L, M, **f32), torch.empty(B, L, M, **f32)
+    y = torch.empty(B, L, M, **f32)
+    y_var = torch.empty(B, L, M, **f32) if with_var else torch.empty(0, **f32)
     lam_fin, eta_fin = torch.empty(B, M, S, **f32), torch.empty(B, M, S, **f32)
     n_ck = int(_lib.lib().kla_fused_checkpoints(L))
     ck_lam = torch.empty(B, n_ck, M, S, **f32) if save else torch.empty(0, **f32)
@@ -225,31 +230,36 @@ def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torc
     sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
     pt = _lib.ptr
     _lib.check("kla_fused_scan_sensors_fwd", _lib.lib().kla_fused_scan_sensors_fwd(
-        ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam0), pt(eta0), pt(y), pt(y_var), pt(lam_fin),
+        ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam0), pt(eta0), pt(y), pt(y_var) if with_var else None,
+        pt(lam_fin),
         pt(eta_fin), pt(ck_lam) if save else None, pt(ck_eta) if save else None, int(decode_from_prior),
         B, L, M, S, torch.cuda.current_stream(dev).cuda_stream))
     return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
 
 
 @_sensors_fwd_op.register_fake
-def _(v, obs, k, q, a, p, lam0, eta0, log_var, obs_var_min, obs_var_max, decode_from_prior, save):
+def _(v, obs, k, q, a, p, lam0, eta0, log_var, obs_var_min, obs_var_max, decode_from_prior, save, with_var):
     B, L, M = v.shape
     S = k.shape[2]
     n_ck = (L + 15) // 16
     f = dict(dtype=_F32)
     ck = k.new_empty(B, n_ck, M, S, **f) if save else k.new_empty(0, **f)
-    return (k.new_empty(B, L, M, **f), k.new_empty(B, L, M, **f), k.new_empty(B, M, S, **f),
-            k.new_empty(B, M, S, **f), ck, torch.empty_like(ck))
+    y_var = k.new_empty(B, L, M, **f) if with_var else k.new_empty(0, **f)
+    return (k.new_empty(B, L, M, **f), y_var, k.new_empty(B, M, S, **f), k.new_empty(B, M, S, **f), ck,
+            torch.empty_like(ck))
 
 
 @torch.library.custom_op("kla_hip::kla_scan_fused_sensors_backward", mutates_args=())
-def _sensors_bwd_op(dy: torch.Tensor, dy_var: torch.Tensor, dlam_fin: torch.Tensor, deta_fin: torch.Tensor,
+def _sensors_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: Optional[torch.Tensor],
+                    deta_fin: Optional[torch.Tensor],
                     v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
                     p: torch.Tensor, ck_lam: torch.Tensor, ck_eta: torch.Tensor, log_var: bool,
                     obs_var_min: float, obs_var_max: float, decode_from_prior: bool
                     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                                torch.Tensor, torch.Tensor]:
-    """(dv, dobs, dk, dq, da, dp, dlam0, deta0); dv and dobs dense in the sensors' dtype."""
+    """(dv, dobs, dk, dq, da, dp, dlam0, deta0); dv and dobs dense in the sensors' dtype.
+    dy_var, dlam_fin, deta_fin None: zero (without dy_var the variance read-out's
+    adjoint is skipped)."""
     dev = _require_device(dy, dy_var, dlam_fin, deta_fin, v, obs, k, q, a, p, ck_lam, ck_eta)
     B, L, M, S = _check(v, obs, k, q, a, p, None, None)
     _check_sensors(v, obs)
@@ -281,30 +291,28 @@ def _(dy, dy_var, dlam_fin, deta_fin, v, obs, k, q, a, p, ck_lam, ck_eta, log_va
 
 
 def _sensors_setup(ctx, inputs, output):
-    v, obs, k, q, a, p, lam0, eta0, log_var, obs_var_min, obs_var_max, decode_from_prior, save = inputs
+    v, obs, k, q, a, p, lam0, eta0, log_var, obs_var_min, obs_var_max, decode_from_prior, save, with_var = inputs
     _, _, _, _, ck_lam, ck_eta = output
     if not save:
         raise RuntimeError("kla_scan_fused_sensors was run without checkpoints but a gradient is required")
     ctx.opts = (log_var, obs_var_min, obs_var_max, decode_from_prior)
     ctx.has_lam0, ctx.has_eta0 = lam0 is not None, eta0 is not None
     ctx.save_for_backward(v, obs, k, q, a, p, ck_lam, ck_eta)
+    ctx.set_materialize_grads(False)
 
 
 def _sensors_backward(ctx, dy, dy_var, dlam_fin, deta_fin, _dck_lam, _dck_eta):
     v, obs, k, q, a, p, ck_lam, ck_eta = ctx.saved_tensors
 
-    def g(t, like):
-        return torch.zeros_like(like) if t is None else t.to(_F32).contiguous()
+    def f32(t):
+        return None if t is None or t.numel() == 0 else t.to(_F32).contiguous()
 
     B, L, M = v.shape
-    S = k.shape[2]
-    out = k.new_empty(B, L, M)
-    state = k.new_empty(B, M, S)
+    dy = k.new_zeros(B, L, M) if dy is None else f32(dy)
     dv, dobs, dk, dq, da, dp, dlam0, deta0 = _sensors_bwd_op(
-        g(dy, out), g(dy_var, out), g(dlam_fin, state), g(deta_fin, state), v, obs, k, q, a, p, ck_lam, ck_eta,
-        *ctx.opts)
+        dy, f32(dy_var), f32(dlam_fin), f32(deta_fin), v, obs, k, q, a, p, ck_lam, ck_eta, *ctx.opts)
     return (dv, dobs, dk, dq, da, dp, dlam0 if ctx.has_lam0 else None, deta0 if ctx.has_eta0 else None,
-            None, None, None, None, None)
+            None, None, None, None, None, None)
 
 
 _sensors_fwd_op.register_autograd(_sensors_backward, setup_context=_sensors_setup)
@@ -312,7 +320,7 @@ _sensors_fwd_op.register_autograd(_sensors_backward, setup_context=_sensors_setu
 
 def kla_scan_fused_sensors(v, obs, k, q, a, p, lam0=None, eta0=None, *, log_var: bool = True,
                            obs_var_min: float = 1e-4, obs_var_max: Optional[float] = None,
-                           decode_from_prior: bool = False):
+                           decode_from_prior: bool = False, with_var: bool = True):
     """(y, y_var, lam_fin, eta_fin) of the KLA scan with the layer's sensor read-out fused in.
 
     v and obs are [B, L, M] -- views such as column slices of the sensor
@@ -321,7 +329,8 @@ def kla_scan_fused_sensors(v, obs, k, q, a, p, lam0=None, eta0=None, *, log_var:
     the kernel, as KLALayer._project_sensors forms it (reference
     kla_layer.py:224-230); otherwise obs is lambda_v. bf16 sensors stay bf16 and
     their gradients come back in bf16; fp32 otherwise. k, q, a, p and the state
-    are computed in fp32.
+    are computed in fp32. With ``with_var=False`` y_var is not computed and comes
+    back as None.
     """
     if v.dtype != obs.dtype or v.dtype not in (torch.float32, torch.bfloat16):
         v, obs = v.float(), obs.float()
@@ -334,5 +343,6 @@ def kla_scan_fused_sensors(v, obs, k, q, a, p, lam0=None, eta0=None, *, log_var:
         t is not None and t.requires_grad for t in (v, obs, k, q, a, p, lam0, eta0))
     ov_max = math.inf if obs_var_max is None else float(obs_var_max)
     y, y_var, lam_fin, eta_fin, _, _ = _sensors_fwd_op(v, obs, k, q, a, p, lam0, eta0, bool(log_var),
-                                                       float(obs_var_min), ov_max, bool(decode_from_prior), save)
-    return y, y_var, lam_fin, eta_fin
+                                                       float(obs_var_min), ov_max, bool(decode_from_prior), save,
+                                                       bool(with_var))
+    return y, (y_var if with_var else None), lam_fin, eta_fin

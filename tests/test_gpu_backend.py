@@ -620,15 +620,17 @@ def _views(proj, M):
     return proj[..., :M], proj[..., M + 1:2 * M + 1]
 
 
+@pytest.mark.parametrize("with_var", [True, False])
 @pytest.mark.parametrize("obs_var_max", [None, 1.5])
 @pytest.mark.parametrize("decode_from_prior", [False, True])
 @pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 150, 20, 16), (3, 1, 7, 4), (1, 70, 9, 32)])
-def test_fused_sensors_match_float64_autograd(cuda, shape, decode_from_prior, obs_var_max):
+def test_fused_sensors_match_float64_autograd(cuda, shape, decode_from_prior, obs_var_max, with_var):
     """kla_scan_fused_sensors on strided fp32 column slices of a projection: outputs
     and every gradient (through the projection, so the untouched columns must get
     zeros) against float64 autograd of the layer's read-out tail, softplus, clamp
     and reciprocal (reference kla_layer.py:224-230), feeding oracle.torch_ref's
-    filter."""
+    filter. Without the variance (with_var=False) the kernels skip the y_var
+    read-out and its adjoint, and the loss has no y_var term."""
     from kla.ops.hip.fused import kla_scan_fused_sensors
     import torch.nn.functional as F
 
@@ -643,7 +645,8 @@ def test_fused_sensors_match_float64_autograd(cuda, shape, decode_from_prior, ob
 
     def loss(y, y_var, lam, eta):
         w = [t.to(device=y.device, dtype=y.dtype) for t in (wy, wv, wl, we)]
-        return (w[0] * y).sum() + (w[1] * y_var).sum() + (w[2] * lam).sum() + (w[3] * eta).sum()
+        var_term = (w[1] * y_var).sum() if with_var else 0.0
+        return (w[0] * y).sum() + var_term + (w[2] * lam).sum() + (w[3] * eta).sum()
 
     xs = [t.double().requires_grad_(True) for t in (proj, k, q, a, p, st.lam, st.eta)]
     v64, lv64 = _views(xs[0], M)
@@ -656,9 +659,11 @@ def test_fused_sensors_match_float64_autograd(cuda, shape, decode_from_prior, ob
     gs = [t.to(cuda).requires_grad_(True) for t in (proj, k, q, a, p, st.lam, st.eta)]
     v, lv = _views(gs[0], M)
     out = kla_scan_fused_sensors(v, lv, *gs[1:], log_var=True, obs_var_min=ov_min, obs_var_max=obs_var_max,
-                                 decode_from_prior=decode_from_prior)
+                                 decode_from_prior=decode_from_prior, with_var=with_var)
+    assert (out[1] is None) == (not with_var)
     for name, got, want in zip(("y", "y_var", "lam", "eta"), out, ref):
-        check(name, got, want.detach().numpy())
+        if got is not None:
+            check(name, got, want.detach().numpy())
     loss(*out).backward()
     for name, got, want in zip(("proj", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
         check("d" + name, got.grad, want.grad.numpy())
@@ -714,12 +719,12 @@ def test_fused_sensors_reject_bad_layouts(cuda):
     ins = [t.to(cuda) for t in make_inputs(B, L, M, S)]
     with pytest.raises(TypeError):
         _sensors_fwd_op(ins[0], ins[1].to(torch.bfloat16), *ins[2:], None, None, True, 1e-4, float("inf"), False,
-                        False)
+                        False, True)
     with pytest.raises(ValueError):
         _sensors_fwd_op(ins[0].transpose(1, 2).contiguous().transpose(1, 2), ins[1], *ins[2:], None, None, True,
-                        1e-4, float("inf"), False, False)
+                        1e-4, float("inf"), False, False, True)
     with pytest.raises(_lib.KLAHipError):
-        _sensors_fwd_op(ins[0], ins[1], *ins[2:], None, None, True, 1e-4, 0.0, False, False)
+        _sensors_fwd_op(ins[0], ins[1], *ins[2:], None, None, True, 1e-4, 0.0, False, False, True)
 
 
 LAYER_SENSOR_CASES = {
@@ -760,3 +765,40 @@ def test_layer_sensors_on_hip_match_torch_readout(cuda, tag, autocast):
     assert outs[0][3].keys() == outs[1][3].keys()
     for n in outs[0][3]:
         check("d" + n, outs[0][3][n], outs[1][3][n].cpu().numpy(), **tol)
+
+
+def test_variance_free_kernels_equal_the_full_ones(cuda):
+    """Skipping the variance read-out changes nothing else: y and the state equal
+    the full kernel's bit for bit, and a backward without a y_var gradient (NULL,
+    the variance-free adjoint) equals one given an explicit zero gradient."""
+    from kla.ops.hip.fused import kla_scan_fused, kla_scan_fused_sensors
+
+    B, L, M, S = 2, 77, 12, 16
+    ins = make_inputs(B, L, M, S, seed=13)
+    proj = _projection(B, L, M, S, seed=14, dtype=torch.bfloat16)
+    runs = {}
+    for tag in ("none", "zero", "off"):
+        pj = proj.to(cuda).requires_grad_(True)
+        xs = [t.to(cuda).requires_grad_(True) for t in ins[2:]]
+        v, lv = _views(pj, M)
+        y, y_var, lam, eta = kla_scan_fused_sensors(v, lv, *xs, with_var=tag != "off")
+        loss = y.square().sum() + lam.sum() + eta.square().sum()
+        if tag == "zero":
+            loss = loss + (0.0 * y_var).sum()
+        loss.backward()
+        runs[tag] = [y, lam, eta, pj.grad] + [t.grad for t in xs]
+    for tag in ("none", "off"):
+        for got, want in zip(runs[tag], runs["zero"]):
+            assert torch.equal(got, want), tag
+
+    dense = {}
+    for tag in ("none", "zero"):
+        xs = [t.to(cuda).requires_grad_(True) for t in ins]
+        y, y_var, lam, eta = kla_scan_fused(*xs)
+        loss = y.square().sum() + lam.sum()
+        if tag == "zero":
+            loss = loss + (0.0 * y_var).sum()
+        loss.backward()
+        dense[tag] = [t.grad for t in xs]
+    for got, want in zip(dense["none"], dense["zero"]):
+        assert torch.equal(got, want)
