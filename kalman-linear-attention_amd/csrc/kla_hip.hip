@@ -17,7 +17,7 @@
 #include "kla_hip.h"
 #pragma GCC visibility pop
 
-#include "causal_conv.hpp"
+#include "gate_skip.hpp"
 #include "fused_kla.hpp"
 #include "lookback_scan.hpp"
 
@@ -25,7 +25,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 5;
+constexpr int kAbiVersion = 6;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -417,6 +417,41 @@ int fused_bwd(const char *fn, const float *dy, const float *dy_var, const float 
   }
   if ((rc = reduce(part_a, da, 1, batch, M * S)) != KLA_OK) return rc;
   return reduce(part_p, dp, 1, batch, M * S);
+}
+
+int check_tail(const char *fn, int dtype, const void *res, int64_t ld_res, const void *gate, int64_t ld_gate,
+               const float *lam, int act, int64_t rows, int64_t M) {
+  if (rows < 0 || M < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative shape", fn);
+  if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16)
+    return fail(KLA_ERR_DTYPE, "%s: unsupported dtype %d", fn, dtype);
+  if (act < kActNone || act > kActRelu) return fail(KLA_ERR_INVALID_ARG, "%s: unknown activation %d", fn, act);
+  if (res && !lam) return fail(KLA_ERR_INVALID_ARG, "%s: a residual needs lambda_skip", fn);
+  if ((res && ld_res < M) || (gate && ld_gate < M))
+    return fail(KLA_ERR_INVALID_ARG, "%s: row stride below M", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (misaligned_bytes(res, el) || misaligned_bytes(gate, el))
+    return fail(KLA_ERR_ALIGN, "%s: residual or gate not aligned to its element size", fn);
+  return KLA_OK;
+}
+
+template <class F>
+int with_io(int dtype, F &&f) {
+  if (dtype == KLA_DTYPE_F32) return f(float{});
+  return f(bf16_t{});
+}
+
+dim3 tail_grid(int64_t rows, int64_t M, int V) {
+  return dim3(static_cast<uint32_t>((rows + kTailRows - 1) / kTailRows),
+              static_cast<uint32_t>((M + kTailThreads * V - 1) / (kTailThreads * V)));
+}
+
+// The 8-wide tail kernels need every row start 16-byte aligned: M and the row
+// strides multiples of 8, and the base pointers 16-byte aligned.
+bool tail_wide(int64_t M, int64_t ld_res, int64_t ld_gate, std::initializer_list<const void *> ptrs) {
+  if (M % 8 || ld_res % 8 || ld_gate % 8) return false;
+  for (const void *q : ptrs)
+    if (q && reinterpret_cast<uintptr_t>(q) % 16) return false;
+  return true;
 }
 
 }  // namespace
@@ -864,6 +899,120 @@ int kla_causal_conv_bwd(int dtype, const void *dy, const void *x, int64_t ld_t, 
     return hip_status(fn, hipGetLastError());
   };
   return dtype == KLA_DTYPE_F32 ? run(float{}) : run(bf16_t{});
+}
+
+
+// ------------------------------------------------------- layer output tail
+
+size_t kla_gate_skip_workspace_bytes(int64_t rows, int64_t M) {
+  if (rows < 0 || M < 0) return 0;
+  const int64_t nblk = (rows + kTailRows - 1) / kTailRows;
+  return std::max<size_t>(256, static_cast<size_t>(nblk * M + M + 1) * sizeof(float));
+}
+
+int kla_gate_skip_fwd(int dtype, const float *y, const void *residual, int64_t ld_res, const void *gate,
+                      int64_t ld_gate, const float *lambda_skip, int lambda_vector, int activation, float *out,
+                      int64_t rows, int64_t M, hipStream_t stream) {
+  const char *fn = "kla_gate_skip_fwd";
+  int rc = check_tail(fn, dtype, residual, ld_res, gate, ld_gate, lambda_skip, activation, rows, M);
+  if (rc != KLA_OK) return rc;
+  if (rows == 0 || M == 0) return KLA_OK;
+  if (!y || !out) return fail(KLA_ERR_INVALID_ARG, "%s: y and out must not be NULL", fn);
+  if (!all_aligned(4, {y, lambda_skip, out})) return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if ((rows + kTailRows - 1) / kTailRows >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
+  return with_io(dtype, [&](auto io) {
+    using IO = decltype(io);
+    TailParams<IO> p{};
+    p.y = y;
+    p.res = static_cast<const IO *>(residual);
+    p.gate = static_cast<const IO *>(gate);
+    p.ld_res = ld_res;
+    p.ld_gate = ld_gate;
+    p.lam = lambda_skip;
+    p.lam_vector = lambda_vector ? 1 : 0;
+    p.act = activation;
+    p.rows = rows;
+    p.M = M;
+    p.out = out;
+    if (tail_wide(M, ld_res, ld_gate, {y, residual, gate, lambda_vector ? lambda_skip : nullptr, out}))
+      hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, 8>), tail_grid(rows, M, 8), dim3(kTailThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, 1>), tail_grid(rows, M, 1), dim3(kTailThreads), 0, stream, p);
+    return hip_status(fn, hipGetLastError());
+  });
+}
+
+int kla_gate_skip_bwd(int dtype, const float *dout, const float *y, const void *residual, int64_t ld_res,
+                      const void *gate, int64_t ld_gate, const float *lambda_skip, int lambda_vector, int activation,
+                      float *dy, void *dres, void *dgate, float *dlambda, int64_t rows, int64_t M, void *workspace,
+                      size_t workspace_bytes, hipStream_t stream) {
+  const char *fn = "kla_gate_skip_bwd";
+  int rc = check_tail(fn, dtype, residual, ld_res, gate, ld_gate, lambda_skip, activation, rows, M);
+  if (rc != KLA_OK) return rc;
+  if (M == 0) return KLA_OK;
+  if (residual && !dlambda) return fail(KLA_ERR_INVALID_ARG, "%s: a residual needs dlambda", fn);
+  const int64_t nblk = (rows + kTailRows - 1) / kTailRows;
+  if (nblk >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
+  if (rows > 0 && (!dout || !y || !dy)) return fail(KLA_ERR_INVALID_ARG, "%s: dout, y and dy must not be NULL", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (!all_aligned(4, {dout, y, lambda_skip, dy, dlambda}) || misaligned_bytes(dres, el) ||
+      misaligned_bytes(dgate, el))
+    return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
+  float *ws = static_cast<float *>(workspace);
+  if (residual) {
+    if (!ws) return fail(KLA_ERR_WORKSPACE, "%s: workspace is NULL", fn);
+    if (misaligned_bytes(workspace, 256)) return fail(KLA_ERR_WORKSPACE, "%s: workspace not 256-byte aligned", fn);
+    const size_t need = kla_gate_skip_workspace_bytes(rows, M);
+    if (workspace_bytes < need)
+      return fail(KLA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
+  }
+  return with_io(dtype, [&](auto io) {
+    using IO = decltype(io);
+    float *part = ws;
+    float *colsum = ws ? ws + nblk * M : nullptr;
+    if (rows > 0) {
+      TailParams<IO> p{};
+      p.y = y;
+      p.res = static_cast<const IO *>(residual);
+      p.gate = static_cast<const IO *>(gate);
+      p.ld_res = ld_res;
+      p.ld_gate = ld_gate;
+      p.lam = lambda_skip;
+      p.lam_vector = lambda_vector ? 1 : 0;
+      p.act = activation;
+      p.rows = rows;
+      p.M = M;
+      p.dout = dout;
+      p.dy = dy;
+      p.dres = static_cast<IO *>(dres);
+      p.dgate = static_cast<IO *>(dgate);
+      p.part_lam = part;
+      if (tail_wide(M, ld_res, ld_gate,
+                    {dout, y, residual, gate, lambda_vector ? lambda_skip : nullptr, dy, dres, dgate, part}))
+        hipLaunchKernelGGL((gate_skip_bwd_kernel<IO, 8>), tail_grid(rows, M, 8), dim3(kTailThreads), 0, stream, p);
+      else
+        hipLaunchKernelGGL((gate_skip_bwd_kernel<IO, 1>), tail_grid(rows, M, 1), dim3(kTailThreads), 0, stream, p);
+      int st = hip_status(fn, hipGetLastError());
+      if (st != KLA_OK) return st;
+    }
+    if (!residual) return KLA_OK;
+    // d lambda: column sums over the row blocks, in a fixed order.
+    float *dst = lambda_vector ? dlambda : colsum;
+    if (rows == 0) {
+      hipLaunchKernelGGL(fill_zero_kernel, dim3(static_cast<uint32_t>((M + 255) / 256)), dim3(256), 0, stream, dst, M);
+    } else if (!launch_reduce_rows(part, dst, 1, nblk, M, stream)) {
+      hipLaunchKernelGGL(reduce_groups_kernel, dim3(static_cast<uint32_t>((M + 255) / 256)), dim3(256), 0, stream,
+                         part, dst, int64_t{1}, nblk, M);
+    }
+    int st = hip_status(fn, hipGetLastError());
+    if (st != KLA_OK || lambda_vector) return st;
+    // A 0-dim lambda: the columns summed in order, rounded to the residual's dtype.
+    float *total = colsum + M;
+    if (!launch_reduce_rows(colsum, total, 1, M, 1, stream))
+      hipLaunchKernelGGL(reduce_groups_kernel, dim3(1), dim3(256), 0, stream, colsum, total, int64_t{1}, M, int64_t{1});
+    hipLaunchKernelGGL(round_scalar_kernel<IO>, dim3(1), dim3(64), 0, stream, total, dlambda);
+    return hip_status(fn, hipGetLastError());
+  });
 }
 
 }  // extern "C"

@@ -220,6 +220,23 @@ class KLALayer(nn.Module):
         return (backend in ("hip", "hip_fused") and self.d_state <= 64 and z.dtype != torch.float64
                 and _step_on_hip(backend, z))
 
+    def _tail_on_hip(self, y: torch.Tensor, residual: torch.Tensor, gate: torch.Tensor | None) -> bool:
+        """Whether the skip + gate after the scan run on the MI355X kernels: a
+        hip-family backend on a ROCm GPU, fp32 y, residual and gate of one dtype
+        (fp32 or bf16), and a skip or a gate to apply. Not with return_variance
+        and a gate: act(gate) then also scales y_var, and torch adds the two
+        bf16 gradients of act(gate) before the activation's backward."""
+        from kla.ops.kla_ops import _step_on_hip
+
+        skip = self.lambda_skip is not None
+        if not (skip or gate is not None) or y.dtype != torch.float32:
+            return False
+        if self.config.return_variance and gate is not None:
+            return False
+        dtypes = {t.dtype for t in ((residual,) if skip else ()) + ((gate,) if gate is not None else ())}
+        return (len(dtypes) == 1 and dtypes <= {torch.float32, torch.bfloat16} and y.dim() == 3
+                and _step_on_hip(self.config.backend, y))
+
     def _decode_on_hip(self, projected: torch.Tensor) -> bool:
         """Whether a one-token step runs on the MI355X decode kernels: inference
         (no gradient), fp32 activations on a ROCm GPU, a hip-family backend."""
@@ -305,13 +322,20 @@ class KLALayer(nn.Module):
             y = y.to(x.dtype)
             y_var = y_var.to(x.dtype) if cfg.return_variance else None
 
-            if self.lambda_skip is not None:
-                y = y + self.lambda_skip * residual
-            if gate is not None:
-                g = self.gate_act(gate)
-                y = y * g
-                if y_var is not None:
-                    y_var = y_var * g.pow(2)
+            if self._tail_on_hip(y, residual, gate):
+                # skip + gate as one HIP kernel each way (kla.ops.hip.tail); same values.
+                from kla.ops.hip.tail import gate_skip_hip
+
+                y = gate_skip_hip(y, residual if self.lambda_skip is not None else None, gate, self.lambda_skip,
+                                  cfg.gating_activation)
+            else:
+                if self.lambda_skip is not None:
+                    y = y + self.lambda_skip * residual
+                if gate is not None:
+                    g = self.gate_act(gate)
+                    y = y * g
+                    if y_var is not None:
+                        y_var = y_var * g.pow(2)
 
         out = self.out_proj(y)
         result = (out, F.linear(y_var, self.out_proj.weight.pow(2))) if cfg.return_variance else out

@@ -293,3 +293,33 @@ def test_sensor_row_layouts():
     assert _sensor_rows(proj[:, :5, :6]) is None          # batch stride 140 != 5 * 20
     assert _sensor_rows(proj[..., :6].transpose(0, 1).contiguous().transpose(0, 1)) is None
     assert _sensor_rows(proj.transpose(1, 2)[..., :6]) is None
+
+
+def test_gate_skip_validation(lib):
+    P = ALIGNED
+
+    def fwd(dtype=_lib.KLA_DTYPE_BF16, y=P, res=P, ld_res=8, gate=P, ld_gate=16, lam=P, vec=0, act=1, out=P,
+            shape=(5, 8)):
+        return lib.kla_gate_skip_fwd(dtype, y, res, ld_res, gate, ld_gate, lam, vec, act, out, *shape, None)
+
+    assert fwd(dtype=9) == _lib.KLA_ERR_DTYPE
+    assert fwd(act=4) == _lib.KLA_ERR_INVALID_ARG
+    assert fwd(lam=None) == _lib.KLA_ERR_INVALID_ARG
+    assert "needs lambda_skip" in err(lib)
+    assert fwd(ld_gate=7) == _lib.KLA_ERR_INVALID_ARG
+    assert fwd(res=P + 1) == _lib.KLA_ERR_ALIGN
+    assert fwd(out=None) == _lib.KLA_ERR_INVALID_ARG
+    assert fwd(y=ODD) == _lib.KLA_ERR_ALIGN
+    assert fwd(shape=(0, 8), y=None) == _lib.KLA_OK
+    n = lib.kla_gate_skip_workspace_bytes(5, 8)
+    assert n >= 4 * (1 * 8 + 8 + 1)
+
+    def bwd(dl=P, ws=WS, nbytes=n, dres=P, dy=P):
+        return lib.kla_gate_skip_bwd(_lib.KLA_DTYPE_BF16, P, P, P, 8, P, 16, P, 0, 1, dy, dres, P, dl, 5, 8, ws,
+                                     nbytes, None)
+
+    assert bwd(dl=None) == _lib.KLA_ERR_INVALID_ARG
+    assert bwd(ws=None) == _lib.KLA_ERR_WORKSPACE
+    assert bwd(nbytes=n - 4) == _lib.KLA_ERR_WORKSPACE
+    assert bwd(dres=P + 1) == _lib.KLA_ERR_ALIGN
+    assert bwd(dy=None) == _lib.KLA_ERR_INVALID_ARG

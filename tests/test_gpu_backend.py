@@ -802,3 +802,99 @@ def test_variance_free_kernels_equal_the_full_ones(cuda):
         dense[tag] = [t.grad for t in xs]
     for got, want in zip(dense["none"], dense["zero"]):
         assert torch.equal(got, want)
+
+
+# ------------------------------------------------ the layer's skip + gate tail
+
+
+def _tail_reference(y, res, gate, lam, act):
+    """The reference layer's lines (kla_layer.py:333-337) in torch, same dtypes."""
+    import torch.nn.functional as F
+
+    acts = {"silu": F.silu, "gelu": F.gelu, "relu": F.relu}
+    if res is not None:
+        y = y + lam * res
+    if gate is not None:
+        y = y * acts[act](gate)
+    return y
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("act,skip", [(a, k) for a in ("silu", "gelu", "relu", None)
+                                      for k in ("scalar", "vector", None) if a or k])
+@pytest.mark.parametrize("shape", [(2, 70, 300), (1, 33, 7), (3, 16, 256)])
+def test_gate_skip_matches_torch_autograd(cuda, shape, act, skip, dtype):
+    """gate_skip_hip against torch's own chain and autograd on the same tensors:
+    the output, dy, d residual, d gate (a strided half of a projection) and
+    d lambda_skip, with torch's bf16 roundings (0-dim lambda * bf16 residual in
+    bf16, act(gate) in the gate's dtype, gradients cast where autograd casts)."""
+    from kla.ops.hip.tail import gate_skip_hip
+
+    B, L, M = shape
+    g = torch.Generator().manual_seed(21)
+    y = torch.randn(B, L, M, generator=g).to(cuda)
+    res = torch.randn(B, L, M, generator=g).to(dtype).to(cuda)
+    proj = torch.randn(B, L, 2 * M, generator=g).to(dtype).to(cuda)
+    lam = (torch.randn(M if skip == "vector" else (), generator=g) - 1.0).to(cuda)
+    dout = torch.randn(B, L, M, generator=g).to(cuda)
+    outs = []
+    for fused in (True, False):
+        yy = y.clone().requires_grad_(True)
+        rr = res.clone().requires_grad_(True)
+        pj = proj.clone().requires_grad_(True)
+        ll = lam.clone().requires_grad_(True)
+        gate = pj[..., M:] if act is not None else None
+        r_in = rr if skip is not None else None
+        if fused:
+            out = gate_skip_hip(yy, r_in, gate, ll if skip is not None else None, act or "silu")
+        else:
+            out = _tail_reference(yy, r_in, gate, ll, act)
+        assert out.dtype == torch.float32
+        out.backward(dout)
+        outs.append((out.detach(), yy.grad, rr.grad, pj.grad, ll.grad))
+    tol = dict(rtol=1e-5, atol=1e-6) if dtype == torch.float32 else dict(rtol=8e-3, atol=2e-3)
+    names = ("out", "dy", "dres", "dproj", "dlam")
+    for name, a, b in zip(names, outs[0], outs[1]):
+        if b is None:
+            assert a is None or not a.any(), name
+            continue
+        assert a.dtype == b.dtype, name
+        check(name, a.float(), b.float().cpu().numpy(), **tol)
+
+
+LAYER_TAIL_CASES = {
+    "default": (48, dict(d_state=8)),
+    "vector_gelu": (40, dict(d_state=8, lambda_skip_mode="vector", gating_activation="gelu")),
+    "no_gate": (32, dict(d_state=4, use_gating=False)),
+    "no_skip_relu": (32, dict(d_state=4, use_lambda_skip=False, gating_activation="relu")),
+    "variance_no_gate": (32, dict(d_state=4, return_variance=True, use_gating=False)),
+}
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+@pytest.mark.parametrize("tag", sorted(LAYER_TAIL_CASES))
+def test_layer_tail_on_hip_matches_torch_tail(cuda, tag, autocast):
+    """A KLALayer training step with its skip + gate on the HIP kernels equals the
+    same layer with torch's lines: output(s) and every parameter gradient."""
+    import copy
+
+    d_model, cfg = LAYER_TAIL_CASES[tag]
+    torch.manual_seed(0)
+    layer = KLALayer(d_model, KLAConfig(backend="hip", **cfg)).to(cuda).train()
+    other = copy.deepcopy(layer)
+    other._tail_on_hip = lambda *a: False
+    x = torch.randn(2, 70, d_model, generator=torch.Generator().manual_seed(1)).to(cuda)
+    outs = []
+    for m in (layer, other):
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            out = m(x)
+        ys = out if isinstance(out, tuple) else (out,)
+        sum(u.float().square().mean() for u in ys).backward()
+        outs.append(([u.detach().float() for u in ys],
+                     {n: p.grad.detach().clone() for n, p in m.named_parameters() if p.grad is not None}))
+    tol = dict(rtol=1e-2, atol=1e-3) if autocast else dict(rtol=5e-5, atol=5e-6)
+    for i, (a, b) in enumerate(zip(outs[0][0], outs[1][0])):
+        check(f"out{i}", a, b.cpu().numpy(), **tol)
+    assert outs[0][1].keys() == outs[1][1].keys()
+    for n in outs[0][1]:
+        check("d" + n, outs[0][1][n], outs[1][1][n].cpu().numpy(), **tol)
