@@ -359,19 +359,28 @@ __device__ __forceinline__ const void *sensor_at(const void *base, int64_t row, 
   return static_cast<const char *>(base) + (row * ld + m0) * (BF16 ? 2 : 4);
 }
 
-// LDS [W][TB + 4] -> dense rows of a tensor of the sensor dtype; with F, each
-// value times lam^2 f (the log sigma^2 gradient from that of Lambda^v).
+// The sensor gradients of a flushed block from the per-(step, channel) sums over
+// s of dr k (P) and d phi k^2 (Q): dv = Lambda P, d Lambda = Q + v P. Called with
+// sum = P and pv = NULL for dv (scaled by lam), or with sum = Q and pv = P for
+// d Lambda; with F, d Lambda is then carried to log sigma^2 (times lam^2 f).
+// LDS [W][TB + 4] -> dense rows of a tensor of the sensor dtype.
 template <int TB, int W, bool BF16, bool F>
-__device__ __forceinline__ void lds_to_global_sensor(const float (*lds)[TB + kPad], const float (*lam)[TB + kPad],
-                                                     const float (*f)[TB + kPad], void *base, int64_t ld,
-                                                     int64_t rows, int64_t cols) {
+__device__ __forceinline__ void lds_to_global_sensor(const float (*sum)[TB + kPad], const float (*lam)[TB + kPad],
+                                                     const float (*v)[TB + kPad], const float (*f)[TB + kPad],
+                                                     void *base, int64_t ld, int64_t rows, int64_t cols,
+                                                     const float (*pv)[TB + kPad] = nullptr) {
   const int tid = static_cast<int>(threadIdx.x);
 #pragma unroll
   for (int i = 0; i < (TB * W + kFusedThreads - 1) / kFusedThreads; ++i) {
     const int e = tid + i * kFusedThreads;
     const int t = e / W, c = e % W;
     if (e < TB * W && t < rows && c < cols) {
-      float d = lds[c][t];
+      float d;
+      if (pv) {
+        d = sum[c][t] + v[c][t] * pv[c][t];
+      } else {
+        d = lam[c][t] * sum[c][t];
+      }
       if constexpr (F) {
         const float l = lam[c][t];
         d = d * (l * l) * f[c][t];
@@ -619,11 +628,13 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     constexpr int64_t el = BF16 ? 2 : 4;
     void *dvb = static_cast<char *>(prm.dv) + (offM + t0 * M) * el;
     void *dlb = static_cast<char *>(prm.dlv) + (offM + t0 * M) * el;
-    lds_to_global_sensor<TB, CH, BF16, false>(s_dv[buf], nullptr, nullptr, dvb, M, L - t0, cols_m);
+    lds_to_global_sensor<TB, CH, BF16, false>(s_dv[buf], s_l[buf], s_v[buf], nullptr, dvb, M, L - t0, cols_m);
     if (sn.log_var)
-      lds_to_global_sensor<TB, CH, BF16, true>(s_dl[buf], s_l[buf], s_lf[buf], dlb, M, L - t0, cols_m);
+      lds_to_global_sensor<TB, CH, BF16, true>(s_dl[buf], s_l[buf], s_v[buf], s_lf[buf], dlb, M, L - t0, cols_m,
+                                               s_dv[buf]);
     else
-      lds_to_global_sensor<TB, CH, BF16, false>(s_dl[buf], nullptr, nullptr, dlb, M, L - t0, cols_m);
+      lds_to_global_sensor<TB, CH, BF16, false>(s_dl[buf], nullptr, s_v[buf], nullptr, dlb, M, L - t0, cols_m,
+                                                s_dv[buf]);
     for (int i = tid; i < 2 * TB * SP; i += kFusedThreads) {
       const int which = i / (TB * SP);
       const int j = (i / SP) % TB;
@@ -657,7 +668,10 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     float lh[TB + 1], eh[TB + 1], idn[TB], vr[TB];
     // da, dp sum over all steps: accumulate each block apart and add the block
     // totals (two-level summation keeps fp32 rounding at ~(TB + L/TB) ulp).
-    float blk_a = 0.0f, blk_a2 = 0.0f, blk_p = 0.0f;
+    // The terms through A = (1 + p' phi)/a2 and C = p'/a2 are gathered as
+    // X = sum (dA phi + dC) and Y = sum dA and applied once per block:
+    // dp += X/a2, d(a2) -= (Y + p' X)/a2^2.
+    float blk_a = 0.0f, blk_a2 = 0.0f, blk_p = 0.0f, blk_x = 0.0f, blk_y = 0.0f;
     {
       const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
       float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
@@ -703,10 +717,11 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         const float lam_t = lh[j + 1], eta_t = eh[j + 1];
         const float inv_den = idn[j], var = vr[j];
         // The step's intermediates (filter_step) from the kept 1/den.
-        const float phi = sig * (kk * kk);
-        const float A = (1.0f + pp * phi) * inv_a2;
+        const float kk2 = kk * kk;
+        const float phi = sig * kk2;
+        const float idn_a = inv_den * inv_a2;   // d lam_t / d lam' = 1/(a2 den^2) = idn_a / den
         const bool da_ok = a2 + pp * lp >= kEps;
-        const float inv_Da = inv_Da_of(inv_den, inv_a2, da_ok);
+        const float inv_Da = da_ok ? idn_a : kInvEps;
         const float alpha = a_s * inv_Da;
         const float mean = eta_t * var;
         const float mean_o = PRIOR ? a_s * mean : mean;
@@ -747,26 +762,28 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         const float dDa = da_ok ? -dalpha * alpha * inv_Da : 0.0f;
         blk_a2 += dDa;
         blk_p += dDa * lp;
-        // lam_t = (A lam' + phi) / den, den = C lam' + 1;  d lam_t / d lam' = 1/(a2 den^2)
+        // lam_t = (A lam' + phi) / den, den = C lam' + 1: dA = u lam', dC = -u lam_t lam'
         const float u = gl_t * inv_den;
         const float dA = u * lp;
-        const float dC = -u * lam_t * lp;
-        gl = u * inv_den * inv_a2 + dDa * pp;
-        // A = (1 + p' phi)/a2, C = p'/a2
-        const float dphi = u + dA * pp * inv_a2;
-        blk_p += (dA * phi + dC) * inv_a2;
-        blk_a2 -= (dA * A + dC * C) * inv_a2;
-        // phi = Lv k^2, r = (v Lv) k
-        const float dmsi = dr * kk;
-        const float dsig_c = dphi * (kk * kk) + dmsi * vv;
-        const float dv_c = dmsi * sig;
-        dk_c = dphi * 2.0f * sig * kk + dr * (vv * sig);
+        // (Explicit fmaf where a sum of two products could be contracted either
+        // way, so every kernel variant rounds alike.)
+        blk_x = fmaf(dA, phi - lam_t, blk_x);   // dA phi + dC
+        blk_y += dA;
+        gl = fmaf(u, idn_a, dDa * pp);
+        // A = (1 + p' phi)/a2: d phi = u + dA p'/a2 = u + dA C
+        const float dphi = fmaf(dA, C, u);
+        // phi = Lv k^2, r = (v Lv) k. Per lane the s-sums need only dr k and
+        // d phi k^2: dv = Lv sum(dr k), dLv = sum(d phi k^2) + v sum(dr k), formed
+        // once per (step, channel) when the block is flushed.
+        const float pk = dr * kk;
+        const float qk = dphi * kk2;
+        dk_c = sig * fmaf(2.0f * dphi, kk, dr * vv);
         if constexpr (kTr) {
-          dv_w[j] = dv_c;
-          dl_w[j] = dsig_c;
+          dv_w[j] = pk;
+          dl_w[j] = qk;
         } else {
-          const float dv_s = group_sum<SP>(dv_c);
-          const float dl_s = group_sum<SP>(dsig_c);
+          const float dv_s = group_sum<SP>(pk);
+          const float dl_s = group_sum<SP>(qk);
           if (ln.s == 0) {
             s_dv[cur][c][j] = dv_s;
             s_dl[cur][c][j] = dl_s;
@@ -808,8 +825,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       }
     }
     acc_a += blk_a;
-    acc_a2 += blk_a2;
-    acc_p += blk_p;
+    acc_a2 += fmaf(-fmaf(pp, blk_x, blk_y), inv_a2 * inv_a2, blk_a2);
+    acc_p += fmaf(blk_x, inv_a2, blk_p);
     if (i + 1 < n_ck) stage(cur ^ 1);
     __syncthreads();
   }
