@@ -663,6 +663,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     if (i + 1 < n_ck) load(t0 - TB);
     if (i > 0) flush(blk + 1, cur ^ 1);
 
+    // Steps of this block inside the sequence, as a 32-bit count: the per-step
+    // bound is then a scalar compare (there is no 64-bit scalar less-than).
+    const int nv = static_cast<int>(L - t0 < TB ? L - t0 : TB);
     // Over the block: lam_{t-1}, eta_{t-1} (lh[TB], eh[TB]: the state after the
     // block), and each step's 1/den and posterior variance, kept from the replay.
     float lh[TB + 1], eh[TB + 1], idn[TB], vr[TB];
@@ -682,7 +685,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         eh[j] = eta;
         idn[j] = 0.0f;
         vr[j] = 0.0f;
-        if (t0 + j < L) {
+        if (j < nv) {
           StepIO io;
           lam = filter_step(lam, eta, s_l[cur][c][j], s_v[cur][c][j], s_k[cur][ln.s][j], a_s, a2, pp, inv_a2, C,
                             io);
@@ -703,13 +706,12 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     float dk_w[kRows ? TB : 1], dq_w[kRows ? TB : 1];
 #pragma unroll
     for (int j = TB - 1; j >= 0; --j) {
-      const int64_t t = t0 + j;
       float dk_c = 0.0f, dq_c = 0.0f;
       if constexpr (kTr) {
         dv_w[j] = 0.0f;
         dl_w[j] = 0.0f;
       }
-      if (t < L) {
+      if (j < nv) {
         const float vv = s_v[cur][c][j], sig = s_l[cur][c][j];
         const float dy = s_dy[cur][c][j];
         const float kk = s_k[cur][ln.s][j], qq = s_q[cur][ln.s][j];
