@@ -246,6 +246,15 @@ __device__ __forceinline__ float filter_step(float lam, float &eta, float sig, f
 
 constexpr int kPad = 4;
 
+// Four consecutive steps of one LDS tile row (16-byte aligned: rows are TB + 4
+// floats, TB a multiple of 4), read with one ds_read_b128; pick4 takes step i % 4.
+__device__ __forceinline__ float4 lds4(const float *row, int j) {
+  return *reinterpret_cast<const float4 *>(row + j);
+}
+__device__ __forceinline__ float pick4(const float4 &v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
 // Global -> registers: element e = tid + 256 i of the [TB, W] tile whose rows
 // are `row0 + t * ld` (t < rows) and columns c < cols of a row.
 template <int TB, int W>
@@ -409,8 +418,8 @@ template <int SP, bool PRIOR, bool BF16, bool VAR>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int TB = kFusedTB;
-  __shared__ float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
-  __shared__ float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
+  __shared__ __align__(16) float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
+  __shared__ __align__(16) float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
   __shared__ float s_y[2][CH][TB + kPad], s_yv[2][CH][TB + kPad];
 
   const FusedLane ln = fused_lane<SP>(g);
@@ -564,9 +573,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
   constexpr int CH = kFusedThreads / SP;
   constexpr int NW = kFusedThreads / kWave;
   constexpr int TB = kCkpt;
-  __shared__ float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
-  __shared__ float s_dy[2][CH][TB + kPad], s_dyv[2][CH][TB + kPad];
-  __shared__ float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
+  __shared__ __align__(16) float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
+  __shared__ __align__(16) float s_dy[2][CH][TB + kPad], s_dyv[2][CH][TB + kPad];
+  __shared__ __align__(16) float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
   __shared__ float s_dv[2][CH][TB + kPad], s_dl[2][CH][TB + kPad];
   __shared__ float s_lf[2][CH][TB + kPad];   // log sigma^2 gradient factors (log_var sensors)
   __shared__ float s_red[2][2][TB][NW][SP];
@@ -663,6 +672,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     if (i + 1 < n_ck) load(t0 - TB);
     if (i > 0) flush(blk + 1, cur ^ 1);
 
+    // Tile values four steps per LDS read, where the registers that hold them
+    // do not cost occupancy (16 or more lanes per channel).
+    constexpr bool kVecLds = SP >= 16;
     // Steps of this block inside the sequence, as a 32-bit count: the per-step
     // bound is then a scalar compare (there is no 64-bit scalar less-than).
     const int nv = static_cast<int>(L - t0 < TB ? L - t0 : TB);
@@ -679,16 +691,24 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
       float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
       float eta = ln.active ? prm.ck_eta[ci] : 0.0f;
+      float4 l4{}, v4{}, k4{};
 #pragma unroll
       for (int j = 0; j < TB; ++j) {
+        if (kVecLds && j % 4 == 0) {
+          l4 = lds4(s_l[cur][c], j);
+          v4 = lds4(s_v[cur][c], j);
+          k4 = lds4(s_k[cur][ln.s], j);
+        }
         lh[j] = lam;
         eh[j] = eta;
         idn[j] = 0.0f;
         vr[j] = 0.0f;
         if (j < nv) {
           StepIO io;
-          lam = filter_step(lam, eta, s_l[cur][c][j], s_v[cur][c][j], s_k[cur][ln.s][j], a_s, a2, pp, inv_a2, C,
-                            io);
+          const float sig = kVecLds ? pick4(l4, j % 4) : s_l[cur][c][j];
+          const float vv = kVecLds ? pick4(v4, j % 4) : s_v[cur][c][j];
+          const float kk = kVecLds ? pick4(k4, j % 4) : s_k[cur][ln.s][j];
+          lam = filter_step(lam, eta, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
           idn[j] = io.inv_den;
           vr[j] = rcp(fmaxf(lam, kEps));
         }
@@ -704,17 +724,27 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     // walk (cross_row_transpose_sum) when SP = 16.
     constexpr bool kRows = SP == 16;
     float dk_w[kRows ? TB : 1], dq_w[kRows ? TB : 1];
+    float4 v4{}, l4{}, dy4{}, k4{}, q4{};
 #pragma unroll
     for (int j = TB - 1; j >= 0; --j) {
+      if (kVecLds && j % 4 == 3) {
+        v4 = lds4(s_v[cur][c], j - 3);
+        l4 = lds4(s_l[cur][c], j - 3);
+        dy4 = lds4(s_dy[cur][c], j - 3);
+        k4 = lds4(s_k[cur][ln.s], j - 3);
+        q4 = lds4(s_q[cur][ln.s], j - 3);
+      }
       float dk_c = 0.0f, dq_c = 0.0f;
       if constexpr (kTr) {
         dv_w[j] = 0.0f;
         dl_w[j] = 0.0f;
       }
       if (j < nv) {
-        const float vv = s_v[cur][c][j], sig = s_l[cur][c][j];
-        const float dy = s_dy[cur][c][j];
-        const float kk = s_k[cur][ln.s][j], qq = s_q[cur][ln.s][j];
+        const float vv = kVecLds ? pick4(v4, j % 4) : s_v[cur][c][j];
+        const float sig = kVecLds ? pick4(l4, j % 4) : s_l[cur][c][j];
+        const float dy = kVecLds ? pick4(dy4, j % 4) : s_dy[cur][c][j];
+        const float kk = kVecLds ? pick4(k4, j % 4) : s_k[cur][ln.s][j];
+        const float qq = kVecLds ? pick4(q4, j % 4) : s_q[cur][ln.s][j];
         const float lp = lh[j], ep = eh[j];
         const float lam_t = lh[j + 1], eta_t = eh[j + 1];
         const float inv_den = idn[j], var = vr[j];
