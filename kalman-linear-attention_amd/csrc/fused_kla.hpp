@@ -487,17 +487,23 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
     // the half (transpose_sum) when a channel's lanes fit one 16-lane row.
     constexpr bool kTr = SP <= 16;
     float yw[kTr ? kCkpt : 1], vw[kTr ? kCkpt : 1];
-    // One step at block position j (position jj within its half).
-    auto step = [&](int j, int jj) {
+    constexpr bool kVecLds = SP >= 16;
+    // One step at block position j (position jj within its half); with x4, the
+    // step's tile values come from four-step LDS reads.
+    float4 l4{}, v4{}, k4{}, q4{};
+    auto step = [&](int j, int jj, bool x4) {
       StepIO io;
-      lam = filter_step(lam, eta, s_l[cur][c][j], s_v[cur][c][j], s_k[cur][ln.s][j], a_s, a2, pp, inv_a2, C, io);
+      const float sig = x4 ? pick4(l4, j % 4) : s_l[cur][c][j];
+      const float vv = x4 ? pick4(v4, j % 4) : s_v[cur][c][j];
+      const float kk = x4 ? pick4(k4, j % 4) : s_k[cur][ln.s][j];
+      lam = filter_step(lam, eta, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
       const float var = rcp(fmaxf(lam, kEps));
       float mean = eta * var, vo = var;
       if (PRIOR) {
         mean = a_s * mean;
         vo = a2 * var + pp;
       }
-      const float qq = s_q[cur][ln.s][j];
+      const float qq = x4 ? pick4(q4, j % 4) : s_q[cur][ln.s][j];
       if constexpr (kTr) {
         yw[jj] = qq * mean;
         if constexpr (VAR) vw[jj] = (qq * qq) * vo;
@@ -522,13 +528,22 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
         if (th + kCkpt <= L) {
           // The whole half lies inside the sequence: no per-step bound.
 #pragma unroll
-          for (int j = 0; j < kCkpt; ++j) step(h * kCkpt + j, j);
+          for (int j = 0; j < kCkpt; ++j) {
+            const int jb = h * kCkpt + j;
+            if (kVecLds && jb % 4 == 0) {
+              l4 = lds4(s_l[cur][c], jb);
+              v4 = lds4(s_v[cur][c], jb);
+              k4 = lds4(s_k[cur][ln.s], jb);
+              q4 = lds4(s_q[cur][ln.s], jb);
+            }
+            step(jb, j, kVecLds);
+          }
         } else if constexpr (kTr) {
           // Unrolled: the terms live in registers indexed by j.
 #pragma unroll
           for (int j = 0; j < kCkpt; ++j) {
             if (th + j < L) {
-              step(h * kCkpt + j, j);
+              step(h * kCkpt + j, j, false);
             } else {
               yw[j] = 0.0f;
               if constexpr (VAR) vw[j] = 0.0f;
@@ -536,7 +551,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
           }
         } else {
           for (int j = 0; j < kCkpt; ++j)
-            if (th + j < L) step(h * kCkpt + j, j);
+            if (th + j < L) step(h * kCkpt + j, j, false);
         }
         if constexpr (kTr) {
           transpose_sum<SP, kCkpt>(yw, lane);
