@@ -318,16 +318,19 @@ int kla_causal_conv_bwd(int dtype, const void *dy, const void *x, int64_t ld_t, 
 /*
  * The KLALayer output tail after the scan (reference src/kla/layers/kla_layer.py:333-337):
  *   t = y + lambda_skip * residual,  out = t * act(gate)
- * y, out, dout, dy: fp32 [rows, M] dense. residual, gate: [rows, M] of `dtype`
- * (KLA_DTYPE_F32 or KLA_DTYPE_BF16) with rows ld_res / ld_gate elements apart, or
- * NULL when the layer has no skip / no gate. lambda_skip: fp32 [M] (lambda_vector
- * = 1) or one value (0-dim: with bf16 residuals lambda * residual is rounded to
- * bf16, as torch's type promotion leaves it). activation: 0 none, 1 silu, 2 gelu,
- * 3 relu; act(gate) is rounded to `dtype`.
+ * y, dy: fp32 [rows, M] dense. out, dout: [rows, M] dense of `out_dtype`
+ * (KLA_DTYPE_F32, or KLA_DTYPE_BF16 where the consumer of out -- the output
+ * projection under autocast -- rounds it to bf16 anyway). residual, gate:
+ * [rows, M] of `dtype` (KLA_DTYPE_F32 or KLA_DTYPE_BF16) with rows ld_res /
+ * ld_gate elements apart, or NULL when the layer has no skip / no gate.
+ * lambda_skip: fp32 [M] (lambda_vector = 1) or one value (0-dim: with bf16
+ * residuals lambda * residual is rounded to bf16, as torch's type promotion
+ * leaves it). activation: 0 none, 1 silu, 2 gelu, 3 relu; act(gate) is rounded
+ * to `dtype`.
  */
-int kla_gate_skip_fwd(int dtype, const float *y, const void *residual, int64_t ld_res, const void *gate,
-                      int64_t ld_gate, const float *lambda_skip, int lambda_vector, int activation, float *out,
-                      int64_t rows, int64_t M, hipStream_t stream);
+int kla_gate_skip_fwd(int dtype, int out_dtype, const float *y, const void *residual, int64_t ld_res,
+                      const void *gate, int64_t ld_gate, const float *lambda_skip, int lambda_vector, int activation,
+                      void *out, int64_t rows, int64_t M, hipStream_t stream);
 
 /* Bytes of workspace kla_gate_skip_bwd needs (column partial sums; no zero-fill needed). */
 size_t kla_gate_skip_workspace_bytes(int64_t rows, int64_t M);
@@ -339,10 +342,10 @@ size_t kla_gate_skip_workspace_bytes(int64_t rows, int64_t M);
  * Replaces the autograd backward of those lines (MulBackward0, AddBackward0 and
  * the activation's backward).
  */
-int kla_gate_skip_bwd(int dtype, const float *dout, const float *y, const void *residual, int64_t ld_res,
-                      const void *gate, int64_t ld_gate, const float *lambda_skip, int lambda_vector, int activation,
-                      float *dy, void *dres, void *dgate, float *dlambda, int64_t rows, int64_t M, void *workspace,
-                      size_t workspace_bytes, hipStream_t stream);
+int kla_gate_skip_bwd(int dtype, int out_dtype, const void *dout, const float *y, const void *residual,
+                      int64_t ld_res, const void *gate, int64_t ld_gate, const float *lambda_skip, int lambda_vector,
+                      int activation, float *dy, void *dres, void *dgate, float *dlambda, int64_t rows, int64_t M,
+                      void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

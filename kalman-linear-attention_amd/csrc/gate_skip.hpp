@@ -4,9 +4,11 @@
 //   t = y + lambda_skip * residual        (when the layer has a lambda skip)
 //   out = t * act(gate)                   (when the layer has a gate)
 //
-// y and out are fp32 [rows, M]; residual and gate are [rows, M] rows of one IO
-// type (fp32, or bf16 under autocast), each with its own row stride (the gate is
-// one half of the input projection). lambda_skip is a 0-dim or [M] fp32 tensor.
+// y is fp32 [rows, M]; out is [rows, M] fp32, or bf16 when its consumer (the
+// output projection under autocast) would round it to bf16 anyway; residual and
+// gate are [rows, M] rows of one IO type (fp32, or bf16 under autocast), each
+// with its own row stride (the gate is one half of the input projection).
+// lambda_skip is a 0-dim or [M] fp32 tensor.
 // torch forms this chain as four or five elementwise passes plus their backward
 // passes; here it is one pass each way.
 //
@@ -27,7 +29,7 @@ namespace kla {
 constexpr int kTailThreads = 256;
 constexpr int kTailRows = 16;   // rows per workgroup (one partial row of d lambda per workgroup)
 
-template <class IO>
+template <class IO, class OUT>
 struct TailParams {
   const float *y;                // [rows, M] dense
   const IO *res;                 // rows ld_res apart, or NULL (no skip)
@@ -38,9 +40,9 @@ struct TailParams {
   int act;
   int64_t rows, M;
   // forward
-  float *out;                    // [rows, M] dense
+  OUT *out;                      // [rows, M] dense
   // backward
-  const float *dout;             // [rows, M] dense
+  const OUT *dout;               // [rows, M] dense
   float *dy;                     // [rows, M] dense
   IO *dres, *dgate;              // [rows, M] dense, or NULL
   float *part_lam;               // [n_row_blocks, M]: per-block column sums of d lambda terms
@@ -95,8 +97,8 @@ __device__ __forceinline__ void vstore(bf16_t *p, const float (&x)[V]) {
 
 // V elements of the forward chain at row r, columns m..m+V: t (before the gate),
 // the gate factor gg, and the residual and raw gate values.
-template <class IO, int V>
-__device__ __forceinline__ void tail_values(const TailParams<IO> &p, int64_t r, int64_t m, const float (&y)[V],
+template <class IO, class OUT, int V>
+__device__ __forceinline__ void tail_values(const TailParams<IO, OUT> &p, int64_t r, int64_t m, const float (&y)[V],
                                             float (&t)[V], float (&gg)[V], float (&resv)[V], float (&gatev)[V]) {
 #pragma unroll
   for (int v = 0; v < V; ++v) {
@@ -129,8 +131,8 @@ __device__ __forceinline__ void tail_values(const TailParams<IO> &p, int64_t r, 
 }
 
 // Grid (ceil(rows / kTailRows), ceil(M / (256 V))); thread = V consecutive columns of a row block.
-template <class IO, int V>
-__global__ void __launch_bounds__(kTailThreads) gate_skip_fwd_kernel(TailParams<IO> p) {
+template <class IO, class OUT, int V>
+__global__ void __launch_bounds__(kTailThreads) gate_skip_fwd_kernel(TailParams<IO, OUT> p) {
   const int64_t m = (static_cast<int64_t>(blockIdx.y) * kTailThreads + threadIdx.x) * V;
   if (m >= p.M) return;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kTailRows;
@@ -138,7 +140,7 @@ __global__ void __launch_bounds__(kTailThreads) gate_skip_fwd_kernel(TailParams<
   for (int64_t r = r0; r < r1; ++r) {
     float y[V], t[V], gg[V], resv[V], gatev[V];
     vload<V>(p.y + r * p.M + m, y);
-    tail_values<IO, V>(p, r, m, y, t, gg, resv, gatev);
+    tail_values<IO, OUT, V>(p, r, m, y, t, gg, resv, gatev);
     if (p.gate) {
 #pragma unroll
       for (int v = 0; v < V; ++v) t[v] *= gg[v];
@@ -147,8 +149,8 @@ __global__ void __launch_bounds__(kTailThreads) gate_skip_fwd_kernel(TailParams<
   }
 }
 
-template <class IO, int V>
-__global__ void __launch_bounds__(kTailThreads) gate_skip_bwd_kernel(TailParams<IO> p) {
+template <class IO, class OUT, int V>
+__global__ void __launch_bounds__(kTailThreads) gate_skip_bwd_kernel(TailParams<IO, OUT> p) {
   const int64_t m = (static_cast<int64_t>(blockIdx.y) * kTailThreads + threadIdx.x) * V;
   if (m >= p.M) return;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kTailRows;
@@ -171,7 +173,7 @@ __global__ void __launch_bounds__(kTailThreads) gate_skip_bwd_kernel(TailParams<
     const int64_t i = r * p.M + m;
     float y[V], t[V], gg[V], resv[V], gatev[V], dout[V], dt[V];
     vload<V>(p.y + i, y);
-    tail_values<IO, V>(p, r, m, y, t, gg, resv, gatev);
+    tail_values<IO, OUT, V>(p, r, m, y, t, gg, resv, gatev);
     vload<V>(p.dout + i, dout);
 #pragma unroll
     for (int v = 0; v < V; ++v) dt[v] = dout[v];

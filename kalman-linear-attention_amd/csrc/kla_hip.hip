@@ -25,7 +25,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 6;
+constexpr int kAbiVersion = 7;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -910,53 +910,63 @@ size_t kla_gate_skip_workspace_bytes(int64_t rows, int64_t M) {
   return std::max<size_t>(256, static_cast<size_t>(nblk * M + M + 1) * sizeof(float));
 }
 
-int kla_gate_skip_fwd(int dtype, const float *y, const void *residual, int64_t ld_res, const void *gate,
-                      int64_t ld_gate, const float *lambda_skip, int lambda_vector, int activation, float *out,
-                      int64_t rows, int64_t M, hipStream_t stream) {
+int kla_gate_skip_fwd(int dtype, int out_dtype, const float *y, const void *residual, int64_t ld_res,
+                      const void *gate, int64_t ld_gate, const float *lambda_skip, int lambda_vector, int activation,
+                      void *out, int64_t rows, int64_t M, hipStream_t stream) {
   const char *fn = "kla_gate_skip_fwd";
   int rc = check_tail(fn, dtype, residual, ld_res, gate, ld_gate, lambda_skip, activation, rows, M);
   if (rc != KLA_OK) return rc;
+  if (out_dtype != KLA_DTYPE_F32 && out_dtype != KLA_DTYPE_BF16)
+    return fail(KLA_ERR_DTYPE, "%s: unsupported out dtype %d", fn, out_dtype);
   if (rows == 0 || M == 0) return KLA_OK;
   if (!y || !out) return fail(KLA_ERR_INVALID_ARG, "%s: y and out must not be NULL", fn);
-  if (!all_aligned(4, {y, lambda_skip, out})) return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if (!all_aligned(4, {y, lambda_skip}) || misaligned_bytes(out, out_dtype == KLA_DTYPE_F32 ? 4 : 2))
+    return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
   if ((rows + kTailRows - 1) / kTailRows >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
   return with_io(dtype, [&](auto io) {
-    using IO = decltype(io);
-    TailParams<IO> p{};
-    p.y = y;
-    p.res = static_cast<const IO *>(residual);
-    p.gate = static_cast<const IO *>(gate);
-    p.ld_res = ld_res;
-    p.ld_gate = ld_gate;
-    p.lam = lambda_skip;
-    p.lam_vector = lambda_vector ? 1 : 0;
-    p.act = activation;
-    p.rows = rows;
-    p.M = M;
-    p.out = out;
-    if (tail_wide(M, ld_res, ld_gate, {y, residual, gate, lambda_vector ? lambda_skip : nullptr, out}))
-      hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, 8>), tail_grid(rows, M, 8), dim3(kTailThreads), 0, stream, p);
-    else
-      hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, 1>), tail_grid(rows, M, 1), dim3(kTailThreads), 0, stream, p);
-    return hip_status(fn, hipGetLastError());
+    return with_io(out_dtype, [&](auto ov) {
+      using IO = decltype(io);
+      using OUT = decltype(ov);
+      TailParams<IO, OUT> p{};
+      p.y = y;
+      p.res = static_cast<const IO *>(residual);
+      p.gate = static_cast<const IO *>(gate);
+      p.ld_res = ld_res;
+      p.ld_gate = ld_gate;
+      p.lam = lambda_skip;
+      p.lam_vector = lambda_vector ? 1 : 0;
+      p.act = activation;
+      p.rows = rows;
+      p.M = M;
+      p.out = static_cast<OUT *>(out);
+      if (tail_wide(M, ld_res, ld_gate, {y, residual, gate, lambda_vector ? lambda_skip : nullptr, out}))
+        hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, OUT, 8>), tail_grid(rows, M, 8), dim3(kTailThreads), 0, stream,
+                           p);
+      else
+        hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, OUT, 1>), tail_grid(rows, M, 1), dim3(kTailThreads), 0, stream,
+                           p);
+      return hip_status(fn, hipGetLastError());
+    });
   });
 }
 
-int kla_gate_skip_bwd(int dtype, const float *dout, const float *y, const void *residual, int64_t ld_res,
-                      const void *gate, int64_t ld_gate, const float *lambda_skip, int lambda_vector, int activation,
-                      float *dy, void *dres, void *dgate, float *dlambda, int64_t rows, int64_t M, void *workspace,
-                      size_t workspace_bytes, hipStream_t stream) {
+int kla_gate_skip_bwd(int dtype, int out_dtype, const void *dout, const float *y, const void *residual,
+                      int64_t ld_res, const void *gate, int64_t ld_gate, const float *lambda_skip, int lambda_vector,
+                      int activation, float *dy, void *dres, void *dgate, float *dlambda, int64_t rows, int64_t M,
+                      void *workspace, size_t workspace_bytes, hipStream_t stream) {
   const char *fn = "kla_gate_skip_bwd";
   int rc = check_tail(fn, dtype, residual, ld_res, gate, ld_gate, lambda_skip, activation, rows, M);
   if (rc != KLA_OK) return rc;
+  if (out_dtype != KLA_DTYPE_F32 && out_dtype != KLA_DTYPE_BF16)
+    return fail(KLA_ERR_DTYPE, "%s: unsupported out dtype %d", fn, out_dtype);
   if (M == 0) return KLA_OK;
   if (residual && !dlambda) return fail(KLA_ERR_INVALID_ARG, "%s: a residual needs dlambda", fn);
   const int64_t nblk = (rows + kTailRows - 1) / kTailRows;
   if (nblk >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
   if (rows > 0 && (!dout || !y || !dy)) return fail(KLA_ERR_INVALID_ARG, "%s: dout, y and dy must not be NULL", fn);
   const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
-  if (!all_aligned(4, {dout, y, lambda_skip, dy, dlambda}) || misaligned_bytes(dres, el) ||
-      misaligned_bytes(dgate, el))
+  if (!all_aligned(4, {y, lambda_skip, dy, dlambda}) || misaligned_bytes(dres, el) ||
+      misaligned_bytes(dgate, el) || misaligned_bytes(dout, out_dtype == KLA_DTYPE_F32 ? 4 : 2))
     return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
   float *ws = static_cast<float *>(workspace);
   if (residual) {
@@ -971,28 +981,33 @@ int kla_gate_skip_bwd(int dtype, const float *dout, const float *y, const void *
     float *part = ws;
     float *colsum = ws ? ws + nblk * M : nullptr;
     if (rows > 0) {
-      TailParams<IO> p{};
-      p.y = y;
-      p.res = static_cast<const IO *>(residual);
-      p.gate = static_cast<const IO *>(gate);
-      p.ld_res = ld_res;
-      p.ld_gate = ld_gate;
-      p.lam = lambda_skip;
-      p.lam_vector = lambda_vector ? 1 : 0;
-      p.act = activation;
-      p.rows = rows;
-      p.M = M;
-      p.dout = dout;
-      p.dy = dy;
-      p.dres = static_cast<IO *>(dres);
-      p.dgate = static_cast<IO *>(dgate);
-      p.part_lam = part;
-      if (tail_wide(M, ld_res, ld_gate,
-                    {dout, y, residual, gate, lambda_vector ? lambda_skip : nullptr, dy, dres, dgate, part}))
-        hipLaunchKernelGGL((gate_skip_bwd_kernel<IO, 8>), tail_grid(rows, M, 8), dim3(kTailThreads), 0, stream, p);
-      else
-        hipLaunchKernelGGL((gate_skip_bwd_kernel<IO, 1>), tail_grid(rows, M, 1), dim3(kTailThreads), 0, stream, p);
-      int st = hip_status(fn, hipGetLastError());
+      const int st = with_io(out_dtype, [&](auto ov) {
+        using OUT = decltype(ov);
+        TailParams<IO, OUT> p{};
+        p.y = y;
+        p.res = static_cast<const IO *>(residual);
+        p.gate = static_cast<const IO *>(gate);
+        p.ld_res = ld_res;
+        p.ld_gate = ld_gate;
+        p.lam = lambda_skip;
+        p.lam_vector = lambda_vector ? 1 : 0;
+        p.act = activation;
+        p.rows = rows;
+        p.M = M;
+        p.dout = static_cast<const OUT *>(dout);
+        p.dy = dy;
+        p.dres = static_cast<IO *>(dres);
+        p.dgate = static_cast<IO *>(dgate);
+        p.part_lam = part;
+        if (tail_wide(M, ld_res, ld_gate,
+                      {dout, y, residual, gate, lambda_vector ? lambda_skip : nullptr, dy, dres, dgate, part}))
+          hipLaunchKernelGGL((gate_skip_bwd_kernel<IO, OUT, 8>), tail_grid(rows, M, 8), dim3(kTailThreads), 0,
+                             stream, p);
+        else
+          hipLaunchKernelGGL((gate_skip_bwd_kernel<IO, OUT, 1>), tail_grid(rows, M, 1), dim3(kTailThreads), 0,
+                             stream, p);
+        return hip_status(fn, hipGetLastError());
+      });
       if (st != KLA_OK) return st;
     }
     if (!residual) return KLA_OK;

@@ -326,8 +326,13 @@ class KLALayer(nn.Module):
                 # skip + gate as one HIP kernel each way (kla.ops.hip.tail); same values.
                 from kla.ops.hip.tail import gate_skip_hip
 
+                # Under bf16 autocast the output projection takes y in bf16: the
+                # kernel writes it rounded (the same values), so no cast follows.
+                autocast_bf16 = (torch.is_autocast_enabled(y.device.type)
+                                 and torch.get_autocast_dtype(y.device.type) == torch.bfloat16)
                 y = gate_skip_hip(y, residual if self.lambda_skip is not None else None, gate, self.lambda_skip,
-                                  cfg.gating_activation)
+                                  cfg.gating_activation,
+                                  out_dtype=torch.bfloat16 if autocast_bf16 else torch.float32)
             else:
                 if self.lambda_skip is not None:
                     y = y + self.lambda_skip * residual

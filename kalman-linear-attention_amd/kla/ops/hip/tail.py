@@ -31,24 +31,28 @@ def _ld(t: Optional[torch.Tensor]) -> int:
     return 0 if t is None else _sensor_rows(t)
 
 
+def _code(dtype: torch.dtype) -> int:
+    return _lib.KLA_DTYPE_BF16 if dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32
+
+
 @torch.library.custom_op("kla_hip::gate_skip", mutates_args=())
 def _tail_op(y: torch.Tensor, residual: Optional[torch.Tensor], gate: Optional[torch.Tensor],
-             lambda_skip: Optional[torch.Tensor], activation: int) -> torch.Tensor:
-    """out [B, L, M] fp32 = (y + lambda_skip * residual) * act(gate)."""
+             lambda_skip: Optional[torch.Tensor], activation: int, out_bf16: bool) -> torch.Tensor:
+    """out [B, L, M] = (y + lambda_skip * residual) * act(gate), fp32 or (out_bf16) bf16."""
     dev = _require_device(y, residual, gate, lambda_skip)
     B, L, M = y.shape
-    out = torch.empty(B, L, M, dtype=torch.float32, device=dev)
+    out = torch.empty(B, L, M, dtype=torch.bfloat16 if out_bf16 else torch.float32, device=dev)
     pt = _lib.ptr
     _lib.check("kla_gate_skip_fwd", _lib.lib().kla_gate_skip_fwd(
-        _io(residual, gate), pt(y), pt(residual), _ld(residual), pt(gate), _ld(gate), pt(lambda_skip),
-        int(lambda_skip is not None and lambda_skip.dim() == 1), activation, pt(out), B * L, M,
+        _io(residual, gate), _code(out.dtype), pt(y), pt(residual), _ld(residual), pt(gate), _ld(gate),
+        pt(lambda_skip), int(lambda_skip is not None and lambda_skip.dim() == 1), activation, pt(out), B * L, M,
         torch.cuda.current_stream(dev).cuda_stream))
     return out
 
 
 @_tail_op.register_fake
-def _(y, residual, gate, lambda_skip, activation):
-    return torch.empty_like(y)
+def _(y, residual, gate, lambda_skip, activation, out_bf16):
+    return torch.empty_like(y, dtype=torch.bfloat16 if out_bf16 else torch.float32)
 
 
 @torch.library.custom_op("kla_hip::gate_skip_backward", mutates_args=())
@@ -69,8 +73,8 @@ def _tail_bwd_op(dout: torch.Tensor, y: torch.Tensor, residual: Optional[torch.T
     ws, stream = _lib.scratch(need, dev)
     pt = _lib.ptr
     _lib.check("kla_gate_skip_bwd", _lib.lib().kla_gate_skip_bwd(
-        _io(residual, gate), pt(dout), pt(y), pt(residual), _ld(residual), pt(gate), _ld(gate), pt(lambda_skip),
-        int(lambda_skip is not None and lambda_skip.dim() == 1), activation, pt(dy),
+        _io(residual, gate), _code(dout.dtype), pt(dout), pt(y), pt(residual), _ld(residual), pt(gate), _ld(gate),
+        pt(lambda_skip), int(lambda_skip is not None and lambda_skip.dim() == 1), activation, pt(dy),
         pt(dres) if dres.numel() else None, pt(dgate) if dgate.numel() else None,
         pt(dlam) if residual is not None else None, rows, M, pt(ws), ws.numel(), stream))
     return dy, dres, dgate, dlam
@@ -85,7 +89,7 @@ def _(dout, y, residual, gate, lambda_skip, activation, need_res, need_gate):
 
 
 def _setup(ctx, inputs, output):
-    y, residual, gate, lambda_skip, activation = inputs
+    y, residual, gate, lambda_skip, activation, out_bf16 = inputs
     ctx.activation = activation
     ctx.has = (residual is not None, gate is not None, lambda_skip is not None)
     ctx.save_for_backward(y, residual, gate, lambda_skip)
@@ -99,23 +103,28 @@ def _backward(ctx, dout):
     lambda_skip = lambda_skip if has_lam else None
     need_res = has_res and ctx.needs_input_grad[1]
     need_gate = has_gate and ctx.needs_input_grad[2]
-    dy, dres, dgate, dlam = _tail_bwd_op(dout.float().contiguous(), y, residual, gate, lambda_skip,
-                                         ctx.activation, need_res, need_gate)
+    if dout.dtype not in (torch.float32, torch.bfloat16):
+        dout = dout.float()
+    dy, dres, dgate, dlam = _tail_bwd_op(dout.contiguous(), y, residual, gate, lambda_skip, ctx.activation,
+                                         need_res, need_gate)
     return (dy, dres if need_res else None, dgate if need_gate else None,
-            dlam if has_res and ctx.needs_input_grad[3] else None, None)
+            dlam if has_res and ctx.needs_input_grad[3] else None, None, None)
 
 
 _tail_op.register_autograd(_backward, setup_context=_setup)
 
 
 def gate_skip_hip(y: torch.Tensor, residual: Optional[torch.Tensor], gate: Optional[torch.Tensor],
-                  lambda_skip: Optional[torch.Tensor], activation: str = "silu") -> torch.Tensor:
-    """(y + lambda_skip * residual) * act(gate), fp32 [B, L, M].
+                  lambda_skip: Optional[torch.Tensor], activation: str = "silu",
+                  out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """(y + lambda_skip * residual) * act(gate), [B, L, M] of ``out_dtype``.
 
     y: fp32 [B, L, M]. residual, gate: [B, L, M] of one dtype (fp32 or bf16) with
     rows that share one stride (views such as a half of the input projection are
     read in place), or None when the layer has no skip / no gate. lambda_skip:
-    fp32 0-dim or [M] tensor, required with a residual.
+    fp32 0-dim or [M] tensor, required with a residual. ``out_dtype`` bf16 gives
+    the fp32 result rounded to nearest even -- what autocast hands the output
+    projection -- without a separate cast; its gradient comes back in bf16.
     """
     if residual is not None and lambda_skip is None:
         raise ValueError("a residual needs lambda_skip")
@@ -128,4 +137,7 @@ def gate_skip_hip(y: torch.Tensor, residual: Optional[torch.Tensor], gate: Optio
     lam = lambda_skip if residual is not None else None
     if lam is not None and (lam.dtype != torch.float32 or not lam.is_contiguous()):
         lam = lam.float().contiguous()
-    return _tail_op(y.float().contiguous(), residual, gate, lam, ACTIVATIONS[activation])
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"out_dtype must be float32 or bfloat16, got {out_dtype}")
+    return _tail_op(y.float().contiguous(), residual, gate, lam, ACTIVATIONS[activation],
+                    out_dtype == torch.bfloat16)

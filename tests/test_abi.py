@@ -298,11 +298,13 @@ def test_sensor_row_layouts():
 def test_gate_skip_validation(lib):
     P = ALIGNED
 
-    def fwd(dtype=_lib.KLA_DTYPE_BF16, y=P, res=P, ld_res=8, gate=P, ld_gate=16, lam=P, vec=0, act=1, out=P,
-            shape=(5, 8)):
-        return lib.kla_gate_skip_fwd(dtype, y, res, ld_res, gate, ld_gate, lam, vec, act, out, *shape, None)
+    def fwd(dtype=_lib.KLA_DTYPE_BF16, odt=_lib.KLA_DTYPE_F32, y=P, res=P, ld_res=8, gate=P, ld_gate=16, lam=P,
+            vec=0, act=1, out=P, shape=(5, 8)):
+        return lib.kla_gate_skip_fwd(dtype, odt, y, res, ld_res, gate, ld_gate, lam, vec, act, out, *shape, None)
 
     assert fwd(dtype=9) == _lib.KLA_ERR_DTYPE
+    assert fwd(odt=9) == _lib.KLA_ERR_DTYPE
+    assert fwd(odt=_lib.KLA_DTYPE_BF16, out=P + 1) == _lib.KLA_ERR_ALIGN
     assert fwd(act=4) == _lib.KLA_ERR_INVALID_ARG
     assert fwd(lam=None) == _lib.KLA_ERR_INVALID_ARG
     assert "needs lambda_skip" in err(lib)
@@ -314,12 +316,13 @@ def test_gate_skip_validation(lib):
     n = lib.kla_gate_skip_workspace_bytes(5, 8)
     assert n >= 4 * (1 * 8 + 8 + 1)
 
-    def bwd(dl=P, ws=WS, nbytes=n, dres=P, dy=P):
-        return lib.kla_gate_skip_bwd(_lib.KLA_DTYPE_BF16, P, P, P, 8, P, 16, P, 0, 1, dy, dres, P, dl, 5, 8, ws,
-                                     nbytes, None)
+    def bwd(dl=P, ws=WS, nbytes=n, dres=P, dy=P, dout=P):
+        return lib.kla_gate_skip_bwd(_lib.KLA_DTYPE_BF16, _lib.KLA_DTYPE_BF16, dout, P, P, 8, P, 16, P, 0, 1, dy,
+                                     dres, P, dl, 5, 8, ws, nbytes, None)
 
     assert bwd(dl=None) == _lib.KLA_ERR_INVALID_ARG
     assert bwd(ws=None) == _lib.KLA_ERR_WORKSPACE
     assert bwd(nbytes=n - 4) == _lib.KLA_ERR_WORKSPACE
     assert bwd(dres=P + 1) == _lib.KLA_ERR_ALIGN
     assert bwd(dy=None) == _lib.KLA_ERR_INVALID_ARG
+    assert bwd(dout=P + 1) == _lib.KLA_ERR_ALIGN

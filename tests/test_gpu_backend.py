@@ -819,11 +819,12 @@ def _tail_reference(y, res, gate, lam, act):
     return y
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("act,skip", [(a, k) for a in ("silu", "gelu", "relu", None)
                                       for k in ("scalar", "vector", None) if a or k])
 @pytest.mark.parametrize("shape", [(2, 70, 300), (1, 33, 7), (3, 16, 256)])
-def test_gate_skip_matches_torch_autograd(cuda, shape, act, skip, dtype):
+def test_gate_skip_matches_torch_autograd(cuda, shape, act, skip, dtype, out_dtype):
     """gate_skip_hip against torch's own chain and autograd on the same tensors:
     the output, dy, d residual, d gate (a strided half of a projection) and
     d lambda_skip, with torch's bf16 roundings (0-dim lambda * bf16 residual in
@@ -846,19 +847,22 @@ def test_gate_skip_matches_torch_autograd(cuda, shape, act, skip, dtype):
         gate = pj[..., M:] if act is not None else None
         r_in = rr if skip is not None else None
         if fused:
-            out = gate_skip_hip(yy, r_in, gate, ll if skip is not None else None, act or "silu")
+            out = gate_skip_hip(yy, r_in, gate, ll if skip is not None else None, act or "silu", out_dtype=out_dtype)
         else:
-            out = _tail_reference(yy, r_in, gate, ll, act)
-        assert out.dtype == torch.float32
-        out.backward(dout)
+            # bf16 out: torch's fp32 result cast, as autocast casts the output projection's input.
+            out = _tail_reference(yy, r_in, gate, ll, act).to(out_dtype)
+        assert out.dtype == out_dtype
+        out.backward(dout.to(out_dtype))
         outs.append((out.detach(), yy.grad, rr.grad, pj.grad, ll.grad))
-    tol = dict(rtol=1e-5, atol=1e-6) if dtype == torch.float32 else dict(rtol=8e-3, atol=2e-3)
+    tight, loose = dict(rtol=1e-5, atol=1e-6), dict(rtol=8e-3, atol=2e-3)
     names = ("out", "dy", "dres", "dproj", "dlam")
     for name, a, b in zip(names, outs[0], outs[1]):
         if b is None:
             assert a is None or not a.any(), name
             continue
         assert a.dtype == b.dtype, name
+        # A bf16 value may sit one bf16 ulp apart where an fp32 ulp decides its rounding.
+        tol = tight if a.dtype == torch.float32 and dtype == torch.float32 else loose
         check(name, a.float(), b.float().cpu().numpy(), **tol)
 
 
