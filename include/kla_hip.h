@@ -347,6 +347,23 @@ int kla_gate_skip_bwd(int dtype, int out_dtype, const void *dout, const float *y
                       int activation, float *dy, void *dres, void *dgate, float *dlambda, int64_t rows, int64_t M,
                       void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Inference kernels of the sequence model around the KLA layers (no gradient):
+ * RMSNorm, y = ((x * rsqrt(mean(x^2) + eps)) * weight) in x's dtype, over rows
+ * of `dim` (x, y dense [rows, dim] of `dtype`, weight fp32 [dim]); replaces
+ * RMSNorm.forward (reference src/kla/layers/common.py:45-55).
+ */
+int kla_rms_norm_fwd(int dtype, const void *x, const float *weight, float eps, void *y, int64_t rows, int64_t dim,
+                     hipStream_t stream);
+
+/*
+ * SwiGLU activation: out = silu(h[:, :hidden]) * h[:, hidden:2 hidden] (h rows
+ * ld_h elements apart, out dense [rows, hidden], both of `dtype`); replaces the
+ * `F.silu(gate) * up` of MLP.forward (reference src/kla/layers/common.py:120-123).
+ */
+int kla_swiglu_fwd(int dtype, const void *h, int64_t ld_h, void *out, int64_t rows, int64_t hidden,
+                   hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,7 @@
 #pragma GCC visibility pop
 
 #include "gate_skip.hpp"
+#include "model_ops.hpp"
 #include "fused_kla.hpp"
 #include "lookback_scan.hpp"
 
@@ -25,7 +26,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 7;
+constexpr int kAbiVersion = 8;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -1028,6 +1029,53 @@ int kla_gate_skip_bwd(int dtype, int out_dtype, const void *dout, const float *y
     hipLaunchKernelGGL(round_scalar_kernel<IO>, dim3(1), dim3(64), 0, stream, total, dlambda);
     return hip_status(fn, hipGetLastError());
   });
+}
+
+// ------------------------------------------------------- sequence-model kernels
+
+int kla_rms_norm_fwd(int dtype, const void *x, const float *weight, float eps, void *y, int64_t rows, int64_t dim,
+                     hipStream_t stream) {
+  const char *fn = "kla_rms_norm_fwd";
+  if (rows < 0 || dim < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative shape", fn);
+  if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16) return fail(KLA_ERR_DTYPE, "%s: unsupported dtype %d", fn, dtype);
+  if (rows == 0 || dim == 0) return KLA_OK;
+  if (!x || !weight || !y) return fail(KLA_ERR_INVALID_ARG, "%s: x, weight and y must not be NULL", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (misaligned_bytes(x, el) || misaligned_bytes(y, el) || misaligned(weight))
+    return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
+  const int64_t per = kNormThreads / kWave;
+  if ((rows + per - 1) / per >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
+  const dim3 grid(static_cast<uint32_t>((rows + per - 1) / per));
+  if (dtype == KLA_DTYPE_F32)
+    hipLaunchKernelGGL(rms_norm_fwd_kernel<float>, grid, dim3(kNormThreads), 0, stream, static_cast<const float *>(x),
+                       weight, eps, static_cast<float *>(y), rows, dim);
+  else
+    hipLaunchKernelGGL(rms_norm_fwd_kernel<bf16_t>, grid, dim3(kNormThreads), 0, stream,
+                       static_cast<const bf16_t *>(x), weight, eps, static_cast<bf16_t *>(y), rows, dim);
+  return hip_status(fn, hipGetLastError());
+}
+
+int kla_swiglu_fwd(int dtype, const void *h, int64_t ld_h, void *out, int64_t rows, int64_t hidden,
+                   hipStream_t stream) {
+  const char *fn = "kla_swiglu_fwd";
+  if (rows < 0 || hidden < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative shape", fn);
+  if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16) return fail(KLA_ERR_DTYPE, "%s: unsupported dtype %d", fn, dtype);
+  if (rows == 0 || hidden == 0) return KLA_OK;
+  if (!h || !out) return fail(KLA_ERR_INVALID_ARG, "%s: h and out must not be NULL", fn);
+  if (ld_h < 2 * hidden) return fail(KLA_ERR_INVALID_ARG, "%s: row stride below 2 * hidden", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (misaligned_bytes(h, el) || misaligned_bytes(out, el))
+    return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
+  const int64_t n = rows * hidden;
+  if ((n + 255) / 256 >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many elements", fn);
+  const dim3 grid(static_cast<uint32_t>((n + 255) / 256));
+  if (dtype == KLA_DTYPE_F32)
+    hipLaunchKernelGGL(swiglu_fwd_kernel<float>, grid, dim3(256), 0, stream, static_cast<const float *>(h), ld_h,
+                       static_cast<float *>(out), rows, hidden);
+  else
+    hipLaunchKernelGGL(swiglu_fwd_kernel<bf16_t>, grid, dim3(256), 0, stream, static_cast<const bf16_t *>(h), ld_h,
+                       static_cast<bf16_t *>(out), rows, hidden);
+  return hip_status(fn, hipGetLastError());
 }
 
 }  // extern "C"

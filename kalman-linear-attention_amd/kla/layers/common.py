@@ -39,15 +39,35 @@ def inv_softplus_dt_init(shape, dt_min: float, dt_max: float, dt_init_floor: flo
     return dt + torch.log(-torch.expm1(-dt))
 
 
+def _hip_inference(backend: str, *tensors: torch.Tensor) -> bool:
+    """Whether a module with kla backend ``backend`` runs its inference kernel on
+    the MI355X: a hip-family backend on a ROCm GPU and no gradient to carry."""
+    if backend == "torch" or not tensors[0].is_cuda:
+        return False
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        return False
+    from kla.ops.kla_ops import _step_on_hip
+
+    return _step_on_hip(backend, tensors[0])
+
+
 class RMSNorm(nn.Module):
-    """x * rsqrt(mean(x^2) + eps) * weight, computed in float32."""
+    """x * rsqrt(mean(x^2) + eps) * weight, computed in float32.
+
+    ``backend`` is the kla backend of the model it sits in (set by the model);
+    on a hip-family backend, inference (no gradient) uses one HIP kernel."""
 
     def __init__(self, dim: int, eps: float = 1e-5):
         super().__init__()
         self.eps = eps
         self.weight = nn.Parameter(torch.ones(dim))
+        self.backend = "torch"
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.dtype in (torch.float32, torch.bfloat16) and _hip_inference(self.backend, x, self.weight):
+            from kla.ops.hip.model_ops import rms_norm_hip
+
+            return rms_norm_hip(x, self.weight, self.eps)
         xf = x.float()
         xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
         return (xf * self.weight.float()).to(x.dtype)
@@ -112,6 +132,7 @@ class MLP(nn.Module):
         super().__init__()
         hidden = int(dim * ratio)
         self.kind = kind
+        self.backend = "torch"   # the model's kla backend (see RMSNorm)
         if kind == "swiglu":
             hidden = int(2 * hidden / 3)
             self.w12 = nn.Linear(dim, 2 * hidden, bias=bias)
@@ -124,6 +145,11 @@ class MLP(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.kind == "swiglu":
-            gate, up = self.w12(x).chunk(2, dim=-1)
+            h = self.w12(x)
+            if h.dtype in (torch.float32, torch.bfloat16) and _hip_inference(self.backend, h):
+                from kla.ops.hip.model_ops import swiglu_hip
+
+                return self.w3(swiglu_hip(h))
+            gate, up = h.chunk(2, dim=-1)
             return self.w3(F.silu(gate) * up)
         return self.w2(F.gelu(self.w1(x)))

@@ -51,6 +51,11 @@ class Block(nn.Module):
         else:
             self.mlp_norm = None
             self.mlp = None
+        # The norms and the MLP follow the mixer's kla backend for their inference kernels.
+        backend = getattr(mixer_config, "backend", "torch")
+        for m in (self.mixer_norm, self.mlp_norm, self.mlp):
+            if m is not None:
+                m.backend = backend
 
     def mix(self, x: torch.Tensor):
         """Sequence-mixing half: (x + mixer(norm(x)), variance or None). Stateless."""
@@ -90,6 +95,7 @@ class SequenceModel(MarginalReadout, nn.Module):
         self.embedding = nn.Embedding(config.vocab_size, config.d_model)
         self.blocks = nn.ModuleList(Block(config.d_model, m, config) for m in mixers)
         self.norm_f = RMSNorm(config.d_model, config.norm_eps)
+        self.norm_f.backend = getattr(mixers[-1], "backend", "torch") if mixers else "torch"
         self.lm_head = nn.Linear(config.d_model, config.vocab_size, bias=False)
         if config.tie_embeddings:
             self.lm_head.weight = self.embedding.weight

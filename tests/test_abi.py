@@ -326,3 +326,15 @@ def test_gate_skip_validation(lib):
     assert bwd(dres=P + 1) == _lib.KLA_ERR_ALIGN
     assert bwd(dy=None) == _lib.KLA_ERR_INVALID_ARG
     assert bwd(dout=P + 1) == _lib.KLA_ERR_ALIGN
+
+
+def test_model_kernels_validation(lib):
+    P = ALIGNED
+    assert lib.kla_rms_norm_fwd(5, P, P, 1e-5, P, 4, 8, None) == _lib.KLA_ERR_DTYPE
+    assert lib.kla_rms_norm_fwd(_lib.KLA_DTYPE_F32, None, P, 1e-5, P, 4, 8, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_rms_norm_fwd(_lib.KLA_DTYPE_F32, ODD, P, 1e-5, P, 4, 8, None) == _lib.KLA_ERR_ALIGN
+    assert lib.kla_rms_norm_fwd(_lib.KLA_DTYPE_F32, None, None, 1e-5, None, 0, 8, None) == _lib.KLA_OK
+    assert lib.kla_swiglu_fwd(_lib.KLA_DTYPE_BF16, P, 7, P, 4, 4, None) == _lib.KLA_ERR_INVALID_ARG
+    assert "row stride" in err(lib)
+    assert lib.kla_swiglu_fwd(_lib.KLA_DTYPE_BF16, P + 1, 8, P, 4, 4, None) == _lib.KLA_ERR_ALIGN
+    assert lib.kla_swiglu_fwd(_lib.KLA_DTYPE_BF16, None, 8, None, 0, 4, None) == _lib.KLA_OK

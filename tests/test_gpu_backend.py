@@ -902,3 +902,71 @@ def test_layer_tail_on_hip_matches_torch_tail(cuda, tag, autocast):
     assert outs[0][1].keys() == outs[1][1].keys()
     for n in outs[0][1]:
         check("d" + n, outs[0][1][n], outs[1][1][n].cpu().numpy(), **tol)
+
+
+# ------------------------------------------- sequence-model inference kernels
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(16, 1, 512), (3, 7, 100), (2, 300, 64), (5, 3)])
+def test_rms_norm_kernel_matches_torch(cuda, shape, dtype):
+    """rms_norm_hip against the RMSNorm formula (reference common.py:45-55) in torch."""
+    from kla.ops.hip.model_ops import rms_norm_hip
+
+    g = torch.Generator().manual_seed(31)
+    x = (torch.randn(*shape, generator=g) * 3).to(dtype).to(cuda)
+    w = (torch.rand(shape[-1], generator=g) + 0.5).to(cuda)
+    xf = x.float()
+    want = (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + 1e-5) * w).to(dtype)
+    got = rms_norm_hip(x, w, 1e-5)
+    assert got.dtype == dtype and got.shape == x.shape
+    tol = dict(rtol=2e-6, atol=1e-7) if dtype == torch.float32 else dict(rtol=8e-3, atol=1e-3)
+    check("rmsnorm", got.float(), want.float().cpu().numpy(), **tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(16, 1, 2 * 1365), (2, 37, 2 * 7), (4, 2 * 64)])
+def test_swiglu_kernel_matches_torch(cuda, shape, dtype):
+    """swiglu_hip against F.silu(gate) * up of MLP.forward (reference common.py:120-123)."""
+    import torch.nn.functional as F
+
+    from kla.ops.hip.model_ops import swiglu_hip
+
+    h = torch.randn(*shape, generator=torch.Generator().manual_seed(32)).to(dtype).to(cuda)
+    gate, up = h.chunk(2, dim=-1)
+    want = F.silu(gate) * up
+    got = swiglu_hip(h)
+    assert got.dtype == dtype and got.shape == want.shape
+    if dtype == torch.float32:
+        check("swiglu", got, want.cpu().numpy(), rtol=2e-6, atol=1e-7)
+    else:
+        assert torch.equal(got, want)
+
+
+def test_sequence_model_inference_kernels_match_torch(cuda):
+    """A SequenceModel on the hip backend with its norms and SwiGLU on the HIP
+    kernels equals the same model with those modules on torch: prefill logits and
+    state, then decode steps."""
+    import copy
+
+    torch.manual_seed(0)
+    model = SequenceModel(ModelConfig(vocab_size=300, d_model=64, n_layers=2),
+                          KLAConfig(d_state=8, backend="hip")).to(cuda).eval()
+    other = copy.deepcopy(model)
+    for m in other.modules():
+        if hasattr(m, "backend") and not isinstance(m, KLALayer):
+            m.backend = "torch"
+    ids = torch.randint(0, 300, (3, 40), generator=torch.Generator().manual_seed(1)).to(cuda)
+    with torch.no_grad():
+        outs = []
+        for m in (model, other):
+            st = m.init_state(3)
+            logits, st = m(ids, state=st)
+            steps = [logits]
+            tok = logits[:, -1:].argmax(-1)
+            for _ in range(3):
+                lg, st = m(tok, state=st)
+                steps.append(lg)
+            outs.append(steps)
+    for i, (a, b) in enumerate(zip(*outs)):
+        check(f"logits{i}", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
