@@ -1133,8 +1133,10 @@ __global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodePa
 // One token of the depthwise causal conv (CausalConv1d, reference common.py:70-96):
 // window = [state[b, d, :], x[b, d]], y = act(sum_j w[d, j] window[j] + bias[d]),
 // new state = window[1:]. One thread per (b, d).
-__global__ void conv_step_kernel(const float *__restrict__ x, int64_t ld_x, const float *__restrict__ state,
-                                 float *__restrict__ state_out, const float *__restrict__ w,
+// state_out may alias state: each thread reads its window before writing it, and
+// the shift writes position j only after reading j + 1 (no __restrict__ on either).
+__global__ void conv_step_kernel(const float *__restrict__ x, int64_t ld_x, const float *state,
+                                 float *state_out, const float *__restrict__ w,
                                  const float *__restrict__ bias, int act, float *__restrict__ y, int64_t batch,
                                  int64_t D, int K) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;

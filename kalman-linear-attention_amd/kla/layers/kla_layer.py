@@ -80,6 +80,9 @@ class KLALayer(nn.Module):
             self.lambda_skip = None
 
         self.gate_act = get_activation(cfg.gating_activation) if cfg.use_gating else None
+        # One-token hip decode writes the new state over the state it was given
+        # (set by a decode graph that owns its state buffers); otherwise new tensors.
+        self._decode_in_place = False
         self.out_proj = nn.Linear(M, d_model, bias=cfg.bias)
         self.reset_parameters()
 
@@ -268,13 +271,15 @@ class KLALayer(nn.Module):
         if self.var_expand is not None:
             log_var = self.var_expand(log_var)
         skip = self.lambda_skip.float() if self.lambda_skip is not None else None
+        lam, eta = ssm_state.lam.contiguous(), ssm_state.eta.contiguous()
+        in_place = self._decode_in_place and lam is ssm_state.lam and eta is ssm_state.eta
         y, y_var, lam, eta = decode_step_hip(
-            v, log_var, k, q, self.delta.float(), self.lambda_log.float(), self.process_noise.float(),
-            ssm_state.lam.contiguous(), ssm_state.eta.contiguous(), residual=residual[:, 0] if skip is not None else None, lambda_skip=skip,
+            v, log_var, k, q, self.delta.float(), self.lambda_log.float(), self.process_noise.float(), lam, eta,
+            residual=residual[:, 0] if skip is not None else None, lambda_skip=skip,
             gate=gate[:, 0] if gate is not None else None, gate_activation=cfg.gating_activation,
             discretization=cfg.discretization, zero_process_noise=cfg.zero_process_noise, qk_norm=cfg.qk_norm,
             clip_value=cfg.clip_value, obs_var_min=cfg.obs_var_min, obs_var_max=cfg.obs_var_max,
-            decode_from_prior=cfg.decode_from_prior)
+            decode_from_prior=cfg.decode_from_prior, in_place=in_place)
         return y.unsqueeze(1), y_var.unsqueeze(1), KLAState(lam=lam, eta=eta)
 
     def forward(self, x: torch.Tensor, state: KLALayerState | None = None, return_state: bool = False):
@@ -302,8 +307,10 @@ class KLALayer(nn.Module):
                 from kla.ops.hip.decode import conv_step_hip
 
                 # A torch prefill leaves the window as a view of its padded input.
-                zc, conv_state = conv_step_hip(z[:, 0], conv_state.to(z.dtype).contiguous(),
-                                               self.conv.weight[:, 0, :], self.conv.bias, cfg.conv_activation)
+                window = conv_state.to(z.dtype).contiguous()
+                zc, conv_state = conv_step_hip(z[:, 0], window, self.conv.weight[:, 0, :], self.conv.bias,
+                                               cfg.conv_activation,
+                                               in_place=self._decode_in_place and window is state.conv)
                 z = zc.unsqueeze(1)
             else:
                 z, conv_state = self.conv(z, conv_state, hip=self._conv_on_hip(z))

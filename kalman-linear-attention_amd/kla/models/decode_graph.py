@@ -64,24 +64,37 @@ class DecodeGraph:
         def run():
             logits, new_state = model(self.token, state=self.state)
             for dst, src in zip(static, _flat(new_state)):
-                dst.copy_(src)
+                if src is not dst:
+                    dst.copy_(src)
             return logits
 
-        # Warm up on a side stream (allocator pools, library handles), then
-        # restore the prefill state and capture.
-        saved = [t.clone() for t in static]
-        side = torch.cuda.Stream(device)
-        side.wait_stream(torch.cuda.current_stream(device))
-        with torch.no_grad(), torch.cuda.stream(side):
-            for _ in range(warmup):
-                run()
-        torch.cuda.current_stream(device).wait_stream(side)
-        with torch.no_grad():
-            for dst, src in zip(static, saved):
-                dst.copy_(src)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.no_grad(), torch.cuda.graph(self.graph):
-            self.logits = run()
+        # Layers whose one-token step can write its new state over the old one
+        # (the hip decode kernels) do so here: the graph owns the state buffers,
+        # so no copy-back is captured for them.
+        in_place = [m for m in model.modules() if hasattr(m, "_decode_in_place")]
+        flags = [m._decode_in_place for m in in_place]
+        for m in in_place:
+            m._decode_in_place = True
+
+        try:
+            # Warm up on a side stream (allocator pools, library handles), then
+            # restore the prefill state and capture.
+            saved = [t.clone() for t in static]
+            side = torch.cuda.Stream(device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.no_grad(), torch.cuda.stream(side):
+                for _ in range(warmup):
+                    run()
+            torch.cuda.current_stream(device).wait_stream(side)
+            with torch.no_grad():
+                for dst, src in zip(static, saved):
+                    dst.copy_(src)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.no_grad(), torch.cuda.graph(self.graph):
+                self.logits = run()
+        finally:
+            for m, f in zip(in_place, flags):
+                m._decode_in_place = f
         # Capture does not execute the work; the state is still the prefill state.
 
     @torch.no_grad()

@@ -12,8 +12,10 @@ kernel (``kla_decode_step_fwd``). It covers:
 :func:`conv_step_hip` is the one-token depthwise causal conv with its window
 update (``src/kla/layers/common.py:70-96``).
 
-Both are forward-only and fp32, and both return new tensors for the new state
-instead of updating it in place, as the torch path does. The layer routes a
+Both are forward-only and fp32. By default both return new tensors for the new
+state, as the torch path does; with ``in_place=True`` they write it over the
+state they were given and return those tensors (a replayed decode graph keeps
+its state in fixed buffers that way, with no copies). The layer routes a
 one-token step here only when no gradient is required; every other call keeps
 the torch code.
 """
@@ -40,7 +42,7 @@ def _row_stride(t: torch.Tensor) -> int:
 def decode_step_hip(v, log_var, k, q, delta, lambda_log, process_noise, lam, eta, *, residual=None,
                     lambda_skip=None, gate=None, gate_activation="silu", discretization="ou",
                     zero_process_noise=False, qk_norm=True, clip_value=None, obs_var_min=1e-4, obs_var_max=None,
-                    decode_from_prior=False):
+                    decode_from_prior=False, in_place=False):
     """One SSM step of a KLALayer for one token.
 
     Inputs:
@@ -63,7 +65,12 @@ def decode_step_hip(v, log_var, k, q, delta, lambda_log, process_noise, lam, eta
     if (residual is None) != (lambda_skip is None):
         raise ValueError("residual and lambda_skip come together")
     y, y_var = torch.empty(B, M, device=dev), torch.empty(B, M, device=dev)
-    lam_out, eta_out = torch.empty_like(lam), torch.empty_like(eta)
+    if in_place:
+        if not (lam.is_contiguous() and eta.is_contiguous()):
+            raise ValueError("in-place decode needs contiguous state tensors")
+        lam_out, eta_out = lam, eta
+    else:
+        lam_out, eta_out = torch.empty_like(lam), torch.empty_like(eta)
     if B * M * S == 0:
         return y, y_var, lam_out, eta_out
     cfg = _lib.DecodeConfig(
@@ -91,13 +98,14 @@ def decode_step_hip(v, log_var, k, q, delta, lambda_log, process_noise, lam, eta
     return y, y_var, lam_out, eta_out
 
 
-def conv_step_hip(x, state, weight, bias, activation="silu"):
+def conv_step_hip(x, state, weight, bias, activation="silu", in_place=False):
     """One conv token: x [B, D] row view, state [B, D, K-1], weight [D, K], bias [D] or None.
-    Returns (y [B, D], new_state [B, D, K-1])."""
+    Returns (y [B, D], new_state [B, D, K-1]); with in_place, new_state is ``state``
+    itself, overwritten."""
     B, D = x.shape
     K = weight.shape[-1]
     y = torch.empty(B, D, device=x.device)
-    state_out = torch.empty_like(state)
+    state_out = state if in_place else torch.empty_like(state)
     if B * D == 0:
         return y, state_out
     pt = _lib.ptr

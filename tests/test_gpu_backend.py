@@ -970,3 +970,32 @@ def test_sequence_model_inference_kernels_match_torch(cuda):
             outs.append(steps)
     for i, (a, b) in enumerate(zip(*outs)):
         check(f"logits{i}", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
+
+
+def test_decode_kernels_in_place_equal_out_of_place(cuda):
+    """The one-token conv and SSM kernels give the same values when they write the
+    new state over the old one (what a decode graph does) as into new tensors."""
+    from kla.ops.hip.decode import conv_step_hip, decode_step_hip
+
+    g = torch.Generator().manual_seed(41)
+    B, D, K, M, S = 3, 40, 4, 40, 16
+    x = torch.randn(B, D, generator=g).to(cuda)
+    st = torch.randn(B, D, K - 1, generator=g).to(cuda)
+    w = torch.randn(D, K, generator=g).to(cuda)
+    bias = torch.randn(D, generator=g).to(cuda)
+    y0, s0 = conv_step_hip(x, st.clone(), w, bias)
+    st_in = st.clone()
+    y1, s1 = conv_step_hip(x, st_in, w, bias, in_place=True)
+    assert s1 is st_in and torch.equal(y0, y1) and torch.equal(s0, s1)
+
+    proj = torch.randn(B, 2 * M + 2 * S, generator=g).to(cuda)
+    v, lv, k, q = torch.split(proj, [M, M, S, S], dim=-1)
+    delta, ll, pn = (torch.randn(M, S, generator=g).to(cuda) * 0.3 for _ in range(3))
+    lam = (torch.rand(B, M, S, generator=g) + 0.5).to(cuda)
+    eta = torch.randn(B, M, S, generator=g).to(cuda)
+    out0 = decode_step_hip(v, lv, k, q, delta, ll, pn.abs(), lam.clone(), eta.clone())
+    lam_in, eta_in = lam.clone(), eta.clone()
+    out1 = decode_step_hip(v, lv, k, q, delta, ll, pn.abs(), lam_in, eta_in, in_place=True)
+    assert out1[2] is lam_in and out1[3] is eta_in
+    for a, b in zip(out0, out1):
+        assert torch.equal(a, b)
