@@ -64,13 +64,23 @@ WORKLOADS = {
 }
 DEFAULT_WORKLOAD = "mobius_affine_b8_t4096_l2048"
 
-# Compulsory HBM bytes per element (each input read once, each output written
-# once). Moebius with D == 1: fwd reads A, B, C and writes lam; bwd reads dlam,
-# A, B, C, lam and writes dA, dB, dC. Affine: fwd reads g, u and writes h; bwd
-# reads dh, g, h and writes dg, du. [batch, lanes] state tensors are excluded.
+# Compulsory HBM bytes per element of the reference's algorithm (each input read
+# once, each output written once). Moebius with D == 1: fwd reads A, B, C and
+# writes lam; bwd reads dlam, A, B, C, lam and writes dA, dB, dC. Affine: fwd
+# reads g, u and writes h; bwd reads dh, g, h and writes dg, du. [batch, lanes]
+# state tensors are excluded. The roofline's `achieved` is priced on these.
 def alg_bytes_per_elem(kernel: str, affine_dtype: torch.dtype) -> int:
     e = 2 if affine_dtype == torch.bfloat16 else 4
     return {"mobius_fwd": 16, "mobius_bwd": 32, "affine_fwd": 3 * e, "affine_bwd": 5 * e}[kernel]
+
+
+# Bytes per element the kernels themselves must move: the same, except that the
+# Moebius backward reads the saved lam once per 16 steps and recomputes the rest
+# from A, B, C (so 28 + 4/16 instead of 32).
+def kernel_bytes_per_elem(kernel: str, affine_dtype: torch.dtype) -> float:
+    if kernel == "mobius_bwd":
+        return 28 + 4 / 16
+    return float(alg_bytes_per_elem(kernel, affine_dtype))
 
 
 # ------------------------------------------------------------------ inputs
@@ -421,8 +431,11 @@ def main(argv=None) -> int:
     per_kernel_ms = time_kernels_in_step(kernels, args.steps, stream)
     per_kernel = {}
     for name, ms in per_kernel_ms.items():
-        nbytes = alg_bytes_per_elem(name, adt if name.startswith("affine") else torch.float32) * elems
-        per_kernel[name] = {"ms": round(ms, 4), "alg_bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        kdt = adt if name.startswith("affine") else torch.float32
+        nbytes = alg_bytes_per_elem(name, kdt) * elems
+        own = int(kernel_bytes_per_elem(name, kdt) * elems)
+        per_kernel[name] = {"ms": round(ms, 4), "alg_bytes": nbytes, "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                            "kernel_bytes": own, "kernel_GBps": round(own / (ms * 1e-3) / 1e9, 1)}
     dom = max(per_kernel, key=lambda k: per_kernel[k]["ms"])
     step_bytes = sum(v["alg_bytes"] for v in per_kernel.values())
     tokens = batch * steps
@@ -468,6 +481,10 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(per_kernel[dom]["GBps"] / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
+            # The same launch priced on the bytes the kernel itself must move.
+            "kernel_bytes": per_kernel[dom]["kernel_bytes"],
+            "kernel_GBps": per_kernel[dom]["kernel_GBps"],
+            "kernel_frac": round(per_kernel[dom]["kernel_GBps"] / PEAK_HBM_GBPS, 4),
         },
         "kernels": per_kernel,
         "wall_s": round(wall, 4),

@@ -92,7 +92,11 @@ int kla_mobius_scan_fwd(const float *A, const float *B, const float *C, const fl
  *   nu_t = dlam_t + gain_{t+1}*nu_{t+1}          (reverse scan, nu_T = 0)
  *   dA = nu*l_{t-1}/den, dB = nu/den, dC = -nu*l_t*l_{t-1}/den, dD = -nu*l_t/den
  *   dlam0 = nu_0*gain_0
- * lam: the forward's output. D, dD, lam0, dlam0 may be NULL (dD is written only
+ * lam: the forward's output. It is read only where a thread's block of steps
+ * begins (one row in 16); the values in between are recomputed from A, B, C, D
+ * with the forward's own step, which reproduces the forward's lam bit for bit,
+ * so lam must be exactly what kla_mobius_scan_fwd wrote for these inputs.
+ * D, dD, lam0, dlam0 may be NULL (dD is written only
  * when both D and dD are given); dA, dB, dC may be NULL to skip that output.
  * Replaces TiledMobiusScan.backward (tiled_mobius_scan.py:266-279).
  */

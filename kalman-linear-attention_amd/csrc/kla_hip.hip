@@ -43,7 +43,7 @@ struct Shape3 {
   static constexpr int W = W_, S = S_, V = V_;
 };
 using MobiusFwdTile = Shape3<void, 8, 12, 1>;
-using MobiusBwdTile = Shape3<void, 8, 32, 1>;
+using MobiusBwdTile = Shape3<void, 16, 16, 1>;
 using AffineFwdTile = Shape3<void, 16, 24, 1>;
 using AffineBwdTile = Shape3<void, 12, 32, 1>;
 using AffineFwdBf16Tile = Shape3<void, 8, 24, 2>;
@@ -91,14 +91,28 @@ Geom make_geom(Shape s, int W, int S, int V) {
   return g;
 }
 
-// A forward scan's output is stored cached (for the backward that follows) when
-// the whole [batch, steps, lanes] output fits MI355X's 256 MiB memory-side
-// cache; larger outputs stream. Measured in the fwd + bwd step with the output
-// cached: 256 MiB outputs (8 x 4096 x 2048 fp32, 8 x 8192 x 2048 bf16) gain
-// 1.5-3%, a 512 MiB output (8 x 8192 x 2048 fp32) loses 2-3%.
+// The affine forward's output h is stored cached (for the backward that reads it
+// next) when the whole [batch, steps, lanes] output fits MI355X's 256 MiB
+// memory-side cache; larger outputs stream. Measured in the fwd + bwd step with
+// the output cached: 256 MiB outputs (8 x 4096 x 2048 fp32, 8 x 8192 x 2048
+// bf16) gain 1.5-3%, a 512 MiB output (8 x 8192 x 2048 fp32) loses 2-3%.
 constexpr int64_t kCachedOutputBytes = 256ll << 20;
 
 bool output_fits_cache(Shape s, int64_t elem) { return s.batch * s.steps * s.lanes * elem <= kCachedOutputBytes; }
+
+// First scan position from which the Moebius forward loads its `tensors` fp32
+// inputs cached: the last steps whose inputs fill the memory-side cache (every
+// step when they all fit). The backward starts at the end of the sequence and
+// finds them there. Measured in the headline fwd + bwd step (8 x 4096 x 2048,
+// 768 MiB of A, B, C, the last third cached): Moebius bwd 350 -> 332 us and the
+// affine forward that follows 149 -> 139 us, for 197 -> 220 us in the Moebius
+// forward; caching the last sixth or all of the inputs gains less.
+int64_t cached_tail_from(Shape s, int64_t tensors) {
+  const int64_t per_step = s.batch * s.lanes * tensors * 4;
+  if (per_step <= 0) return 0;
+  const int64_t tail_steps = kCachedOutputBytes / per_step;
+  return tail_steps >= s.steps ? 0 : s.steps - tail_steps;
+}
 
 template <class T>
 Geom make_geom(Shape s) {
@@ -499,15 +513,13 @@ int kla_mobius_scan_fwd(const float *A, const float *B, const float *C, const fl
     return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
   rc = check_launch(fn, KLA_SCAN_MOBIUS_FWD, s, workspace, workspace_bytes);
   if (rc != KLA_OK) return rc;
-  auto run = [&](auto has_d, auto cached) {
-    using P = MobiusFwd<decltype(has_d)::value, decltype(cached)::value>;
-    return launch<P, MobiusFwdTile>(fn, typename P::Params{A, B, C, D, lam0, lam}, s, workspace, stream);
-  };
-  using T = std::true_type;
-  using F = std::false_type;
-  const bool cached = output_fits_cache(s, 4);
-  if (D) return cached ? run(T{}, T{}) : run(T{}, F{});
-  return cached ? run(F{}, T{}) : run(F{}, F{});
+  const int64_t from = cached_tail_from(s, D ? 4 : 3);
+  if (D) {
+    using P = MobiusFwd<true>;
+    return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, D, lam0, lam, from}, s, workspace, stream);
+  }
+  using P = MobiusFwd<false>;
+  return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, nullptr, lam0, lam, from}, s, workspace, stream);
 }
 
 int kla_mobius_scan_bwd(const float *dlam, const float *A, const float *B, const float *C,

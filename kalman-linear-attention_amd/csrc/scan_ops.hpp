@@ -226,6 +226,26 @@ __device__ __forceinline__ void store_v_cached(bf16_t *p, const float (&x)[V]) {
   }
 }
 
+// V consecutive sequence elements read with ordinary (cached) loads: the lines
+// stay in L2 and the memory-side cache for a kernel that reads them next.
+template <int V>
+__device__ __forceinline__ void load_v_cached(const float *p, float (&o)[V]) {
+  if constexpr (V == 1) {
+    o[0] = p[0];
+  } else if constexpr (V == 2) {
+    const f32x2 t = *reinterpret_cast<const f32x2 *>(p);
+    o[0] = t.x;
+    o[1] = t.y;
+  } else {
+    static_assert(V == 4, "V must be 1, 2 or 4");
+    const f32x4 t = *reinterpret_cast<const f32x4 *>(p);
+    o[0] = t.x;
+    o[1] = t.y;
+    o[2] = t.z;
+    o[3] = t.w;
+  }
+}
+
 // V consecutive elements of a [batch, lanes] fp32 state tensor (ordinary access).
 template <int V>
 __device__ __forceinline__ void load_state_v(const float *p, float (&o)[V]) {
@@ -350,15 +370,30 @@ __device__ __forceinline__ float mobius_apply(const Agg<4> &m, float x) {
   return (m.v[0] * x + m.v[1]) / fmaxf(m.v[2] * x + m.v[3], kEps);
 }
 
-// ================================================================ MobiusFwd
+// One step of the recurrence, lam_t = (A lam_{t-1} + B) / den_t with
+// den_t = max(C lam_{t-1} + D, EPS), as the forward walk computes it. The
+// backward recomputes lam_t with these same two functions (explicit fmaf, one
+// IEEE division), so its values equal the forward's stored lam bit for bit.
+__device__ __forceinline__ float mobius_den(float c, float d, float x) { return fmaxf(fmaf(c, x, d), kEps); }
+__device__ __forceinline__ float mobius_next(float a, float b, float x, float den) { return fmaf(a, x, b) / den; }
 
-template <bool HAS_D, bool CACHED = false>
+// ================================================================ MobiusFwd
+// The backward (MobiusBwd) walks time in reverse right after this kernel and
+// reads A, B, C (D) again, starting at the end of the sequence. Scan positions
+// from `cache_from` on are therefore loaded with ordinary loads, which leave
+// them in the memory-side cache for the backward's first chunks; the host picks
+// cache_from so that this tail fits the cache (all of it for small problems).
+// Earlier positions, and lam, stream (nontemporal): the backward reads lam only
+// once per S steps.
+
+template <bool HAS_D>
 struct MobiusFwd {
   static constexpr int AGG = 4;
   using IO = float;
   struct Params {
     const float *A, *B, *C, *D, *lam0;
     float *lam;
+    int64_t cache_from;   // first scan position whose inputs are loaded cached
   };
   template <int S, int V>
   struct Raw {
@@ -366,6 +401,28 @@ struct MobiusFwd {
   };
   template <int S, int V>
   using Regs = Raw<S, V>;
+
+  template <int S, int V, bool CACHED>
+  __device__ __forceinline__ static void load_steps(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q,
+                                    int64_t row, int nvalid) {
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+      if (j < nvalid) {
+        const int64_t rj = row + j * g.lanes;
+        if constexpr (CACHED) {
+          load_v_cached<V>(at(p.A, rj, q), r.a[j]);
+          load_v_cached<V>(at(p.B, rj, q), r.b[j]);
+          load_v_cached<V>(at(p.C, rj, q), r.c[j]);
+          if (HAS_D) load_v_cached<V>(at(p.D, rj, q), r.d[HAS_D ? j : 0]);
+        } else {
+          load_v<V>(at(p.A, rj, q), r.a[j]);
+          load_v<V>(at(p.B, rj, q), r.b[j]);
+          load_v<V>(at(p.C, rj, q), r.c[j]);
+          if (HAS_D) load_v<V>(at(p.D, rj, q), r.d[HAS_D ? j : 0]);
+        }
+      }
+    }
+  }
 
   template <int S, int V>
   __device__ __forceinline__ static void fetch(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q, int64_t s0,
@@ -379,15 +436,15 @@ struct MobiusFwd {
       if (HAS_D) fill_v(r.d[HAS_D ? j : 0], 1.0f);
     }
     if (!q.ok) return;
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      if (j < nvalid) {
-        const int64_t rj = row + j * g.lanes;
-        load_v<V>(at(p.A, rj, q), r.a[j]);
-        load_v<V>(at(p.B, rj, q), r.b[j]);
-        load_v<V>(at(p.C, rj, q), r.c[j]);
-        if (HAS_D) load_v<V>(at(p.D, rj, q), r.d[HAS_D ? j : 0]);
-      }
+    // The empty asm statements are compiler barriers: without them the two
+    // branches' loads, identical but for the nontemporal hint, are merged into
+    // one set and the hint is lost (the branch is wave-uniform).
+    if (s0 >= p.cache_from) {
+      asm volatile("" ::: "memory");
+      load_steps<S, V, true>(p, g, r, q, row, nvalid);
+      asm volatile("" ::: "memory");
+    } else {
+      load_steps<S, V, false>(p, g, r, q, row, nvalid);
     }
   }
 
@@ -426,14 +483,9 @@ struct MobiusFwd {
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           const float d = HAS_D ? r.d[HAS_D ? j : 0][v] : 1.0f;
-          x[v] = (r.a[j][v] * x[v] + r.b[j][v]) / fmaxf(r.c[j][v] * x[v] + d, kEps);
+          x[v] = mobius_next(r.a[j][v], r.b[j][v], x[v], mobius_den(r.c[j][v], d, x[v]));
         }
-        if (q.ok) {
-          if constexpr (CACHED)
-            store_v_cached<V>(at(p.lam, row + j * g.lanes, q), x);
-          else
-            store_v<V>(at(p.lam, row + j * g.lanes, q), x);
-        }
+        if (q.ok) store_v<V>(at(p.lam, row + j * g.lanes, q), x);
       }
     }
   }
@@ -447,6 +499,14 @@ struct MobiusFwd {
 //   q = nu_t / den_t:  dA = q lam_{t-1}, dB = q, dC = -q lam_t lam_{t-1}, dD = -q lam_t
 //   dlam0 = w_0
 // Scan position s0 + j is time t = T-1-s0-j, at row `row - j * lanes`.
+//
+// The saved lam is read once per thread: the value entering the thread's S
+// steps (lam at time T-1-s0-nvalid, or lam0 once the scan has passed time 0).
+// The thread recomputes lam over its steps from A, B, C, D, which it loads for
+// the adjoint anyway, with the forward walk's own step (mobius_den /
+// mobius_next), so the values are the forward's bit for bit. That takes the
+// per-element traffic from 32 to 28 bytes plus 4 / S (dlam, A, B, C in;
+// dA, dB, dC out) for D = 1.
 
 template <bool HAS_D>
 struct MobiusBwd {
@@ -458,11 +518,12 @@ struct MobiusBwd {
   };
   template <int S, int V>
   struct Raw {
-    // lv[j] = lam at step j's time t, lv[j+1] = lam_{t-1} (lam0 before time 0).
-    float dl[S][V], a[S][V], b[S][V], c[S][V], d[HAS_D ? S : 1][V], lv[S + 1][V];
+    // lin = lam entering the thread's steps, i.e. lam_{t-1} of its earliest step.
+    float dl[S][V], a[S][V], b[S][V], c[S][V], d[HAS_D ? S : 1][V], lin[V];
   };
   template <int S, int V>
   struct Regs {
+    // lv[j] = lam at step j's time t, lv[j+1] = lam_{t-1}.
     float dl[S][V], den[S][V], gain[S][V], lv[S + 1][V];
   };
 
@@ -477,22 +538,13 @@ struct MobiusBwd {
       fill_v(r.b[j], 0.0f);
       fill_v(r.c[j], 0.0f);
       if (HAS_D) fill_v(r.d[HAS_D ? j : 0], 1.0f);
-      fill_v(r.lv[j], 1.0f);
     }
-    fill_v(r.lv[S], 1.0f);
+    fill_v(r.lin, 1.0f);
     if (!q.ok) return;
-#pragma unroll
-    for (int j = 0; j <= S; ++j) {
-      if (j < nvalid) {
-        load_v<V>(at(p.lam, row - j * g.lanes, q), r.lv[j]);
-      } else if (j == nvalid) {
-        // Time T-1-s0-nvalid: lam there, or lam0 once the scan has passed time 0.
-        if (s0 + nvalid < g.steps) {
-          load_v<V>(at(p.lam, row - j * g.lanes, q), r.lv[j]);
-        } else if (p.lam0) {
-          load_state_v<V>(p.lam0 + state_index(g, q), r.lv[j]);
-        }
-      }
+    if (s0 + nvalid < g.steps) {
+      load_v<V>(at(p.lam, row - static_cast<int64_t>(nvalid) * g.lanes, q), r.lin);
+    } else if (p.lam0) {
+      load_state_v<V>(p.lam0 + state_index(g, q), r.lin);
     }
 #pragma unroll
     for (int j = 0; j < S; ++j) {
@@ -507,18 +559,20 @@ struct MobiusBwd {
     }
   }
 
+  // Recomputes lam forward in time (j from S-1 down to 0). Steps j >= nvalid
+  // hold the fills A = D = 1, B = C = 0: the identity map, which carries lin
+  // unchanged (lin > 0) to the earliest valid step.
   template <int S, int V>
   __device__ __forceinline__ static void prep(const Raw<S, V> &raw, Regs<S, V> &r) {
 #pragma unroll
-    for (int j = 0; j <= S; ++j)
+    for (int v = 0; v < V; ++v) r.lv[S][v] = raw.lin[v];
 #pragma unroll
-      for (int v = 0; v < V; ++v) r.lv[j][v] = raw.lv[j][v];
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
+    for (int j = S - 1; j >= 0; --j) {
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const float D = HAS_D ? raw.d[HAS_D ? j : 0][v] : 1.0f;
-        const float den = fmaxf(raw.c[j][v] * raw.lv[j + 1][v] + D, kEps);
+        const float den = mobius_den(raw.c[j][v], D, r.lv[j + 1][v]);
+        r.lv[j][v] = mobius_next(raw.a[j][v], raw.b[j][v], r.lv[j + 1][v], den);
         r.dl[j][v] = raw.dl[j][v];
         r.den[j][v] = den;
         r.gain[j][v] = (raw.a[j][v] * D - raw.b[j][v] * raw.c[j][v]) / (den * den);

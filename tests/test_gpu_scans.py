@@ -93,6 +93,32 @@ def test_mobius_explicit_D(cuda, shape):
         _close(name, got.grad, w)
 
 
+@pytest.mark.parametrize("shape", [(2, 1000, 130), (1, 4096, 64), (1, 17, 3)])
+@pytest.mark.parametrize("with_D", [False, True])
+def test_mobius_bwd_recomputes_lam_bitwise(cuda, shape, with_D):
+    """The backward reads the saved lam only where a thread's steps begin and
+    recomputes the rest with the forward's own step, so the recomputed values
+    are the stored ones bit for bit: poisoning every other row of lam (with NaN)
+    leaves every gradient bitwise unchanged. Threads hold 16 consecutive steps
+    in reverse time (a multiple of 16 also passes), so the rows read are
+    t = T-1-16m, m >= 1."""
+    from kla.ops.hip import scans as hs
+
+    B, T, N = shape
+    A, Bm, C, lam0, dlam = (t.to(cuda) for t in mobius_inputs(B, T, N, seed=21))
+    D = (torch.rand(B, T, N, generator=torch.Generator().manual_seed(22)) + 0.5).to(cuda) if with_D else None
+    lam = hs._mobius_scan_op(A, Bm, C, D, lam0)
+    ref_grads = hs._mobius_scan_bwd_op(dlam, A, Bm, C, D, lam0, lam)
+    t = torch.arange(T, device=cuda)
+    keep = ((T - 1 - t) % 16 == 0) & (t != T - 1)
+    poisoned = torch.where(keep[None, :, None], lam, torch.full_like(lam, float("nan")))
+    got = hs._mobius_scan_bwd_op(dlam, A, Bm, C, D, lam0, poisoned)
+    names = ("dA", "dB", "dC", "dD", "dlam0")
+    for name, a, b in zip(names, ref_grads, got):  # dD is empty without D
+        assert torch.isfinite(a).all(), name
+        assert torch.equal(a, b), f"{name}: the backward read a poisoned row of lam"
+
+
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("with_h0", [True, False])
 def test_affine_fwd_bwd_matches_oracle(cuda, shape, with_h0):
