@@ -319,7 +319,7 @@ def bench_layer(args, device, stream) -> dict:
     def prefill():
         st = model.init_state(16)
         logits, st = model(ids, state=st)
-        state["s"], state["tok"] = st, logits[:, -1].argmax(-1, keepdim=True)
+        state["s"], state["tok"] = st, model._sample(logits[:, -1], 0.0, None)   # greedy
 
     pre_ms = _timed(prefill, max(1, args.steps // 4), 1, stream)
 
@@ -328,7 +328,7 @@ def bench_layer(args, device, stream) -> dict:
         st, tok = state["s"], state["tok"]
         for _ in range(256):
             logits, st = model(tok, state=st)
-            tok = logits[:, -1].argmax(-1, keepdim=True)
+            tok = model._sample(logits[:, -1], 0.0, None)
 
     dec_ms = _timed(decode256, 1, 1, stream)
     out = {"metric": "SequenceModel(d=512, 6 layers) prefill tokens/s (16x2048) + decode ms/token (256 steps)",
@@ -343,7 +343,7 @@ def bench_layer(args, device, stream) -> dict:
         def decode256_graph():
             tok = state["tok"]
             for _ in range(256):
-                tok = graph.step(tok)[:, -1].argmax(-1, keepdim=True)
+                tok = model._sample(graph.step(tok)[:, -1], 0.0, None)
 
         out["decode_graph_ms_per_token"] = round(_timed(decode256_graph, 1, 1, stream) / 256, 4)
     out["peak_mem_GiB"] = round(torch.cuda.max_memory_allocated(device) / 2**30, 2)

@@ -368,6 +368,48 @@ int kla_rms_norm_fwd(int dtype, const void *x, const float *weight, float eps, v
 int kla_swiglu_fwd(int dtype, const void *h, int64_t ld_h, void *out, int64_t rows, int64_t hidden,
                    hipStream_t stream);
 
+/*
+ * Embedding rows of one decode step: out[r, :] = table[ids[r], :] for r < rows
+ * (table rows ld_table elements apart, vocab of them; out rows ld_out apart;
+ * both of `dtype`, ids int64). An id outside [0, vocab) reads nothing and
+ * writes a row of NaN. Replaces nn.Embedding in SequenceModel.forward
+ * (reference src/kla/models/sequence_model.py:157) for a one-token step.
+ */
+int kla_gather_rows(int dtype, const void *table, int64_t ld_table, int64_t vocab, const int64_t *ids, void *out,
+                    int64_t ld_out, int64_t rows, int64_t dim, hipStream_t stream);
+
+/*
+ * Greedy token choice: out[r * ld_out] = argmax_j x[r, j] over n > 0 fp32 values
+ * (rows ldx apart), in torch.argmax's order: NaN above every number, ties to
+ * the smaller index. Replaces logits.argmax(dim=-1) of SequenceModel._sample
+ * with temperature 0 (reference src/kla/models/sequence_model.py, generate).
+ */
+int kla_argmax_rows(const float *x, int64_t ldx, int64_t rows, int64_t n, int64_t *out, int64_t ld_out,
+                    hipStream_t stream);
+
+/* Epilogues of kla_rows_linear_fwd. */
+enum { KLA_ROWS_PLAIN = 0, KLA_ROWS_RESIDUAL = 1, KLA_ROWS_SWIGLU = 2 };
+
+/*
+ * A linear layer on a few rows (one-token decode: rows = batch), fp32, with
+ * the block's norm and residual or the MLP's activation fused in:
+ *   xn  = norm_w ? (x * rsqrt(mean(x^2) + eps)) * norm_w : x      (per row of k)
+ *   acc = xn W^T + bias                 W [n_w, k] rows ldw apart, bias [n_w] or NULL
+ *   y   = acc                               (KLA_ROWS_PLAIN)
+ *         res + acc                         (KLA_ROWS_RESIDUAL, res [rows, n])
+ *         silu(acc[:, j]) * acc[:, glu_off + j]  (KLA_ROWS_SWIGLU, j < n)
+ * x [rows, k] (ldx), y [rows, n] (ldy), res (ldres). W must hold n rows (n +
+ * glu_off for KLA_ROWS_SWIGLU). No gradient; deterministic (fixed-order sums).
+ * Replaces, in decode, the nn.Linear calls of KLALayer (in_proj, sensor_proj,
+ * out_proj; reference src/kla/layers/kla_layer.py:61, :88, :127, :311, :340),
+ * RMSNorm.forward before them (src/kla/layers/common.py:45-55), the block's
+ * residual adds (src/kla/models/sequence_model.py:71-87), MLP.forward
+ * (common.py:99-123) and the LM head on the final norm (sequence_model.py:169).
+ */
+int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
+                        const float *norm_w, float eps, const float *res, int64_t ldres, float *y, int64_t ldy,
+                        int64_t rows, int64_t n, int64_t k, int64_t glu_off, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

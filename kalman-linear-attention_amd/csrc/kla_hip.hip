@@ -19,6 +19,7 @@
 
 #include "gate_skip.hpp"
 #include "model_ops.hpp"
+#include "rows_linear.hpp"
 #include "fused_kla.hpp"
 #include "lookback_scan.hpp"
 
@@ -26,7 +27,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 8;
+constexpr int kAbiVersion = 9;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -1087,6 +1088,125 @@ int kla_swiglu_fwd(int dtype, const void *h, int64_t ld_h, void *out, int64_t ro
   else
     hipLaunchKernelGGL(swiglu_fwd_kernel<bf16_t>, grid, dim3(256), 0, stream, static_cast<const bf16_t *>(h), ld_h,
                        static_cast<bf16_t *>(out), rows, hidden);
+  return hip_status(fn, hipGetLastError());
+}
+
+int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
+                        const float *norm_w, float eps, const float *res, int64_t ldres, float *y, int64_t ldy,
+                        int64_t rows, int64_t n, int64_t k, int64_t glu_off, hipStream_t stream) {
+  const char *fn = "kla_rows_linear_fwd";
+  if (epilogue != KLA_ROWS_PLAIN && epilogue != KLA_ROWS_RESIDUAL && epilogue != KLA_ROWS_SWIGLU)
+    return fail(KLA_ERR_INVALID_ARG, "%s: unknown epilogue %d", fn, epilogue);
+  if (rows < 0 || n < 0 || k < 0 || glu_off < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  if (rows == 0 || n == 0) return KLA_OK;
+  if (!y || (k > 0 && (!x || !w))) return fail(KLA_ERR_INVALID_ARG, "%s: x, w and y must not be NULL", fn);
+  if (epilogue == KLA_ROWS_RESIDUAL && !res)
+    return fail(KLA_ERR_INVALID_ARG, "%s: the residual epilogue needs res", fn);
+  if (epilogue == KLA_ROWS_SWIGLU && glu_off < n)
+    return fail(KLA_ERR_INVALID_ARG, "%s: glu_off %lld below n %lld (the halves overlap)", fn, (long long)glu_off,
+                (long long)n);
+  if (ldx < k || ldw < k || ldy < n || (epilogue == KLA_ROWS_RESIDUAL && ldres < n))
+    return fail(KLA_ERR_INVALID_ARG, "%s: a row stride is below its row length", fn);
+  if (norm_w && k == 0) return fail(KLA_ERR_INVALID_ARG, "%s: RMSNorm over zero columns", fn);
+  if (misaligned(x) || misaligned(w) || misaligned(bias) || misaligned(norm_w) || misaligned(res) || misaligned(y))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  const int64_t tiles_n = (n + kRowsLinTile - 1) / kRowsLinTile;
+  const int64_t tiles_m = (rows + kRowsLinTile - 1) / kRowsLinTile;
+  if (tiles_n >= (1ll << 31) || tiles_m >= 65536) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+  RowsLinearParams p;
+  p.x = x;
+  p.w = w;
+  p.bias = bias;
+  p.norm_w = norm_w;
+  p.res = res;
+  p.y = y;
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.ldres = ldres;
+  p.ldy = ldy;
+  p.rows = rows;
+  p.n = n;
+  p.k = k;
+  p.glu_off = glu_off;
+  p.eps = eps;
+  // k split over the workgroup's waves in multiples of 16.
+  const int64_t per = ((k + kRowsLinWaves - 1) / kRowsLinWaves + 15) / 16 * 16;
+  if (per > (1 << 30)) return fail(KLA_ERR_INVALID_ARG, "%s: k too large", fn);
+  p.k_per_wave = static_cast<int>(per > 0 ? per : 16);
+  // Rows that start 16-byte aligned load four k at a time; a ragged last group
+  // of a row (k not a multiple of 4) falls back to single loads in the kernel.
+  const bool vec = ldx % 4 == 0 && ldw % 4 == 0 && all_aligned(16, {x, w, norm_w});
+  // One workgroup per CU at most (a 1024-thread workgroup fills a CU): more
+  // column tiles than that are walked by each workgroup in turn.
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+  }
+  const int64_t per_cu = (cus + tiles_m - 1) / tiles_m;
+  const int64_t ctas_n = tiles_n < per_cu ? tiles_n : per_cu;
+  const dim3 grid(static_cast<uint32_t>(ctas_n), static_cast<uint32_t>(tiles_m));
+  const bool pipe = p.k_per_wave <= 16 * rows_lin_steps(epilogue, norm_w != nullptr);
+  auto go = [&](auto epi_c, auto norm_c, auto vec_c) {
+    if (pipe)
+      hipLaunchKernelGGL((rows_linear_kernel<decltype(epi_c)::value, decltype(norm_c)::value,
+                                             decltype(vec_c)::value, true>),
+                         grid, dim3(kRowsLinThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((rows_linear_kernel<decltype(epi_c)::value, decltype(norm_c)::value,
+                                             decltype(vec_c)::value, false>),
+                         grid, dim3(kRowsLinThreads), 0, stream, p);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  auto by_vec = [&](auto epi_c, auto norm_c) { vec ? go(epi_c, norm_c, T{}) : go(epi_c, norm_c, F{}); };
+  auto by_norm = [&](auto epi_c) { norm_w ? by_vec(epi_c, T{}) : by_vec(epi_c, F{}); };
+  if (epilogue == KLA_ROWS_PLAIN)
+    by_norm(std::integral_constant<int, kEpiPlain>{});
+  else if (epilogue == KLA_ROWS_RESIDUAL)
+    by_norm(std::integral_constant<int, kEpiResidual>{});
+  else
+    by_norm(std::integral_constant<int, kEpiSwiglu>{});
+  return hip_status(fn, hipGetLastError());
+}
+
+int kla_gather_rows(int dtype, const void *table, int64_t ld_table, int64_t vocab, const int64_t *ids, void *out,
+                    int64_t ld_out, int64_t rows, int64_t dim, hipStream_t stream) {
+  const char *fn = "kla_gather_rows";
+  if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16) return fail(KLA_ERR_DTYPE, "%s: unsupported dtype %d", fn, dtype);
+  if (rows < 0 || dim < 0 || vocab < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  if (rows == 0 || dim == 0) return KLA_OK;
+  if (!table || !ids || !out) return fail(KLA_ERR_INVALID_ARG, "%s: table, ids and out must not be NULL", fn);
+  if (ld_table < dim || ld_out < dim) return fail(KLA_ERR_INVALID_ARG, "%s: a row stride is below dim", fn);
+  if (rows >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (misaligned_bytes(table, el) || misaligned_bytes(out, el) || misaligned_bytes(ids, 8))
+    return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
+  const dim3 grid(static_cast<uint32_t>(rows));
+  if (dtype == KLA_DTYPE_F32)
+    hipLaunchKernelGGL(gather_rows_kernel<float>, grid, dim3(256), 0, stream, static_cast<const float *>(table),
+                       ld_table, vocab, ids, static_cast<float *>(out), ld_out, dim);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<bf16_t>, grid, dim3(256), 0, stream, static_cast<const bf16_t *>(table),
+                       ld_table, vocab, ids, static_cast<bf16_t *>(out), ld_out, dim);
+  return hip_status(fn, hipGetLastError());
+}
+
+int kla_argmax_rows(const float *x, int64_t ldx, int64_t rows, int64_t n, int64_t *out, int64_t ld_out,
+                    hipStream_t stream) {
+  const char *fn = "kla_argmax_rows";
+  if (rows < 0 || n < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  if (rows == 0) return KLA_OK;
+  if (n == 0) return fail(KLA_ERR_INVALID_ARG, "%s: argmax over zero values", fn);
+  if (!x || !out) return fail(KLA_ERR_INVALID_ARG, "%s: x and out must not be NULL", fn);
+  if (ldx < n || ld_out < 1) return fail(KLA_ERR_INVALID_ARG, "%s: bad row stride", fn);
+  if (rows >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
+  if (misaligned(x) || misaligned_bytes(out, 8)) return fail(KLA_ERR_ALIGN, "%s: operand not aligned", fn);
+  const dim3 grid(static_cast<uint32_t>(rows));
+  if (ldx % 4 == 0 && all_aligned(16, {x}))
+    hipLaunchKernelGGL(argmax_rows_kernel<true>, grid, dim3(kArgmaxThreads), 0, stream, x, ldx, n, out, ld_out);
+  else
+    hipLaunchKernelGGL(argmax_rows_kernel<false>, grid, dim3(kArgmaxThreads), 0, stream, x, ldx, n, out, ld_out);
   return hip_status(fn, hipGetLastError());
 }
 

@@ -45,4 +45,105 @@ __global__ void __launch_bounds__(256) swiglu_fwd_kernel(const IO *__restrict__ 
   io_store(out + i, g * io_load(h + r * ld_h + hidden + c));
 }
 
+// out[r, :] = table[ids[r], :] (the embedding lookup of one decode step,
+// reference src/kla/models/sequence_model.py:157, nn.Embedding). An id outside
+// [0, vocab) reads nothing and writes a row of NaN. One workgroup per row.
+template <class IO>
+__global__ void __launch_bounds__(256) gather_rows_kernel(const IO *__restrict__ table, int64_t ld_table,
+                                                          int64_t vocab, const int64_t *__restrict__ ids,
+                                                          IO *__restrict__ out, int64_t ld_out, int64_t dim) {
+  const int64_t r = blockIdx.x;
+  const int64_t id = ids[r];
+  const bool ok = id >= 0 && id < vocab;
+  const IO *src = table + (ok ? id : 0) * ld_table;
+  IO *dst = out + r * ld_out;
+  for (int64_t i = threadIdx.x; i < dim; i += 256)
+    io_store(dst + i, ok ? io_load(src + i) : __builtin_nanf(""));
+}
+
+// (value, index) of the larger of two candidates in torch.argmax's order: NaN
+// above every number, then the larger value, ties to the smaller index.
+__device__ __forceinline__ bool argmax_before(float a, int64_t ia, float b, int64_t ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
+constexpr int kArgmaxThreads = 1024;
+
+// out[r] = argmax_j x[r, j] (greedy decoding over the vocabulary, reference
+// SequenceModel._sample with temperature 0, logits.argmax(dim=-1)). One
+// 1024-thread workgroup per row: every thread has its loads in flight at once,
+// then (value, index) pairs meet in a wave and an LDS reduction.
+template <bool VEC>
+__global__ void __launch_bounds__(kArgmaxThreads) argmax_rows_kernel(const float *__restrict__ x, int64_t ldx,
+                                                                     int64_t n, int64_t *__restrict__ out,
+                                                                     int64_t ld_out) {
+  __shared__ float s_v[kArgmaxThreads / kWave];
+  __shared__ int64_t s_i[kArgmaxThreads / kWave];
+  const int tid = static_cast<int>(threadIdx.x);
+  const float *xr = x + static_cast<int64_t>(blockIdx.x) * ldx;
+  float best = -__builtin_inff();
+  int64_t bi = n;   // no candidate yet: above every index
+  if constexpr (VEC) {
+    // Batches of U vector loads per thread, all in flight before the compares.
+    constexpr int U = 8;
+    const int64_t n4 = n / 4;
+    for (int64_t q0 = tid; q0 < n4; q0 += static_cast<int64_t>(U) * kArgmaxThreads) {
+      f32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t q = q0 + static_cast<int64_t>(u) * kArgmaxThreads;
+        v[u] = q < n4 ? *reinterpret_cast<const f32x4 *>(xr + 4 * q) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t q = q0 + static_cast<int64_t>(u) * kArgmaxThreads;
+        if (q < n4) {
+          const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (argmax_before(e[j], 4 * q + j, best, bi)) {
+              best = e[j];
+              bi = 4 * q + j;
+            }
+        }
+      }
+    }
+    for (int64_t i = 4 * n4 + tid; i < n; i += kArgmaxThreads)
+      if (argmax_before(xr[i], i, best, bi)) {
+        best = xr[i];
+        bi = i;
+      }
+  } else {
+    for (int64_t i = tid; i < n; i += kArgmaxThreads)
+      if (argmax_before(xr[i], i, best, bi)) {
+        best = xr[i];
+        bi = i;
+      }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off /= 2) {
+    const float ov = __shfl_xor(best, off);
+    const int64_t oi = __shfl_xor(bi, off);
+    if (argmax_before(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  if (tid % kWave == 0) {
+    s_v[tid / kWave] = best;
+    s_i[tid / kWave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w)
+      if (argmax_before(s_v[w], s_i[w], best, bi)) {
+        best = s_v[w];
+        bi = s_i[w];
+      }
+    out[static_cast<int64_t>(blockIdx.x) * ld_out] = bi;
+  }
+}
+
 }  // namespace kla

@@ -143,6 +143,27 @@ class MLP(nn.Module):
         else:
             raise ValueError(f"Unknown MLP kind {kind!r}")
 
+    def block_decode_ok(self, x: torch.Tensor, norm: "RMSNorm") -> bool:
+        """Whether :meth:`block_decode_hip` serves ``x + self(norm(x))`` here: a SwiGLU
+        MLP in inference on a hip backend, fp32 throughout, at most 64 rows."""
+        if self.kind != "swiglu" or x.dtype != torch.float32 or x.numel() // max(x.shape[-1], 1) > 64:
+            return False
+        if any(p.dtype != torch.float32 for p in (self.w12.weight, self.w3.weight, norm.weight)):
+            return False
+        return _hip_inference(self.backend, x, self.w12.weight, self.w3.weight, norm.weight)
+
+    def block_decode_hip(self, x: torch.Tensor, norm: "RMSNorm") -> torch.Tensor:
+        """``x + self(norm(x))`` as two row kernels (kla.ops.hip.model_ops.rows_linear_hip):
+        norm + w12 + SwiGLU, then w3 + the residual add. The values are those of the
+        torch lines (reference src/kla/layers/common.py:45-55, :116-123 and the
+        block's residual, src/kla/models/sequence_model.py:77) up to the order of
+        the fp32 sums."""
+        from kla.ops.hip.model_ops import rows_linear_hip
+
+        x2 = x.reshape(-1, x.shape[-1])
+        h = rows_linear_hip(x2, self.w12.weight, self.w12.bias, norm_weight=norm.weight, eps=norm.eps, swiglu=True)
+        return rows_linear_hip(h, self.w3.weight, self.w3.bias, residual=x2).reshape(x.shape)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.kind == "swiglu":
             h = self.w12(x)

@@ -255,14 +255,20 @@ class KLALayer(nn.Module):
         return (z.dtype in (torch.float32, torch.bfloat16) and self.conv.kernel_size <= 8
                 and _step_on_hip(self.config.backend, z))
 
-    def _decode_step_hip(self, z, gate, residual, ssm_state):
+    def _decode_step_hip(self, z, gate, residual, ssm_state, rows_linear: bool = False):
         """The one-token SSM step with the lambda skip and the gate, as one HIP kernel
-        (kla.ops.hip.decode); the same values as _run_ssm_step plus the tail of forward."""
+        (kla.ops.hip.decode); the same values as _run_ssm_step plus the tail of forward.
+        ``rows_linear``: the sensor projection runs on kla.ops.hip.model_ops.rows_linear_hip."""
         from kla.ops.hip.decode import decode_step_hip
 
         cfg = self.config
         S = self.d_state
-        proj = self.sensor_proj(z)[:, 0]
+        if rows_linear:
+            from kla.ops.hip.model_ops import rows_linear_hip
+
+            proj = rows_linear_hip(z[:, 0], self.sensor_proj.weight, self.sensor_proj.bias)
+        else:
+            proj = self.sensor_proj(z)[:, 0]
         v, log_var, k, q = torch.split(proj, [self._w_value, self._w_var, S, S], dim=-1)
         if self._value_rank == "conv":
             v = z[:, 0]
@@ -281,6 +287,57 @@ class KLALayer(nn.Module):
             clip_value=cfg.clip_value, obs_var_min=cfg.obs_var_min, obs_var_max=cfg.obs_var_max,
             decode_from_prior=cfg.decode_from_prior, in_place=in_place)
         return y.unsqueeze(1), y_var.unsqueeze(1), KLAState(lam=lam, eta=eta)
+
+    def _one_token_hip(self, z, gate, state, rows_linear: bool = False):
+        """Conv step and SSM step (with skip and gate) of one token on the HIP decode
+        kernels (kla.ops.hip.decode): (y, y_var, conv_state, ssm_state)."""
+        cfg = self.config
+        conv_state = state.conv
+        if self.conv is not None:
+            from kla.ops.hip.decode import conv_step_hip
+
+            # A torch prefill leaves the window as a view of its padded input.
+            window = conv_state.to(z.dtype).contiguous()
+            zc, conv_state = conv_step_hip(z[:, 0], window, self.conv.weight[:, 0, :], self.conv.bias,
+                                           cfg.conv_activation,
+                                           in_place=self._decode_in_place and window is state.conv)
+            z = zc.unsqueeze(1)
+        y, y_var, ssm_state = self._decode_step_hip(z, gate, z, state.ssm, rows_linear=rows_linear)
+        return y, y_var, conv_state, ssm_state
+
+    def block_decode_ok(self, x: torch.Tensor, state: KLALayerState | None) -> bool:
+        """Whether :meth:`block_decode_hip` serves this one-token step: the HIP decode
+        kernels apply (inference, fp32, hip backend), fp32 projection weights, and a
+        batch small enough for the row kernels (at most 64 rows)."""
+        if state is None or x.dim() != 3 or x.shape[1] != 1 or x.shape[0] > 64 or x.dtype != torch.float32:
+            return False
+        if state.ssm.lam.dtype != torch.float32 or not self._decode_on_hip(x):
+            return False
+        if self.value_expand is not None or self.var_expand is not None:
+            return False
+        return all(m.weight.dtype == torch.float32 for m in (self.in_proj, self.sensor_proj, self.out_proj))
+
+    def block_decode_hip(self, x: torch.Tensor, norm_weight: torch.Tensor, eps: float, state: KLALayerState):
+        """``x + self(rms_norm(x), state)`` for one token (x [B, 1, d_model]), returning
+        (that, new_state): the block's pre-norm is fused into in_proj and the
+        residual add into out_proj (kla.ops.hip.model_ops.rows_linear_hip), the
+        sensor projection runs on the same row kernel, and the conv and SSM steps
+        are the HIP decode kernels. The values are those of the block's torch
+        lines (reference src/kla/models/sequence_model.py:79-87) up to the order
+        of the fp32 sums."""
+        from kla.ops.hip.model_ops import rows_linear_hip
+
+        cfg = self.config
+        x2 = x[:, 0]
+        projected = rows_linear_hip(x2, self.in_proj.weight, self.in_proj.bias, norm_weight=norm_weight,
+                                    eps=eps).unsqueeze(1)
+        if cfg.use_gating:
+            z, gate = projected.chunk(2, dim=-1)
+        else:
+            z, gate = projected, None
+        y, _, conv_state, ssm_state = self._one_token_hip(z, gate, state, rows_linear=True)
+        out = rows_linear_hip(y[:, 0], self.out_proj.weight, self.out_proj.bias, residual=x2)
+        return out.unsqueeze(1), KLALayerState(conv=conv_state, ssm=ssm_state)
 
     def forward(self, x: torch.Tensor, state: KLALayerState | None = None, return_state: bool = False):
         """x [B, L, d_model] -> out, or (out, new_state) when a state is passed or requested.
@@ -301,25 +358,14 @@ class KLALayer(nn.Module):
         hip_decode = (state is not None and L == 1 and state.ssm.lam.dtype == torch.float32
                       and self._decode_on_hip(projected))
 
-        conv_state = state.conv if state is not None else None
-        if self.conv is not None:
-            if hip_decode:
-                from kla.ops.hip.decode import conv_step_hip
-
-                # A torch prefill leaves the window as a view of its padded input.
-                window = conv_state.to(z.dtype).contiguous()
-                zc, conv_state = conv_step_hip(z[:, 0], window, self.conv.weight[:, 0, :], self.conv.bias,
-                                               cfg.conv_activation,
-                                               in_place=self._decode_in_place and window is state.conv)
-                z = zc.unsqueeze(1)
-            else:
-                z, conv_state = self.conv(z, conv_state, hip=self._conv_on_hip(z))
-        residual = z
-
-        ssm_state = state.ssm if state is not None else None
         if hip_decode:
-            y, y_var, ssm_state = self._decode_step_hip(z, gate, residual, ssm_state)
+            y, y_var, conv_state, ssm_state = self._one_token_hip(z, gate, state)
         else:
+            conv_state = state.conv if state is not None else None
+            if self.conv is not None:
+                z, conv_state = self.conv(z, conv_state, hip=self._conv_on_hip(z))
+            residual = z
+            ssm_state = state.ssm if state is not None else None
             if state is not None and L == 1:
                 y, y_var, ssm_state = self._run_ssm_step(z, ssm_state)
             else:

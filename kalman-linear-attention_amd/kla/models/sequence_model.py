@@ -69,6 +69,16 @@ class Block(nn.Module):
 
     def forward(self, x: torch.Tensor, state=None, return_state: bool = False):
         emit_state = return_state or state is not None
+        if (state is not None and isinstance(self.mixer, KLALayer)
+                and self.mixer.block_decode_ok(x, state) and self.mixer_norm.weight.dtype == torch.float32):
+            # One-token step on the MI355X row kernels: norm + in_proj, the conv and
+            # SSM steps, out_proj + residual; then norm + w12 + SwiGLU, w3 + residual.
+            x, new_state = self.mixer.block_decode_hip(x, self.mixer_norm.weight, self.mixer_norm.eps, state)
+            if self.mlp is not None and self.mlp.block_decode_ok(x, self.mlp_norm):
+                x = self.mlp.block_decode_hip(x, self.mlp_norm)
+            else:
+                x = self.channel(x)
+            return x, new_state
         if emit_state:
             mixed, new_state = self.mixer(self.mixer_norm(x), state=state, return_state=True)
             if isinstance(mixed, tuple):
@@ -119,14 +129,45 @@ class SequenceModel(MarginalReadout, nn.Module):
         return [blk.mixer.init_state(batch, device=device, dtype=dtype) for blk in self.blocks]
 
     def _logits(self, x: torch.Tensor) -> torch.Tensor:
-        logits = self.lm_head(self.norm_f(x))
+        if self._head_on_rows(x):
+            # One-token step: final norm + LM head as one row kernel.
+            from kla.ops.hip.model_ops import rows_linear_hip
+
+            logits = rows_linear_hip(x.reshape(-1, x.shape[-1]), self.lm_head.weight, self.lm_head.bias,
+                                     norm_weight=self.norm_f.weight, eps=self.norm_f.eps)
+            logits = logits.reshape(*x.shape[:-1], logits.shape[-1])
+        else:
+            logits = self.lm_head(self.norm_f(x))
         cap = self.config.logit_softcap
         return logits if cap is None else cap * torch.tanh(logits / cap)
+
+    def _embed(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """Token embeddings; in inference on a hip backend one gather kernel
+        (kla.ops.hip.model_ops.gather_rows_hip) instead of torch's index kernel."""
+        w = self.embedding.weight
+        if w.dtype in (torch.float32, torch.bfloat16) and input_ids.dtype == torch.int64:
+            from kla.layers.common import _hip_inference
+
+            if _hip_inference(self.norm_f.backend, w):
+                from kla.ops.hip.model_ops import gather_rows_hip
+
+                return gather_rows_hip(w, input_ids)
+        return self.embedding(input_ids)
+
+    def _head_on_rows(self, x: torch.Tensor) -> bool:
+        """Whether the final norm + LM head of a one-token step runs as one row kernel."""
+        if x.dim() != 3 or x.shape[1] != 1 or x.shape[0] > 64 or x.dtype != torch.float32:
+            return False
+        if self.lm_head.weight.dtype != torch.float32 or self.norm_f.weight.dtype != torch.float32:
+            return False
+        from kla.layers.common import _hip_inference
+
+        return _hip_inference(self.norm_f.backend, x, self.lm_head.weight, self.norm_f.weight)
 
     def forward(self, input_ids: torch.Tensor, state: Optional[list] = None, return_state: bool = False):
         """input_ids [B, L] -> logits [B, L, vocab]; per-layer state in/out for prefill and decode."""
         emit_state = return_state or state is not None
-        x = self.embedding(input_ids)
+        x = self._embed(input_ids)
         new_states = []
         for i, blk in enumerate(self.blocks):
             if emit_state:
@@ -184,9 +225,15 @@ class SequenceModel(MarginalReadout, nn.Module):
         out.append(token)
         return torch.cat(out, dim=1)
 
-    @staticmethod
-    def _sample(logits: torch.Tensor, temperature: float, top_k: Optional[int]) -> torch.Tensor:
+    def _sample(self, logits: torch.Tensor, temperature: float, top_k: Optional[int]) -> torch.Tensor:
         if temperature <= 0:
+            from kla.layers.common import _hip_inference
+
+            if logits.dtype == torch.float32 and logits.shape[-1] > 0 and _hip_inference(self.norm_f.backend, logits):
+                # Greedy choice as one kernel (torch.argmax's order: NaN first, ties to the lower id).
+                from kla.ops.hip.model_ops import argmax_rows_hip
+
+                return argmax_rows_hip(logits)
             return logits.argmax(dim=-1, keepdim=True)
         logits = logits / temperature
         if top_k is not None:

@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -28,6 +28,10 @@ KLA_ERR_HIP = 5
 
 KLA_DTYPE_F32 = 0
 KLA_DTYPE_BF16 = 1
+
+KLA_ROWS_PLAIN = 0
+KLA_ROWS_RESIDUAL = 1
+KLA_ROWS_SWIGLU = 2
 
 KLA_SCAN_MOBIUS_FWD = 0
 KLA_SCAN_MOBIUS_BWD = 1
@@ -64,6 +68,10 @@ _SIGNATURES = {
     "kla_gate_skip_workspace_bytes": (ctypes.c_size_t, [_i64] * 2),
     "kla_rms_norm_fwd": (ctypes.c_int, [ctypes.c_int, _p, _p, ctypes.c_float, _p, _i64, _i64, _p]),
     "kla_swiglu_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _i64, _p]),
+    "kla_gather_rows": (ctypes.c_int, [ctypes.c_int, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p]),
+    "kla_argmax_rows": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _p]),
+    "kla_rows_linear_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _p, _p, ctypes.c_float, _p, _i64, _p,
+                                           _i64, _i64, _i64, _i64, _i64, _p]),
     "kla_gate_skip_bwd": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _p, _p, _p, _i64, _p, _i64, _p, ctypes.c_int,
                                          ctypes.c_int] + [_p] * 4 + [_i64] * 2 + [_p, ctypes.c_size_t, _p]),
     "kla_causal_conv_bwd": (ctypes.c_int, [ctypes.c_int, _p, _p, _i64, _i64, _p, _p, _p, ctypes.c_int, _p, _p, _p,

@@ -972,6 +972,144 @@ def test_sequence_model_inference_kernels_match_torch(cuda):
         check(f"logits{i}", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
 
 
+@pytest.mark.parametrize("epilogue", ["plain", "residual", "swiglu"])
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("rows,k,n", [(16, 512, 2048), (5, 1365, 512), (17, 64, 50), (1, 7, 3), (40, 1024, 1056),
+                                      (3, 2048, 33)])
+@pytest.mark.parametrize("aligned_x", [True, False])
+def test_rows_linear_matches_float64(cuda, epilogue, norm, rows, k, n, aligned_x):
+    """rows_linear_hip (norm + product + epilogue) against the same lines in float64
+    on the CPU. The bound is the fp32 summation error of each output: 2e-6 of
+    sum_k |xn_k w_k| (plus the residual's own ulp), carried through silu(a) * b
+    for the SwiGLU epilogue. x is a strided view (row stride > k): with aligned
+    rows the kernel loads four k at a time (k = 1365, 7: a ragged last group;
+    the weight gets an aligned copy), otherwise one at a time."""
+    import torch.nn.functional as F
+
+    from kla.ops.hip.model_ops import rows_linear_hip
+
+    g = torch.Generator().manual_seed(rows * 1000 + k)
+    n_w = 2 * n if epilogue == "swiglu" else n
+    ld = (k + 3) // 4 * 4 + 4
+    xb = torch.randn(rows, ld, generator=g) * 2
+    off = 0 if aligned_x else 1             # row stride ld; rows 16-byte aligned or not
+    x = xb[:, off:off + k]
+    w = torch.randn(n_w, k, generator=g) / k ** 0.5
+    bias = torch.randn(n_w, generator=g) * 0.1 if n % 2 else None
+    gw = torch.rand(k, generator=g) + 0.5 if norm else None
+    res = torch.randn(rows, n, generator=g) if epilogue == "residual" else None
+
+    xd = x.double()
+    if norm:
+        xd = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-5) * gw.double()
+    acc = xd @ w.double().T
+    mag = xd.abs() @ w.double().abs().T
+    if bias is not None:
+        acc = acc + bias.double()
+    tol = 2e-6 * mag + 1e-7
+    if epilogue == "swiglu":
+        a, b = acc[:, :n], acc[:, n:]
+        want = F.silu(a) * b
+        tol = 1.2 * b.abs() * tol[:, :n] + F.silu(a).abs() * tol[:, n:] + 1e-7
+    elif epilogue == "residual":
+        want = res.double() + acc
+        tol = tol + 1e-7 * res.double().abs()
+    else:
+        want = acc
+
+    dev = lambda t: None if t is None else t.to(cuda)  # noqa: E731
+    got = rows_linear_hip(dev(xb)[:, off:off + k], dev(w), dev(bias), norm_weight=dev(gw), eps=1e-5,
+                          residual=dev(res), swiglu=epilogue == "swiglu")
+    assert got.shape == (rows, n) and got.dtype == torch.float32
+    err = (got.double().cpu() - want).abs()
+    worst = float((err / tol).max())
+    print(f"  rows_linear {epilogue} norm={norm} {rows}x{k}->{n}: worst err/bound {worst:.3f}", flush=True)
+    assert worst <= 1.0
+
+
+@pytest.mark.parametrize("tag,batch,cfg,mcfg", [
+    ("default", 16, dict(), dict()),
+    ("odd-batch-bias", 17, dict(bias=True, d_state=8), dict()),
+    ("no-gate-no-conv", 3, dict(use_gating=False, use_conv=False), dict()),
+    ("gelu-mlp", 5, dict(gating_activation="gelu"), dict(mlp="gelu")),
+    ("no-mlp-s64", 2, dict(d_state=64), dict(mlp="none")),
+])
+def test_block_decode_fused_matches_unfused(cuda, monkeypatch, tag, batch, cfg, mcfg):
+    """A model's one-token steps through the fused block path (norm + projection,
+    conv and SSM kernels, projection + residual, norm + w12 + SwiGLU, w3 +
+    residual, final norm + LM head) against the same model with the fused path
+    switched off (the hip decode kernels between torch's norms and GEMMs): logits
+    and every state tensor over four steps after a prefill."""
+    from kla.layers.common import MLP
+
+    torch.manual_seed(0)
+    model = SequenceModel(ModelConfig(vocab_size=301, d_model=48, n_layers=2, **mcfg),
+                          KLAConfig(backend="hip", **cfg)).to(cuda).eval()
+    ids = torch.randint(0, 301, (batch, 9), generator=torch.Generator().manual_seed(3)).to(cuda)
+    toks = torch.randint(0, 301, (batch, 4), generator=torch.Generator().manual_seed(4)).to(cuda)
+
+    def run():
+        with torch.no_grad():
+            _, st = model(ids, state=model.init_state(batch))
+            outs = []
+            for i in range(4):
+                lg, st = model(toks[:, i:i + 1], state=st)
+                outs.append(lg)
+        return outs, st
+
+    fused_out, fused_st = run()
+    monkeypatch.setattr(KLALayer, "block_decode_ok", lambda self, x, state: False)
+    monkeypatch.setattr(MLP, "block_decode_ok", lambda self, x, norm: False)
+    monkeypatch.setattr(SequenceModel, "_head_on_rows", lambda self, x: False)
+    plain_out, plain_st = run()
+    for i, (a, b) in enumerate(zip(fused_out, plain_out)):
+        check(f"{tag} logits{i}", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
+    for la, lb in zip(fused_st, plain_st):
+        check(f"{tag} lam", la.ssm.lam, lb.ssm.lam.cpu().numpy(), rtol=2e-5, atol=0)
+        check(f"{tag} eta", la.ssm.eta, lb.ssm.eta.cpu().numpy(), rtol=2e-5, atol=2e-6)
+        if la.conv is not None:
+            check(f"{tag} conv", la.conv, lb.conv.cpu().numpy(), rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ids_shape", [(16, 1), (3, 7), (1,)])
+def test_gather_rows_matches_embedding(cuda, dtype, ids_shape):
+    """gather_rows_hip against nn.Embedding's lookup, bit for bit; ids outside
+    [0, vocab) give rows of NaN (the kernel reads nothing for them)."""
+    from kla.ops.hip.model_ops import gather_rows_hip
+
+    g = torch.Generator().manual_seed(51)
+    w = torch.randn(301, 40, generator=g).to(dtype).to(cuda)
+    ids = torch.randint(0, 301, ids_shape, generator=g).to(cuda)
+    got = gather_rows_hip(w, ids)
+    assert got.shape == (*ids_shape, 40) and got.dtype == dtype
+    assert torch.equal(got, torch.nn.functional.embedding(ids, w))
+    bad = torch.tensor([0, 301, -1, 300], device=cuda)
+    out = gather_rows_hip(w, bad)
+    assert torch.equal(out[0], w[0]) and torch.equal(out[3], w[300])
+    assert torch.isnan(out[1].float()).all() and torch.isnan(out[2].float()).all()
+
+
+@pytest.mark.parametrize("rows,n", [(16, 50304), (3, 7), (5, 1), (2, 4099)])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_argmax_rows_matches_torch(cuda, rows, n, aligned):
+    """argmax_rows_hip against torch.argmax(dim=-1, keepdim=True): values drawn from
+    a few integers so that ties are common (the lower index wins), a NaN in one
+    row (it wins), an all -inf row; rows 16-byte aligned or not."""
+    from kla.ops.hip.model_ops import argmax_rows_hip
+
+    g = torch.Generator().manual_seed(rows * 7 + n)
+    base = torch.randint(-3, 4, (rows, n + 1), generator=g).float().to(cuda)
+    x = base[:, :n].contiguous() if aligned else base[:, 1:]   # row stride n or n + 1 (offset 1)
+    if rows > 1 and n > 2:
+        x[1, n // 2] = float("nan")
+        x[rows - 1] = float("-inf")
+    got = argmax_rows_hip(x)
+    want = x.argmax(dim=-1, keepdim=True)
+    assert got.dtype == torch.int64 and got.shape == (rows, 1)
+    assert torch.equal(got, want), (got.view(-1)[:8], want.view(-1)[:8])
+
+
 def test_decode_kernels_in_place_equal_out_of_place(cuda):
     """The one-token conv and SSM kernels give the same values when they write the
     new state over the old one (what a decode graph does) as into new tensors."""
