@@ -269,3 +269,67 @@ def test_headline_shape_subset_of_lanes(cuda):
     dg, du, _ = ref.affine_scan_bwd(sub(dh), sub(g), hw)
     _close("dg", sub(gg.grad.cpu()), dg)
     _close("du", sub(uu.grad.cpu()), du)
+
+
+def test_scans_past_2_31_elements(cuda):
+    """Element indices past 2^31 need 64-bit offsets: (4, 65536, 8193) is 2^31 +
+    262144 elements (8.6 GB per fp32 tensor; MI355X holds the whole Moebius fwd +
+    bwd and a bf16 affine fwd + bwd). Inputs are drawn on the GPU from the bench's
+    families; five lanes of every batch -- tile edges and the ragged last lane,
+    whose elements in the last batch lie past 2^31 -- are checked against the
+    float64 oracle, and no look-back wait gave up."""
+    import torch.nn.functional as F
+
+    from kla.ops.hip import _lib
+    from kla.ops.hip import scans as hs
+
+    B, T, N = 4, 65536, 8193
+    assert B * T * N > 2 ** 31 and (B - 1) * T * N + (T - 1) * N + (N - 1) >= 2 ** 31
+    lanes = torch.tensor([0, 63, 64, 8191, 8192])
+    gen = torch.Generator(device=cuda).manual_seed(5)
+
+    def draw(fn):
+        return fn(torch.randn(B, T, N, device=cuda, generator=gen))
+
+    sub = lambda t: t[..., lanes.to(cuda)].float().cpu()  # noqa: E731
+    _log("[2^31] Moebius inputs")
+    A = draw(lambda z: torch.exp(-F.softplus(z)))
+    Bm = draw(F.softplus)
+    C = draw(F.softplus)
+    lam0 = F.softplus(torch.randn(B, N, device=cuda, generator=gen))
+    lam = hs._mobius_scan_op(A, Bm, C, None, lam0)
+    dlam = draw(lambda z: z)
+    dA, dB, dC, _, dl0 = hs._mobius_scan_bwd_op(dlam, A, Bm, C, None, lam0, lam)
+    torch.cuda.synchronize()
+    assert _lib.workspace_failures(cuda) == 0
+    for t in (lam, dA, dB, dC, dl0):
+        assert torch.isfinite(t).all()
+    sA, sB, sC, sl0, sdl = sub(A), sub(Bm), sub(C), lam0[:, lanes.to(cuda)].cpu(), sub(dlam)
+    got = [sub(t) for t in (lam, dA, dB, dC)] + [dl0[:, lanes.to(cuda)].cpu()]
+    del A, Bm, C, lam, dlam, dA, dB, dC
+    torch.cuda.empty_cache()
+    _log("[2^31] Moebius oracle")
+    want = ref.mobius_scan_fwd(sA, sB, sC, None, sl0)
+    _close("lam", got[0], want)
+    wA, wB, wC, _, wl0 = ref.mobius_scan_bwd(sdl, sA, sB, sC, None, sl0, want)
+    for name, g_, w in (("dA", got[1], wA), ("dB", got[2], wB), ("dC", got[3], wC), ("dlam0", got[4], wl0)):
+        _close(name, g_, w)
+
+    _log("[2^31] affine bf16 inputs")
+    g = draw(torch.sigmoid).to(torch.bfloat16)
+    u = draw(lambda z: z).to(torch.bfloat16)
+    h = hs._affine_scan_op(g, u, None)
+    dh = draw(lambda z: z).to(torch.bfloat16)
+    dg, du, _ = hs._affine_scan_bwd_op(dh, g, h, None)
+    torch.cuda.synchronize()
+    assert _lib.workspace_failures(cuda) == 0
+    sg, su, sdh = sub(g), sub(u), sub(dh)
+    got = [sub(t) for t in (h, dg, du)]
+    del g, u, h, dh, dg, du
+    torch.cuda.empty_cache()
+    _log("[2^31] affine oracle")
+    hw = ref.affine_scan_fwd(sg, su)
+    _close("h", got[0], hw, rtol=2e-2, atol=1e-2)
+    dgw, duw, _ = ref.affine_scan_bwd(sdh, sg, hw)
+    _close("dg", got[1], dgw, rtol=2e-2, atol=1e-2)
+    _close("du", got[2], duw, rtol=2e-2, atol=1e-2)
