@@ -410,6 +410,25 @@ int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *
                         const float *norm_w, float eps, const float *res, int64_t ldres, float *y, int64_t ldy,
                         int64_t rows, int64_t n, int64_t k, int64_t glu_off, hipStream_t stream);
 
+/*
+ * kla_rows_linear_fwd's plain product (same x, w, bias, norm_w, eps, y, rows, n,
+ * k) with one token of the depthwise causal conv applied to output columns
+ * j < conv_n (in_proj's z half in one-token decode):
+ *   y[r, j] = act(sum_{i < conv_k-1} conv_w[j, i] window[r, j, i] + conv_w[j, conv_k-1] a[r, j] + conv_b[j])
+ *   window_out[r, j, :] = (window[r, j, 1:], a[r, j])
+ * with a the product (plus bias); columns j >= conv_n are y = a. conv_w
+ * [conv_n, conv_k] dense, conv_b [conv_n] or NULL, window and window_out
+ * [rows, conv_n, conv_k - 1] dense fp32 (window_out may alias window), conv_k
+ * in [1, 8], activation 0 identity, 1 silu, 2 gelu (exact erf), 3 relu.
+ * Replaces, in decode, in_proj followed by the one-token path of
+ * CausalConv1d.forward (reference src/kla/layers/kla_layer.py:311-316,
+ * src/kla/layers/common.py:70-96).
+ */
+int kla_rows_linear_conv_fwd(const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
+                             const float *norm_w, float eps, float *y, int64_t ldy, int64_t rows, int64_t n,
+                             int64_t k, const float *conv_w, const float *conv_b, const float *window,
+                             float *window_out, int64_t conv_n, int conv_k, int activation, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

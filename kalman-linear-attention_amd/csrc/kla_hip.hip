@@ -1091,51 +1091,37 @@ int kla_swiglu_fwd(int dtype, const void *h, int64_t ld_h, void *out, int64_t ro
   return hip_status(fn, hipGetLastError());
 }
 
-int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
-                        const float *norm_w, float eps, const float *res, int64_t ldres, float *y, int64_t ldy,
-                        int64_t rows, int64_t n, int64_t k, int64_t glu_off, hipStream_t stream) {
-  const char *fn = "kla_rows_linear_fwd";
-  if (epilogue != KLA_ROWS_PLAIN && epilogue != KLA_ROWS_RESIDUAL && epilogue != KLA_ROWS_SWIGLU)
-    return fail(KLA_ERR_INVALID_ARG, "%s: unknown epilogue %d", fn, epilogue);
-  if (rows < 0 || n < 0 || k < 0 || glu_off < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+}  // extern "C"
+
+namespace {
+
+// Validates the product part of a row-linear call, fills `p` and launches the
+// kernel variant for `epi` (the caller has filled the epilogue's own fields).
+int rows_linear_launch(const char *fn, int epi, RowsLinearParams &p, hipStream_t stream) {
+  const int64_t rows = p.rows, n = p.n, k = p.k;
+  if (rows < 0 || n < 0 || k < 0 || p.glu_off < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
   if (rows == 0 || n == 0) return KLA_OK;
-  if (!y || (k > 0 && (!x || !w))) return fail(KLA_ERR_INVALID_ARG, "%s: x, w and y must not be NULL", fn);
-  if (epilogue == KLA_ROWS_RESIDUAL && !res)
-    return fail(KLA_ERR_INVALID_ARG, "%s: the residual epilogue needs res", fn);
-  if (epilogue == KLA_ROWS_SWIGLU && glu_off < n)
-    return fail(KLA_ERR_INVALID_ARG, "%s: glu_off %lld below n %lld (the halves overlap)", fn, (long long)glu_off,
-                (long long)n);
-  if (ldx < k || ldw < k || ldy < n || (epilogue == KLA_ROWS_RESIDUAL && ldres < n))
+  if (!p.y || (k > 0 && (!p.x || !p.w))) return fail(KLA_ERR_INVALID_ARG, "%s: x, w and y must not be NULL", fn);
+  if (epi == kEpiResidual && !p.res) return fail(KLA_ERR_INVALID_ARG, "%s: the residual epilogue needs res", fn);
+  if (epi == kEpiSwiglu && p.glu_off < n)
+    return fail(KLA_ERR_INVALID_ARG, "%s: glu_off %lld below n %lld (the halves overlap)", fn,
+                (long long)p.glu_off, (long long)n);
+  if (p.ldx < k || p.ldw < k || p.ldy < n || (epi == kEpiResidual && p.ldres < n))
     return fail(KLA_ERR_INVALID_ARG, "%s: a row stride is below its row length", fn);
-  if (norm_w && k == 0) return fail(KLA_ERR_INVALID_ARG, "%s: RMSNorm over zero columns", fn);
-  if (misaligned(x) || misaligned(w) || misaligned(bias) || misaligned(norm_w) || misaligned(res) || misaligned(y))
+  if (p.norm_w && k == 0) return fail(KLA_ERR_INVALID_ARG, "%s: RMSNorm over zero columns", fn);
+  if (misaligned(p.x) || misaligned(p.w) || misaligned(p.bias) || misaligned(p.norm_w) || misaligned(p.res) ||
+      misaligned(p.y))
     return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
   const int64_t tiles_n = (n + kRowsLinTile - 1) / kRowsLinTile;
   const int64_t tiles_m = (rows + kRowsLinTile - 1) / kRowsLinTile;
   if (tiles_n >= (1ll << 31) || tiles_m >= 65536) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
-  RowsLinearParams p;
-  p.x = x;
-  p.w = w;
-  p.bias = bias;
-  p.norm_w = norm_w;
-  p.res = res;
-  p.y = y;
-  p.ldx = ldx;
-  p.ldw = ldw;
-  p.ldres = ldres;
-  p.ldy = ldy;
-  p.rows = rows;
-  p.n = n;
-  p.k = k;
-  p.glu_off = glu_off;
-  p.eps = eps;
   // k split over the workgroup's waves in multiples of 16.
   const int64_t per = ((k + kRowsLinWaves - 1) / kRowsLinWaves + 15) / 16 * 16;
   if (per > (1 << 30)) return fail(KLA_ERR_INVALID_ARG, "%s: k too large", fn);
   p.k_per_wave = static_cast<int>(per > 0 ? per : 16);
   // Rows that start 16-byte aligned load four k at a time; a ragged last group
   // of a row (k not a multiple of 4) falls back to single loads in the kernel.
-  const bool vec = ldx % 4 == 0 && ldw % 4 == 0 && all_aligned(16, {x, w, norm_w});
+  const bool vec = p.ldx % 4 == 0 && p.ldw % 4 == 0 && all_aligned(16, {p.x, p.w, p.norm_w});
   // One workgroup per CU at most (a 1024-thread workgroup fills a CU): more
   // column tiles than that are walked by each workgroup in turn.
   int dev = 0, cus = 256;
@@ -1146,7 +1132,7 @@ int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *
   const int64_t per_cu = (cus + tiles_m - 1) / tiles_m;
   const int64_t ctas_n = tiles_n < per_cu ? tiles_n : per_cu;
   const dim3 grid(static_cast<uint32_t>(ctas_n), static_cast<uint32_t>(tiles_m));
-  const bool pipe = p.k_per_wave <= 16 * rows_lin_steps(epilogue, norm_w != nullptr);
+  const bool pipe = p.k_per_wave <= 16 * rows_lin_steps(epi, p.norm_w != nullptr);
   auto go = [&](auto epi_c, auto norm_c, auto vec_c) {
     if (pipe)
       hipLaunchKernelGGL((rows_linear_kernel<decltype(epi_c)::value, decltype(norm_c)::value,
@@ -1160,14 +1146,83 @@ int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *
   using T = std::true_type;
   using F = std::false_type;
   auto by_vec = [&](auto epi_c, auto norm_c) { vec ? go(epi_c, norm_c, T{}) : go(epi_c, norm_c, F{}); };
-  auto by_norm = [&](auto epi_c) { norm_w ? by_vec(epi_c, T{}) : by_vec(epi_c, F{}); };
-  if (epilogue == KLA_ROWS_PLAIN)
-    by_norm(std::integral_constant<int, kEpiPlain>{});
-  else if (epilogue == KLA_ROWS_RESIDUAL)
-    by_norm(std::integral_constant<int, kEpiResidual>{});
-  else
-    by_norm(std::integral_constant<int, kEpiSwiglu>{});
+  auto by_norm = [&](auto epi_c) { p.norm_w ? by_vec(epi_c, T{}) : by_vec(epi_c, F{}); };
+  switch (epi) {
+    case kEpiPlain:
+      by_norm(std::integral_constant<int, kEpiPlain>{});
+      break;
+    case kEpiResidual:
+      by_norm(std::integral_constant<int, kEpiResidual>{});
+      break;
+    case kEpiSwiglu:
+      by_norm(std::integral_constant<int, kEpiSwiglu>{});
+      break;
+    default:
+      by_norm(std::integral_constant<int, kEpiConv>{});
+      break;
+  }
   return hip_status(fn, hipGetLastError());
+}
+
+RowsLinearParams rows_params(const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
+                             const float *norm_w, float eps, float *y, int64_t ldy, int64_t rows, int64_t n,
+                             int64_t k) {
+  RowsLinearParams p{};
+  p.x = x;
+  p.w = w;
+  p.bias = bias;
+  p.norm_w = norm_w;
+  p.y = y;
+  p.ldx = ldx;
+  p.ldw = ldw;
+  p.ldy = ldy;
+  p.rows = rows;
+  p.n = n;
+  p.k = k;
+  p.eps = eps;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
+                        const float *norm_w, float eps, const float *res, int64_t ldres, float *y, int64_t ldy,
+                        int64_t rows, int64_t n, int64_t k, int64_t glu_off, hipStream_t stream) {
+  const char *fn = "kla_rows_linear_fwd";
+  if (epilogue != KLA_ROWS_PLAIN && epilogue != KLA_ROWS_RESIDUAL && epilogue != KLA_ROWS_SWIGLU)
+    return fail(KLA_ERR_INVALID_ARG, "%s: unknown epilogue %d", fn, epilogue);
+  RowsLinearParams p = rows_params(x, ldx, w, ldw, bias, norm_w, eps, y, ldy, rows, n, k);
+  p.res = res;
+  p.ldres = ldres;
+  p.glu_off = glu_off;
+  const int epi = epilogue == KLA_ROWS_PLAIN ? kEpiPlain : epilogue == KLA_ROWS_RESIDUAL ? kEpiResidual : kEpiSwiglu;
+  return rows_linear_launch(fn, epi, p, stream);
+}
+
+int kla_rows_linear_conv_fwd(const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
+                             const float *norm_w, float eps, float *y, int64_t ldy, int64_t rows, int64_t n,
+                             int64_t k, const float *conv_w, const float *conv_b, const float *window,
+                             float *window_out, int64_t conv_n, int conv_k, int activation, hipStream_t stream) {
+  const char *fn = "kla_rows_linear_conv_fwd";
+  if (conv_n < 0 || conv_n > n) return fail(KLA_ERR_INVALID_ARG, "%s: conv_n outside [0, n]", fn);
+  if (conv_k < 1 || conv_k > kRowsLinMaxConvK)
+    return fail(KLA_ERR_INVALID_ARG, "%s: conv_k %d outside [1, %d]", fn, conv_k, kRowsLinMaxConvK);
+  if (activation < 0 || activation > 3) return fail(KLA_ERR_INVALID_ARG, "%s: unknown activation %d", fn, activation);
+  if (rows > 0 && conv_n > 0 && (!conv_w || (conv_k > 1 && (!window || !window_out))))
+    return fail(KLA_ERR_INVALID_ARG, "%s: conv_w, window and window_out must not be NULL", fn);
+  if (misaligned(conv_w) || misaligned(conv_b) || misaligned(window) || misaligned(window_out))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  RowsLinearParams p = rows_params(x, ldx, w, ldw, bias, norm_w, eps, y, ldy, rows, n, k);
+  p.conv_w = conv_w;
+  p.conv_b = conv_b;
+  p.window = window;
+  p.window_out = window_out;
+  p.conv_n = conv_n;
+  p.conv_k = conv_k;
+  p.conv_act = activation;
+  return rows_linear_launch(fn, kEpiConv, p, stream);
 }
 
 int kla_gather_rows(int dtype, const void *table, int64_t ld_table, int64_t vocab, const int64_t *ids, void *out,

@@ -19,6 +19,10 @@
 //             residual: y = res + acc (the block's x + sublayer(x))
 //             swiglu: y[m, j] = silu(acc[m, j]) * acc[m, glu_off + j]
 //             (MLP.forward, common.py:116-123: h = w12(x); silu(gate) * up)
+//             conv: columns n < conv_n (in_proj's z half) go through one token of
+//             the depthwise causal conv, y = act(sum_j w[n, j] window[j] + b[n])
+//             over window = [state[m, n, :], acc], and the state shifts by one
+//             (CausalConv1d.forward, common.py:70-96); other columns are plain
 //
 // Work split. A workgroup of 16 waves owns 16 rows and walks 16-column tiles
 // (tile, tile + gridDim.x, ...; the grid is sized to the CUs); wave w takes a
@@ -39,7 +43,9 @@ constexpr int kRowsLinWaves = 16;
 constexpr int kRowsLinThreads = kRowsLinWaves * kWave;
 constexpr int kRowsLinTile = 16;    // rows and columns per workgroup
 
-enum RowsLinEpilogue { kEpiPlain = 0, kEpiResidual = 1, kEpiSwiglu = 2 };
+enum RowsLinEpilogue { kEpiPlain = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiConv = 3 };
+
+constexpr int kRowsLinMaxConvK = 8;   // conv taps the kEpiConv epilogue supports
 
 // 16-wide k steps a wave keeps in flight (one pass covers k <= 16 * 16 * steps):
 // 6, fewer where two weight tiles (SwiGLU) and the norm weights would push the
@@ -60,6 +66,13 @@ struct RowsLinearParams {
   int64_t glu_off;       // kEpiSwiglu: W row of the `up` half of output column 0
   float eps;
   int k_per_wave;        // multiple of 16
+  // kEpiConv: the one-token depthwise causal conv on output columns < conv_n
+  // (the z half of in_proj): conv_w [conv_n, conv_k], conv_b [conv_n] or NULL,
+  // window [rows, conv_n, conv_k - 1] dense; window_out may alias window.
+  const float *conv_w, *conv_b, *window;
+  float *window_out;
+  int64_t conv_n;
+  int conv_k, conv_act;
 };
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -190,11 +203,23 @@ __global__ void __launch_bounds__(kRowsLinThreads) rows_linear_kernel(RowsLinear
     const int64_t on = n0 + e_lane % kRowsLinTile;
     const bool out_ok = epi_thread && om < p.rows && on < p.n;
     float res = 0.0f, b0 = 0.0f, b1 = 0.0f;
+    float win[EPI == kEpiConv ? kRowsLinMaxConvK : 1], cw[EPI == kEpiConv ? kRowsLinMaxConvK : 1];
+    const bool conv_col = EPI == kEpiConv && out_ok && on < p.conv_n;
     if (out_ok) {
       if constexpr (EPI == kEpiResidual) res = p.res[om * p.ldres + on];
       if (p.bias) {
         b0 = p.bias[on];
         if constexpr (NT == 2) b1 = p.bias[on + p.glu_off];
+      }
+    }
+    if constexpr (EPI == kEpiConv) {
+      if (conv_col) {
+        const float *st = p.window + (om * p.conv_n + on) * (p.conv_k - 1);
+#pragma unroll
+        for (int j = 0; j < kRowsLinMaxConvK; ++j) {
+          win[j] = j < p.conv_k - 1 ? st[j] : 0.0f;
+          cw[j] = j < p.conv_k ? p.conv_w[on * p.conv_k + j] : 0.0f;
+        }
       }
     }
     prefetch();
@@ -249,6 +274,27 @@ __global__ void __launch_bounds__(kRowsLinThreads) rows_linear_kernel(RowsLinear
         out = activation(kActSilu, v[0]) * v[1];
       } else if constexpr (EPI == kEpiResidual) {
         out = res + v[0];
+      } else if constexpr (EPI == kEpiConv) {
+        out = v[0];
+        if (conv_col) {
+          // The conv step's order: taps over the state, then the new input, then the bias.
+          const float xt = v[0];
+          float a = 0.0f;
+#pragma unroll
+          for (int j = 0; j < kRowsLinMaxConvK - 1; ++j)
+            if (j < p.conv_k - 1) a += win[j] * cw[j];
+#pragma unroll
+          for (int j = 0; j < kRowsLinMaxConvK; ++j)
+            if (j == p.conv_k - 1) a += xt * cw[j];
+          if (p.conv_b) a = a + p.conv_b[on];
+          out = activation(p.conv_act, a);
+          // This thread alone reads and writes its window, so window_out may alias it.
+          float *so = p.window_out + (om * p.conv_n + on) * (p.conv_k - 1);
+#pragma unroll
+          for (int j = 0; j + 1 < kRowsLinMaxConvK - 1; ++j)
+            if (j + 1 < p.conv_k - 1) so[j] = win[j + 1];
+          if (p.conv_k > 1) so[p.conv_k - 2] = xt;
+        }
       } else {
         out = v[0];
       }

@@ -319,23 +319,34 @@ class KLALayer(nn.Module):
 
     def block_decode_hip(self, x: torch.Tensor, norm_weight: torch.Tensor, eps: float, state: KLALayerState):
         """``x + self(rms_norm(x), state)`` for one token (x [B, 1, d_model]), returning
-        (that, new_state): the block's pre-norm is fused into in_proj and the
-        residual add into out_proj (kla.ops.hip.model_ops.rows_linear_hip), the
-        sensor projection runs on the same row kernel, and the conv and SSM steps
-        are the HIP decode kernels. The values are those of the block's torch
+        (that, new_state): the block's pre-norm and the conv step are fused into
+        in_proj and the residual add into out_proj (kla.ops.hip.model_ops row
+        kernels), the sensor projection runs on the same row kernel, and the SSM
+        step is the HIP decode kernel. The values are those of the block's torch
         lines (reference src/kla/models/sequence_model.py:79-87) up to the order
         of the fp32 sums."""
         from kla.ops.hip.model_ops import rows_linear_hip
 
         cfg = self.config
         x2 = x[:, 0]
-        projected = rows_linear_hip(x2, self.in_proj.weight, self.in_proj.bias, norm_weight=norm_weight,
-                                    eps=eps).unsqueeze(1)
-        if cfg.use_gating:
-            z, gate = projected.chunk(2, dim=-1)
+        window = state.conv
+        if (self.conv is not None and self.conv.kernel_size <= 8 and window.dtype == torch.float32
+                and window.is_contiguous()):
+            # The conv step rides in in_proj's epilogue on the z columns.
+            from kla.ops.hip.model_ops import rows_linear_conv_hip
+
+            projected, conv_state = rows_linear_conv_hip(
+                x2, self.in_proj.weight, self.in_proj.bias, norm_weight=norm_weight, eps=eps,
+                conv_weight=self.conv.weight[:, 0, :], conv_bias=self.conv.bias, window=window,
+                activation=cfg.conv_activation, in_place=self._decode_in_place)
+            projected = projected.unsqueeze(1)
+            z, gate = projected.chunk(2, dim=-1) if cfg.use_gating else (projected, None)
+            y, _, ssm_state = self._decode_step_hip(z, gate, z, state.ssm, rows_linear=True)
         else:
-            z, gate = projected, None
-        y, _, conv_state, ssm_state = self._one_token_hip(z, gate, state, rows_linear=True)
+            projected = rows_linear_hip(x2, self.in_proj.weight, self.in_proj.bias, norm_weight=norm_weight,
+                                        eps=eps).unsqueeze(1)
+            z, gate = projected.chunk(2, dim=-1) if cfg.use_gating else (projected, None)
+            y, _, conv_state, ssm_state = self._one_token_hip(z, gate, state, rows_linear=True)
         out = rows_linear_hip(y[:, 0], self.out_proj.weight, self.out_proj.bias, residual=x2)
         return out.unsqueeze(1), KLALayerState(conv=conv_state, ssm=ssm_state)
 

@@ -68,6 +68,8 @@ _SIGNATURES = {
     "kla_gate_skip_workspace_bytes": (ctypes.c_size_t, [_i64] * 2),
     "kla_rms_norm_fwd": (ctypes.c_int, [ctypes.c_int, _p, _p, ctypes.c_float, _p, _i64, _i64, _p]),
     "kla_swiglu_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _i64, _p]),
+    "kla_rows_linear_conv_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, ctypes.c_float, _p, _i64, _i64, _i64,
+                                                _i64, _p, _p, _p, _p, _i64, ctypes.c_int, ctypes.c_int, _p]),
     "kla_gather_rows": (ctypes.c_int, [ctypes.c_int, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p]),
     "kla_argmax_rows": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _p]),
     "kla_rows_linear_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _p, _p, ctypes.c_float, _p, _i64, _p,

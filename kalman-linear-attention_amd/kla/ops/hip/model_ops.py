@@ -165,3 +165,35 @@ def argmax_rows_hip(x: torch.Tensor) -> torch.Tensor:
         x2.data_ptr(), x2.stride(0), x2.shape[0], x2.shape[1], out.data_ptr(), 1,
         torch.cuda.current_stream(x.device).cuda_stream))
     return out.view(*x.shape[:-1], 1)
+
+
+_CONV_ACT = {"identity": 0, "silu": 1, "gelu": 2, "relu": 3}
+
+
+def rows_linear_conv_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, *,
+                         norm_weight: torch.Tensor | None, eps: float, conv_weight: torch.Tensor,
+                         conv_bias: torch.Tensor | None, window: torch.Tensor, activation: str = "silu",
+                         in_place: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """``norm(x) @ weight.T + bias`` for fp32 x [rows, k] with one token of the
+    depthwise causal conv applied to the first ``D = conv_weight.shape[0]`` output
+    columns: returns (y [rows, n], new window [rows, D, K - 1]). ``window`` is the
+    conv state [rows, D, K - 1] (contiguous fp32); with ``in_place`` the new window
+    is written over it and returned as the same tensor."""
+    if x.dim() != 2 or x.stride(-1) != 1:
+        x = x.reshape(-1, x.shape[-1]).contiguous()
+    w = _rows_aligned(weight if weight.stride(-1) == 1 else weight.contiguous())
+    rows, k = x.shape
+    n = w.shape[0]
+    D, K = conv_weight.shape
+    cw = conv_weight.contiguous()
+    if window.shape != (rows, D, K - 1) or not window.is_contiguous() or window.dtype != torch.float32:
+        raise ValueError(f"rows_linear_conv_hip: window {tuple(window.shape)} is not a dense fp32 [rows, D, K-1]")
+    win_out = window if in_place else torch.empty_like(window)
+    y = torch.empty(rows, (n + 3) // 4 * 4, dtype=torch.float32, device=x.device)[:, :n]
+    p = _lib.ptr
+    g = norm_weight.contiguous() if norm_weight is not None else None
+    _lib.check("kla_rows_linear_conv_fwd", _lib.lib().kla_rows_linear_conv_fwd(
+        p(x), x.stride(0), p(w), w.stride(0), p(bias.contiguous() if bias is not None else None), p(g), float(eps),
+        p(y), y.stride(0), rows, n, k, p(cw), p(conv_bias.contiguous() if conv_bias is not None else None),
+        p(window), p(win_out), D, K, _CONV_ACT[activation], torch.cuda.current_stream(x.device).cuda_stream))
+    return y, win_out

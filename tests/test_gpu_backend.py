@@ -1033,6 +1033,7 @@ def test_rows_linear_matches_float64(cuda, epilogue, norm, rows, k, n, aligned_x
     ("no-gate-no-conv", 3, dict(use_gating=False, use_conv=False), dict()),
     ("gelu-mlp", 5, dict(gating_activation="gelu"), dict(mlp="gelu")),
     ("no-mlp-s64", 2, dict(d_state=64), dict(mlp="none")),
+    ("conv-k2-relu", 4, dict(conv_kernel_size=2, conv_activation="relu"), dict()),
 ])
 def test_block_decode_fused_matches_unfused(cuda, monkeypatch, tag, batch, cfg, mcfg):
     """A model's one-token steps through the fused block path (norm + projection,
@@ -1108,6 +1109,41 @@ def test_argmax_rows_matches_torch(cuda, rows, n, aligned):
     want = x.argmax(dim=-1, keepdim=True)
     assert got.dtype == torch.int64 and got.shape == (rows, 1)
     assert torch.equal(got, want), (got.view(-1)[:8], want.view(-1)[:8])
+
+
+@pytest.mark.parametrize("K", [1, 2, 4, 8])
+@pytest.mark.parametrize("act", ["silu", "gelu", "relu", "identity"])
+@pytest.mark.parametrize("gated,with_bias", [(True, True), (False, False)])
+def test_rows_linear_conv_matches_two_kernels(cuda, K, act, gated, with_bias):
+    """The conv epilogue (in_proj + one conv token) against the product alone
+    followed by the conv step kernel: the conv columns to 2e-6 of their scale,
+    the gate columns and the new window equal; written in place it gives the
+    same values as into a new window."""
+    from kla.ops.hip.decode import conv_step_hip
+    from kla.ops.hip.model_ops import rows_linear_conv_hip, rows_linear_hip
+
+    g = torch.Generator().manual_seed(61 + K)
+    rows, k, D = 5, 96, 40
+    n = 2 * D if gated else D
+    x = torch.randn(rows, k, generator=g).to(cuda)
+    w = (torch.randn(n, k, generator=g) / k ** 0.5).to(cuda)
+    gw = (torch.rand(k, generator=g) + 0.5).to(cuda)
+    cw = torch.randn(D, K, generator=g).to(cuda)
+    cb = torch.randn(D, generator=g).to(cuda) if with_bias else None
+    win = torch.randn(rows, D, K - 1, generator=g).to(cuda)
+
+    y, new_win = rows_linear_conv_hip(x, w, None, norm_weight=gw, eps=1e-5, conv_weight=cw, conv_bias=cb,
+                                      window=win, activation=act)
+    a = rows_linear_hip(x, w, norm_weight=gw, eps=1e-5)
+    zs, want_win = conv_step_hip(a[:, :D], win.clone(), cw, cb, act)
+    check(f"conv K={K} {act}", y[:, :D], zs.cpu().numpy(), rtol=2e-6, atol=2e-6)
+    if gated:
+        assert torch.equal(y[:, D:], a[:, D:])
+    assert torch.equal(new_win, want_win)
+    win_in = win.clone()
+    y2, w2 = rows_linear_conv_hip(x, w, None, norm_weight=gw, eps=1e-5, conv_weight=cw, conv_bias=cb,
+                                  window=win_in, activation=act, in_place=True)
+    assert w2 is win_in and torch.equal(w2, new_win) and torch.equal(y2, y)
 
 
 def test_decode_kernels_in_place_equal_out_of_place(cuda):
