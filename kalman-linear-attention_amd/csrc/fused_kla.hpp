@@ -1046,17 +1046,24 @@ __device__ __forceinline__ float activation(int act, float x) {
   return x;
 }
 
-template <int SP, bool PRIOR>
+// Workgroup w covers channel group w % groups of batch rows [BB (w / groups),
+// + BB): each thread discretises its (m, s) once and runs the step for its BB
+// rows (the discretisation is the step's costliest part: exp, softplus, expm1).
+template <int SP, bool PRIOR, int BB>
 __global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodeParams prm, FusedGeom g) {
-  const FusedLane ln = fused_lane<SP>(g);
+  constexpr int CH = kFusedThreads / SP;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int sl = tid % SP;
+  const int64_t b0 = (static_cast<int64_t>(blockIdx.x) / g.groups) * BB;
+  const int64_t m = (static_cast<int64_t>(blockIdx.x) % g.groups) * CH + tid / SP;
   const int64_t M = g.M, S = g.S;
-  const bool mok = ln.m < M, sok = ln.s < S;
-  const int64_t ms = ln.m * S + ln.s;
-  const int64_t bms = ln.b * M * S + ms;
+  const bool mok = m < M, sok = sl < S;
+  const bool active = mok && sok;
+  const int64_t ms = m * S + sl;
 
   // (a_bar, p_bar) of this (m, s).
   float a_bar = 1.0f, p_bar = 0.0f;
-  if (ln.active) {
+  if (active) {
     const float a = -expf(prm.lambda_log[ms]);
     float p = prm.pnoise[ms];
     if (prm.zero_pn) {
@@ -1074,59 +1081,66 @@ __global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodePa
       p_bar = p * delta;
     }
   }
-
-  // Sensors: k, q (l2-normalised over the S states, clipped), Lambda^v = 1 / obs_var.
-  float kk = sok ? prm.k[ln.b * prm.ld_kq + ln.s] : 0.0f;
-  float qq = sok ? prm.q[ln.b * prm.ld_kq + ln.s] : 0.0f;
-  if (prm.qk_norm) {
-    kk = kk / fmaxf(sqrtf(group_sum<SP>(kk * kk)), 1e-12f);
-    qq = qq / fmaxf(sqrtf(group_sum<SP>(qq * qq)), 1e-12f);
-  }
-  if (prm.has_clip) {
-    kk = fminf(fmaxf(kk, -prm.clip), prm.clip);
-    qq = fminf(fmaxf(qq, -prm.clip), prm.clip);
-  }
-  const float vv = mok ? prm.v[ln.b * prm.ld_v + ln.m] : 0.0f;
-  float ov = (mok ? softplus_t(prm.lv[ln.b * prm.ld_lv + ln.m]) : 1.0f) + prm.ov_min;
-  ov = fminf(ov, prm.ov_max);
-  const float sig = 1.0f / ov;
-
-  // The filter step (as kla_step_kernel).
   const float a_s = a_bar;
   const float pp = fmaxf(p_bar, kEps);
   const float a2 = fmaxf(a_s * a_s, kEps);
-  float lam = ln.active ? prm.lam[bms] : 1.0f;
-  float eta = ln.active ? prm.eta[bms] : 0.0f;
-  const float phi = fmaxf(sig * (kk * kk), kEps);
-  const float r = (vv * sig) * kk;
-  const float denom = fmaxf(a2 + pp * lam, kEps);
-  lam = lam / denom + phi;
-  eta = (a_s / denom) * eta + r;
-  const float var = 1.0f / fmaxf(lam, kEps);
-  float mean = eta * var, vo = var;
-  if (PRIOR) {
-    mean = a_s * mean;
-    vo = a2 * var + pp;
-  }
-  const float ys = group_sum<SP>(mean * qq);
-  const float vs = group_sum<SP>(vo * (qq * qq));
-  if (ln.s == 0 && mok) {
-    float yo = ys, vo2 = vs;
-    if (prm.z) {
-      const float lsk = prm.skip_vector ? prm.skip[ln.m] : prm.skip[0];
-      yo = yo + lsk * prm.z[ln.b * prm.ld_z + ln.m];
+
+#pragma unroll
+  for (int bb = 0; bb < BB; ++bb) {
+    const int64_t b = b0 + bb;
+    if (b >= g.batch) break;   // workgroup-uniform
+    const int64_t bms = b * M * S + ms;
+    // Sensors: k, q (l2-normalised over the S states, clipped), Lambda^v = 1 / obs_var.
+    float kk = sok ? prm.k[b * prm.ld_kq + sl] : 0.0f;
+    float qq = sok ? prm.q[b * prm.ld_kq + sl] : 0.0f;
+    if (prm.qk_norm) {
+      kk = kk / fmaxf(sqrtf(group_sum<SP>(kk * kk)), 1e-12f);
+      qq = qq / fmaxf(sqrtf(group_sum<SP>(qq * qq)), 1e-12f);
     }
-    if (prm.gate) {
-      const float gg = activation(prm.gate_act, prm.gate[ln.b * prm.ld_gate + ln.m]);
-      yo = yo * gg;
-      vo2 = vo2 * (gg * gg);
+    if (prm.has_clip) {
+      kk = fminf(fmaxf(kk, -prm.clip), prm.clip);
+      qq = fminf(fmaxf(qq, -prm.clip), prm.clip);
     }
-    prm.y[ln.b * M + ln.m] = yo;
-    prm.yvar[ln.b * M + ln.m] = vo2;
-  }
-  if (ln.active) {
-    prm.lam_out[bms] = lam;
-    prm.eta_out[bms] = eta;
+    const float vv = mok ? prm.v[b * prm.ld_v + m] : 0.0f;
+    float ov = (mok ? softplus_t(prm.lv[b * prm.ld_lv + m]) : 1.0f) + prm.ov_min;
+    ov = fminf(ov, prm.ov_max);
+    const float sig = 1.0f / ov;
+
+    // The filter step (as kla_step_kernel).
+    float lam = active ? prm.lam[bms] : 1.0f;
+    float eta = active ? prm.eta[bms] : 0.0f;
+    const float phi = fmaxf(sig * (kk * kk), kEps);
+    const float r = (vv * sig) * kk;
+    const float denom = fmaxf(a2 + pp * lam, kEps);
+    lam = lam / denom + phi;
+    eta = (a_s / denom) * eta + r;
+    const float var = 1.0f / fmaxf(lam, kEps);
+    float mean = eta * var, vo = var;
+    if (PRIOR) {
+      mean = a_s * mean;
+      vo = a2 * var + pp;
+    }
+    const float ys = group_sum<SP>(mean * qq);
+    const float vs = group_sum<SP>(vo * (qq * qq));
+    if (sl == 0 && mok) {
+      float yo = ys, vo2 = vs;
+      if (prm.z) {
+        const float lsk = prm.skip_vector ? prm.skip[m] : prm.skip[0];
+        yo = yo + lsk * prm.z[b * prm.ld_z + m];
+      }
+      if (prm.gate) {
+        const float gg = activation(prm.gate_act, prm.gate[b * prm.ld_gate + m]);
+        yo = yo * gg;
+        vo2 = vo2 * (gg * gg);
+      }
+      prm.y[b * M + m] = yo;
+      prm.yvar[b * M + m] = vo2;
+    }
+    // This thread alone reads and writes (b, m, s): lam_out / eta_out may alias lam / eta.
+    if (active) {
+      prm.lam_out[bms] = lam;
+      prm.eta_out[bms] = eta;
+    }
   }
 }
 
