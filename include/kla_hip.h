@@ -387,6 +387,22 @@ int kla_gather_rows(int dtype, const void *table, int64_t ld_table, int64_t voca
 int kla_argmax_rows(const float *x, int64_t ldx, int64_t rows, int64_t n, int64_t *out, int64_t ld_out,
                     hipStream_t stream);
 
+/*
+ * A KLA layer's static dynamics over n = M * S elements, fp32
+ * (KLALayer._compute_aq, reference src/kla/layers/kla_layer.py:164-190):
+ *   a = -exp(lambda_log);  p = pnoise + 1e-12 (zero_process_noise) or min(max(pnoise, 1e-7), clip)
+ *   d = softplus(delta) + 1e-7;  a_bar = exp(d a)
+ *   ou: p_bar = (p / (2 rate)) (-expm1(-2 rate d)), rate = max(|a|, 1e-8);  else p_bar = p d
+ * has_clip: whether clip applies. The backward takes the gradients of a_bar and
+ * p_bar (either may be NULL: zero) and writes those of delta, lambda_log and pnoise.
+ */
+int kla_discretize_fwd(const float *delta, const float *lambda_log, const float *pnoise, int64_t n, int ou,
+                       int zero_process_noise, int has_clip, float clip, float *a_bar, float *p_bar,
+                       hipStream_t stream);
+int kla_discretize_bwd(const float *delta, const float *lambda_log, const float *pnoise, int64_t n, int ou,
+                       int zero_process_noise, int has_clip, float clip, const float *g_a_bar, const float *g_p_bar,
+                       float *d_delta, float *d_lambda_log, float *d_pnoise, hipStream_t stream);
+
 /* Epilogues of kla_rows_linear_fwd. */
 enum { KLA_ROWS_PLAIN = 0, KLA_ROWS_RESIDUAL = 1, KLA_ROWS_SWIGLU = 2 };
 

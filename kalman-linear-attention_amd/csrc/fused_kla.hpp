@@ -1144,6 +1144,106 @@ __global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodePa
   }
 }
 
+// The static dynamics of a KLA layer, per (m, s) (reference kla_layer.py:164-190,
+// KLALayer._continuous_params / _discretize / _compute_aq):
+//   a = -exp(lambda_log);  p = pn + 1e-12 (zero_pn) or min(max(pn, 1e-7), clip)
+//   d = softplus(delta) + 1e-7;  a_bar = exp(d a)
+//   OU: rate = max(|a|, 1e-8), p_bar = (p / (2 rate)) (-expm1((-2 rate) d));  ZOH: p_bar = p d
+// The backward is the chain rule through those same operations, term by term as
+// torch's autograd forms it (clamp gradients pass at equality, softplus's
+// gradient is 1 above the threshold 20, expm1's is exp).
+struct DiscParams {
+  const float *delta, *lambda_log, *pnoise;
+  float *a_bar, *p_bar;                 // forward outputs
+  const float *g_a, *g_p;               // backward: gradients of a_bar, p_bar (NULL: zero)
+  float *d_delta, *d_ll, *d_pn;         // backward outputs
+  int64_t n;
+  int ou, zero_pn, has_clip;
+  float clip;
+};
+
+__global__ void __launch_bounds__(256) discretize_fwd_kernel(DiscParams q) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= q.n) return;
+  const float a = -expf(q.lambda_log[i]);
+  float p = q.pnoise[i];
+  if (q.zero_pn) {
+    p = p + 1e-12f;
+  } else {
+    p = fmaxf(p, 1e-7f);
+    if (q.has_clip) p = fminf(p, q.clip);
+  }
+  const float d = softplus_t(q.delta[i]) + 1e-7f;
+  q.a_bar[i] = expf(d * a);
+  if (q.ou) {
+    const float rate = fmaxf(fabsf(a), 1e-8f);
+    q.p_bar[i] = (p / (2.0f * rate)) * (-expm1f((-2.0f * rate) * d));
+  } else {
+    q.p_bar[i] = p * d;
+  }
+}
+
+__global__ void __launch_bounds__(256) discretize_bwd_kernel(DiscParams q) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= q.n) return;
+  const float ll = q.lambda_log[i], pn = q.pnoise[i], dl = q.delta[i];
+  const float g_a = q.g_a ? q.g_a[i] : 0.0f, g_p = q.g_p ? q.g_p[i] : 0.0f;
+  const float a = -expf(ll);
+  float p = pn, g_pmask = 1.0f;
+  if (q.zero_pn) {
+    p = p + 1e-12f;
+  } else {
+    if (!(pn >= 1e-7f)) g_pmask = 0.0f;
+    p = fmaxf(p, 1e-7f);
+    if (q.has_clip) {
+      if (!(p <= q.clip)) g_pmask = 0.0f;
+      p = fminf(p, q.clip);
+    }
+  }
+  const float d = softplus_t(dl) + 1e-7f;
+  const float a_bar = expf(d * a);
+  // a_bar = exp(t), t = d a
+  const float g_t = g_a * a_bar;
+  float g_d = g_t * a;
+  float g_ac = g_t * d;   // gradient of the continuous a
+  float g_pp;             // gradient of the floored / clipped p
+  if (q.ou) {
+    const float absa = fabsf(a);
+    const float rate = fmaxf(absa, 1e-8f);
+    const float two_rate = 2.0f * rate;
+    const float q1 = p / two_rate;
+    const float c = -2.0f * rate;
+    const float u = c * d;
+    const float E = -expm1f(u);
+    // p_bar = q1 E
+    const float g_q1 = g_p * E;
+    const float g_E = g_p * q1;
+    // E = -expm1(u)
+    const float g_u = -g_E * expf(u);
+    // u = c d
+    const float g_c = g_u * d;
+    g_d += g_u * c;
+    // q1 = p / two_rate
+    g_pp = g_q1 / two_rate;
+    const float g_two_rate = -g_q1 * p / (two_rate * two_rate);
+    // two_rate = 2 rate, c = -2 rate
+    const float g_rate = 2.0f * g_two_rate + -2.0f * g_c;
+    // rate = max(|a|, 1e-8)
+    const float g_abs = absa >= 1e-8f ? g_rate : 0.0f;
+    const float sgn = a > 0.0f ? 1.0f : (a < 0.0f ? -1.0f : 0.0f);
+    g_ac += g_abs * sgn;
+  } else {
+    g_pp = g_p * d;
+    g_d += g_p * p;
+  }
+  // d = softplus(delta) + 1e-7 (threshold 20)
+  const float z = expf(dl);
+  q.d_delta[i] = dl > 20.0f ? g_d : g_d * z / (z + 1.0f);
+  // a = -exp(lambda_log)
+  q.d_ll[i] = g_ac * a;
+  q.d_pn[i] = g_pp * g_pmask;
+}
+
 // One token of the depthwise causal conv (CausalConv1d, reference common.py:70-96):
 // window = [state[b, d, :], x[b, d]], y = act(sum_j w[d, j] window[j] + bias[d]),
 // new state = window[1:]. One thread per (b, d).

@@ -27,7 +27,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 9;
+constexpr int kAbiVersion = 10;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -1267,6 +1267,61 @@ int kla_argmax_rows(const float *x, int64_t ldx, int64_t rows, int64_t n, int64_
     hipLaunchKernelGGL(argmax_rows_kernel<true>, grid, dim3(kArgmaxThreads), 0, stream, x, ldx, n, out, ld_out);
   else
     hipLaunchKernelGGL(argmax_rows_kernel<false>, grid, dim3(kArgmaxThreads), 0, stream, x, ldx, n, out, ld_out);
+  return hip_status(fn, hipGetLastError());
+}
+
+int kla_discretize_fwd(const float *delta, const float *lambda_log, const float *pnoise, int64_t n, int ou,
+                       int zero_process_noise, int has_clip, float clip, float *a_bar, float *p_bar,
+                       hipStream_t stream) {
+  const char *fn = "kla_discretize_fwd";
+  if (n < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  if (n == 0) return KLA_OK;
+  if (!delta || !lambda_log || !pnoise || !a_bar || !p_bar)
+    return fail(KLA_ERR_INVALID_ARG, "%s: NULL operand", fn);
+  if (!all_aligned(4, {delta, lambda_log, pnoise, a_bar, p_bar}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if ((n + 255) / 256 >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many elements", fn);
+  DiscParams q{};
+  q.delta = delta;
+  q.lambda_log = lambda_log;
+  q.pnoise = pnoise;
+  q.a_bar = a_bar;
+  q.p_bar = p_bar;
+  q.n = n;
+  q.ou = ou != 0;
+  q.zero_pn = zero_process_noise != 0;
+  q.has_clip = has_clip != 0;
+  q.clip = clip;
+  hipLaunchKernelGGL(discretize_fwd_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream, q);
+  return hip_status(fn, hipGetLastError());
+}
+
+int kla_discretize_bwd(const float *delta, const float *lambda_log, const float *pnoise, int64_t n, int ou,
+                       int zero_process_noise, int has_clip, float clip, const float *g_a_bar, const float *g_p_bar,
+                       float *d_delta, float *d_lambda_log, float *d_pnoise, hipStream_t stream) {
+  const char *fn = "kla_discretize_bwd";
+  if (n < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  if (n == 0) return KLA_OK;
+  if (!delta || !lambda_log || !pnoise || !d_delta || !d_lambda_log || !d_pnoise)
+    return fail(KLA_ERR_INVALID_ARG, "%s: NULL operand", fn);
+  if (!all_aligned(4, {delta, lambda_log, pnoise, g_a_bar, g_p_bar, d_delta, d_lambda_log, d_pnoise}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if ((n + 255) / 256 >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many elements", fn);
+  DiscParams q{};
+  q.delta = delta;
+  q.lambda_log = lambda_log;
+  q.pnoise = pnoise;
+  q.g_a = g_a_bar;
+  q.g_p = g_p_bar;
+  q.d_delta = d_delta;
+  q.d_ll = d_lambda_log;
+  q.d_pn = d_pnoise;
+  q.n = n;
+  q.ou = ou != 0;
+  q.zero_pn = zero_process_noise != 0;
+  q.has_clip = has_clip != 0;
+  q.clip = clip;
+  hipLaunchKernelGGL(discretize_bwd_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, stream, q);
   return hip_status(fn, hipGetLastError());
 }
 

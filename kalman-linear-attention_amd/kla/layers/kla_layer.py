@@ -133,6 +133,14 @@ class KLALayer(nn.Module):
 
     def _compute_aq(self):
         """Discrete (a_bar, p_bar), each [M, S]."""
+        if self._aq_on_hip():
+            # One HIP kernel each way for the ~40 small torch kernels below.
+            from kla.ops.hip.dynamics import discretize_hip
+
+            cfg = self.config
+            return discretize_hip(self.delta, self.lambda_log, self.process_noise,
+                                  discretization=cfg.discretization, zero_process_noise=cfg.zero_process_noise,
+                                  clip_value=cfg.clip_value)
         a, p = self._continuous_params()
         delta = F.softplus(self.delta.float()) + 1e-7
         return self._discretize(delta, a, p)
@@ -210,6 +218,15 @@ class KLALayer(nn.Module):
             y, y_var, new_state = kla_step(v[:, 0], lambda_v[:, 0], k[:, 0], q[:, 0], a_bar, p_bar, ssm_state,
                                            decode_from_prior=cfg.decode_from_prior, backend=cfg.backend)
         return y.unsqueeze(1), y_var.unsqueeze(1), new_state
+
+    def _aq_on_hip(self) -> bool:
+        """Whether (a_bar, p_bar) come from the MI355X kernels: fp32 parameters on a
+        ROCm GPU and a hip-family backend."""
+        from kla.ops.kla_ops import _step_on_hip
+
+        params = (self.delta, self.lambda_log, self.process_noise)
+        return (all(t.dtype == torch.float32 for t in params)
+                and _step_on_hip(self.config.backend, self.delta))
 
     def _sensors_on_hip(self, z: torch.Tensor) -> bool:
         """Whether the sequence scan runs on the fused hip kernel with the sensor

@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -70,6 +70,8 @@ _SIGNATURES = {
     "kla_swiglu_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _i64, _p]),
     "kla_rows_linear_conv_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, ctypes.c_float, _p, _i64, _i64, _i64,
                                                 _i64, _p, _p, _p, _p, _i64, ctypes.c_int, ctypes.c_int, _p]),
+    "kla_discretize_fwd": (ctypes.c_int, [_p] * 3 + [_i64] + [ctypes.c_int] * 3 + [ctypes.c_float] + [_p] * 3),
+    "kla_discretize_bwd": (ctypes.c_int, [_p] * 3 + [_i64] + [ctypes.c_int] * 3 + [ctypes.c_float] + [_p] * 6),
     "kla_gather_rows": (ctypes.c_int, [ctypes.c_int, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p]),
     "kla_argmax_rows": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _p]),
     "kla_rows_linear_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _p, _p, ctypes.c_float, _p, _i64, _p,

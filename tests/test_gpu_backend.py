@@ -1146,6 +1146,59 @@ def test_rows_linear_conv_matches_two_kernels(cuda, K, act, gated, with_bias):
     assert w2 is win_in and torch.equal(w2, new_win) and torch.equal(y2, y)
 
 
+@pytest.mark.parametrize("discretization", ["ou", "zoh"])
+@pytest.mark.parametrize("zero_pn,clip", [(False, None), (False, 0.5), (True, None)])
+def test_discretize_matches_float64_autograd(cuda, discretization, zero_pn, clip):
+    """discretize_hip (a_bar, p_bar and the gradients of delta, lambda_log and
+    process_noise) against the layer's own torch lines evaluated in float64 with
+    autograd. The parameters cover every branch: softplus above its threshold
+    (delta > 20), process noise below the 1e-7 floor and above the clip, and
+    |a| = exp(lambda_log) below the 1e-8 rate floor."""
+    from kla.ops.hip.dynamics import discretize_hip
+
+    g = torch.Generator().manual_seed(71)
+    M, S = 37, 16
+    delta = torch.randn(M, S, generator=g) * 3
+    delta[0, :4] = torch.tensor([21.0, 25.0, -30.0, 19.5])
+    lam_log = torch.randn(M, S, generator=g)
+    lam_log[1, :3] = torch.tensor([-25.0, -19.0, 3.0])     # |a| = e^-25 < 1e-8
+    pn = torch.rand(M, S, generator=g)
+    pn[2, :3] = torch.tensor([1e-9, 0.9, 0.0])             # below the floor, above a 0.5 clip
+    cfg = KLAConfig(discretization=discretization, zero_process_noise=zero_pn, clip_value=clip)
+
+    def torch_lines(delta, ll, pn):
+        # KLALayer._continuous_params / _discretize / _compute_aq, in the dtype given.
+        a = -torch.exp(ll)
+        p = pn
+        if cfg.zero_process_noise:
+            p = p + 1e-12
+        else:
+            p = p.clamp_min(1e-7)
+            if cfg.clip_value is not None:
+                p = p.clamp_max(cfg.clip_value)
+        d = torch.nn.functional.softplus(delta) + 1e-7
+        a_bar = torch.exp(d * a)
+        if cfg.discretization == "ou":
+            rate = a.abs().clamp_min(1e-8)
+            p_bar = (p / (2.0 * rate)) * (-torch.expm1(-2.0 * rate * d))
+        else:
+            p_bar = p * d
+        return a_bar, p_bar
+
+    ins64 = [t.double().requires_grad_(True) for t in (delta, lam_log, pn)]
+    a64, p64 = torch_lines(*ins64)
+    ga, gp = torch.randn(M, S, generator=g), torch.randn(M, S, generator=g)
+    torch.autograd.backward([a64, p64], [ga.double(), gp.double()])
+
+    ins = [t.to(cuda).requires_grad_(True) for t in (delta, lam_log, pn)]
+    a_bar, p_bar = discretize_hip(*ins, discretization=discretization, zero_process_noise=zero_pn, clip_value=clip)
+    torch.autograd.backward([a_bar, p_bar], [ga.to(cuda), gp.to(cuda)])
+    check("a_bar", a_bar, a64.detach().numpy(), rtol=1e-5, atol=1e-6)
+    check("p_bar", p_bar, p64.detach().numpy(), rtol=1e-5, atol=1e-6)
+    for name, got, want in zip(("d delta", "d lambda_log", "d pnoise"), ins, ins64):
+        check(name, got.grad, want.grad.numpy(), rtol=1e-5, atol=1e-6)
+
+
 def test_decode_kernels_in_place_equal_out_of_place(cuda):
     """The one-token conv and SSM kernels give the same values when they write the
     new state over the old one (what a decode graph does) as into new tensors."""
