@@ -403,6 +403,23 @@ int kla_discretize_bwd(const float *delta, const float *lambda_log, const float 
                        int zero_process_noise, int has_clip, float clip, const float *g_a_bar, const float *g_p_bar,
                        float *d_delta, float *d_lambda_log, float *d_pnoise, hipStream_t stream);
 
+/*
+ * The k and q sensors of a KLA layer (KLALayer._project_sensors_raw, reference
+ * src/kla/layers/kla_layer.py:194-231): per row of S values,
+ *   y = clamp(l2_norm(x), -clip, clip) in fp32,  l2_norm(x) = x / max(||x||_2, 1e-12)
+ * (norm: whether to normalise; has_clip: whether to clip), rounding to `dtype`
+ * after each operation as torch does for that dtype. k, q: [rows, S] of `dtype`
+ * with rows ld_k / ld_q elements apart (column slices of the sensor
+ * projection); yk, yq: [rows, S] dense fp32. The backward takes the gradients of
+ * yk, yq ([rows, S] dense fp32) and writes dk, dq ([rows, S] dense, `dtype`)
+ * through torch's autograd chain of the same operations.
+ */
+int kla_qk_sensors_fwd(int dtype, const void *k, int64_t ld_k, const void *q, int64_t ld_q, float *yk, float *yq,
+                       int64_t rows, int64_t S, int norm, int has_clip, float clip, hipStream_t stream);
+int kla_qk_sensors_bwd(int dtype, const void *k, int64_t ld_k, const void *q, int64_t ld_q, const float *dyk,
+                       const float *dyq, void *dk, void *dq, int64_t rows, int64_t S, int norm, int has_clip,
+                       float clip, hipStream_t stream);
+
 /* Epilogues of kla_rows_linear_fwd. */
 enum { KLA_ROWS_PLAIN = 0, KLA_ROWS_RESIDUAL = 1, KLA_ROWS_SWIGLU = 2 };
 

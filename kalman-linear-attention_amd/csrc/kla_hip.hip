@@ -1326,3 +1326,77 @@ int kla_discretize_bwd(const float *delta, const float *lambda_log, const float 
 }
 
 }  // extern "C"
+
+namespace {
+
+int qk_sensors_launch(const char *fn, bool bwd, int dtype, QkParams &p, hipStream_t stream) {
+  if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16) return fail(KLA_ERR_DTYPE, "%s: unsupported dtype %d", fn, dtype);
+  if (p.rows < 0 || p.S < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  if (p.rows == 0 || p.S == 0) return KLA_OK;
+  if (p.S > 64) return fail(KLA_ERR_INVALID_ARG, "%s: S = %lld above 64", fn, (long long)p.S);
+  if (p.ld[0] < p.S || p.ld[1] < p.S) return fail(KLA_ERR_INVALID_ARG, "%s: a row stride is below S", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  for (int i = 0; i < 2; ++i) {
+    if (!p.x[i] || (!bwd && !p.y[i]) || (bwd && (!p.dy[i] || !p.dx[i])))
+      return fail(KLA_ERR_INVALID_ARG, "%s: NULL operand", fn);
+    if (misaligned_bytes(p.x[i], el) || misaligned(p.y[i]) || misaligned(p.dy[i]) || misaligned_bytes(p.dx[i], el))
+      return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
+  }
+  return with_sp(p.S, [&](auto sp) {
+    constexpr int SP = decltype(sp)::value;
+    const int64_t threads = 2 * p.rows * SP;
+    if ((threads + 255) / 256 >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
+    const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
+    auto go = [&](auto io, auto b) {
+      hipLaunchKernelGGL((qk_sensors_kernel<decltype(io), SP, decltype(b)::value>), grid, dim3(256), 0, stream, p);
+    };
+    if (dtype == KLA_DTYPE_F32)
+      bwd ? go(float{}, std::true_type{}) : go(float{}, std::false_type{});
+    else
+      bwd ? go(bf16_t{}, std::true_type{}) : go(bf16_t{}, std::false_type{});
+    return hip_status(fn, hipGetLastError());
+  });
+}
+
+}  // namespace
+
+extern "C" {
+
+int kla_qk_sensors_fwd(int dtype, const void *k, int64_t ld_k, const void *q, int64_t ld_q, float *yk, float *yq,
+                       int64_t rows, int64_t S, int norm, int has_clip, float clip, hipStream_t stream) {
+  QkParams p{};
+  p.x[0] = k;
+  p.x[1] = q;
+  p.ld[0] = ld_k;
+  p.ld[1] = ld_q;
+  p.y[0] = yk;
+  p.y[1] = yq;
+  p.rows = rows;
+  p.S = S;
+  p.norm = norm != 0;
+  p.has_clip = has_clip != 0;
+  p.clip = clip;
+  return qk_sensors_launch("kla_qk_sensors_fwd", false, dtype, p, stream);
+}
+
+int kla_qk_sensors_bwd(int dtype, const void *k, int64_t ld_k, const void *q, int64_t ld_q, const float *dyk,
+                       const float *dyq, void *dk, void *dq, int64_t rows, int64_t S, int norm, int has_clip,
+                       float clip, hipStream_t stream) {
+  QkParams p{};
+  p.x[0] = k;
+  p.x[1] = q;
+  p.ld[0] = ld_k;
+  p.ld[1] = ld_q;
+  p.dy[0] = dyk;
+  p.dy[1] = dyq;
+  p.dx[0] = dk;
+  p.dx[1] = dq;
+  p.rows = rows;
+  p.S = S;
+  p.norm = norm != 0;
+  p.has_clip = has_clip != 0;
+  p.clip = clip;
+  return qk_sensors_launch("kla_qk_sensors_bwd", true, dtype, p, stream);
+}
+
+}  // extern "C"

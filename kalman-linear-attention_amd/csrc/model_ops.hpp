@@ -45,6 +45,64 @@ __global__ void __launch_bounds__(256) swiglu_fwd_kernel(const IO *__restrict__ 
   io_store(out + i, g * io_load(h + r * ld_h + hidden + c));
 }
 
+// The k, q sensors of KLALayer._project_sensors_raw (reference kla_layer.py:194-231):
+//   y = clamp(l2_norm(x), -clip, clip).float(),  l2_norm(x) = x / max(||x||_2, 1e-12)
+// over the S states of each row, with torch's rounding to the input dtype after
+// every operation (bf16 under autocast: the norm, the clamp_min, the quotient and
+// the clip each round). The backward is torch's autograd chain through the same
+// operations, rounding where autograd rounds: the gradient cast back to the
+// input dtype, the clamp mask (bounds cast to the input dtype, as torch compares),
+// the quotient's -g ((x / n) / n) summed over the row, the clamp_min mask, the
+// norm's x (g_n / n), and the two terms' sum.
+// One thread per (row, s), SP lanes per row; k rows first, then q rows.
+struct QkParams {
+  const void *x[2];        // k, q rows, ld[i] elements apart
+  int64_t ld[2];
+  float *y[2];             // forward: [rows, S] dense fp32
+  const float *dy[2];      // backward: gradients of y, [rows, S] dense
+  void *dx[2];             // backward: [rows, S] dense, the input dtype
+  int64_t rows, S;
+  int norm, has_clip;
+  float clip;
+};
+
+template <class IO, int SP, bool BWD>
+__global__ void __launch_bounds__(256) qk_sensors_kernel(QkParams p) {
+  const int64_t g = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / SP;   // row over both tensors
+  const int s = static_cast<int>(threadIdx.x) % SP;
+  if (g >= 2 * p.rows) return;   // whole SP-lane groups leave together
+  const int which = g >= p.rows ? 1 : 0;
+  const int64_t r = g - which * p.rows;
+  const bool ok = s < p.S;
+  const IO *xr = static_cast<const IO *>(p.x[which]) + r * p.ld[which];
+  const float x = ok ? io_load(xr + s) : 0.0f;
+  float n0 = 0.0f, n = 1.0f, yn = x;
+  if (p.norm) {
+    n0 = io_round<IO>(sqrtf(group_sum<SP>(x * x)));
+    n = io_round<IO>(fmaxf(n0, 1e-12f));
+    yn = io_round<IO>(x / n);
+  }
+  // torch's clamp backward compares with the bounds cast to the tensor's dtype.
+  const bool in_clip = !p.has_clip || (yn >= io_round<IO>(-p.clip) && yn <= io_round<IO>(p.clip));
+  if constexpr (!BWD) {
+    const float y = p.has_clip ? io_round<IO>(fminf(fmaxf(yn, -p.clip), p.clip)) : yn;
+    if (ok) p.y[which][r * p.S + s] = y;
+  } else {
+    float gy = ok ? io_round<IO>(p.dy[which][r * p.S + s]) : 0.0f;
+    if (!in_clip) gy = 0.0f;
+    float gx = gy;
+    if (p.norm) {
+      const float gx1 = io_round<IO>(gy / n);
+      const float t = io_round<IO>(io_round<IO>(x / n) / n);
+      float gn = io_round<IO>(group_sum<SP>(io_round<IO>(-gy * t)));
+      if (!(n0 >= 1e-12f)) gn = 0.0f;
+      const float gx2 = n0 == 0.0f ? 0.0f : io_round<IO>(x * io_round<IO>(gn / n0));
+      gx = io_round<IO>(gx1 + gx2);
+    }
+    if (ok) io_store(static_cast<IO *>(p.dx[which]) + r * p.S + s, gx);
+  }
+}
+
 // out[r, :] = table[ids[r], :] (the embedding lookup of one decode step,
 // reference src/kla/models/sequence_model.py:157, nn.Embedding). An id outside
 // [0, vocab) reads nothing and writes a row of NaN. One workgroup per row.

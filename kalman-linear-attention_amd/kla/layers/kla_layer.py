@@ -159,6 +159,12 @@ class KLALayer(nn.Module):
             v = self.value_expand(v)
         if self.var_expand is not None:
             log_var = self.var_expand(log_var)
+        if self._qk_on_hip(k):
+            # Norm, clip and .float() of both as one HIP kernel each way (same values).
+            from kla.ops.hip.sensors import qk_sensors_hip
+
+            k, q = qk_sensors_hip(k, q, norm=cfg.qk_norm, clip=cfg.clip_value)
+            return v, log_var, k, q
         if cfg.qk_norm:
             k, q = l2_norm(k), l2_norm(q)
         if cfg.clip_value is not None:
@@ -218,6 +224,16 @@ class KLALayer(nn.Module):
             y, y_var, new_state = kla_step(v[:, 0], lambda_v[:, 0], k[:, 0], q[:, 0], a_bar, p_bar, ssm_state,
                                            decode_from_prior=cfg.decode_from_prior, backend=cfg.backend)
         return y.unsqueeze(1), y_var.unsqueeze(1), new_state
+
+    def _qk_on_hip(self, k: torch.Tensor) -> bool:
+        """Whether the k, q sensors come from the MI355X kernels: a hip-family backend
+        on a ROCm GPU, fp32 or bf16 projection, d_state <= 64, and a norm or a clip
+        to apply."""
+        from kla.ops.kla_ops import _step_on_hip
+
+        cfg = self.config
+        return ((cfg.qk_norm or cfg.clip_value is not None) and k.dtype in (torch.float32, torch.bfloat16)
+                and self.d_state <= 64 and k.dim() == 3 and _step_on_hip(cfg.backend, k))
 
     def _aq_on_hip(self) -> bool:
         """Whether (a_bar, p_bar) come from the MI355X kernels: fp32 parameters on a

@@ -1199,6 +1199,58 @@ def test_discretize_matches_float64_autograd(cuda, discretization, zero_pn, clip
         check(name, got.grad, want.grad.numpy(), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("S", [16, 7, 64])
+@pytest.mark.parametrize("norm,clip", [(True, None), (True, 0.3), (False, 0.5)])
+def test_qk_sensors_match_torch(cuda, dtype, S, norm, clip):
+    """qk_sensors_hip (l2 norm over S, clip, .float()) on column views of a wider
+    projection, against torch's lines: in bf16 the values equal torch's bit for
+    bit but for rare reduction-order differences (at most 1% of them, each within
+    one bf16 ulp) and the gradients follow torch's bf16 autograd within a few
+    ulp; in fp32 both match float64 autograd. One row is all zeros (norm 0: the
+    clamp and the norm's masked gradient) and clip values are exceeded."""
+    from kla.layers.common import l2_norm
+    from kla.ops.hip.sensors import qk_sensors_hip
+
+    g = torch.Generator().manual_seed(81 + S)
+    B, L, W = 3, 37, 2 * S + 40
+    proj = torch.randn(B, L, W, generator=g)
+    proj[0, 0, 40:40 + S] = 0.0
+    gk, gq = torch.randn(B, L, S, generator=g), torch.randn(B, L, S, generator=g)
+
+    def lines(k, q):
+        if norm:
+            k, q = l2_norm(k), l2_norm(q)
+        if clip is not None:
+            k, q = k.clamp(-clip, clip), q.clamp(-clip, clip)
+        return k.float(), q.float()
+
+    ref_dtype = dtype if dtype == torch.bfloat16 else torch.float64
+    pr = proj.to(ref_dtype).requires_grad_(True)
+    wk, wq = lines(pr[..., 40:40 + S], pr[..., 40 + S:40 + 2 * S])
+    torch.autograd.backward([wk, wq], [gk.to(wk.dtype), gq.to(wq.dtype)])
+    want_dk, want_dq = pr.grad[..., 40:40 + S], pr.grad[..., 40 + S:40 + 2 * S]
+
+    pd = proj.to(dtype).to(cuda).requires_grad_(True)
+    yk, yq = qk_sensors_hip(pd[..., 40:40 + S], pd[..., 40 + S:40 + 2 * S], norm=norm, clip=clip)
+    assert yk.dtype == torch.float32 and yk.shape == (B, L, S)
+    torch.autograd.backward([yk, yq], [gk.to(cuda), gq.to(cuda)])
+    got_dk, got_dq = pd.grad[..., 40:40 + S], pd.grad[..., 40 + S:40 + 2 * S]
+    assert torch.count_nonzero(pd.grad[..., :40]) == 0
+    if dtype == torch.bfloat16:
+        for name, a, b in (("k", yk, wk), ("q", yq, wq)):
+            a, b = a.cpu(), b.detach()
+            assert float((a != b).float().mean()) <= 0.01, name
+            check(name, a, b.numpy(), rtol=8e-3, atol=8e-3)
+        for name, a, b in (("dk", got_dk, want_dk), ("dq", got_dq, want_dq)):
+            check(name, a.float(), b.float().numpy(), rtol=3e-2, atol=3e-2)
+    else:
+        check("k", yk, wk.detach().numpy(), rtol=1e-5, atol=1e-6)
+        check("q", yq, wq.detach().numpy(), rtol=1e-5, atol=1e-6)
+        check("dk", got_dk, want_dk.numpy(), rtol=1e-5, atol=1e-6)
+        check("dq", got_dq, want_dq.numpy(), rtol=1e-5, atol=1e-6)
+
+
 def test_decode_kernels_in_place_equal_out_of_place(cuda):
     """The one-token conv and SSM kernels give the same values when they write the
     new state over the old one (what a decode graph does) as into new tensors."""
