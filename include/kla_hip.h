@@ -420,6 +420,17 @@ int kla_qk_sensors_bwd(int dtype, const void *k, int64_t ld_k, const void *q, in
                        const float *dyq, void *dk, void *dq, int64_t rows, int64_t S, int norm, int has_clip,
                        float clip, hipStream_t stream);
 
+/*
+ * out[r, :] = [piece_0[r, :], ..., piece_{n-1}[r, :]]: dense out [rows, sum of
+ * widths] of `dtype` from n <= 4 pieces, piece i rows of widths[i] elements
+ * ld[i] apart (pieces[i] NULL: zeros). The backward of splitting a projection's
+ * last dimension (torch.split / chunk in KLALayer, reference
+ * src/kla/layers/kla_layer.py:206, :313-316): autograd's concatenation of the
+ * pieces' gradients.
+ */
+int kla_cat_cols(int dtype, int n, const void *const *pieces, const int64_t *ld, const int64_t *widths, void *out,
+                 int64_t rows, hipStream_t stream);
+
 /* Epilogues of kla_rows_linear_fwd. */
 enum { KLA_ROWS_PLAIN = 0, KLA_ROWS_RESIDUAL = 1, KLA_ROWS_SWIGLU = 2 };
 

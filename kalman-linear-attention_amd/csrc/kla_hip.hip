@@ -1399,4 +1399,63 @@ int kla_qk_sensors_bwd(int dtype, const void *k, int64_t ld_k, const void *q, in
   return qk_sensors_launch("kla_qk_sensors_bwd", true, dtype, p, stream);
 }
 
+int kla_cat_cols(int dtype, int n, const void *const *pieces, const int64_t *ld, const int64_t *widths, void *out,
+                 int64_t rows, hipStream_t stream) {
+  const char *fn = "kla_cat_cols";
+  if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16) return fail(KLA_ERR_DTYPE, "%s: unsupported dtype %d", fn, dtype);
+  if (n < 1 || n > kCatMaxPieces) return fail(KLA_ERR_INVALID_ARG, "%s: %d pieces (1 to %d)", fn, n, kCatMaxPieces);
+  if (!pieces || !ld || !widths) return fail(KLA_ERR_INVALID_ARG, "%s: NULL piece arrays", fn);
+  if (rows < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative rows", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  const int vec = static_cast<int>(16 / el);
+  int64_t W = 0;
+  bool can_vec = true;
+  int64_t start[kCatMaxPieces + 1];
+  for (int i = 0; i < n; ++i) {
+    if (widths[i] < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative width", fn);
+    if (pieces[i] && ld[i] < widths[i]) return fail(KLA_ERR_INVALID_ARG, "%s: piece %d stride below its width", fn, i);
+    if (misaligned_bytes(pieces[i], el)) return fail(KLA_ERR_ALIGN, "%s: piece %d not aligned", fn, i);
+    start[i] = W;
+    W += widths[i];
+    if (widths[i] % vec || (pieces[i] && (ld[i] % vec || !all_aligned(16, {pieces[i]})))) can_vec = false;
+  }
+  start[n] = W;
+  if (rows == 0 || W == 0) return KLA_OK;
+  if (!out) return fail(KLA_ERR_INVALID_ARG, "%s: NULL out", fn);
+  if (misaligned_bytes(out, el)) return fail(KLA_ERR_ALIGN, "%s: out not aligned", fn);
+  if (W % vec || !all_aligned(16, {out})) can_vec = false;
+  if (rows >= 65536 * 32768ll) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
+  auto go = [&](auto io) {
+    using IO = decltype(io);
+    CatParams<IO> p{};
+    for (int i = 0; i < n; ++i) {
+      p.src[i] = static_cast<const IO *>(pieces[i]);
+      p.ld[i] = ld[i];
+    }
+    for (int i = 0; i <= n; ++i) p.start[i] = start[i];
+    p.n = n;
+    p.out = static_cast<IO *>(out);
+    p.rows = rows;
+    p.W = W;
+    const int v = can_vec ? vec : 1;
+    const int64_t per = 256ll * v;
+    // rows go on grid.y (at most 65535): larger row counts take several launches.
+    for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+      const int64_t rr = rows - r0 < 65535 ? rows - r0 : 65535;
+      CatParams<IO> q = p;
+      for (int i = 0; i < n; ++i)
+        if (q.src[i]) q.src[i] += r0 * q.ld[i];
+      q.out += r0 * W;
+      q.rows = rr;
+      const dim3 grid(static_cast<uint32_t>((W + per - 1) / per), static_cast<uint32_t>(rr));
+      if (can_vec)
+        hipLaunchKernelGGL((cat_cols_kernel<IO, 16 / sizeof(IO)>), grid, dim3(256), 0, stream, q);
+      else
+        hipLaunchKernelGGL((cat_cols_kernel<IO, 1>), grid, dim3(256), 0, stream, q);
+    }
+    return hip_status(fn, hipGetLastError());
+  };
+  return dtype == KLA_DTYPE_F32 ? go(float{}) : go(bf16_t{});
+}
+
 }  // extern "C"

@@ -103,6 +103,41 @@ __global__ void __launch_bounds__(256) qk_sensors_kernel(QkParams p) {
   }
 }
 
+// out[r, :] = [piece_0[r, :], ..., piece_{n-1}[r, :]] for dense out [rows, W]:
+// the backward of splitting the last dimension (torch.split / chunk of a
+// projection: autograd concatenates the pieces' gradients). A piece is rows of
+// widths[i] elements ld[i] apart, or NULL for zeros. VEC elements per thread
+// (one 16-byte access) when every boundary, stride and base allows it.
+constexpr int kCatMaxPieces = 4;
+
+template <class IO>
+struct CatParams {
+  const IO *src[kCatMaxPieces];
+  int64_t ld[kCatMaxPieces];
+  int64_t start[kCatMaxPieces + 1];   // column where piece i starts; start[n] = W
+  int n;
+  IO *out;
+  int64_t rows, W;
+};
+
+template <class IO, int VEC>
+__global__ void __launch_bounds__(256) cat_cols_kernel(CatParams<IO> p) {
+  const int64_t r = blockIdx.y;
+  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC;
+  if (c0 >= p.W) return;
+  int i = 0;
+  while (i + 1 < p.n && c0 >= p.start[i + 1]) ++i;
+  IO *dst = p.out + r * p.W + c0;
+  const IO *src = p.src[i] ? p.src[i] + r * p.ld[i] + (c0 - p.start[i]) : nullptr;
+  if constexpr (VEC > 1) {
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const u32x4v v = src ? *reinterpret_cast<const u32x4v *>(src) : u32x4v{0u, 0u, 0u, 0u};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4v *>(dst));
+  } else {
+    *dst = src ? *src : IO{};
+  }
+}
+
 // out[r, :] = table[ids[r], :] (the embedding lookup of one decode step,
 // reference src/kla/models/sequence_model.py:157, nn.Embedding). An id outside
 // [0, vocab) reads nothing and writes a row of NaN. One workgroup per row.

@@ -152,7 +152,8 @@ class KLALayer(nn.Module):
         [B, L, S] float32 after the norm and the clip)."""
         cfg = self.config
         S = self.d_state
-        v, log_var, k, q = torch.split(self.sensor_proj(z), [self._w_value, self._w_var, S, S], dim=-1)
+        proj = self.sensor_proj(z)
+        v, log_var, k, q = self._split(proj, [self._w_value, self._w_var, S, S])
         if self._value_rank == "conv":
             v = z
         elif self.value_expand is not None:
@@ -224,6 +225,17 @@ class KLALayer(nn.Module):
             y, y_var, new_state = kla_step(v[:, 0], lambda_v[:, 0], k[:, 0], q[:, 0], a_bar, p_bar, ssm_state,
                                            decode_from_prior=cfg.decode_from_prior, backend=cfg.backend)
         return y.unsqueeze(1), y_var.unsqueeze(1), new_state
+
+    def _split(self, t: torch.Tensor, sizes: list[int]):
+        """torch.split(t, sizes, dim=-1); on a hip-family backend with a gradient to
+        carry, the split whose backward concatenates on the MI355X."""
+        from kla.ops.kla_ops import _step_on_hip
+
+        if t.requires_grad and torch.is_grad_enabled() and _step_on_hip(self.config.backend, t):
+            from kla.ops.hip.split import split_last
+
+            return split_last(t, sizes)
+        return torch.split(t, sizes, dim=-1)
 
     def _qk_on_hip(self, k: torch.Tensor) -> bool:
         """Whether the k, q sensors come from the MI355X kernels: a hip-family backend
@@ -394,7 +406,7 @@ class KLALayer(nn.Module):
 
         projected = self.in_proj(x)
         if cfg.use_gating:
-            z, gate = projected.chunk(2, dim=-1)
+            z, gate = self._split(projected, [self.d_inner, self.d_inner])
         else:
             z, gate = projected, None
         # One-token inference step on the GPU: the conv step and the SSM step

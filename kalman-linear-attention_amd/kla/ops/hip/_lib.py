@@ -76,6 +76,7 @@ _SIGNATURES = {
                                           ctypes.c_int, ctypes.c_float, _p]),
     "kla_qk_sensors_bwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_float, _p]),
+    "kla_cat_cols": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _p, _p, _p, _p, _i64, _p]),
     "kla_gather_rows": (ctypes.c_int, [ctypes.c_int, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p]),
     "kla_argmax_rows": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _p]),
     "kla_rows_linear_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _p, _p, ctypes.c_float, _p, _i64, _p,

@@ -1251,6 +1251,49 @@ def test_qk_sensors_match_torch(cuda, dtype, S, norm, clip):
         check("dq", got_dq, want_dq.numpy(), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("widths,rows", [([2048, 2048], 64), ([2048, 2048, 16, 16], 33), ([7, 5, 3, 1], 19),
+                                         ([8, 16], 70001)])
+def test_cat_cols_equals_torch_cat(cuda, dtype, widths, rows):
+    """kla_cat_cols (the split backward) against torch.cat, bit for bit: strided
+    pieces (column views of wider tensors), a missing piece written as zeros,
+    the 16-byte path and the single-element one (ragged widths), and more rows
+    than one launch covers."""
+    from kla.ops.hip.split import cat_cols_hip
+
+    g = torch.Generator().manual_seed(91)
+    pieces = []
+    for i, w in enumerate(widths):
+        wide = torch.randn(rows, w + 8, generator=g).to(dtype).to(cuda)
+        pieces.append(wide[:, 8:] if i % 2 else wide[:, :w])
+    like = torch.empty(rows, sum(widths), dtype=dtype, device=cuda)
+    got = cat_cols_hip(pieces, widths, like)
+    assert torch.equal(got, torch.cat(pieces, dim=-1))
+    missing = [None] + pieces[1:]
+    got = cat_cols_hip(missing, widths, like)
+    want = torch.cat([torch.zeros_like(pieces[0])] + pieces[1:], dim=-1)
+    assert torch.equal(got, want)
+
+
+def test_split_last_gradient_equals_torch_split(cuda):
+    """split_last's pieces are torch.split's views, and its backward gives the
+    gradient torch.split's does, bit for bit, also when a piece gets none."""
+    from kla.ops.hip.split import split_last
+
+    g = torch.Generator().manual_seed(92)
+    x = torch.randn(3, 50, 96, generator=g).to(torch.bfloat16).to(cuda)
+    sizes = [40, 40, 8, 8]
+    gs = [torch.randn(3, 50, w, generator=g).to(torch.bfloat16).to(cuda) for w in sizes]
+    grads = []
+    for split in (split_last, lambda t, s: torch.split(t, s, dim=-1)):
+        xx = x.clone().requires_grad_(True)
+        parts = split(xx, sizes)
+        assert all(torch.equal(a, b) for a, b in zip(parts, torch.split(x, sizes, dim=-1)))
+        torch.autograd.backward([parts[0], parts[1], parts[3]], [gs[0], gs[1], gs[3]])
+        grads.append(xx.grad)
+    assert torch.equal(grads[0], grads[1])
+
+
 def test_decode_kernels_in_place_equal_out_of_place(cuda):
     """The one-token conv and SSM kernels give the same values when they write the
     new state over the old one (what a decode graph does) as into new tensors."""
