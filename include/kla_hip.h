@@ -385,7 +385,11 @@ int kla_gather_rows(int dtype, const void *table, int64_t ld_table, int64_t voca
  * with temperature 0 (reference src/kla/models/sequence_model.py, generate).
  */
 int kla_argmax_rows(const float *x, int64_t ldx, int64_t rows, int64_t n, int64_t *out, int64_t ld_out,
-                    hipStream_t stream);
+                    void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes with which kla_argmax_rows splits each row over several
+ * workgroups (with a smaller or NULL workspace it runs one workgroup per row). */
+size_t kla_argmax_workspace_bytes(int64_t rows, int64_t n);
 
 /*
  * A KLA layer's static dynamics over n = M * S elements, fp32

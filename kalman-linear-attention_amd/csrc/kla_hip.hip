@@ -27,7 +27,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 10;
+constexpr int kAbiVersion = 11;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -1169,6 +1169,20 @@ int rows_linear_launch(const char *fn, int epi, RowsLinearParams &p, hipStream_t
   return hip_status(fn, hipGetLastError());
 }
 
+// Parts per row of the split argmax: about 256 workgroups in all, chunks of at
+// least 2048 columns, at most 64 parts; 1 means the one-kernel path.
+int64_t argmax_parts(int64_t rows, int64_t n) {
+  int64_t parts = (256 + rows - 1) / rows;
+  if (parts > 64) parts = 64;
+  while (parts > 1 && n / parts < 2048) --parts;
+  return parts;
+}
+
+int64_t argmax_workspace_bytes(int64_t rows, int64_t n) {
+  const int64_t parts = argmax_parts(rows, n);
+  return ((rows * parts * 4 + 255) / 256) * 256 + rows * parts * 8;
+}
+
 RowsLinearParams rows_params(const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
                              const float *norm_w, float eps, float *y, int64_t ldy, int64_t rows, int64_t n,
                              int64_t k) {
@@ -1252,8 +1266,12 @@ int kla_gather_rows(int dtype, const void *table, int64_t ld_table, int64_t voca
   return hip_status(fn, hipGetLastError());
 }
 
+size_t kla_argmax_workspace_bytes(int64_t rows, int64_t n) {
+  return rows > 0 && n > 0 ? static_cast<size_t>(argmax_workspace_bytes(rows, n)) : 0;
+}
+
 int kla_argmax_rows(const float *x, int64_t ldx, int64_t rows, int64_t n, int64_t *out, int64_t ld_out,
-                    hipStream_t stream) {
+                    void *workspace, size_t workspace_bytes, hipStream_t stream) {
   const char *fn = "kla_argmax_rows";
   if (rows < 0 || n < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
   if (rows == 0) return KLA_OK;
@@ -1262,6 +1280,18 @@ int kla_argmax_rows(const float *x, int64_t ldx, int64_t rows, int64_t n, int64_
   if (ldx < n || ld_out < 1) return fail(KLA_ERR_INVALID_ARG, "%s: bad row stride", fn);
   if (rows >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);
   if (misaligned(x) || misaligned_bytes(out, 8)) return fail(KLA_ERR_ALIGN, "%s: operand not aligned", fn);
+  if (workspace && workspace_bytes >= argmax_workspace_bytes(rows, n) && argmax_parts(rows, n) > 1) {
+    // Split: parts per row so that about 256 workgroups stream the rows, then a combine.
+    const int64_t parts = argmax_parts(rows, n);
+    const int64_t chunk = (n + parts - 1) / parts;
+    float *pv = static_cast<float *>(workspace);
+    int64_t *pi = reinterpret_cast<int64_t *>(static_cast<char *>(workspace) + ((rows * parts * 4 + 255) / 256) * 256);
+    hipLaunchKernelGGL(argmax_parts_kernel, dim3(static_cast<uint32_t>(parts), static_cast<uint32_t>(rows)),
+                       dim3(kArgmaxPartThreads), 0, stream, x, ldx, n, chunk, pv, pi);
+    hipLaunchKernelGGL(argmax_combine_kernel, dim3(static_cast<uint32_t>(rows)), dim3(kWave), 0, stream, pv, pi,
+                       parts, n, out, ld_out);
+    return hip_status(fn, hipGetLastError());
+  }
   const dim3 grid(static_cast<uint32_t>(rows));
   if (ldx % 4 == 0 && all_aligned(16, {x}))
     hipLaunchKernelGGL(argmax_rows_kernel<true>, grid, dim3(kArgmaxThreads), 0, stream, x, ldx, n, out, ld_out);

@@ -163,6 +163,92 @@ __device__ __forceinline__ bool argmax_before(float a, int64_t ia, float b, int6
 }
 
 constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxPartThreads = 256;
+
+// Stage 1 of a split argmax: workgroup (part, row) takes columns
+// [part * chunk, (part + 1) * chunk) of its row and writes its (value, index)
+// in torch.argmax's order; stage 2 (argmax_rows_kernel over the parts, VAL_IN)
+// combines a row's parts in part order. Many rows' worth of workgroups keep the
+// whole GPU streaming, where one workgroup per row leaves most CUs idle.
+__global__ void __launch_bounds__(kArgmaxPartThreads) argmax_parts_kernel(const float *__restrict__ x, int64_t ldx,
+                                                                           int64_t n, int64_t chunk,
+                                                                           float *__restrict__ part_v,
+                                                                           int64_t *__restrict__ part_i) {
+  __shared__ float s_v[kArgmaxPartThreads / kWave];
+  __shared__ int64_t s_i[kArgmaxPartThreads / kWave];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int64_t part = blockIdx.x, row = blockIdx.y;
+  const float *xr = x + row * ldx;
+  const int64_t c0 = part * chunk, c1 = c0 + chunk < n ? c0 + chunk : n;
+  float best = -__builtin_inff();
+  int64_t bi = n;
+  constexpr int U = 8;
+  for (int64_t j0 = c0 + tid; j0 < c1; j0 += static_cast<int64_t>(U) * kArgmaxPartThreads) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + static_cast<int64_t>(u) * kArgmaxPartThreads;
+      v[u] = j < c1 ? xr[j] : -__builtin_inff();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = j0 + static_cast<int64_t>(u) * kArgmaxPartThreads;
+      if (j < c1 && argmax_before(v[u], j, best, bi)) {
+        best = v[u];
+        bi = j;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off /= 2) {
+    const float ov = __shfl_xor(best, off);
+    const int64_t oi = __shfl_xor(bi, off);
+    if (argmax_before(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  if (tid % kWave == 0) {
+    s_v[tid / kWave] = best;
+    s_i[tid / kWave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgmaxPartThreads / kWave; ++w)
+      if (argmax_before(s_v[w], s_i[w], best, bi)) {
+        best = s_v[w];
+        bi = s_i[w];
+      }
+    part_v[row * gridDim.x + part] = best;
+    part_i[row * gridDim.x + part] = bi;
+  }
+}
+
+// Stage 2: out[row] = the index of the best of the row's `parts` (value, index)
+// pairs, in part order (one wave per row).
+__global__ void __launch_bounds__(kWave) argmax_combine_kernel(const float *__restrict__ part_v,
+                                                                const int64_t *__restrict__ part_i, int64_t parts,
+                                                                int64_t n, int64_t *__restrict__ out, int64_t ld_out) {
+  const int lane = static_cast<int>(threadIdx.x);
+  const int64_t row = blockIdx.x;
+  float best = -__builtin_inff();
+  int64_t bi = n;
+  for (int64_t j = lane; j < parts; j += kWave)
+    if (argmax_before(part_v[row * parts + j], part_i[row * parts + j], best, bi)) {
+      best = part_v[row * parts + j];
+      bi = part_i[row * parts + j];
+    }
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off /= 2) {
+    const float ov = __shfl_xor(best, off);
+    const int64_t oi = __shfl_xor(bi, off);
+    if (argmax_before(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) out[row * ld_out] = bi;
+}
 
 // out[r] = argmax_j x[r, j] (greedy decoding over the vocabulary, reference
 // SequenceModel._sample with temperature 0, logits.argmax(dim=-1)). One

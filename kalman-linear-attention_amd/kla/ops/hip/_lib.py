@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -78,7 +78,8 @@ _SIGNATURES = {
                                           ctypes.c_int, ctypes.c_int, ctypes.c_float, _p]),
     "kla_cat_cols": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _p, _p, _p, _p, _i64, _p]),
     "kla_gather_rows": (ctypes.c_int, [ctypes.c_int, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p]),
-    "kla_argmax_rows": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _p]),
+    "kla_argmax_rows": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _p, ctypes.c_size_t, _p]),
+    "kla_argmax_workspace_bytes": (ctypes.c_size_t, [_i64, _i64]),
     "kla_rows_linear_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _p, _p, ctypes.c_float, _p, _i64, _p,
                                            _i64, _i64, _i64, _i64, _i64, _p]),
     "kla_gate_skip_bwd": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _p, _p, _p, _i64, _p, _i64, _p, ctypes.c_int,

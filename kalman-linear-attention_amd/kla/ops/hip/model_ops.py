@@ -161,9 +161,11 @@ def argmax_rows_hip(x: torch.Tensor) -> torch.Tensor:
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     out = torch.empty(x2.shape[0], 1, dtype=torch.int64, device=x.device)
+    nbytes = _lib.lib().kla_argmax_workspace_bytes(x2.shape[0], x2.shape[1])
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
     _lib.check("kla_argmax_rows", _lib.lib().kla_argmax_rows(
         x2.data_ptr(), x2.stride(0), x2.shape[0], x2.shape[1], out.data_ptr(), 1,
-        torch.cuda.current_stream(x.device).cuda_stream))
+        ws.data_ptr() if ws is not None else None, nbytes, torch.cuda.current_stream(x.device).cuda_stream))
     return out.view(*x.shape[:-1], 1)
 
 
