@@ -435,6 +435,18 @@ int kla_qk_sensors_bwd(int dtype, const void *k, int64_t ld_k, const void *q, in
 int kla_cat_cols(int dtype, int n, const void *const *pieces, const int64_t *ld, const int64_t *widths, void *out,
                  int64_t rows, hipStream_t stream);
 
+/*
+ * out[i] = sum_{j < nparts} parts[j * n + i] for i < n: fp32 partials added in
+ * j order, rounded once to `dtype` (fp32 or bf16, round to nearest even). The
+ * last step of a projection's weight gradient split over the token dimension
+ * (dW = sum over token chunks of dY_c^T X_c, each chunk's product an fp32
+ * batched GEMM): it replaces the single weight-gradient product of torch's
+ * nn.Linear backward for KLALayer's in_proj, sensor_proj and out_proj
+ * (reference src/kla/layers/kla_layer.py:61, :88, :127), whose few output
+ * tiles leave most CUs idle over a 16384-token reduction.
+ */
+int kla_sum_parts(int dtype, const float *parts, int64_t nparts, int64_t n, void *out, hipStream_t stream);
+
 /* Epilogues of kla_rows_linear_fwd. */
 enum { KLA_ROWS_PLAIN = 0, KLA_ROWS_RESIDUAL = 1, KLA_ROWS_SWIGLU = 2 };
 

@@ -27,7 +27,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 11;
+constexpr int kAbiVersion = 12;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -1483,6 +1483,31 @@ int kla_cat_cols(int dtype, int n, const void *const *pieces, const int64_t *ld,
       else
         hipLaunchKernelGGL((cat_cols_kernel<IO, 1>), grid, dim3(256), 0, stream, q);
     }
+    return hip_status(fn, hipGetLastError());
+  };
+  return dtype == KLA_DTYPE_F32 ? go(float{}) : go(bf16_t{});
+}
+
+int kla_sum_parts(int dtype, const float *parts, int64_t nparts, int64_t n, void *out, hipStream_t stream) {
+  const char *fn = "kla_sum_parts";
+  if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16) return fail(KLA_ERR_DTYPE, "%s: unsupported dtype %d", fn, dtype);
+  if (nparts < 1 || n < 0) return fail(KLA_ERR_INVALID_ARG, "%s: %lld parts of %lld", fn, (long long)nparts, (long long)n);
+  if (n == 0) return KLA_OK;
+  if (!parts || !out) return fail(KLA_ERR_INVALID_ARG, "%s: NULL pointer", fn);
+  const size_t el = dtype == KLA_DTYPE_F32 ? 4 : 2;
+  if (misaligned_bytes(parts, 4) || misaligned_bytes(out, el)) return fail(KLA_ERR_ALIGN, "%s: misaligned", fn);
+  const bool vec = n % 4 == 0 && all_aligned(16, {parts}) && all_aligned(4 * el, {out});
+  const int64_t per = 256ll * (vec ? 4 : 1);
+  // Eight workgroups per CU of 256 (MI355X) at most; each thread walks the rest.
+  int64_t blocks = (n + per - 1) / per;
+  if (blocks > 2048) blocks = 2048;
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  auto go = [&](auto io) {
+    using IO = decltype(io);
+    if (vec)
+      hipLaunchKernelGGL((sum_parts_kernel<IO, 4>), grid, dim3(256), 0, stream, parts, nparts, n, static_cast<IO *>(out));
+    else
+      hipLaunchKernelGGL((sum_parts_kernel<IO, 1>), grid, dim3(256), 0, stream, parts, nparts, n, static_cast<IO *>(out));
     return hip_status(fn, hipGetLastError());
   };
   return dtype == KLA_DTYPE_F32 ? go(float{}) : go(bf16_t{});

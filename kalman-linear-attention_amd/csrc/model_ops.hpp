@@ -138,6 +138,33 @@ __global__ void __launch_bounds__(256) cat_cols_kernel(CatParams<IO> p) {
   }
 }
 
+// out[i] = sum_{j < P} parts[j * N + i], added in j order in fp32 and rounded
+// once to IO (round to nearest even for bf16): the last step of a weight
+// gradient split over the token dimension into P fp32 partial products.
+// Four elements per thread (16-byte partial loads) when N % 4 == 0 and the
+// pointers are 16-byte aligned, else one; grid-stride over N.
+template <class IO, int VEC>
+__global__ void __launch_bounds__(256) sum_parts_kernel(const float *__restrict__ parts, int64_t P, int64_t N,
+                                                        IO *__restrict__ out) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256 * VEC;
+  for (int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC; i < N; i += stride) {
+    if constexpr (VEC == 4) {
+      typedef float f32x4v __attribute__((ext_vector_type(4)));
+      f32x4v acc = __builtin_nontemporal_load(reinterpret_cast<const f32x4v *>(parts + i));
+      for (int64_t j = 1; j < P; ++j)
+        acc += __builtin_nontemporal_load(reinterpret_cast<const f32x4v *>(parts + j * N + i));
+      io_store(out + i, acc.x);
+      io_store(out + i + 1, acc.y);
+      io_store(out + i + 2, acc.z);
+      io_store(out + i + 3, acc.w);
+    } else {
+      float acc = parts[i];
+      for (int64_t j = 1; j < P; ++j) acc += parts[j * N + i];
+      io_store(out + i, acc);
+    }
+  }
+}
+
 // out[r, :] = table[ids[r], :] (the embedding lookup of one decode step,
 // reference src/kla/models/sequence_model.py:157, nn.Embedding). An id outside
 // [0, vocab) reads nothing and writes a row of NaN. One workgroup per row.

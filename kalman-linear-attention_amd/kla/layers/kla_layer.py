@@ -152,7 +152,7 @@ class KLALayer(nn.Module):
         [B, L, S] float32 after the norm and the clip)."""
         cfg = self.config
         S = self.d_state
-        proj = self.sensor_proj(z)
+        proj = self._linear(self.sensor_proj, z)
         v, log_var, k, q = self._split(proj, [self._w_value, self._w_var, S, S])
         if self._value_rank == "conv":
             v = z
@@ -236,6 +236,17 @@ class KLALayer(nn.Module):
 
             return split_last(t, sizes)
         return torch.split(t, sizes, dim=-1)
+
+    def _linear(self, mod: nn.Linear, x: torch.Tensor) -> torch.Tensor:
+        """mod(x); on a hip-family backend with a gradient to carry, the projection
+        whose weight gradient is split over the tokens (kla.ops.hip.linear)."""
+        from kla.ops.kla_ops import _step_on_hip
+
+        if torch.is_grad_enabled() and _step_on_hip(self.config.backend, x):
+            from kla.ops.hip.linear import linear
+
+            return linear(mod, x)
+        return mod(x)
 
     def _qk_on_hip(self, k: torch.Tensor) -> bool:
         """Whether the k, q sensors come from the MI355X kernels: a hip-family backend
@@ -404,7 +415,7 @@ class KLALayer(nn.Module):
         L = x.shape[1]
         emit_state = return_state or state is not None
 
-        projected = self.in_proj(x)
+        projected = self._linear(self.in_proj, x)
         if cfg.use_gating:
             z, gate = self._split(projected, [self.d_inner, self.d_inner])
         else:
@@ -451,7 +462,7 @@ class KLALayer(nn.Module):
                     if y_var is not None:
                         y_var = y_var * g.pow(2)
 
-        out = self.out_proj(y)
+        out = self._linear(self.out_proj, y)
         result = (out, F.linear(y_var, self.out_proj.weight.pow(2))) if cfg.return_variance else out
         if emit_state:
             return result, KLALayerState(conv=conv_state, ssm=ssm_state)

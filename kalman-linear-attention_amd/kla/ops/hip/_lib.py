@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -77,6 +77,7 @@ _SIGNATURES = {
     "kla_qk_sensors_bwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _p, _p, _p, _p, _i64, _i64,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_float, _p]),
     "kla_cat_cols": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _p, _p, _p, _p, _i64, _p]),
+    "kla_sum_parts": (ctypes.c_int, [ctypes.c_int, _p, _i64, _i64, _p, _p]),
     "kla_gather_rows": (ctypes.c_int, [ctypes.c_int, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p]),
     "kla_argmax_rows": (ctypes.c_int, [_p, _i64, _i64, _i64, _p, _i64, _p, ctypes.c_size_t, _p]),
     "kla_argmax_workspace_bytes": (ctypes.c_size_t, [_i64, _i64]),

@@ -338,3 +338,14 @@ def test_model_kernels_validation(lib):
     assert "row stride" in err(lib)
     assert lib.kla_swiglu_fwd(_lib.KLA_DTYPE_BF16, P + 1, 8, P, 4, 4, None) == _lib.KLA_ERR_ALIGN
     assert lib.kla_swiglu_fwd(_lib.KLA_DTYPE_BF16, None, 8, None, 0, 4, None) == _lib.KLA_OK
+
+
+def test_sum_parts_validation(lib):
+    P = ALIGNED
+    assert lib.kla_sum_parts(5, P, 4, 16, P, None) == _lib.KLA_ERR_DTYPE
+    assert lib.kla_sum_parts(_lib.KLA_DTYPE_BF16, P, 0, 16, P, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_sum_parts(_lib.KLA_DTYPE_BF16, P, 4, -1, P, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_sum_parts(_lib.KLA_DTYPE_BF16, None, 4, 16, P, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_sum_parts(_lib.KLA_DTYPE_F32, P + 2, 4, 16, P, None) == _lib.KLA_ERR_ALIGN
+    assert lib.kla_sum_parts(_lib.KLA_DTYPE_F32, P, 4, 16, P + 2, None) == _lib.KLA_ERR_ALIGN
+    assert lib.kla_sum_parts(_lib.KLA_DTYPE_F32, None, 4, 0, None, None) == _lib.KLA_OK

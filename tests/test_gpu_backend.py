@@ -1321,3 +1321,83 @@ def test_decode_kernels_in_place_equal_out_of_place(cuda):
     assert out1[2] is lam_in and out1[3] is eta_in
     for a, b in zip(out0, out1):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("parts,n", [(1, 4096), (4, 4096), (5, 4099), (4, 2048 * 1024 * 3 + 8)])
+def test_sum_parts_equals_ordered_fp32_sum(cuda, dtype, parts, n):
+    """kla_sum_parts against the partials added in order in fp32 by torch and
+    rounded once, bit for bit: the 16-byte path, the single-element one (n not a
+    multiple of 4), and more elements than one pass of the grid covers."""
+    from kla.ops.hip import _lib
+
+    g = torch.Generator().manual_seed(93)
+    p = torch.randn(parts, n, generator=g).to(cuda)
+    want = p[0].clone()
+    for j in range(1, parts):
+        want = want + p[j]
+    want = want.to(dtype)
+    got = torch.empty(n, dtype=dtype, device=cuda)
+    code = _lib.KLA_DTYPE_BF16 if dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32
+    _lib.check("kla_sum_parts", _lib.lib().kla_sum_parts(code, p.data_ptr(), parts, n, got.data_ptr(),
+                                                         torch.cuda.current_stream(cuda).cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("T,n,k", [(8192, 1024, 256), (16384, 2080, 2048)])
+def test_weight_grad_split_matches_float64(cuda, T, n, k):
+    """weight_grad_hip (4 token-chunk fp32 products, summed and rounded once)
+    against the float64 product: within half a bf16 ulp of each value plus the
+    fp32 accumulation error, and within one bf16 ulp of torch's own bf16 GEMM."""
+    from kla.ops.hip.linear import weight_grad_hip
+
+    g = torch.Generator().manual_seed(94)
+    dy = torch.randn(T, n, generator=g).to(torch.bfloat16)
+    x = torch.randn(T, k, generator=g).to(torch.bfloat16)
+    ref = dy.double().t() @ x.double()
+    got = weight_grad_hip(dy.to(cuda), x.to(cuda), 4)
+    assert got.dtype == torch.bfloat16 and got.shape == (n, k)
+    got = got.cpu().double()
+    scale = float(ref.abs().max())
+    assert float(((got - ref).abs() - ref.abs() * 2.0 ** -8).max()) <= 1e-4 * scale
+    torch_bf16 = (dy.to(cuda).t() @ x.to(cuda)).cpu().double()
+    assert float(((got - torch_bf16).abs() - torch_bf16.abs() * 2.0 ** -7).max()) <= 1e-4 * scale
+
+
+def test_layer_split_linear_matches_torch_linear(cuda, monkeypatch):
+    """A KLALayer training step under bf16 autocast with the projections' weight
+    gradients split over the tokens (kla.ops.hip.linear) against the same layer
+    with torch's nn.Linear: the same output bit for bit (the same forward
+    products), and every parameter gradient within bf16 rounding (only the
+    weight gradients' fp32 summation order differs)."""
+    import kla.ops.hip.linear as lin
+
+    torch.manual_seed(95)
+    layer = KLALayer(256, KLAConfig(d_state=16, backend="hip")).to(cuda)
+    x = torch.randn(2, 4096, 256, generator=torch.Generator().manual_seed(96)).to(cuda)
+    M = layer.d_inner
+    assert lin.split_count(2 * 4096, 2 * M, 256, x.device) == 4
+
+    calls = []
+    real = lin._Linear.apply
+    monkeypatch.setattr(lin._Linear, "apply", lambda *a: calls.append(1) or real(*a))
+
+    def step():
+        layer.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = layer(x)
+        out.float().pow(2).mean().backward()
+        return out.detach(), {n: p.grad.detach().clone() for n, p in layer.named_parameters() if p.grad is not None}
+
+    out_split, g_split = step()
+    assert len(calls) == 3
+    monkeypatch.setattr(lin, "split_count", lambda *a: 1)
+    out_ref, g_ref = step()
+    assert len(calls) == 3
+    assert torch.equal(out_split, out_ref)
+    assert g_split.keys() == g_ref.keys()
+    for name in g_ref:
+        a, b = g_split[name].float(), g_ref[name].float()
+        tol = 2e-2 * float(b.abs().max()) + 1e-12
+        assert float((a - b).abs().max()) <= tol, name
