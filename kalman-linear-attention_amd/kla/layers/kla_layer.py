@@ -152,8 +152,7 @@ class KLALayer(nn.Module):
         [B, L, S] float32 after the norm and the clip)."""
         cfg = self.config
         S = self.d_state
-        proj = self._linear(self.sensor_proj, z)
-        v, log_var, k, q = self._split(proj, [self._w_value, self._w_var, S, S])
+        v, log_var, k, q = self._linear_split(self.sensor_proj, z, [self._w_value, self._w_var, S, S])
         if self._value_rank == "conv":
             v = z
         elif self.value_expand is not None:
@@ -247,6 +246,19 @@ class KLALayer(nn.Module):
 
             return linear(mod, x)
         return mod(x)
+
+    def _linear_split(self, mod: nn.Linear, x: torch.Tensor, sizes: list[int]):
+        """self._split(mod(x), sizes); on a hip-family backend with a gradient to
+        carry, the projection and the split as one (kla.ops.hip.linear)."""
+        from kla.ops.kla_ops import _step_on_hip
+
+        if torch.is_grad_enabled() and _step_on_hip(self.config.backend, x):
+            from kla.ops.hip.linear import linear_split
+
+            pieces = linear_split(mod, x, sizes)
+            if pieces is not None:
+                return pieces
+        return self._split(mod(x), sizes)
 
     def _qk_on_hip(self, k: torch.Tensor) -> bool:
         """Whether the k, q sensors come from the MI355X kernels: a hip-family backend
@@ -415,11 +427,12 @@ class KLALayer(nn.Module):
         L = x.shape[1]
         emit_state = return_state or state is not None
 
-        projected = self._linear(self.in_proj, x)
         if cfg.use_gating:
-            z, gate = self._split(projected, [self.d_inner, self.d_inner])
+            z, gate = self._linear_split(self.in_proj, x, [self.d_inner, self.d_inner])
+            projected = z
         else:
-            z, gate = projected, None
+            z = projected = self._linear(self.in_proj, x)
+            gate = None
         # One-token inference step on the GPU: the conv step and the SSM step
         # (with skip and gate) run as two HIP kernels (kla.ops.hip.decode).
         hip_decode = (state is not None and L == 1 and state.ssm.lam.dtype == torch.float32

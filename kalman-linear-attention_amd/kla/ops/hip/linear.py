@@ -14,6 +14,15 @@ in one fp32-output batched GEMM, which gives P times the workgroups.
 ``kla_sum_parts`` then adds the partials in chunk order and rounds them to bf16
 once. The result is torch's value up to the fp32 summation order inside the
 GEMM, which torch does not fix either.
+
+A projection whose output is split right away (``in_proj`` into z and the gate,
+``sensor_proj`` into v, log sigma^2, k and q) goes through
+:func:`linear_split`, which also replaces the split: it returns the pieces, and
+its backward concatenates their gradients with ``kla_cat_cols``. Its weight is
+taken in row blocks of whole 256-row tiles plus the rest (``sensor_proj``'s
+4128 rows: 4096 + 32), each block one forward product and one split weight
+gradient, so a ragged last tile row does not slow the whole product (C4's
+sensor_proj forward 304 -> 231 us, weight gradient 370 -> 294 us on MI355X).
 """
 
 from __future__ import annotations
@@ -24,12 +33,11 @@ import torch
 import torch.nn.functional as F
 
 from kla.ops.hip import _lib
+from kla.ops.hip.split import _Like, cat_cols_hip
 
-# Token chunks per weight gradient: 4 took C4's three products from 657 to
-# 446 us on MI355X (2 and 8 gained less once the partials' sum is counted).
-_PARTS = 4
-# Shortest token chunk worth a split.
-_MIN_CHUNK = 2048
+# At most this many token chunks per weight gradient, each at least this long.
+_MAX_PARTS = 32
+_MIN_CHUNK = 512
 
 
 @functools.cache
@@ -39,76 +47,154 @@ def _cus(index: int) -> int:
 
 def split_count(tokens: int, n: int, k: int, device: torch.device) -> int:
     """Token chunks for the weight gradient of an [n, k] projection over
-    ``tokens`` rows: ``_PARTS`` when 256 x 256 output tiles would leave CUs idle
-    and the chunks stay long, else 1 (one GEMM, as torch does)."""
+    ``tokens`` rows: doubled from 1 while the 256 x 256 output tiles of all
+    chunks are fewer than the CUs, the chunks divide the tokens evenly and stay
+    at least ``_MIN_CHUNK`` long (at most ``_MAX_PARTS``). 1 means one GEMM, as
+    torch does. C4's projections get 4 (in_proj), 8 (out_proj), 2 and 32
+    (sensor_proj's two row blocks)."""
     tiles = -(-n // 256) * -(-k // 256)
-    if tokens % _PARTS or tokens < _PARTS * _MIN_CHUNK or tiles >= _cus(device.index or 0):
-        return 1
-    return _PARTS
+    cus = _cus(device.index or 0)
+    parts = 1
+    while (tiles * parts < cus and parts < _MAX_PARTS and tokens % (2 * parts) == 0
+           and tokens // (2 * parts) >= _MIN_CHUNK):
+        parts *= 2
+    return parts
+
+
+def row_blocks(n: int) -> list[tuple[int, int]]:
+    """[r0, r1) row blocks of an n-row weight: whole 256-row tiles, then the rest."""
+    n1 = n - n % 256
+    return [(0, n1), (n1, n)] if 0 < n1 < n else [(0, n)]
+
+
+def _weight_grad_into(out: torch.Tensor, dy: torch.Tensor, r0: int, r1: int, x: torch.Tensor, parts: int):
+    """out = dy[:, r0:r1]^T x for dense dy [T, n] and x [T, k], out a dense
+    [r1 - r0, k] tensor of dy's dtype: ``parts`` fp32 chunk products summed in
+    chunk order by ``kla_sum_parts`` and rounded once, or torch's single product
+    when ``parts`` is 1."""
+    T, n = dy.shape
+    k = x.shape[1]
+    if parts == 1:
+        torch.mm(dy[:, r0:r1].t(), x, out=out)
+        return
+    c = T // parts
+    # The right operand is a plain contiguous batch (no transposed view).
+    p = torch.bmm(dy.view(parts, c, n)[:, :, r0:r1].transpose(1, 2), x.view(parts, c, k), out_dtype=torch.float32)
+    code = _lib.KLA_DTYPE_BF16 if dy.dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32
+    _lib.check("kla_sum_parts", _lib.lib().kla_sum_parts(
+        code, p.data_ptr(), parts, (r1 - r0) * k, out.data_ptr(), torch.cuda.current_stream(dy.device).cuda_stream))
 
 
 def weight_grad_hip(dy: torch.Tensor, x: torch.Tensor, parts: int) -> torch.Tensor:
-    """dY^T X for dy [T, n], x [T, k] (dense, bf16 or fp32, T divisible by
-    ``parts``) as ``parts`` fp32 chunk products summed by ``kla_sum_parts``,
-    rounded to dy's dtype."""
+    """dY^T X for dy [T, n], x [T, k] (bf16 or fp32, T divisible by ``parts``)
+    as ``parts`` fp32 chunk products summed by ``kla_sum_parts``, rounded to
+    dy's dtype."""
     T, n = dy.shape
-    k = x.shape[1]
-    if x.shape[0] != T or T % parts or dy.dtype != x.dtype:
+    if x.dim() != 2 or x.shape[0] != T or T % parts or dy.dtype != x.dtype:
         raise ValueError(f"weight_grad_hip: dy {tuple(dy.shape)} {dy.dtype}, x {tuple(x.shape)} {x.dtype}, "
                          f"{parts} parts")
-    dy = dy.contiguous()
-    x = x.contiguous()
-    c = T // parts
-    # The right operand is a plain contiguous batch (no transposed view).
-    p = torch.bmm(dy.view(parts, c, n).transpose(1, 2), x.view(parts, c, k), out_dtype=torch.float32)
-    out = torch.empty((n, k), dtype=dy.dtype, device=dy.device)
-    code = _lib.KLA_DTYPE_BF16 if dy.dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32
-    _lib.check("kla_sum_parts", _lib.lib().kla_sum_parts(
-        code, p.data_ptr(), parts, n * k, out.data_ptr(), torch.cuda.current_stream(dy.device).cuda_stream))
+    out = torch.empty((n, x.shape[1]), dtype=dy.dtype, device=dy.device)
+    _weight_grad_into(out, dy.contiguous(), 0, n, x.contiguous(), parts)
     return out
+
+
+def _backward(ctx, dy: torch.Tensor):
+    """(dx, dw) of y = x w^T from dense dy [..., n]: dx = dy w (torch's product),
+    dw per row block with the token split :func:`split_count` picks."""
+    x, w = ctx.saved_tensors
+    n, k = w.shape
+    dy2 = dy.reshape(-1, n).contiguous()
+    dx = dw = None
+    if ctx.needs_input_grad[0]:
+        dx = dy2.mm(w).view(x.shape)
+    if ctx.needs_input_grad[1]:
+        x2 = x.reshape(-1, k).contiguous()
+        T = x2.shape[0]
+        dw = torch.empty_like(w)
+        for r0, r1 in ctx.blocks:
+            _weight_grad_into(dw[r0:r1], dy2, r0, r1, x2, split_count(T, r1 - r0, k, dy.device))
+    return dx, dw
 
 
 class _Linear(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, parts):
+    def forward(ctx, x, w):
         ctx.save_for_backward(x, w)
-        ctx.parts = parts
+        ctx.blocks = row_blocks(w.shape[0])
         return F.linear(x, w)
 
     @staticmethod
     def backward(ctx, dy):
+        return _backward(ctx, dy)
+
+
+class _SplitLinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, sizes):
+        n = w.shape[0]
+        blocks = row_blocks(n)
+        cuts = {sum(sizes[:i]) for i in range(len(sizes) + 1)}
+        if any(r0 not in cuts for r0, _ in blocks):
+            blocks = [(0, n)]   # a piece would straddle two blocks
+        ctx.save_for_backward(x, w)
+        ctx.blocks, ctx.sizes = blocks, list(sizes)
+        outs = [F.linear(x, w[r0:r1]) for r0, r1 in blocks]
+        pieces, c0 = [], 0
+        for size in sizes:
+            b = max(i for i, (r0, _) in enumerate(blocks) if r0 <= c0)
+            r0 = blocks[b][0]
+            pieces.append(outs[b][..., c0 - r0:c0 - r0 + size])
+            c0 += size
+        return tuple(pieces)
+
+    @staticmethod
+    def backward(ctx, *grads):
         x, w = ctx.saved_tensors
-        n, k = w.shape
-        dy2 = dy.reshape(-1, n)
-        dx = dw = None
-        if ctx.needs_input_grad[0]:
-            # autograd's product for a linear layer's input gradient
-            dx = dy2.mm(w).view(x.shape)
-        if ctx.needs_input_grad[1]:
-            dw = weight_grad_hip(dy2, x.reshape(-1, k), ctx.parts)
+        dy = cat_cols_hip(list(grads), ctx.sizes, _Like(x.shape[:-1] + (w.shape[0],), w.dtype, w.device))
+        dx, dw = _backward(ctx, dy)
         return dx, dw, None
 
 
-def linear(mod: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:
-    """``mod(x)`` for a bias-free ``nn.Linear`` on a ROCm GPU in bf16 (under
-    bf16 autocast, or bf16 input and weight), with the weight gradient split
-    over the tokens where :func:`split_count` says so; otherwise ``mod(x)``.
-    The casts autocast would make are made here, so their backward is the same."""
+def _bf16_operands(mod: torch.nn.Linear, x: torch.Tensor):
+    """(x, w) as the bf16 operands of mod(x) -- the casts autocast would make,
+    made here so their backward is the same -- for a bias-free nn.Linear with a
+    gradient to carry on a ROCm GPU under bf16 autocast (or with bf16 x and w);
+    None otherwise."""
     w = mod.weight
     if (mod.bias is not None or not x.is_cuda or not torch.is_grad_enabled()
             or not (x.requires_grad or w.requires_grad)):
-        return mod(x)
+        return None
     dt = (x.dtype, w.dtype)
     if torch.is_autocast_enabled("cuda"):
         if torch.get_autocast_dtype("cuda") != torch.bfloat16 or not all(
                 d in (torch.float32, torch.bfloat16) for d in dt):
-            return mod(x)
+            return None
     elif dt != (torch.bfloat16, torch.bfloat16):
+        return None
+    return x.to(torch.bfloat16), w.to(torch.bfloat16)
+
+
+def linear(mod: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:
+    """``mod(x)``; for a bias-free ``nn.Linear`` in bf16 on a ROCm GPU whose
+    weight gradient :func:`split_count` splits, the product with the split
+    weight gradient."""
+    n, k = mod.weight.shape
+    ops = _bf16_operands(mod, x)
+    if ops is None or split_count(x.numel() // k if k else 0, n, k, x.device) == 1:
         return mod(x)
-    n, k = w.shape
-    parts = split_count(x.numel() // k if k else 0, n, k, x.device)
-    if parts == 1:
-        return mod(x)
-    x, w = x.to(torch.bfloat16), w.to(torch.bfloat16)
     with torch.autocast("cuda", enabled=False):
-        return _Linear.apply(x, w, parts)
+        return _Linear.apply(*ops)
+
+
+def linear_split(mod: torch.nn.Linear, x: torch.Tensor, sizes: list[int]):
+    """``torch.split(mod(x), sizes, dim=-1)`` for a bias-free ``nn.Linear`` in
+    bf16 on a ROCm GPU (at most four pieces): the weight in row blocks, the
+    split weight gradient, the pieces' gradients concatenated on the GPU. None
+    where that does not apply (the caller splits ``mod(x)`` itself)."""
+    if len(sizes) > 4 or sum(sizes) != mod.weight.shape[0]:
+        return None
+    ops = _bf16_operands(mod, x)
+    if ops is None:
+        return None
+    with torch.autocast("cuda", enabled=False):
+        return _SplitLinear.apply(*ops, list(sizes))
