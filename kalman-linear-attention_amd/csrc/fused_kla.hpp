@@ -916,6 +916,37 @@ __global__ void __launch_bounds__(256) reduce_rows_kernel(const float *__restric
   if (r == 0) out[static_cast<int64_t>(blockIdx.x) * INNER + i] = sm[i];
 }
 
+// The sums of reduce_rows_kernel<INNER>, bit for bit, for INNER >= 4: one wave
+// per row block o and 16-byte loads. Lane l sums columns 4 (l % Q) .. + 3
+// (Q = INNER / 4 lanes per row) over the rows j = r, r + R, ... of its phase
+// r = l / Q (R = 64 / Q = 256 / INNER phases, as there), then the phases are
+// added pairwise R/2 apart, R/4 apart, ... -- the same additions in the same
+// order -- over lanes by shuffles, with no LDS and no barrier.
+template <int INNER>
+__global__ void __launch_bounds__(256) reduce_rows_wave_kernel(const float *__restrict__ in, float *__restrict__ out,
+                                                               int64_t outer, int64_t G) {
+  static_assert(INNER >= 4 && INNER <= 64 && 256 % INNER == 0, "INNER must be 4 to 64, a power of two");
+  constexpr int Q = INNER / 4;
+  constexpr int R = kWave / Q;
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  const int lane = static_cast<int>(threadIdx.x) % kWave;
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
+  if (o >= outer) return;   // whole waves leave together
+  const int q = lane % Q, r = lane / Q;
+  const f32x4v *src = reinterpret_cast<const f32x4v *>(in + o * G * INNER) + q;
+  f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+  for (int64_t j = r; j < G; j += R) acc += src[j * Q];
+#pragma unroll
+  for (int off = kWave / 2; off >= Q; off /= 2) {
+    acc.x += __shfl_xor(acc.x, off);
+    acc.y += __shfl_xor(acc.y, off);
+    acc.z += __shfl_xor(acc.z, off);
+    acc.w += __shfl_xor(acc.w, off);
+  }
+  if (r == 0) *reinterpret_cast<f32x4v *>(out + o * INNER + 4 * q) = acc;
+}
+
 // out[i] = sum_j in[j, i] over G rows (outer = 1): a 1024-thread block covers 64
 // columns with 16 row phases, each thread summing every 16th row of its column
 // (coalesced across the 64 columns), then a fixed-order LDS tree adds the 16
@@ -928,8 +959,13 @@ __global__ void __launch_bounds__(1024) reduce_cols_kernel(const float *__restri
   const int c = t % COLS, ph = t / COLS;
   const int64_t col = static_cast<int64_t>(blockIdx.x) * COLS + c;
   float acc = 0.0f;
-  if (col < inner)
+  // Unrolled so that several independent loads are in flight before the
+  // (in-order) additions: a few columns over many rows is otherwise a chain of
+  // cache latencies.
+  if (col < inner) {
+#pragma unroll 8
     for (int64_t j = ph; j < G; j += PH) acc += in[j * inner + col];
+  }
   sm[ph][c] = acc;
   __syncthreads();
 #pragma unroll
