@@ -18,7 +18,8 @@ GEMM, which torch does not fix either.
 A projection whose output is split right away (``in_proj`` into z and the gate,
 ``sensor_proj`` into v, log sigma^2, k and q) goes through
 :func:`linear_split`, which also replaces the split: it returns the pieces, and
-its backward concatenates their gradients with ``kla_cat_cols``. Its weight is
+its backward concatenates their gradients with ``kla_cat_cols`` for dX (with no
+dX to form, each piece's gradient gives its rows of dW directly). Its weight is
 taken in row blocks of whole 256-row tiles plus the rest (``sensor_proj``'s
 4128 rows: 4096 + 32), each block one forward product and one split weight
 gradient, so a ragged last tile row does not slow the whole product (C4's
@@ -150,9 +151,24 @@ class _SplitLinear(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grads):
         x, w = ctx.saved_tensors
-        dy = cat_cols_hip(list(grads), ctx.sizes, _Like(x.shape[:-1] + (w.shape[0],), w.dtype, w.device))
-        dx, dw = _backward(ctx, dy)
-        return dx, dw, None
+        if ctx.needs_input_grad[0]:
+            dy = cat_cols_hip(list(grads), ctx.sizes, _Like(x.shape[:-1] + (w.shape[0],), w.dtype, w.device))
+            dx, dw = _backward(ctx, dy)
+            return dx, dw, None
+        # Without dx each piece's gradient gives its own rows of dw: no concatenation.
+        k = w.shape[1]
+        x2 = x.reshape(-1, k).contiguous()
+        T = x2.shape[0]
+        dw = torch.empty_like(w)
+        c0 = 0
+        for g, size in zip(grads, ctx.sizes):
+            if g is None:
+                dw[c0:c0 + size].zero_()
+            else:
+                g2 = g.to(w.dtype).reshape(-1, size).contiguous()
+                _weight_grad_into(dw[c0:c0 + size], g2, 0, size, x2, split_count(T, size, k, w.device))
+            c0 += size
+        return None, dw, None
 
 
 def _bf16_operands(mod: torch.nn.Linear, x: torch.Tensor):

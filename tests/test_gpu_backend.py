@@ -1365,11 +1365,13 @@ def test_weight_grad_split_matches_float64(cuda, T, n, k):
     assert float(((got - torch_bf16).abs() - torch_bf16.abs() * 2.0 ** -7).max()) <= 1e-4 * scale
 
 
-def test_linear_split_matches_torch(cuda):
+@pytest.mark.parametrize("x_grad", [True, False])
+def test_linear_split_matches_torch(cuda, x_grad):
     """linear_split (row blocks of whole 256-row tiles plus the rest, split
     weight gradients, the split fused in) against torch.split(F.linear(...))
     under bf16 autocast: pieces, dx and dw within bf16 rounding of torch's, a
-    piece without a gradient, and the ragged 32-row block of a 1056-row weight."""
+    piece without a gradient, and the ragged 32-row block of a 1056-row weight;
+    without dx (x_grad False) dw comes from each piece's gradient directly."""
     from kla.ops.hip.linear import linear_split, row_blocks
 
     assert row_blocks(1056) == [(0, 1024), (1024, 1056)] and row_blocks(4096) == [(0, 4096)]
@@ -1380,13 +1382,14 @@ def test_linear_split_matches_torch(cuda):
     gs = [torch.randn(2, 4096, w, generator=g).to(cuda, torch.bfloat16) for w in sizes]
     res = []
     for hip in (True, False):
-        x = x0.clone().requires_grad_(True)
+        x = x0.clone().requires_grad_(x_grad)
         mod.zero_grad(set_to_none=True)
         with torch.autocast("cuda", dtype=torch.bfloat16):
             pieces = linear_split(mod, x, sizes) if hip else torch.split(mod(x), sizes, dim=-1)
         assert [p.shape[-1] for p in pieces] == sizes
         torch.autograd.backward([pieces[0], pieces[1], pieces[3]], [gs[0], gs[1], gs[3]])
-        res.append(([p.detach().float() for p in pieces], x.grad.float(), mod.weight.grad.float()))
+        dx = x.grad.float() if x_grad else torch.zeros(1, device=cuda)
+        res.append(([p.detach().float() for p in pieces], dx, mod.weight.grad.float()))
     (ph, dxh, dwh), (pt, dxt, dwt) = res
     for name, a, b in [(f"piece{i}", a, b) for i, (a, b) in enumerate(zip(ph, pt))] + [("dx", dxh, dxt),
                                                                                     ("dw", dwh, dwt)]:
