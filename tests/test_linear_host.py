@@ -1,0 +1,45 @@
+"""Host-side logic of the split projections (no GPU): how many token chunks a
+weight gradient is split into, how a weight is cut into row blocks, and that
+the projections fall back to torch's nn.Linear where the HIP path does not
+apply (CPU tensors, no gradient, a bias)."""
+
+import torch
+
+from kla.ops.hip import linear as lin
+
+
+def test_split_count_fills_the_cus(monkeypatch):
+    monkeypatch.setattr(lin, "_cus", lambda index: 256)
+    dev = torch.device("cuda", 0)
+    T = 16384
+    # C4's weight-gradient shapes: 64, 32, 128 and 8 output tiles of 256 x 256.
+    assert lin.split_count(T, 4096, 1024, dev) == 4
+    assert lin.split_count(T, 1024, 2048, dev) == 8
+    assert lin.split_count(T, 4096, 2048, dev) == 2
+    assert lin.split_count(T, 32, 2048, dev) == 32
+    # Enough tiles already, too few tokens, or tokens that do not divide: one GEMM.
+    assert lin.split_count(T, 8192, 8192, dev) == 1
+    assert lin.split_count(1000, 64, 64, dev) == 1
+    assert lin.split_count(1536, 64, 64, dev) == 2      # chunks of 768, not 384
+    assert lin.split_count(4097, 64, 64, dev) == 1
+    for tokens in (2048, 6144, 16384, 65536):
+        p = lin.split_count(tokens, 300, 300, dev)
+        assert tokens % p == 0 and (p == 1 or tokens // p >= lin._MIN_CHUNK) and p <= lin._MAX_PARTS
+
+
+def test_row_blocks():
+    assert lin.row_blocks(4128) == [(0, 4096), (4096, 4128)]
+    assert lin.row_blocks(4096) == [(0, 4096)]
+    assert lin.row_blocks(200) == [(0, 200)]
+    assert lin.row_blocks(257) == [(0, 256), (256, 257)]
+
+
+def test_projections_fall_back_to_torch_on_cpu():
+    mod = torch.nn.Linear(8, 12, bias=False)
+    x = torch.randn(2, 5, 8, requires_grad=True)
+    assert torch.equal(lin.linear(mod, x), mod(x))
+    assert lin.linear_split(mod, x, [6, 6]) is None
+    assert lin.linear_split(mod, x, [4, 4]) is None          # sizes must cover the rows
+    assert lin._bf16_operands(torch.nn.Linear(8, 12), x) is None   # a bias
+    with torch.no_grad():
+        assert lin._bf16_operands(mod, x) is None
