@@ -69,18 +69,22 @@ def row_blocks(n: int) -> list[tuple[int, int]]:
 
 
 def _weight_grad_into(out: torch.Tensor, dy: torch.Tensor, r0: int, r1: int, x: torch.Tensor, parts: int):
-    """out = dy[:, r0:r1]^T x for dense dy [T, n] and x [T, k], out a dense
-    [r1 - r0, k] tensor of dy's dtype: ``parts`` fp32 chunk products summed in
-    chunk order by ``kla_sum_parts`` and rounded once, or torch's single product
-    when ``parts`` is 1."""
-    T, n = dy.shape
+    """out = dy[:, r0:r1]^T x for dy [T, n] (unit column stride, any row stride)
+    and dense x [T, k], out a dense [r1 - r0, k] tensor of dy's dtype: ``parts``
+    fp32 chunk products summed in chunk order by ``kla_sum_parts`` and rounded
+    once, or torch's single product when ``parts`` is 1."""
+    T = dy.shape[0]
     k = x.shape[1]
+    g = dy[:, r0:r1]
     if parts == 1:
-        torch.mm(dy[:, r0:r1].t(), x, out=out)
+        torch.mm(g.t(), x, out=out)
         return
     c = T // parts
+    ld = g.stride(0)
+    # Chunk j of g^T: [r1 - r0, c] columns j c .. (j + 1) c - 1, read in place.
     # The right operand is a plain contiguous batch (no transposed view).
-    p = torch.bmm(dy.view(parts, c, n)[:, :, r0:r1].transpose(1, 2), x.view(parts, c, k), out_dtype=torch.float32)
+    gt = g.as_strided((parts, r1 - r0, c), (c * ld, 1, ld))
+    p = torch.bmm(gt, x.view(parts, c, k), out_dtype=torch.float32)
     code = _lib.KLA_DTYPE_BF16 if dy.dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32
     _lib.check("kla_sum_parts", _lib.lib().kla_sum_parts(
         code, p.data_ptr(), parts, (r1 - r0) * k, out.data_ptr(), torch.cuda.current_stream(dy.device).cuda_stream))
@@ -94,8 +98,10 @@ def weight_grad_hip(dy: torch.Tensor, x: torch.Tensor, parts: int) -> torch.Tens
     if x.dim() != 2 or x.shape[0] != T or T % parts or dy.dtype != x.dtype:
         raise ValueError(f"weight_grad_hip: dy {tuple(dy.shape)} {dy.dtype}, x {tuple(x.shape)} {x.dtype}, "
                          f"{parts} parts")
+    if dy.stride(1) != 1:
+        dy = dy.contiguous()
     out = torch.empty((n, x.shape[1]), dtype=dy.dtype, device=dy.device)
-    _weight_grad_into(out, dy.contiguous(), 0, n, x.contiguous(), parts)
+    _weight_grad_into(out, dy, 0, n, x.contiguous(), parts)
     return out
 
 
@@ -165,7 +171,9 @@ class _SplitLinear(torch.autograd.Function):
             if g is None:
                 dw[c0:c0 + size].zero_()
             else:
-                g2 = g.to(w.dtype).reshape(-1, size).contiguous()
+                g2 = g.to(w.dtype).reshape(-1, size)   # a view where the rows allow it
+                if g2.stride(1) != 1:
+                    g2 = g2.contiguous()
                 _weight_grad_into(dw[c0:c0 + size], g2, 0, size, x2, split_count(T, size, k, w.device))
             c0 += size
         return None, dw, None

@@ -1345,23 +1345,28 @@ def test_sum_parts_equals_ordered_fp32_sum(cuda, dtype, parts, n):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("T,n,k", [(8192, 1024, 256), (16384, 2080, 2048)])
-def test_weight_grad_split_matches_float64(cuda, T, n, k):
+@pytest.mark.parametrize("T,n,k,strided", [(8192, 1024, 256, False), (16384, 2080, 2048, False),
+                                            (8192, 1000, 256, True)])
+def test_weight_grad_split_matches_float64(cuda, T, n, k, strided):
     """weight_grad_hip (4 token-chunk fp32 products, summed and rounded once)
     against the float64 product: within half a bf16 ulp of each value plus the
-    fp32 accumulation error, and within one bf16 ulp of torch's own bf16 GEMM."""
+    fp32 accumulation error, and within one bf16 ulp of torch's own bf16 GEMM;
+    also for dy a column slice of a wider tensor (read in place)."""
     from kla.ops.hip.linear import weight_grad_hip
 
     g = torch.Generator().manual_seed(94)
-    dy = torch.randn(T, n, generator=g).to(torch.bfloat16)
+    wide = torch.randn(T, n + 24, generator=g).to(torch.bfloat16)
+    dy = wide[:, 16:16 + n] if strided else wide[:, :n].contiguous()
     x = torch.randn(T, k, generator=g).to(torch.bfloat16)
     ref = dy.double().t() @ x.double()
-    got = weight_grad_hip(dy.to(cuda), x.to(cuda), 4)
+    dyd = wide.to(cuda)[:, 16:16 + n] if strided else dy.to(cuda)
+    assert dyd.is_contiguous() != strided
+    got = weight_grad_hip(dyd, x.to(cuda), 4)
     assert got.dtype == torch.bfloat16 and got.shape == (n, k)
     got = got.cpu().double()
     scale = float(ref.abs().max())
     assert float(((got - ref).abs() - ref.abs() * 2.0 ** -8).max()) <= 1e-4 * scale
-    torch_bf16 = (dy.to(cuda).t() @ x.to(cuda)).cpu().double()
+    torch_bf16 = (dy.contiguous().to(cuda).t() @ x.to(cuda)).cpu().double()
     assert float(((got - torch_bf16).abs() - torch_bf16.abs() * 2.0 ** -7).max()) <= 1e-4 * scale
 
 
