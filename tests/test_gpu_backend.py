@@ -1402,18 +1402,20 @@ def test_linear_split_matches_torch(cuda, x_grad):
         assert err <= 1e-3 * float(b.abs().max()), name
 
 
-def test_layer_split_linear_matches_torch_linear(cuda, monkeypatch):
+@pytest.mark.parametrize("d_model,B,L", [(256, 2, 4096), (1024, 4, 4096)])
+def test_layer_split_linear_matches_torch_linear(cuda, monkeypatch, d_model, B, L):
     """A KLALayer training step under bf16 autocast with its projections on
     kla.ops.hip.linear (row blocks, split weight gradients, the splits fused in)
     against the same layer with torch's nn.Linear and torch.split: the output
-    and every parameter gradient within bf16 rounding."""
+    and every parameter gradient within bf16 rounding; also at the C4 training
+    shape (sensor_proj's 4128 rows, 16384 tokens)."""
     import kla.ops.hip.linear as lin
 
     torch.manual_seed(95)
-    layer = KLALayer(256, KLAConfig(d_state=16, backend="hip")).to(cuda)
-    x = torch.randn(2, 4096, 256, generator=torch.Generator().manual_seed(96)).to(cuda)
+    layer = KLALayer(d_model, KLAConfig(d_state=16, backend="hip")).to(cuda)
+    x = torch.randn(B, L, d_model, generator=torch.Generator().manual_seed(96)).to(cuda)
     M = layer.d_inner
-    assert lin.split_count(2 * 4096, 2 * M, 256, x.device) > 1
+    assert lin.split_count(B * L, 2 * M, d_model, x.device) > 1
 
     calls = []
     for cls in (lin._Linear, lin._SplitLinear):
