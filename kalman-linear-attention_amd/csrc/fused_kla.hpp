@@ -190,14 +190,29 @@ struct FusedLane {
   bool active;   // s < S and m < M
 };
 
+// The workgroup's place in the grid. Workgroups go to MI355X's 8 XCDs round
+// robin (workgroup i to XCD i % 8), each XCD with its own L2. Numbering them
+// (i % 8) * (n / 8) + i / 8 gives every XCD a contiguous run of channel groups,
+// so the short rows of neighbouring groups' tiles (16 channels: 32 bytes of a
+// bf16 row) share that L2's lines instead of every XCD fetching whole lines.
+// The identity when the grid is not a multiple of 8.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int64_t xcd_block() {
+  const int64_t n = gridDim.x, i = blockIdx.x;
+  if (n % kXcds) return i;
+  return (i % kXcds) * (n / kXcds) + i / kXcds;
+}
+
 template <int SP>
 __device__ __forceinline__ FusedLane fused_lane(const FusedGeom &g) {
   constexpr int CH = kFusedThreads / SP;
   FusedLane ln;
   const int tid = static_cast<int>(threadIdx.x);
+  const int64_t blk = xcd_block();
   ln.s = tid % SP;
-  ln.b = static_cast<int64_t>(blockIdx.x) / g.groups;
-  ln.m = (static_cast<int64_t>(blockIdx.x) % g.groups) * CH + tid / SP;
+  ln.b = blk / g.groups;
+  ln.m = (blk % g.groups) * CH + tid / SP;
   ln.active = ln.s < g.S && ln.m < g.M;
   return ln;
 }
@@ -424,7 +439,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
 
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
-  const int64_t m0 = (static_cast<int64_t>(blockIdx.x) % g.groups) * CH;
+  const int64_t m0 = (xcd_block() % g.groups) * CH;
   const int c = static_cast<int>(ln.m - m0);
   const int64_t ms = ln.m * S + ln.s;
   const int64_t bms = ln.b * M * S + ms;
@@ -597,7 +612,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
 
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
-  const int64_t grp = static_cast<int64_t>(blockIdx.x) % g.groups;
+  const int64_t grp = xcd_block() % g.groups;
   const int64_t m0 = grp * CH;
   const int c = static_cast<int>(ln.m - m0);
   const int64_t ms = ln.m * S + ln.s;
