@@ -481,6 +481,9 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(per_kernel[dom]["GBps"] / PEAK_HBM_GBPS, 4),
             "traffic": traffic,
+            # traffic is not counted in this run: it is the calibrated FETCH_SIZE +
+            # WRITE_SIZE bytes per launch from a rocprofv3 --pmc run of this workload.
+            "traffic_source": (os.path.relpath(tfile, REPO) if traffic is not None else None),
             # The same launch priced on the bytes the kernel itself must move.
             "kernel_bytes": per_kernel[dom]["kernel_bytes"],
             "kernel_GBps": per_kernel[dom]["kernel_GBps"],

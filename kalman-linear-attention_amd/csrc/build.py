@@ -21,7 +21,8 @@ REPO = os.path.dirname(PKG_ROOT)
 INCLUDE = os.path.join(REPO, "include")
 DEFAULT_OUT = os.path.join(PKG_ROOT, "kla", "lib", "libkla_hip.so")
 SOURCES = ["kla_hip.hip"]
-HEADERS = ["causal_conv.hpp", "fused_kla.hpp", "gate_skip.hpp", "model_ops.hpp", "lookback_scan.hpp", "scan_ops.hpp"]
+HEADERS = ["causal_conv.hpp", "fused_kla.hpp", "gate_skip.hpp", "lookback_scan.hpp", "model_ops.hpp", "rows_linear.hpp",
+           "scan_ops.hpp"]
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32.
 HIPCC_FLAGS = [

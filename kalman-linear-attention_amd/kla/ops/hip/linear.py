@@ -168,6 +168,8 @@ class _SplitLinear(torch.autograd.Function):
         dw = torch.empty_like(w)
         c0 = 0
         for g, size in zip(grads, ctx.sizes):
+            if size == 0:
+                continue   # an empty piece owns no rows of dw
             if g is None:
                 dw[c0:c0 + size].zero_()
             else:

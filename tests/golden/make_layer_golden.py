@@ -71,6 +71,36 @@ with torch.no_grad():
     logits = logits[0] if isinstance(logits, tuple) else logits
     out["model/logits"] = logits.numpy()
 
+# Stateful chunked prefill (forward with state, reference sequence_model.py:150-173)
+# and a 16-token greedy generate (:201-220). The decode logits are recorded step
+# by step with the same loop generate runs, and the greedy choices must have a
+# clear margin so that float32 reassociation cannot flip them.
+gids = torch.randint(0, 64, (2, 8), generator=torch.Generator().manual_seed(3))
+out["model/gen_ids"] = gids.numpy()
+with torch.no_grad():
+    state = model.init_state(2)
+    l1, state = model(gids[:, :5], state=state)
+    l2, state = model(gids[:, 5:], state=state)
+    out["model/chunk_logits"] = torch.cat([l1, l2], 1).numpy()
+    for i, st in enumerate(state):
+        out[f"model/prefill_lam/{i}"] = st.ssm.lam.numpy()
+        out[f"model/prefill_eta/{i}"] = st.ssm.eta.numpy()
+    gen = model.generate(gids, 16, temperature=0.0)
+    out["model/generate"] = gen.numpy()
+    state = model.init_state(2)
+    logits, state = model(gids, state=state)
+    steps = [logits[:, -1]]
+    for t in range(15):
+        logits, state = model(gen[:, 8 + t : 9 + t], state=state)
+        steps.append(logits[:, -1])
+    steps = torch.stack(steps, 1)
+    out["model/decode_logits"] = steps.numpy()
+    assert torch.equal(steps.argmax(-1), gen[:, 8:]), "step-by-step decode differs from generate"
+    top2 = steps.topk(2, dim=-1).values
+    margin = float((top2[..., 0] - top2[..., 1]).min())
+    print(f"smallest greedy margin {margin:.3e}")
+    assert margin > 1e-4, "greedy choice too close to a tie for an exact token check"
+
 np.savez(sys.argv[2], **out)
 print(f"wrote {len(out)} arrays to {sys.argv[2]}")
 '''

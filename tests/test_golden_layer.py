@@ -69,3 +69,32 @@ def test_sequence_model_matches_reference(golden):
     with torch.no_grad():
         logits = _first(model(torch.from_numpy(golden["model/ids"])))
     np.testing.assert_allclose(logits.numpy(), golden["model/logits"], rtol=1e-5, atol=1e-6)
+
+
+def test_sequence_model_stateful_prefill_and_generate_match_reference(golden):
+    """Chunked stateful prefill (5 + 3 tokens), the per-layer state it leaves, the
+    step-by-step greedy decode logits and the 16 generated token ids, all as the
+    reference's SequenceModel.forward / generate wrote them (reference
+    src/kla/models/sequence_model.py:150-173, :201-220). Token ids must match
+    exactly; the golden script asserts a greedy margin above 1e-4."""
+    torch.manual_seed(0)
+    model = SequenceModel(ModelConfig(vocab_size=64, d_model=32, n_layers=2), KLAConfig(d_state=4, backend="torch"))
+    gids = torch.from_numpy(golden["model/gen_ids"])
+    with torch.no_grad():
+        state = model.init_state(2)
+        l1, state = model(gids[:, :5], state=state)
+        l2, state = model(gids[:, 5:], state=state)
+        np.testing.assert_allclose(torch.cat([l1, l2], 1).numpy(), golden["model/chunk_logits"], rtol=1e-5, atol=1e-6)
+        for i, st in enumerate(state):
+            np.testing.assert_allclose(st.ssm.lam.numpy(), golden[f"model/prefill_lam/{i}"], rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(st.ssm.eta.numpy(), golden[f"model/prefill_eta/{i}"], rtol=1e-5, atol=1e-6)
+        gen = model.generate(gids, 16, temperature=0.0)
+    np.testing.assert_array_equal(gen.numpy(), golden["model/generate"])
+    with torch.no_grad():
+        state = model.init_state(2)
+        logits, state = model(gids, state=state)
+        steps = [logits[:, -1]]
+        for t in range(15):
+            logits, state = model(gen[:, 8 + t: 9 + t], state=state)
+            steps.append(logits[:, -1])
+    np.testing.assert_allclose(torch.stack(steps, 1).numpy(), golden["model/decode_logits"], rtol=1e-5, atol=1e-6)

@@ -4,10 +4,13 @@ Inputs are drawn on the CPU (torch.Generator) and copied, so both sides see
 the same bytes. Parity anchors: the float64 sequential filter (oracle.kla,
 pinned against the covariance-form filter) for outputs and state, and float64
 torch autograd through oracle.torch_ref for every gradient -- including the
-initial-state gradients the stateful prefill needs. The bar is the path's
-fp32 tolerance, |got - want| <= atol + rtol |want| with rtol 1e-5, atol 1e-6
-taken relative to each tensor's scale (atol * max|want|, as the reference's
-tests/test_backends.py rel_err does), and the layer-level checks reuse the
+initial-state gradients the stateful prefill needs. The scan's bar is the
+path's fp32 tolerance, |got - want| <= atol + rtol |want| with rtol 1e-5 and an
+absolute atol 1e-6 (check_scan), except for the gradients that contract over
+many terms (dk, dq over channels; da, dp over batch and time), whose atol is
+1e-6 * max|want|, as the reference's tests/test_backends.py rel_err scales it.
+The layer kernels around the scan are checked against torch's own operations
+relative to each tensor's scale (check), and the layer-level checks reuse the
 reference's golden vectors (tests/golden/layer_golden.npz).
 """
 
@@ -40,12 +43,37 @@ def make_inputs(B=2, L=64, M=16, S=8, seed=0):
     )
 
 
+# Gradients that contract over many terms: dk, dq sum over the M channels, da, dp
+# over batch and time (B*L terms). Their fp32 rounding grows with the magnitude
+# of the terms, not of the (possibly cancelled) result, so their atol is taken
+# relative to the tensor's scale; every other output of the scan meets the
+# absolute rtol 1e-5 / atol 1e-6.
+CONTRACTIONS = ("dk", "dq", "da", "dp")
+
+
+def check_scan(name, got, want):
+    """The KLA scan's tolerance: |got - want| <= 1e-6 + 1e-5 |want| for outputs,
+    state and elementwise gradients; atol 1e-6 * max|want| for CONTRACTIONS."""
+    got = got.detach().double().cpu().numpy()
+    want = np.asarray(want, dtype=np.float64).reshape(got.shape)
+    assert np.isfinite(got).all(), f"{name}: non-finite values"
+    err = np.abs(got - want)
+    atol = ATOL * max(float(np.abs(want).max()), 1e-30) if name in CONTRACTIONS else ATOL
+    worst = float((err / (atol + RTOL * np.abs(want))).max()) if err.size else 0.0
+    kind = "atol 1e-6*max|ref|" if name in CONTRACTIONS else "atol 1e-6"
+    print(f"  {name:10s} worst |d|/(atol+rtol|ref|) = {worst:.3f}  [rtol 1e-5, {kind}]", flush=True)
+    assert worst <= 1.0, f"{name}: outside rtol={RTOL}, {kind} (ratio {worst:.3f})"
+
+
 def check(name, got, want, rtol=RTOL, atol=ATOL):
+    """Tolerance relative to the tensor's scale (atol * max|want|), for the layer
+    kernels checked against torch's own operations at their own tolerances."""
     got = got.detach().double().cpu().numpy()
     want = np.asarray(want, dtype=np.float64).reshape(got.shape)
     assert np.isfinite(got).all(), f"{name}: non-finite values"
     scale = max(float(np.abs(want).max()), 1e-30)
-    worst = float((np.abs(got - want) / (atol * scale + rtol * np.abs(want))).max())
+    err = np.abs(got - want)
+    worst = float((err / (atol * scale + rtol * np.abs(want))).max()) if err.size else 0.0
     print(f"  {name:10s} worst |d|/(atol*scale + rtol|ref|) = {worst:.3f}", flush=True)
     assert worst <= 1.0, f"{name}: outside rtol={rtol} atol={atol} (ratio {worst:.3f})"
 
@@ -75,10 +103,10 @@ def test_forward_and_state_match_oracle(cuda, backend, decode_from_prior, with_s
                              initial_state=None if st is None else KLAState(st.lam.to(cuda), st.eta.to(cuda)))
     assert y.dtype == torch.float32 and y.device.type == "cuda"
     wy, wv, wl, we = oracle(ins, st, decode_from_prior)
-    check("y", y, wy)
-    check("y_var", y_var, wv)
-    check("lam", fin.lam, wl)
-    check("eta", fin.eta, we)
+    check_scan("y", y, wy)
+    check_scan("y_var", y_var, wv)
+    check_scan("lam", fin.lam, wl)
+    check_scan("eta", fin.eta, we)
     assert (y_var >= 0).all()
 
 
@@ -90,10 +118,10 @@ def test_forward_ragged_shapes(cuda, backend, shape):
     ins = make_inputs(B, L, M, S, seed=7)
     y, y_var, fin = kla_scan(*(t.to(cuda) for t in ins), backend=backend)
     wy, wv, wl, we = oracle(ins)
-    check("y", y, wy)
-    check("y_var", y_var, wv)
-    check("lam", fin.lam, wl)
-    check("eta", fin.eta, we)
+    check_scan("y", y, wy)
+    check_scan("y_var", y_var, wv)
+    check_scan("lam", fin.lam, wl)
+    check_scan("eta", fin.eta, we)
 
 
 @pytest.mark.parametrize("backend", BACKENDS)
@@ -111,7 +139,10 @@ def test_chunked_state_carry(cuda, backend):
 @pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("decode_from_prior", [False, True])
 @pytest.mark.parametrize("shape", [(2, 48, 16, 8), (1, 37, 5, 16), (2, 20, 3, 3), (1, 33, 6, 12), (1, 21, 4, 20),
-                                   (2, 150, 20, 16), (1, 260, 6, 4)])
+                                   (2, 150, 20, 16), (1, 260, 6, 4),
+                                   # grids that are multiples of the 8 XCDs (the workgroup
+                                   # renumbering applies) with a ragged last channel group
+                                   (2, 150, 120, 16), (8, 40, 9, 32)])
 def test_gradients_match_float64_autograd(cuda, backend, decode_from_prior, shape):
     """Every input gradient, the initial-state gradients, and gradients flowing in
     through the returned state, against float64 autograd of the reference's
@@ -136,7 +167,7 @@ def test_gradients_match_float64_autograd(cuda, backend, decode_from_prior, shap
                              decode_from_prior=decode_from_prior)
     loss(y, y_var, fin.lam, fin.eta).backward()
     for name, got, want in zip(("v", "lambda_v", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
-        check("d" + name, got.grad, want.grad.numpy())
+        check_scan("d" + name, got.grad, want.grad.numpy())
 
 
 @pytest.mark.parametrize("backend", BACKENDS)
@@ -157,8 +188,8 @@ def test_high_information_tokens_are_not_clipped(cuda, backend):
     ins[1] = ins[1] * 1e4
     y, y_var, _ = kla_scan(*(t.to(cuda) for t in ins), backend=backend)
     wy, wv, _, _ = oracle(ins)
-    check("y", y, wy)
-    check("y_var", y_var, wv)
+    check_scan("y", y, wy)
+    check_scan("y_var", y_var, wv)
 
 
 @pytest.mark.parametrize("backend", BACKENDS)
@@ -222,17 +253,22 @@ def test_layer_on_hip_reproduces_reference_vectors(cuda, tag):
     with np.load(GOLDEN, allow_pickle=False) as z:
         gold = {k: z[k] for k in z.files if k.startswith(tag + "/")}
     d_model, cfg, shape = GOLDEN_CASES[tag]
-    torch.manual_seed(0)
-    layer = KLALayer(d_model, KLAConfig(backend="hip", **cfg)).to(cuda)
+    layer = KLALayer(d_model, KLAConfig(backend="hip", **cfg))
+    # The reference's parameters (their seeded draw order is pinned on the CPU by
+    # tests/test_golden_layer.py; another host CPU may round an initialiser in
+    # the last bit).
+    pre = f"{tag}/param/"
+    layer.load_state_dict({k[len(pre):]: torch.from_numpy(v) for k, v in gold.items() if k.startswith(pre)})
+    layer = layer.to(cuda)
     x = torch.from_numpy(gold[f"{tag}/x"]).to(cuda)
     with torch.no_grad():
-        check("y", _first(layer(x)), gold[f"{tag}/y"], rtol=1e-4, atol=1e-5)
+        check_scan("y", _first(layer(x)), gold[f"{tag}/y"])
         state = layer.init_state(shape[0], device=cuda)
         _, state = layer(x[:, : shape[1] // 2], state=state)
-        check("lam", state.ssm.lam, gold[f"{tag}/prefill_lam"])
-        check("eta", state.ssm.eta, gold[f"{tag}/prefill_eta"], rtol=1e-4, atol=1e-5)
+        check_scan("lam", state.ssm.lam, gold[f"{tag}/prefill_lam"])
+        check_scan("eta", state.ssm.eta, gold[f"{tag}/prefill_eta"])
         step, _ = layer(x[:, shape[1] // 2: shape[1] // 2 + 1], state=state)
-        check("decode", _first(step), gold[f"{tag}/decode_y"], rtol=1e-4, atol=1e-5)
+        check_scan("decode", _first(step), gold[f"{tag}/decode_y"])
 
 
 def test_layer_train_step_and_decode_parity(cuda):
@@ -301,7 +337,7 @@ def test_step_kernel_matches_reference_step(cuda, decode_from_prior, shape):
                        decode_from_prior=decode_from_prior, backend="hip")
     for name, g, w in (("y", got[0], want[0]), ("y_var", got[1], want[1]), ("lam", got[2].lam, want[2].lam),
                        ("eta", got[2].eta, want[2].eta)):
-        check(name, g, w.numpy())
+        check_scan(name, g, w.numpy())
 
 
 def test_decode_graph_replays_match_eager(cuda):
@@ -340,11 +376,15 @@ def test_decode_graph_replays_match_eager(cuda):
 
 def test_fused_at_c4_size(cuda):
     """C4's scan shape (B=4, L=4096, M=2048, S=16), forward + backward on the fused
-    kernels. A channel's outputs, dv, dLv, da and dp depend only on that channel,
-    so a spread of channels is checked exactly against the float64 oracle
-    (forward) / float64 autograd (backward) run on those channels alone; dk and dq
-    contract over every channel and are checked against the independent composed
-    path (HIP Moebius + affine scans, torch glue) on the same inputs."""
+    kernels, every output against the float64 oracle.
+
+    The output gradients dy, dy_var are zero outside a spread of channels (group
+    edges and XCD runs included). A channel's y, y_var, dv, dLv, da and dp depend
+    only on that channel, and dk, dq -- the contractions over all channels and the
+    kernel's 128 channel groups -- then receive contributions from the spread
+    alone: float64 autograd through the reference's torch path on those channels
+    fixes the whole of dk and dq, and dv, dLv, da, dp must be exactly zero on every
+    other channel. The kernels still run and reduce every channel group."""
     B, L, M, S = 4, 4096, 2048, 16
     g = torch.Generator().manual_seed(21)
     v = torch.randn(B, L, M, generator=g)
@@ -353,40 +393,51 @@ def test_fused_at_c4_size(cuda):
     q = torch.randn(B, L, S, generator=g) * 0.3
     a = torch.rand(M, S, generator=g) * 0.5 + 0.45
     p = torch.rand(M, S, generator=g) * 0.05 + 0.01
-    dy = torch.randn(B, L, M, generator=g)
-    dyv = torch.randn(B, L, M, generator=g)
-    outs = {}
-    for backend in ("hip_fused", "hip_composed"):
-        xs = [t.to(cuda).requires_grad_(True) for t in (v, lv, k, q, a, p)]
-        y, y_var, _ = kla_scan(*xs, backend=backend)
-        ((dy.to(cuda) * y).sum() + (dyv.to(cuda) * y_var).sum()).backward()
-        outs[backend] = [y.detach(), y_var.detach()] + [x.grad for x in xs]
-        del xs, y, y_var
-    fused, comp = outs["hip_fused"], outs["hip_composed"]
+    chans = torch.tensor([0, 1, 15, 16, 17, 255, 256, 1023, 1024, 2047])
+    mask = torch.zeros(M)
+    mask[chans] = 1.0
+    dy = torch.randn(B, L, M, generator=g) * mask
+    dyv = torch.randn(B, L, M, generator=g) * mask
+    xs = [t.to(cuda).requires_grad_(True) for t in (v, lv, k, q, a, p)]
+    y, y_var, _ = kla_scan(*xs, backend="hip_fused")
+    ((dy.to(cuda) * y).sum() + (dyv.to(cuda) * y_var).sum()).backward()
+    fused = [y.detach(), y_var.detach()] + [x.grad for x in xs]
+    del xs, y, y_var
     for t in fused:
         assert torch.isfinite(t).all()
-    for name, i in (("dk", 4), ("dq", 5)):
-        check(name, fused[i], comp[i].double().cpu().numpy(), rtol=1e-4, atol=1e-5)
 
-    chans = torch.tensor([0, 1, 15, 16, 17, 255, 256, 1023, 1024, 2047])
+    # Forward on 64 channels (the spread plus a run across two channel groups).
+    fchans = torch.tensor(sorted(set(chans.tolist()) | set(range(1000, 1054))))
+    fsub = [v[..., fchans], lv[..., fchans], k, q, a[fchans], p[fchans]]
+    wy, wv, _, _ = okla.kla_scan_sequential(*(t.double().numpy() for t in fsub))
+    check_scan("y", fused[0][..., fchans.to(cuda)], wy)
+    check_scan("y_var", fused[1][..., fchans.to(cuda)], wv)
+
     sub = [v[..., chans], lv[..., chans], k, q, a[chans], p[chans]]
-    wy, wv, _, _ = okla.kla_scan_sequential(*(t.double().numpy() for t in sub))
-    check("y", fused[0][..., chans.to(cuda)], wy)
-    check("y_var", fused[1][..., chans.to(cuda)], wv)
     xs = [t.double().requires_grad_(True) for t in sub]
     yr, yvr, _, _ = torch_ref.kla_scan_torch(*xs)
     ((dy[..., chans].double() * yr).sum() + (dyv[..., chans].double() * yvr).sum()).backward()
-    for name, i, idx in (("dv", 0, (Ellipsis, chans)), ("dlambda_v", 1, (Ellipsis, chans)), ("da", 4, chans),
-                         ("dp", 5, chans)):
-        check(name, fused[2 + i][tuple(c.to(cuda) if isinstance(c, torch.Tensor) else c for c in
-                                       (idx if isinstance(idx, tuple) else (idx,)))], xs[i].grad.numpy())
+    cg = chans.to(cuda)
+    rest = torch.ones(M, dtype=torch.bool, device=cuda)
+    rest[cg] = False
+    for name, i in (("dv", 0), ("dlambda_v", 1)):
+        check_scan(name, fused[2 + i][..., cg], xs[i].grad.numpy())
+        assert torch.equal(fused[2 + i][..., rest], torch.zeros_like(fused[2 + i][..., rest])), name
+    for name, i in (("da", 4), ("dp", 5)):
+        check_scan(name, fused[2 + i][cg], xs[i].grad.numpy())
+        assert torch.equal(fused[2 + i][rest], torch.zeros_like(fused[2 + i][rest])), name
+    check_scan("dk", fused[4], xs[2].grad.numpy())
+    check_scan("dq", fused[5], xs[3].grad.numpy())
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_affine_scan_at_c3_size(cuda, dtype):
-    """C3 (B=8, T=8192, L=2048), fp32 and bf16 I/O: a spread of lanes against the
-    float64 oracle on the same (dtype-exact) inputs, every value finite, and the
-    forward's state chained in two halves equals one pass."""
+    """C3 (B=8, T=8192, L=2048), fp32 and bf16 I/O: every element of h, dg and du
+    against the float64 oracle on the same (dtype-exact) inputs, one batch row at
+    a time, and the forward's state chained in two halves equals one pass.
+    fp32: rtol 1e-5, atol 1e-6. bf16 I/O: rtol 2e-2 (north_star), with an atol of
+    1e-5 for values that cancel to near zero (the fp32 sum's rounding is relative
+    to its terms, not to the rounded-to-bf16 result)."""
     from kla.ops.hip import affine_scan
     from oracle import scans as ref
 
@@ -400,19 +451,27 @@ def test_affine_scan_at_c3_size(cuda, dtype):
     h.backward(dh.to(cuda))
     for t in (h, gg.grad, uu.grad):
         assert torch.isfinite(t.float()).all()
-    lanes = torch.tensor([0, 1, 63, 64, 127, 128, 255, 256, 1000, 1023, 1024, 2046, 2047])
-    sub = lambda t: t[..., lanes]  # noqa: E731
-    tol = dict(rtol=1e-5, atol=1e-6) if dtype == torch.float32 else dict(rtol=2e-2, atol=1e-2)
-    hw = ref.affine_scan_fwd(sub(g).float(), sub(u).float())
-    check("h", sub(h.cpu()), hw, **tol)
-    dg, du, _ = ref.affine_scan_bwd(sub(dh).float(), sub(g).float(), hw)
-    check("dg", sub(gg.grad.cpu()), dg, **tol)
-    check("du", sub(uu.grad.cpu()), du, **tol)
+    rtol, atol = (1e-5, 1e-6) if dtype == torch.float32 else (2e-2, 1e-5)
+    got = {"h": h.detach().cpu(), "dg": gg.grad.cpu(), "du": uu.grad.cpu()}
+    worst, worst_abs6 = {}, {}
+    for b in range(B):
+        r = slice(b, b + 1)
+        hw = ref.affine_scan_fwd(g[r].float(), u[r].float())
+        dgw, duw, _ = ref.affine_scan_bwd(dh[r].float(), g[r].float(), hw)
+        for name, want in (("h", hw), ("dg", dgw), ("du", duw)):
+            d = np.abs(got[name][r].double().numpy() - want)
+            worst[name] = max(worst.get(name, 0.0), float((d / (atol + rtol * np.abs(want))).max()))
+            worst_abs6[name] = max(worst_abs6.get(name, 0.0), float((d / (1e-6 + rtol * np.abs(want))).max()))
+    for name in worst:
+        print(f"  {name:4s} worst |d|/(atol+rtol|ref|) = {worst[name]:.3f} (with atol 1e-6: {worst_abs6[name]:.3f})",
+              flush=True)
+    assert all(w <= 1.0 for w in worst.values()), worst
     with torch.no_grad():
         h1 = affine_scan(gg[:, :4000].detach(), uu[:, :4000].detach())
         h2 = affine_scan(gg[:, 4000:].detach(), uu[:, 4000:].detach(), h1[:, -1].float())
-        torch.testing.assert_close(torch.cat([h1, h2], 1).float(), h.detach().float(),
-                                   rtol=tol["rtol"], atol=tol["atol"])
+        # bf16: the second half starts from the bf16-rounded state h1[:, -1].
+        chain_atol = atol if dtype == torch.float32 else 1e-2
+        torch.testing.assert_close(torch.cat([h1, h2], 1).float(), h.detach().float(), rtol=rtol, atol=chain_atol)
 
 
 # ------------------------------------------------------- one-token decode kernels
@@ -663,10 +722,10 @@ def test_fused_sensors_match_float64_autograd(cuda, shape, decode_from_prior, ob
     assert (out[1] is None) == (not with_var)
     for name, got, want in zip(("y", "y_var", "lam", "eta"), out, ref):
         if got is not None:
-            check(name, got, want.detach().numpy())
+            check_scan(name, got, want.detach().numpy())
     loss(*out).backward()
     for name, got, want in zip(("proj", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
-        check("d" + name, got.grad, want.grad.numpy())
+        check_scan("d" + name, got.grad, want.grad.numpy())
     assert not gs[0].grad[..., M].any() and not gs[0].grad[..., 2 * M + 1:].any()
 
 

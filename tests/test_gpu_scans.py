@@ -4,10 +4,9 @@ Every case draws its inputs on the CPU (torch.Generator), runs the HIP kernels
 through the public ops (:func:`kla.ops.hip.mobius_scan`, :func:`affine_scan`)
 and compares with oracle.scans in float64 at the path's tolerance:
 rtol 1e-5, atol 1e-6 for fp32 (outputs, final states and every gradient), and
-rtol 2e-2 for bf16 I/O. Shapes cover a single step, ragged lane tiles (lanes not
+rtol 2e-2 (atol 1e-5) for bf16 I/O. Shapes cover a single step, ragged lane tiles (lanes not
 a multiple of 64), ragged chunks (steps not a multiple of the 64-step chunk),
-long sequences (many look-back hops) and the full headline shape (checked on a
-subset of lanes, plus whole-tensor properties).
+long sequences (many look-back hops) and the full headline shape (every element).
 """
 
 import sys
@@ -144,7 +143,8 @@ def test_affine_fwd_bwd_matches_oracle(cuda, shape, with_h0):
 @pytest.mark.parametrize("shape", [(2, 65, 63), (2, 1000, 130), (1, 4096, 64)])
 def test_affine_bf16_io(cuda, shape):
     """bf16 sequence I/O, fp32 accumulation: within rtol 2e-2 of the fp64 oracle run
-    on the same (bf16-exact) inputs; outputs come back in bf16."""
+    on the same (bf16-exact) inputs (atol 1e-5 for values that cancel to near
+    zero); outputs come back in bf16."""
     from kla.ops.hip import affine_scan
 
     B, T, N = shape
@@ -155,10 +155,10 @@ def test_affine_bf16_io(cuda, shape):
     torch.autograd.backward(h, dh.to(cuda))
     assert gg.grad.dtype == torch.bfloat16 and uu.grad.dtype == torch.bfloat16
     want = ref.affine_scan_fwd(g.float(), u.float())
-    _close("h", h, want, rtol=2e-2, atol=1e-2)
+    _close("h", h, want, rtol=2e-2, atol=1e-5)
     dg, du, _ = ref.affine_scan_bwd(dh.float(), g.float(), want)
-    _close("dg", gg.grad, dg, rtol=2e-2, atol=1e-2)
-    _close("du", uu.grad, du, rtol=2e-2, atol=1e-2)
+    _close("dg", gg.grad, dg, rtol=2e-2, atol=1e-5)
+    _close("du", uu.grad, du, rtol=2e-2, atol=1e-5)
 
 
 @pytest.mark.parametrize("lanes", [64, 130, 2048])
@@ -233,9 +233,11 @@ def test_deterministic_bitwise(cuda):
     assert torch.equal(hs[0], hs[1]) and torch.equal(hs[0], hs[2])
 
 
-def test_headline_shape_subset_of_lanes(cuda):
-    """Full (8, 4096, 2048) run; every lane finite, a spread of lanes (tile edges
-    included) against the fp64 oracle, no look-back wait gave up."""
+def test_headline_shape_whole_tensors(cuda):
+    """Full (8, 4096, 2048) Moebius and affine fwd + bwd: every element of every
+    output and gradient against the float64 oracle at rtol 1e-5 / atol 1e-6 (as the
+    reference's tests/test_backends.py:220-249 compares whole tensors), one batch
+    row at a time to bound host memory; no look-back wait gave up."""
     from kla.ops.hip import _lib, affine_scan, mobius_scan
 
     B, T, N = 8, 4096, 2048
@@ -250,25 +252,36 @@ def test_headline_shape_subset_of_lanes(cuda):
     h.backward(dh.to(cuda))
     torch.cuda.synchronize()
     assert _lib.workspace_failures(cuda) == 0
-    for t in [lam, xs[0].grad, xs[1].grad, xs[2].grad, xs[3].grad, h, gg.grad, uu.grad]:
-        assert torch.isfinite(t).all()
+    got = {name: t.detach().cpu() for name, t in (("lam", lam), ("dA", xs[0].grad), ("dB", xs[1].grad),
+                                                  ("dC", xs[2].grad), ("dlam0", xs[3].grad), ("h", h),
+                                                  ("dg", gg.grad), ("du", uu.grad))}
+    del xs, lam, gg, uu, h
+    worst = {}
 
-    lanes = sorted(set(list(range(0, N, 61)) + [63, 64, 127, 128, 1023, 1024, N - 1]))
-    idx = torch.tensor(lanes)
-    sub = lambda t: t[..., idx]  # noqa: E731
-    _log(f"[headline] oracle on {len(lanes)} lanes")
-    want = ref.mobius_scan_fwd(sub(A), sub(Bm), sub(C), None, sub(lam0))
-    _close("lam", sub(lam.cpu()), want)
-    dA, dBm, dC, _, dl0 = ref.mobius_scan_bwd(sub(dlam), sub(A), sub(Bm), sub(C), None, sub(lam0), want)
-    _close("dA", sub(xs[0].grad.cpu()), dA)
-    _close("dB", sub(xs[1].grad.cpu()), dBm)
-    _close("dC", sub(xs[2].grad.cpu()), dC)
-    _close("dlam0", sub(xs[3].grad.cpu()), dl0)
-    hw = ref.affine_scan_fwd(sub(g), sub(u))
-    _close("h", sub(h.cpu()), hw)
-    dg, du, _ = ref.affine_scan_bwd(sub(dh), sub(g), hw)
-    _close("dg", sub(gg.grad.cpu()), dg)
-    _close("du", sub(uu.grad.cpu()), du)
+    def close(name, got_, want):
+        ratio = np.abs(got_.double().numpy() - want) / (ATOL + RTOL * np.abs(want))
+        assert np.isfinite(got_.numpy()).all(), name
+        worst[name] = max(worst.get(name, 0.0), float(ratio.max()))
+
+    for b in range(B):
+        _log(f"[headline] oracle, batch row {b}")
+        r = slice(b, b + 1)
+        want = ref.mobius_scan_fwd(A[r], Bm[r], C[r], None, lam0[r])
+        close("lam", got["lam"][r], want)
+        dA, dBm, dC, _, dl0 = ref.mobius_scan_bwd(dlam[r], A[r], Bm[r], C[r], None, lam0[r], want)
+        close("dA", got["dA"][r], dA)
+        close("dB", got["dB"][r], dBm)
+        close("dC", got["dC"][r], dC)
+        close("dlam0", got["dlam0"][r], dl0)
+        del want, dA, dBm, dC
+        hw = ref.affine_scan_fwd(g[r], u[r])
+        close("h", got["h"][r], hw)
+        dgw, duw, _ = ref.affine_scan_bwd(dh[r], g[r], hw)
+        close("dg", got["dg"][r], dgw)
+        close("du", got["du"][r], duw)
+    for name, w in worst.items():
+        print(f"  {name:8s} worst |d|/(atol+rtol|ref|) = {w:.3f}", flush=True)
+    assert all(w <= 1.0 for w in worst.values()), worst
 
 
 def test_scans_past_2_31_elements(cuda):
@@ -329,7 +342,7 @@ def test_scans_past_2_31_elements(cuda):
     torch.cuda.empty_cache()
     _log("[2^31] affine oracle")
     hw = ref.affine_scan_fwd(sg, su)
-    _close("h", got[0], hw, rtol=2e-2, atol=1e-2)
+    _close("h", got[0], hw, rtol=2e-2, atol=1e-5)
     dgw, duw, _ = ref.affine_scan_bwd(sdh, sg, hw)
-    _close("dg", got[1], dgw, rtol=2e-2, atol=1e-2)
-    _close("du", got[2], duw, rtol=2e-2, atol=1e-2)
+    _close("dg", got[1], dgw, rtol=2e-2, atol=1e-5)
+    _close("du", got[2], duw, rtol=2e-2, atol=1e-5)

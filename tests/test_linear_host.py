@@ -43,3 +43,19 @@ def test_projections_fall_back_to_torch_on_cpu():
     assert lin._bf16_operands(torch.nn.Linear(8, 12), x) is None   # a bias
     with torch.no_grad():
         assert lin._bf16_operands(mod, x) is None
+
+
+def test_split_backward_with_an_empty_piece_and_no_input_gradient(monkeypatch):
+    """The mamba preset (value_rank='conv') splits sensor_proj as [0, rank, S, S]:
+    without an input gradient each piece's gradient forms its own rows of dw, and
+    the empty piece has none (reference src/kla/layers/kla_layer.py:206)."""
+    monkeypatch.setattr(lin, "_cus", lambda index: 256)
+    x = torch.randn(2, 5, 6)
+    w = torch.randn(16, 6, requires_grad=True)
+    sizes = [0, 8, 4, 4]
+    pieces = lin._SplitLinear.apply(x, w, sizes)
+    assert [p.shape[-1] for p in pieces] == sizes
+    gs = [torch.randn(2, 5, s) for s in sizes]
+    torch.autograd.backward([pieces[1], pieces[2], pieces[3]], [gs[1], gs[2], gs[3]])
+    want = torch.cat(gs, -1).reshape(-1, 16).t() @ x.reshape(-1, 6)
+    torch.testing.assert_close(w.grad, want)
