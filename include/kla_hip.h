@@ -87,6 +87,23 @@ int kla_mobius_scan_fwd(const float *A, const float *B, const float *C, const fl
                         hipStream_t stream);
 
 /*
+ * kla_mobius_scan_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. The look-back
+ * records live in a static 32 MiB device array (one per GPU, held until the
+ * process ends), which fits the scan up to (8, 4096, 2048); a larger call
+ * returns KLA_ERR_WORKSPACE and launches nothing. The first call on a device
+ * looks the array up and zero-fills it on `stream` (so make that first call
+ * outside a graph capture); the call itself allocates nothing. Every call on
+ * one GPU shares that GPU's array: calls that overlap in time on one GPU race
+ * (their results are undefined; the bounded look-back waits still end).
+ * Results are bit-identical to kla_mobius_scan_fwd's.
+ */
+int kla_mobius_scan_fwd_noalloc(const float *A, const float *B, const float *C, const float *D,
+                                const float *lam0, float *lam, int64_t batch, int64_t steps,
+                                int64_t lanes, hipStream_t stream);
+
+/*
  * Moebius scan, exact scalar-adjoint backward.
  *   den_t = max(C_t*l_{t-1} + D_t, 1e-12), gain_t = (A_t*D_t - B_t*C_t) / den_t^2
  *   nu_t = dlam_t + gain_{t+1}*nu_{t+1}          (reverse scan, nu_T = 0)

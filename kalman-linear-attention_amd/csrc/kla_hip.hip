@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <initializer_list>
+#include <mutex>
 #include <type_traits>
 
 #pragma GCC visibility push(default)
@@ -27,7 +28,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 12;
+constexpr int kAbiVersion = 13;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -487,6 +488,75 @@ bool tail_wide(int64_t M, int64_t ld_res, int64_t ld_gate, std::initializer_list
   return true;
 }
 
+// Moebius forward after argument checks: `get_ws(&ws, &bytes)` supplies the
+// look-back workspace once the call is known to be valid (so an invalid call
+// touches nothing, not even a first-use scratch set-up).
+template <class GetWs>
+int mobius_fwd(const char *fn, const float *A, const float *B, const float *C, const float *D, const float *lam0,
+               float *lam, int64_t batch, int64_t steps, int64_t lanes, hipStream_t stream, GetWs &&get_ws) {
+  const Shape s{batch, steps, lanes};
+  int rc = check_shape(fn, s);
+  if (rc != KLA_OK) return rc;
+  if (empty(s)) return KLA_OK;
+  if (!A || !B || !C || !lam) return fail(KLA_ERR_INVALID_ARG, "%s: A, B, C and lam must not be NULL", fn);
+  if (misaligned(A) || misaligned(B) || misaligned(C) || misaligned(D) || misaligned(lam0) ||
+      misaligned(lam))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  void *workspace = nullptr;
+  size_t workspace_bytes = 0;
+  if ((rc = get_ws(&workspace, &workspace_bytes)) != KLA_OK) return rc;
+  rc = check_launch(fn, KLA_SCAN_MOBIUS_FWD, s, workspace, workspace_bytes);
+  if (rc != KLA_OK) return rc;
+  const int64_t from = cached_tail_from(s, D ? 4 : 3);
+  if (D) {
+    using P = MobiusFwd<true>;
+    return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, D, lam0, lam, from}, s, workspace, stream);
+  }
+  using P = MobiusFwd<false>;
+  return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, nullptr, lam0, lam, from}, s, workspace, stream);
+}
+
+// ------------------------------------------------ allocation-free workspace
+//
+// kla_mobius_scan_fwd_noalloc keeps its look-back records in `scratch`, a
+// file-scope device array: every GPU the library runs on holds its own copy
+// until the process ends, and the entry point allocates nothing. On the host
+// the array's name is only a stand-in for the device symbol (a kernel given
+// it would fault), so host code uses the address hipGetSymbolAddress returns,
+// looked up once per device with that device current. All calls on one GPU
+// share that GPU's array: calls that overlap in time on one GPU race.
+constexpr size_t kScratchBytes = 32ull << 20;
+static __device__ __align__(256) uint64_t scratch[kScratchBytes / sizeof(uint64_t)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_addr[kMaxDevices] = {};
+
+// The current device's scratch address. The first call on a device looks the
+// symbol up and zero-fills the array on `stream` (the look-back records' start
+// state; the kernels keep it consistent from launch to launch afterwards).
+int scratch_address(const char *fn, hipStream_t stream, void **out) {
+  int dev = -1;
+  int rc = hip_status(fn, hipGetDevice(&dev));
+  if (rc != KLA_OK) return rc;
+  if (dev < 0 || dev >= kMaxDevices) return fail(KLA_ERR_INVALID_ARG, "%s: device %d beyond %d", fn, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void *p = nullptr;
+    rc = hip_status(fn, hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (rc != KLA_OK) return rc;
+    if (p == nullptr || misaligned_bytes(p, 256)) return fail(KLA_ERR_HIP, "%s: bad scratch address", fn);
+    const int64_t count = static_cast<int64_t>(kScratchBytes / sizeof(float));
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(static_cast<uint32_t>((count + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<float *>(p), count);
+    rc = hip_status(fn, hipGetLastError());
+    if (rc != KLA_OK) return rc;
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return KLA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -520,24 +590,26 @@ int kla_mobius_scan_fwd(const float *A, const float *B, const float *C, const fl
                         const float *lam0, float *lam, int64_t batch, int64_t steps,
                         int64_t lanes, void *workspace, size_t workspace_bytes,
                         hipStream_t stream) {
-  const char *fn = "kla_mobius_scan_fwd";
-  const Shape s{batch, steps, lanes};
-  int rc = check_shape(fn, s);
-  if (rc != KLA_OK) return rc;
-  if (empty(s)) return KLA_OK;
-  if (!A || !B || !C || !lam) return fail(KLA_ERR_INVALID_ARG, "%s: A, B, C and lam must not be NULL", fn);
-  if (misaligned(A) || misaligned(B) || misaligned(C) || misaligned(D) || misaligned(lam0) ||
-      misaligned(lam))
-    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
-  rc = check_launch(fn, KLA_SCAN_MOBIUS_FWD, s, workspace, workspace_bytes);
-  if (rc != KLA_OK) return rc;
-  const int64_t from = cached_tail_from(s, D ? 4 : 3);
-  if (D) {
-    using P = MobiusFwd<true>;
-    return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, D, lam0, lam, from}, s, workspace, stream);
-  }
-  using P = MobiusFwd<false>;
-  return launch<P, MobiusFwdTile>(fn, P::Params{A, B, C, nullptr, lam0, lam, from}, s, workspace, stream);
+  return mobius_fwd("kla_mobius_scan_fwd", A, B, C, D, lam0, lam, batch, steps, lanes, stream,
+                    [&](void **ws, size_t *bytes) {
+                      *ws = workspace;
+                      *bytes = workspace_bytes;
+                      return KLA_OK;
+                    });
+}
+
+int kla_mobius_scan_fwd_noalloc(const float *A, const float *B, const float *C, const float *D,
+                                const float *lam0, float *lam, int64_t batch, int64_t steps,
+                                int64_t lanes, hipStream_t stream) {
+  const char *fn = "kla_mobius_scan_fwd_noalloc";
+  return mobius_fwd(fn, A, B, C, D, lam0, lam, batch, steps, lanes, stream, [&](void **ws, size_t *bytes) {
+    const size_t need = workspace_bytes_kind(KLA_SCAN_MOBIUS_FWD, Shape{batch, steps, lanes});
+    if (need > kScratchBytes)
+      return fail(KLA_ERR_WORKSPACE, "%s: the look-back needs %zu bytes, the static scratch holds %zu", fn, need,
+                  kScratchBytes);
+    *bytes = kScratchBytes;
+    return scratch_address(fn, stream, ws);
+  });
 }
 
 int kla_mobius_scan_bwd(const float *dlam, const float *A, const float *B, const float *C,

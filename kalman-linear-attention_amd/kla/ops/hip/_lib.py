@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
                         "lib", "libkla_hip.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -46,6 +46,7 @@ _SIGNATURES = {
     "kla_scan_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, _i64, _i64, _i64]),
     "kla_workspace_failures": (ctypes.c_int, [_p, _p, ctypes.POINTER(ctypes.c_uint32)]),
     "kla_mobius_scan_fwd": (ctypes.c_int, [_p] * 6 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
+    "kla_mobius_scan_fwd_noalloc": (ctypes.c_int, [_p] * 6 + [_i64] * 3 + [_p]),
     "kla_mobius_scan_bwd": (ctypes.c_int, [_p] * 12 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
     "kla_affine_scan_fwd": (ctypes.c_int, [ctypes.c_int] + [_p] * 4 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
     "kla_affine_scan_bwd": (ctypes.c_int, [ctypes.c_int] + [_p] * 7 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),

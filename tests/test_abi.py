@@ -349,3 +349,20 @@ def test_sum_parts_validation(lib):
     assert lib.kla_sum_parts(_lib.KLA_DTYPE_F32, P + 2, 4, 16, P, None) == _lib.KLA_ERR_ALIGN
     assert lib.kla_sum_parts(_lib.KLA_DTYPE_F32, P, 4, 16, P + 2, None) == _lib.KLA_ERR_ALIGN
     assert lib.kla_sum_parts(_lib.KLA_DTYPE_F32, None, 4, 0, None, None) == _lib.KLA_OK
+
+
+def test_mobius_fwd_noalloc_validation(lib):
+    """The allocation-free Moebius forward checks its arguments like
+    kla_mobius_scan_fwd and refuses problems whose look-back records exceed its
+    static 32 MiB scratch, all before touching the GPU."""
+    f = lib.kla_mobius_scan_fwd_noalloc
+    assert f(ALIGNED, ALIGNED, ALIGNED, None, None, ALIGNED, 0, 5, 4, None) == _lib.KLA_OK
+    assert f(None, ALIGNED, ALIGNED, None, None, ALIGNED, 2, 3, 4, None) == _lib.KLA_ERR_INVALID_ARG
+    assert "kla_mobius_scan_fwd_noalloc" in err(lib) and "must not be NULL" in err(lib)
+    assert f(ODD, ALIGNED, ALIGNED, None, None, ALIGNED, 2, 3, 4, None) == _lib.KLA_ERR_ALIGN
+    assert f(ALIGNED, ALIGNED, ALIGNED, None, None, ALIGNED, -1, 3, 4, None) == _lib.KLA_ERR_INVALID_ARG
+    need = lib.kla_scan_workspace_bytes(_lib.KLA_SCAN_MOBIUS_FWD, 16, 4096, 2048)
+    assert need > 32 << 20
+    assert f(ALIGNED, ALIGNED, ALIGNED, None, None, ALIGNED, 16, 4096, 2048, None) == _lib.KLA_ERR_WORKSPACE
+    assert "static scratch holds 33554432" in err(lib)
+    assert lib.kla_scan_workspace_bytes(_lib.KLA_SCAN_MOBIUS_FWD, 8, 4096, 2048) <= 32 << 20
