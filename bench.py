@@ -24,6 +24,9 @@ autocast, loss = mean(out^2); c5 is SequenceModel(vocab 50304, d_model 512,
 6 layers) stateful prefill of (16, 2048) random ids, then 256 one-token decode
 steps (prefill tokens/s and decode ms/token).
 
+``--layer scan --shape B,L,M,S`` times kla_scan alone (fwd + bwd) on ``--backend``
+(the d_state > 64 fused kernels against the composed path).
+
 ``--workload affine_b8_t8192_l2048[_bf16]`` is BASELINE config 3: the standalone
 affine scan alone, fp32 or bf16 I/O.
 
@@ -267,6 +270,34 @@ def _timed(fn, steps, warmup, stream):
     return start.elapsed_time(end) / steps
 
 
+def bench_scan(args, device, stream) -> dict:
+    """The KLA scan alone (kla_scan fwd + bwd: y, y_var, every input gradient) at
+    ``--shape B,L,M,S`` on the chosen backend: the d_state > 64 case of the fused
+    kernels (hip_fused) against the composed path (hip_composed)."""
+    from kla.ops import kla_scan
+
+    B, L, M, S = (int(x) for x in args.shape.split(","))
+    g = torch.Generator().manual_seed(0)
+    ins = [torch.randn(B, L, M, generator=g), torch.rand(B, L, M, generator=g) + 0.5,
+           torch.randn(B, L, S, generator=g) * 0.3, torch.randn(B, L, S, generator=g) * 0.3,
+           torch.rand(M, S, generator=g) * 0.5 + 0.45, torch.rand(M, S, generator=g) * 0.05 + 0.01]
+    dy, dyv = torch.randn(B, L, M, generator=g).to(device), torch.randn(B, L, M, generator=g).to(device)
+    xs = [t.to(device).requires_grad_(True) for t in ins]
+
+    def step():
+        y, y_var, _ = kla_scan(*xs, backend=args.backend)
+        torch.autograd.backward((y, y_var), (dy, dyv))
+        for x in xs:
+            x.grad = None
+
+    ms = _timed(step, args.steps, args.warmup, stream)
+    return {"metric": f"kla_scan fwd+bwd tokens/s, (B, L, M, S) = ({B}, {L}, {M}, {S}), fp32",
+            "value": B * L / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": round(ms, 4),
+            "lane_steps_per_s": B * L * M * S / (ms * 1e-3), "backend": args.backend,
+            "steps": args.steps, "warmup": args.warmup,
+            "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
+
+
 def bench_layer(args, device, stream) -> dict:
     """Layer-level BASELINE configs c1 / c4 / c5 on the chosen kla backend."""
     from kla import KLAConfig, KLALayer, ModelConfig, SequenceModel
@@ -359,8 +390,10 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default=None,
                     choices=["mobius_fwd", "mobius_bwd", "affine_fwd", "affine_bwd", "copy", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--layer", default=None, choices=["c1", "c4", "c5"],
-                    help="measure a layer-level config instead of the headline scan step")
+    ap.add_argument("--layer", default=None, choices=["c1", "c4", "c5", "scan"],
+                    help="measure a layer-level config instead of the headline scan step "
+                         "(scan: kla_scan alone at --shape)")
+    ap.add_argument("--shape", default="2,2048,512,128", help="B,L,M,S for --layer scan")
     ap.add_argument("--backend", default="hip", help="kla backend for --layer (hip, hip_composed, torch)")
     args = ap.parse_args(argv)
 
@@ -374,6 +407,9 @@ def main(argv=None) -> int:
 
     device = torch.device("cuda", 0)
     stream = torch.cuda.current_stream(device)
+    if args.layer == "scan":
+        print(json.dumps(bench_scan(args, device, stream)), flush=True)
+        return 0
     if args.layer:
         print(json.dumps(bench_layer(args, device, stream)), flush=True)
         return 0

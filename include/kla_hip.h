@@ -150,7 +150,7 @@ int kla_affine_scan_bwd(int dtype, const void *dh, const void *g, const void *h,
  * Fused KLA scan: the whole filter of kla_scan_torch in one kernel per direction.
  * Shapes (reference kla_ops.py:23-28): v, lambda_v, y, y_var [batch, steps, M];
  * k, q [batch, steps, S]; a, p [M, S]; lam0, eta0, lam_fin, eta_fin [batch, M, S];
- * all fp32, dense. S <= 64. lam0 / eta0 may be NULL (precision 1, information 0).
+ * all fp32, dense. S <= 256. lam0 / eta0 may be NULL (precision 1, information 0).
  *   phi = lambda_v k^2, r = (v lambda_v) k, a2 = max(a^2, 1e-12), p' = max(p, 1e-12)
  *   lam_t = (A lam_{t-1} + phi) / (C lam_{t-1} + 1), A = (1 + p' phi)/a2, C = p'/a2
  *   eta_t = a / max(a2 + p' lam_{t-1}, 1e-12) * eta_{t-1} + r

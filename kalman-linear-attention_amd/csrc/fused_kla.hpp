@@ -17,9 +17,11 @@
 //
 // Layout. One thread owns one (b, m, s) lane chain and walks time serially; a
 // 256-thread workgroup holds CH = 256/SP channels of SP (= S rounded up to a
-// power of two, at least 4) state lanes, so the SP lanes of a channel are
-// consecutive and the read-out sum over s is a DPP row reduction (SP <= 16)
-// plus cross-row shuffles (SP = 32, 64). Inputs and outputs move through LDS
+// power of two, at least 4, at most 256) state lanes, so the SP lanes of a
+// channel are consecutive and the read-out sum over s is a DPP row reduction
+// (SP <= 16) plus cross-row shuffles (SP = 32, 64). A channel of SP = 128 or
+// 256 lanes spans SP/64 waves: each wave sums its 64 lanes and the waves'
+// partial sums are added in wave order when the block's outputs are written. Inputs and outputs move through LDS
 // in double-buffered blocks of time steps (see "block staging"). Padding lanes (s >= S, m >= M) carry q = 0, k = 0 and
 // take part in every reduction without contributing to it. With 2^17 and more
 // chains (batch * M * S) the lane-serial walk fills the machine; time is not
@@ -103,6 +105,40 @@ __device__ __forceinline__ float group_sum(float x) {
   if constexpr (SP >= 32) x += __shfl_xor(x, 16);
   if constexpr (SP >= 64) x += __shfl_xor(x, 32);
   return x;
+}
+
+// Waves a channel's SP lanes span, and the lanes of a channel within one wave.
+template <int SP>
+constexpr int waves_per_channel() {
+  return SP > kWave ? SP / kWave : 1;
+}
+template <int SP>
+constexpr int lanes_in_wave() {
+  return SP > kWave ? kWave : SP;
+}
+
+// Sum over a channel's SP lanes (every lane of the channel gets it) for SP up
+// to the workgroup size: the in-wave group sum, then for SP > 64 the channel's
+// wave sums added in wave order through LDS. Every thread of the workgroup
+// must make the call.
+template <int SP>
+__device__ __forceinline__ float channel_sum(float x) {
+  if constexpr (SP <= kWave) {
+    return group_sum<SP>(x);
+  } else {
+    constexpr int WPC = SP / kWave;
+    __shared__ float part[kFusedThreads / kWave];
+    x = group_sum<kWave>(x);
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    __syncthreads();   // every reader of the previous call is done
+    if (threadIdx.x % kWave == 0) part[wave] = x;
+    __syncthreads();
+    const int w0 = wave - wave % WPC;
+    float t = part[w0];
+#pragma unroll
+    for (int i = 1; i < WPC; ++i) t += part[w0 + i];
+    return t;
+  }
 }
 
 // x of this lane plus x of the same lane position in the paired row (rows
@@ -313,6 +349,25 @@ __device__ __forceinline__ void lds_to_global(const float (*lds)[TB + kPad], flo
   }
 }
 
+// The same for P partial tiles [P][W][TB + 4] added in order p = 0, 1, ...
+// (the per-wave sums of a channel that spans P waves; P = 1 is lds_to_global).
+template <int TB, int W, int P>
+__device__ __forceinline__ void parts_to_global(const float (*lds)[W][TB + kPad], float *__restrict__ base,
+                                                int64_t ld, int64_t rows, int64_t cols) {
+  const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+  for (int i = 0; i < TileRegs<TB, W>::N; ++i) {
+    const int e = tid + i * kFusedThreads;
+    const int t = e / W, c = e % W;
+    if (e < TB * W && t < rows && c < cols) {
+      float x = lds[0][c][t];
+#pragma unroll
+      for (int p = 1; p < P; ++p) x += lds[p][c][t];
+      __builtin_nontemporal_store(x, base + t * ld + c);
+    }
+  }
+}
+
 // ================================================================ forward
 
 // torch's softplus (threshold 20), for the one-token decode step.
@@ -388,12 +443,19 @@ __device__ __forceinline__ const void *sensor_at(const void *base, int64_t row, 
 // sum = P and pv = NULL for dv (scaled by lam), or with sum = Q and pv = P for
 // d Lambda; with F, d Lambda is then carried to log sigma^2 (times lam^2 f).
 // LDS [W][TB + 4] -> dense rows of a tensor of the sensor dtype.
-template <int TB, int W, bool BF16, bool F>
-__device__ __forceinline__ void lds_to_global_sensor(const float (*sum)[TB + kPad], const float (*lam)[TB + kPad],
+// The sums come as P partial tiles (a channel spanning P waves), added in order.
+template <int TB, int W, int P, bool BF16, bool F>
+__device__ __forceinline__ void lds_to_global_sensor(const float (*sum)[W][TB + kPad], const float (*lam)[TB + kPad],
                                                      const float (*v)[TB + kPad], const float (*f)[TB + kPad],
                                                      void *base, int64_t ld, int64_t rows, int64_t cols,
-                                                     const float (*pv)[TB + kPad] = nullptr) {
+                                                     const float (*pv)[W][TB + kPad] = nullptr) {
   const int tid = static_cast<int>(threadIdx.x);
+  auto total = [&](const float (*x)[W][TB + kPad], int c, int t) {
+    float a = x[0][c][t];
+#pragma unroll
+    for (int p = 1; p < P; ++p) a += x[p][c][t];
+    return a;
+  };
 #pragma unroll
   for (int i = 0; i < (TB * W + kFusedThreads - 1) / kFusedThreads; ++i) {
     const int e = tid + i * kFusedThreads;
@@ -401,9 +463,9 @@ __device__ __forceinline__ void lds_to_global_sensor(const float (*sum)[TB + kPa
     if (e < TB * W && t < rows && c < cols) {
       float d;
       if (pv) {
-        d = sum[c][t] + v[c][t] * pv[c][t];
+        d = total(sum, c, t) + v[c][t] * total(pv, c, t);
       } else {
-        d = lam[c][t] * sum[c][t];
+        d = lam[c][t] * total(sum, c, t);
       }
       if constexpr (F) {
         const float l = lam[c][t];
@@ -432,10 +494,13 @@ __device__ __forceinline__ void to_precision(TileRegs<TB, W> &r, const SensorIn 
 template <int SP, bool PRIOR, bool BF16, bool VAR>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
-  constexpr int TB = kFusedTB;
+  constexpr int WPC = waves_per_channel<SP>();
+  constexpr int SG = lanes_in_wave<SP>();
+  // Wide channels stage shorter blocks: the [SP, TB] k and q tiles fill the LDS.
+  constexpr int TB = SP >= 128 ? kCkpt : kFusedTB;
   __shared__ __align__(16) float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
   __shared__ __align__(16) float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
-  __shared__ float s_y[2][CH][TB + kPad], s_yv[2][CH][TB + kPad];
+  __shared__ float s_y[2][WPC][CH][TB + kPad], s_yv[2][WPC][CH][TB + kPad];
 
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
@@ -495,8 +560,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
     const int64_t t0 = blk * TB;
     if (blk + 1 < nblk) load(t0 + TB);
     if (blk > 0) {
-      lds_to_global<TB, CH>(s_y[cur ^ 1], ybase + (t0 - TB) * M, M, TB, cols_m);
-      if constexpr (VAR) lds_to_global<TB, CH>(s_yv[cur ^ 1], yvbase + (t0 - TB) * M, M, TB, cols_m);
+      parts_to_global<TB, CH, WPC>(s_y[cur ^ 1], ybase + (t0 - TB) * M, M, TB, cols_m);
+      if constexpr (VAR) parts_to_global<TB, CH, WPC>(s_yv[cur ^ 1], yvbase + (t0 - TB) * M, M, TB, cols_m);
     }
     // The read-out terms of a kCkpt-step half of the block, summed over s after
     // the half (transpose_sum) when a channel's lanes fit one 16-lane row.
@@ -523,11 +588,11 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
         yw[jj] = qq * mean;
         if constexpr (VAR) vw[jj] = (qq * qq) * vo;
       } else {
-        const float ys = group_sum<SP>(qq * mean);
-        if (ln.s == 0) s_y[cur][c][j] = ys;
+        const float ys = group_sum<SG>(qq * mean);
+        if (ln.s % SG == 0) s_y[cur][ln.s / SG][c][j] = ys;
         if constexpr (VAR) {
-          const float vs = group_sum<SP>((qq * qq) * vo);
-          if (ln.s == 0) s_yv[cur][c][j] = vs;
+          const float vs = group_sum<SG>((qq * qq) * vo);
+          if (ln.s % SG == 0) s_yv[cur][ln.s / SG][c][j] = vs;
         }
       }
     };
@@ -573,8 +638,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
           if constexpr (VAR) transpose_sum<SP, kCkpt>(vw, lane);
 #pragma unroll
           for (int r = 0; r < kCkpt / SP; ++r) {
-            s_y[cur][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = yw[r];
-            if constexpr (VAR) s_yv[cur][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = vw[r];
+            s_y[cur][0][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = yw[r];
+            if constexpr (VAR) s_yv[cur][0][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = vw[r];
           }
         }
       }
@@ -585,8 +650,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
   if (nblk > 0) {
     const int last = static_cast<int>((nblk - 1) & 1);
     const int64_t t0 = (nblk - 1) * TB;
-    lds_to_global<TB, CH>(s_y[last], ybase + t0 * M, M, L - t0, cols_m);
-    if constexpr (VAR) lds_to_global<TB, CH>(s_yv[last], yvbase + t0 * M, M, L - t0, cols_m);
+    parts_to_global<TB, CH, WPC>(s_y[last], ybase + t0 * M, M, L - t0, cols_m);
+    if constexpr (VAR) parts_to_global<TB, CH, WPC>(s_yv[last], yvbase + t0 * M, M, L - t0, cols_m);
   }
   if (ln.active) {
     prm.lam_fin[bms] = lam;
@@ -602,13 +667,15 @@ template <int SP, bool PRIOR, bool BF16, bool VAR>
 __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int NW = kFusedThreads / kWave;
+  constexpr int WPC = waves_per_channel<SP>();
+  constexpr int SG = lanes_in_wave<SP>();
   constexpr int TB = kCkpt;
   __shared__ __align__(16) float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
   __shared__ __align__(16) float s_dy[2][CH][TB + kPad], s_dyv[2][CH][TB + kPad];
   __shared__ __align__(16) float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
-  __shared__ float s_dv[2][CH][TB + kPad], s_dl[2][CH][TB + kPad];
+  __shared__ float s_dv[2][WPC][CH][TB + kPad], s_dl[2][WPC][CH][TB + kPad];
   __shared__ float s_lf[2][CH][TB + kPad];   // log sigma^2 gradient factors (log_var sensors)
-  __shared__ float s_red[2][2][TB][NW][SP];
+  __shared__ float s_red[2][2][TB][NW / WPC][SP];   // per-(step, s) sums of a channel slot
 
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
@@ -667,13 +734,13 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     constexpr int64_t el = BF16 ? 2 : 4;
     void *dvb = static_cast<char *>(prm.dv) + (offM + t0 * M) * el;
     void *dlb = static_cast<char *>(prm.dlv) + (offM + t0 * M) * el;
-    lds_to_global_sensor<TB, CH, BF16, false>(s_dv[buf], s_l[buf], s_v[buf], nullptr, dvb, M, L - t0, cols_m);
+    lds_to_global_sensor<TB, CH, WPC, BF16, false>(s_dv[buf], s_l[buf], s_v[buf], nullptr, dvb, M, L - t0, cols_m);
     if (sn.log_var)
-      lds_to_global_sensor<TB, CH, BF16, true>(s_dl[buf], s_l[buf], s_v[buf], s_lf[buf], dlb, M, L - t0, cols_m,
-                                               s_dv[buf]);
+      lds_to_global_sensor<TB, CH, WPC, BF16, true>(s_dl[buf], s_l[buf], s_v[buf], s_lf[buf], dlb, M, L - t0,
+                                                    cols_m, s_dv[buf]);
     else
-      lds_to_global_sensor<TB, CH, BF16, false>(s_dl[buf], nullptr, s_v[buf], nullptr, dlb, M, L - t0, cols_m,
-                                                s_dv[buf]);
+      lds_to_global_sensor<TB, CH, WPC, BF16, false>(s_dl[buf], nullptr, s_v[buf], nullptr, dlb, M, L - t0, cols_m,
+                                                     s_dv[buf]);
     for (int i = tid; i < 2 * TB * SP; i += kFusedThreads) {
       const int which = i / (TB * SP);
       const int j = (i / SP) % TB;
@@ -682,7 +749,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       if (t < L && s < S) {
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) sum += s_red[buf][which][j][w][s];
+        for (int w = 0; w < NW / WPC; ++w) sum += s_red[buf][which][j][w][s];
         float *part = which == 0 ? prm.part_k : prm.part_q;
         part[((ln.b * L + t) * g.groups + grp) * S + s] = sum;
       }
@@ -844,11 +911,11 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
           dv_w[j] = pk;
           dl_w[j] = qk;
         } else {
-          const float dv_s = group_sum<SP>(pk);
-          const float dl_s = group_sum<SP>(qk);
-          if (ln.s == 0) {
-            s_dv[cur][c][j] = dv_s;
-            s_dl[cur][c][j] = dl_s;
+          const float dv_s = group_sum<SG>(pk);
+          const float dl_s = group_sum<SG>(qk);
+          if (ln.s % SG == 0) {
+            s_dv[cur][ln.s / SG][c][j] = dv_s;
+            s_dl[cur][ln.s / SG][c][j] = dl_s;
           }
         }
       }
@@ -858,11 +925,13 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         dk_w[j] = dk_c;
         dq_w[j] = dq_c;
       } else {
+        // (For SP >= 64 a wave holds one channel's lanes or part of them:
+        // nothing to add within the wave, and every lane stores its s.)
         dk_c = cross_group_sum<SP>(dk_c);
         dq_c = cross_group_sum<SP>(dq_c);
-        if (lane < SP) {
-          s_red[cur][0][j][wave][lane] = dk_c;
-          s_red[cur][1][j][wave][lane] = dq_c;
+        if (SP >= kWave || lane < SP) {
+          s_red[cur][0][j][wave / WPC][ln.s] = dk_c;
+          s_red[cur][1][j][wave / WPC][ln.s] = dq_c;
         }
       }
     }
@@ -882,8 +951,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       transpose_sum<SP, TB>(dl_w, lane);
 #pragma unroll
       for (int r = 0; r < TB / SP; ++r) {
-        s_dv[cur][c][(TB / SP) * ln.s + r] = dv_w[r];
-        s_dl[cur][c][(TB / SP) * ln.s + r] = dl_w[r];
+        s_dv[cur][0][c][(TB / SP) * ln.s + r] = dv_w[r];
+        s_dl[cur][0][c][(TB / SP) * ln.s + r] = dl_w[r];
       }
     }
     acc_a += blk_a;
@@ -1051,8 +1120,8 @@ __global__ void __launch_bounds__(kFusedThreads) kla_step_kernel(StepParams prm,
     mean = a_s * mean;
     vo = a2 * var + pp;
   }
-  const float ys = group_sum<SP>(mean * qq);
-  const float vs = group_sum<SP>(vo * (qq * qq));
+  const float ys = channel_sum<SP>(mean * qq);
+  const float vs = channel_sum<SP>(vo * (qq * qq));
   if (ln.s == 0 && mok) {
     prm.y[ln.b * M + ln.m] = ys;
     prm.yvar[ln.b * M + ln.m] = vs;
@@ -1145,8 +1214,8 @@ __global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodePa
     float kk = sok ? prm.k[b * prm.ld_kq + sl] : 0.0f;
     float qq = sok ? prm.q[b * prm.ld_kq + sl] : 0.0f;
     if (prm.qk_norm) {
-      kk = kk / fmaxf(sqrtf(group_sum<SP>(kk * kk)), 1e-12f);
-      qq = qq / fmaxf(sqrtf(group_sum<SP>(qq * qq)), 1e-12f);
+      kk = kk / fmaxf(sqrtf(channel_sum<SP>(kk * kk)), 1e-12f);
+      qq = qq / fmaxf(sqrtf(channel_sum<SP>(qq * qq)), 1e-12f);
     }
     if (prm.has_clip) {
       kk = fminf(fmaxf(kk, -prm.clip), prm.clip);
@@ -1171,8 +1240,8 @@ __global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodePa
       mean = a_s * mean;
       vo = a2 * var + pp;
     }
-    const float ys = group_sum<SP>(mean * qq);
-    const float vs = group_sum<SP>(vo * (qq * qq));
+    const float ys = channel_sum<SP>(mean * qq);
+    const float vs = channel_sum<SP>(vo * (qq * qq));
     if (sl == 0 && mok) {
       float yo = ys, vo2 = vs;
       if (prm.z) {

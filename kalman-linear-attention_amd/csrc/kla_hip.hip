@@ -216,7 +216,12 @@ int zero_state(const char *fn, float *p, int64_t count, hipStream_t stream) {
 
 // ----------------------------------------------------------- fused scan
 
-// State lanes per channel in the fused kernels: S rounded up to a power of two, at least 4.
+// The fused kernels and the decode steps hold a channel's S state lanes in one
+// 256-thread workgroup.
+constexpr int kMaxFusedState = kFusedThreads;
+
+// State lanes per channel in the fused kernels: S rounded up to a power of two,
+// at least 4 (S <= kMaxFusedState, so at most one 256-thread workgroup).
 int sp_of(int64_t S) {
   int sp = 4;
   while (sp < S) sp *= 2;
@@ -244,21 +249,30 @@ int check_fused_shape(const char *fn, int64_t batch, int64_t steps, int64_t M, i
   if (batch < 0 || steps < 0 || M < 0 || S < 0)
     return fail(KLA_ERR_INVALID_ARG, "%s: negative size (batch=%lld steps=%lld M=%lld S=%lld)", fn,
                 (long long)batch, (long long)steps, (long long)M, (long long)S);
-  if (S > 64) return fail(KLA_ERR_INVALID_ARG, "%s: d_state S=%lld above 64", fn, (long long)S);
+  if (S > kMaxFusedState)
+    return fail(KLA_ERR_INVALID_ARG, "%s: d_state S=%lld above %d", fn, (long long)S, kMaxFusedState);
   if (batch > (1ll << 31) || steps > (1ll << 31) || M > (1ll << 31))
     return fail(KLA_ERR_INVALID_ARG, "%s: dimension above 2^31", fn);
   return KLA_OK;
 }
 
-template <class F>
+// f(std::integral_constant<int, sp_of(S)>) for S validated to at most MAX_SP
+// (kernels that serve at most 64 lanes per channel instantiate no wider copy).
+template <int MAX_SP = kMaxFusedState, class F>
 int with_sp(int64_t S, F &&f) {
   switch (sp_of(S)) {
     case 4: return f(std::integral_constant<int, 4>{});
     case 8: return f(std::integral_constant<int, 8>{});
     case 16: return f(std::integral_constant<int, 16>{});
     case 32: return f(std::integral_constant<int, 32>{});
-    default: return f(std::integral_constant<int, 64>{});
+    case 64: return f(std::integral_constant<int, 64>{});
+    default: break;
   }
+  if constexpr (MAX_SP >= 256) {
+    if (sp_of(S) > 128) return f(std::integral_constant<int, 256>{});
+  }
+  if constexpr (MAX_SP >= 128) return f(std::integral_constant<int, 128>{});
+  return f(std::integral_constant<int, 64>{});
 }
 
 template <class F>
@@ -1456,7 +1470,7 @@ int qk_sensors_launch(const char *fn, bool bwd, int dtype, QkParams &p, hipStrea
     if (misaligned_bytes(p.x[i], el) || misaligned(p.y[i]) || misaligned(p.dy[i]) || misaligned_bytes(p.dx[i], el))
       return fail(KLA_ERR_ALIGN, "%s: operand not aligned to its element size", fn);
   }
-  return with_sp(p.S, [&](auto sp) {
+  return with_sp<64>(p.S, [&](auto sp) {
     constexpr int SP = decltype(sp)::value;
     const int64_t threads = 2 * p.rows * SP;
     if ((threads + 255) / 256 >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: too many rows", fn);

@@ -282,13 +282,14 @@ class KLALayer(nn.Module):
     def _sensors_on_hip(self, z: torch.Tensor) -> bool:
         """Whether the sequence scan runs on the fused hip kernel with the sensor
         read-out inside it: a backend that picks the fused scan ("hip", "hip_fused"
-        or "auto" on a ROCm GPU), d_state <= 64, a ROCm GPU."""
+        or "auto" on a ROCm GPU), d_state <= 256, a ROCm GPU."""
+        from kla.ops.hip.fused import MAX_STATE
         from kla.ops.kla_ops import _resolve_auto, _step_on_hip
 
         backend = self.config.backend
         if backend == "auto":
             backend = _resolve_auto(z)
-        return (backend in ("hip", "hip_fused") and self.d_state <= 64 and z.dtype != torch.float64
+        return (backend in ("hip", "hip_fused") and self.d_state <= MAX_STATE and z.dtype != torch.float64
                 and _step_on_hip(backend, z))
 
     def _tail_on_hip(self, y: torch.Tensor, residual: torch.Tensor, gate: torch.Tensor | None) -> bool:
@@ -310,10 +311,12 @@ class KLALayer(nn.Module):
 
     def _decode_on_hip(self, projected: torch.Tensor) -> bool:
         """Whether a one-token step runs on the MI355X decode kernels: inference
-        (no gradient), fp32 activations on a ROCm GPU, a hip-family backend."""
+        (no gradient), fp32 activations on a ROCm GPU, a hip-family backend,
+        d_state <= 256."""
+        from kla.ops.hip.fused import MAX_STATE
         from kla.ops.kla_ops import _step_on_hip
 
-        return (not torch.is_grad_enabled() and projected.dtype == torch.float32 and self.d_state <= 64
+        return (not torch.is_grad_enabled() and projected.dtype == torch.float32 and self.d_state <= MAX_STATE
                 and _step_on_hip(self.config.backend, projected))
 
     def _conv_on_hip(self, z: torch.Tensor) -> bool:

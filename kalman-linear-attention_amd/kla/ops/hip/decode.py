@@ -60,8 +60,10 @@ def decode_step_hip(v, log_var, k, q, delta, lambda_log, process_noise, lam, eta
     B, M = v.shape
     S = k.shape[1]
     dev = v.device
-    if S > 64:
-        raise NotImplementedError("the hip decode step supports d_state <= 64")
+    from kla.ops.hip.fused import MAX_STATE
+
+    if S > MAX_STATE:
+        raise NotImplementedError(f"the hip decode step supports d_state <= {MAX_STATE}")
     if (residual is None) != (lambda_skip is None):
         raise ValueError("residual and lambda_skip come together")
     y, y_var = torch.empty(B, M, device=dev), torch.empty(B, M, device=dev)

@@ -27,7 +27,8 @@ from kla.ops.hip import _lib
 from kla.ops.hip.scans import _require_device
 
 _F32 = torch.float32
-MAX_STATE = 64
+# d_state the fused kernels take: a channel's S lanes in one 256-thread workgroup.
+MAX_STATE = 256
 
 
 def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:

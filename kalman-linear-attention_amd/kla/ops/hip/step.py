@@ -26,8 +26,10 @@ def _step_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.
                            ("p", p, (M, S)), ("lam", lam, (B, M, S)), ("eta", eta, (B, M, S))):
         if tuple(t.shape) != shape:
             raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {shape}")
-    if S > 64:
-        raise NotImplementedError("the hip decode step supports d_state <= 64")
+    from kla.ops.hip.fused import MAX_STATE
+
+    if S > MAX_STATE:
+        raise NotImplementedError(f"the hip decode step supports d_state <= {MAX_STATE}")
     y, y_var = v.new_empty(B, M), v.new_empty(B, M)
     lam_out, eta_out = torch.empty_like(lam), torch.empty_like(eta)
     if B * M * S == 0:

@@ -1,6 +1,6 @@
 """The ``"hip"`` KLA backend: the KLA scan on MI355X kernels.
 
-Fused path (``kernel="fused"``, the default for d_state <= 64): the whole
+Fused path (``kernel="fused"``, the default for d_state <= 256): the whole
 filter in one kernel per direction (:mod:`kla.ops.hip.fused`); nothing of shape
 [B, L, M, S] is materialised, and the backward is the exact adjoint.
 

@@ -178,8 +178,8 @@ def test_python_errors_carry_the_message():
 def test_fused_and_step_validation(lib):
     p = [ALIGNED] * 14
     shape = (2, 5, 6, 16)
-    assert lib.kla_fused_scan_fwd(*p[:12], None, None, 0, 2, 5, 6, 65, None) == _lib.KLA_ERR_INVALID_ARG
-    assert "above 64" in err(lib)
+    assert lib.kla_fused_scan_fwd(*p[:12], None, None, 0, 2, 5, 6, 257, None) == _lib.KLA_ERR_INVALID_ARG
+    assert "above 256" in err(lib)
     assert lib.kla_fused_scan_fwd(*p[:12], ALIGNED, None, 0, *shape, None) == _lib.KLA_ERR_INVALID_ARG
     assert "both checkpoint buffers" in err(lib)
     assert lib.kla_fused_scan_fwd(None, *p[1:12], None, None, 0, *shape, None) == _lib.KLA_ERR_INVALID_ARG
@@ -194,7 +194,7 @@ def test_fused_and_step_validation(lib):
     assert lib.kla_fused_scan_bwd(*q[:4], None, *q[5:], 0, *shape, WS, n, None) == _lib.KLA_ERR_INVALID_ARG
     assert lib.kla_step_fwd(*[ALIGNED] * 11, None, 0, 2, 6, 16, None) == _lib.KLA_ERR_INVALID_ARG
     assert lib.kla_step_fwd(*[ALIGNED] * 11, ODD, 0, 2, 6, 16, None) == _lib.KLA_ERR_ALIGN
-    assert lib.kla_step_fwd(*[ALIGNED] * 12, 0, 2, 6, 100, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_step_fwd(*[ALIGNED] * 12, 0, 2, 6, 257, None) == _lib.KLA_ERR_INVALID_ARG
 
 
 def test_decode_and_conv_step_validation(lib):
@@ -209,7 +209,7 @@ def test_decode_and_conv_step_validation(lib):
 
     assert dec(c=None) == _lib.KLA_ERR_INVALID_ARG
     assert "cfg must not be NULL" in err(lib)
-    assert dec(shape=(2, 8, 65)) == _lib.KLA_ERR_INVALID_ARG
+    assert dec(shape=(2, 8, 257)) == _lib.KLA_ERR_INVALID_ARG
     assert dec(v=None) == _lib.KLA_ERR_INVALID_ARG
     assert dec(z=P, ld_z=8) == _lib.KLA_ERR_INVALID_ARG
     assert "residual and lambda_skip" in err(lib)
@@ -257,7 +257,7 @@ def test_fused_sensors_validation(lib):
     assert fwd(sensors(v=ODD, dtype=_lib.KLA_DTYPE_F32)) == _lib.KLA_ERR_ALIGN
     assert fwd(sensors(v=None)) == _lib.KLA_ERR_INVALID_ARG
     assert fwd(sensors(), k=ODD) == _lib.KLA_ERR_ALIGN
-    assert fwd(sensors(), shape=(2, 5, 6, 65)) == _lib.KLA_ERR_INVALID_ARG
+    assert fwd(sensors(), shape=(2, 5, 6, 257)) == _lib.KLA_ERR_INVALID_ARG
     assert fwd(sensors(), shape=(0, 5, 6, 16)) == _lib.KLA_OK
 
     n = lib.kla_fused_workspace_bytes(*shape)

@@ -112,7 +112,8 @@ def test_forward_and_state_match_oracle(cuda, backend, decode_from_prior, with_s
 
 @pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("shape", [(1, 1, 3, 2), (3, 257, 5, 16), (2, 1000, 8, 8), (1, 40, 70, 3), (2, 33, 9, 64),
-                                   (1, 17, 300, 1), (2, 64, 3, 40), (2, 50, 7, 24), (1, 45, 20, 12)])
+                                   (1, 17, 300, 1), (2, 64, 3, 40), (2, 50, 7, 24), (1, 45, 20, 12),
+                                   (2, 300, 3, 128), (1, 70, 2, 256), (2, 45, 5, 65)])
 def test_forward_ragged_shapes(cuda, backend, shape):
     B, L, M, S = shape
     ins = make_inputs(B, L, M, S, seed=7)
@@ -142,7 +143,9 @@ def test_chunked_state_carry(cuda, backend):
                                    (2, 150, 20, 16), (1, 260, 6, 4),
                                    # grids that are multiples of the 8 XCDs (the workgroup
                                    # renumbering applies) with a ragged last channel group
-                                   (2, 150, 120, 16), (8, 40, 9, 32)])
+                                   (2, 150, 120, 16), (8, 40, 9, 32),
+                                   # d_state above 64: a channel spans 2 or 4 waves (ragged S too)
+                                   (2, 40, 5, 128), (1, 37, 3, 100), (1, 21, 2, 256), (2, 19, 3, 200)])
 def test_gradients_match_float64_autograd(cuda, backend, decode_from_prior, shape):
     """Every input gradient, the initial-state gradients, and gradients flowing in
     through the returned state, against float64 autograd of the reference's
@@ -320,7 +323,8 @@ def test_sequence_model_prefill_and_decode_on_hip(cuda):
 
 
 @pytest.mark.parametrize("decode_from_prior", [False, True])
-@pytest.mark.parametrize("shape", [(2, 16, 8), (3, 70, 5), (1, 9, 64), (4, 33, 1)])
+@pytest.mark.parametrize("shape", [(2, 16, 8), (3, 70, 5), (1, 9, 64), (4, 33, 1), (2, 5, 128), (3, 4, 256),
+                                   (2, 3, 150)])
 def test_step_kernel_matches_reference_step(cuda, decode_from_prior, shape):
     """kla_step(backend="hip") (one HIP kernel) against the reference's step
     formula evaluated in float64 (kla_ops.py:293-331, phi floored)."""
@@ -488,6 +492,8 @@ DECODE_CASES = {
     "relu_gate_lowrank": (40, dict(d_state=12, gating_activation="relu", conv_activation="gelu",
                                    value_rank=6, var_rank=5)),
     "no_gate_k2": (32, dict(d_state=16, use_gating=False, conv_kernel_size=2)),
+    "wide_state_128": (24, dict(d_state=128)),
+    "wide_state_200_prior": (16, dict(d_state=200, decode_from_prior=True, return_variance=True, qk_norm=True)),
 }
 
 
@@ -1500,3 +1506,30 @@ def test_layer_split_linear_matches_torch_linear(cuda, monkeypatch, d_model, B, 
         a, b = g_hip[name].float(), g_ref[name].float()
         tol = 2e-2 * float(b.abs().max()) + 1e-12
         assert float((a - b).abs().max()) <= tol, name
+
+
+def test_layer_with_wide_state_runs_the_fused_kernels(cuda, monkeypatch):
+    """KLALayer(d_state=128) on "hip": the scan goes to the fused kernels (the
+    composed path is never called) and an fp32 forward + backward matches the
+    same layer on the torch backend."""
+    import copy
+
+    from kla.ops import hip_backend
+
+    def no_composed(*args, **kwargs):
+        raise AssertionError("the composed path ran")
+
+    torch.manual_seed(0)
+    hip = KLALayer(64, KLAConfig(d_state=128, backend="hip")).to(cuda)
+    ref = copy.deepcopy(hip)
+    ref.config = KLAConfig(d_state=128, backend="torch")
+    x = torch.randn(2, 40, 64, generator=torch.Generator().manual_seed(1)).to(cuda)
+    monkeypatch.setattr(hip_backend, "_sufficient_stats", no_composed)
+    outs = []
+    for layer in (hip, ref):
+        xx = x.clone().requires_grad_(True)
+        y = _first(layer(xx))
+        (y * torch.linspace(-1, 1, y.shape[-1], device=cuda)).sum().backward()
+        outs.append([y.detach(), xx.grad] + [p.grad for p in layer.parameters()])
+    for i, (a, b) in enumerate(zip(*outs)):
+        check(f"t{i}", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)

@@ -33,7 +33,8 @@ def _inputs(B, L, M, S, seed):
     ]
 
 
-@pytest.mark.parametrize("shape", [(4, 4096, 2048, 16), (2, 150, 120, 16), (8, 40, 9, 32), (3, 100, 50, 64)])
+@pytest.mark.parametrize("shape", [(4, 4096, 2048, 16), (2, 150, 120, 16), (8, 40, 9, 32), (3, 100, 50, 64),
+                                   (2, 300, 40, 128), (2, 100, 9, 256)])
 def test_fused_backward_is_bitwise_repeatable(cuda, shape):
     """The fused scan's forward and every gradient are bit-identical over three runs
     (C4's shape with 128 channel groups per batch row, and ragged multi-group
