@@ -353,6 +353,11 @@ def bench_layer(args, device, stream) -> dict:
         state["s"], state["tok"] = st, model._sample(logits[:, -1], 0.0, None)   # greedy
 
     pre_ms = _timed(prefill, max(1, args.steps // 4), 1, stream)
+    if args.c5_phase == "prefill":
+        return {"metric": "SequenceModel(d=512, 6 layers) prefill tokens/s (16x2048)",
+                "value": 16 * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
+                "backend": args.backend,
+                "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
 
     @torch.no_grad()
     def decode256():
@@ -394,6 +399,8 @@ def main(argv=None) -> int:
                     help="measure a layer-level config instead of the headline scan step "
                          "(scan: kla_scan alone at --shape)")
     ap.add_argument("--shape", default="2,2048,512,128", help="B,L,M,S for --layer scan")
+    ap.add_argument("--c5-phase", default="all", choices=["all", "prefill"],
+                    help="--layer c5: time the prefill and the decode (all) or the prefill only")
     ap.add_argument("--backend", default="hip", help="kla backend for --layer (hip, hip_composed, torch)")
     args = ap.parse_args(argv)
 

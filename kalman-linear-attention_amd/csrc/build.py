@@ -40,6 +40,21 @@ HIPCC_FLAGS = [
 ]
 
 
+# Host-sanitised build (AddressSanitizer + UndefinedBehaviorSanitizer on the host
+# code only; each -fsanitize= goes to the host pass, the device code is built
+# unoptimised and never run): the C ABI's argument checks and size arithmetic
+# under the sanitizers, loaded by tests/test_abi_sanitized.py with the ASan
+# runtime preloaded.
+SANITIZE_FLAGS = [
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+    "-Xarch_host", "-fno-omit-frame-pointer",
+    "-Xarch_host", "-O1",
+    "-Xarch_device", "-O0",
+]
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -47,11 +62,13 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (looked at $HIPCC, /opt/rocm/bin/hipcc, PATH)")
 
 
-def build(out: str = DEFAULT_OUT, save_temps: str | None = None, verbose: bool = True) -> str:
+def build(out: str = DEFAULT_OUT, save_temps: str | None = None, verbose: bool = True,
+          sanitize: bool = False) -> str:
     out = os.path.abspath(out)
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", INCLUDE, "-I", HERE]
+    flags = [f for f in HIPCC_FLAGS if not (sanitize and f == "-O3")] + (SANITIZE_FLAGS if sanitize else [])
+    cmd = [hipcc(), *flags, "-I", INCLUDE, "-I", HERE]
     if save_temps:
         os.makedirs(save_temps, exist_ok=True)
         cmd += ["-save-temps"]
@@ -76,8 +93,9 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--out", default=DEFAULT_OUT)
     ap.add_argument("--save-temps", default=None, help="directory for compiler intermediates (ISA)")
+    ap.add_argument("--sanitize", action="store_true", help="host AddressSanitizer + UBSan build (CPU checks only)")
     args = ap.parse_args(argv)
-    build(args.out, args.save_temps)
+    build(args.out, args.save_temps, sanitize=args.sanitize)
     return 0
 
 

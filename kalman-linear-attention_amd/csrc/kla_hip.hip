@@ -73,6 +73,23 @@ struct Shape {
   int64_t batch, steps, lanes;
 };
 
+// Workspace sizes are products of caller-given counts: they are formed with
+// these saturating operations (nonnegative operands), which stop at kHuge = 2^62
+// bytes or elements instead of overflowing. No device holds kHuge bytes, so a
+// saturated size is a problem too large to run: the *_workspace_bytes queries
+// return 0 for it and the entry points reject it before launching.
+constexpr int64_t kHuge = int64_t(1) << 62;
+
+int64_t smul(int64_t a, int64_t b) {
+  int64_t r;
+  return (__builtin_mul_overflow(a, b, &r) || r > kHuge) ? kHuge : r;
+}
+
+int64_t sadd(int64_t a, int64_t b) {
+  int64_t r;
+  return (__builtin_add_overflow(a, b, &r) || r > kHuge) ? kHuge : r;
+}
+
 int check_shape(const char *fn, Shape s) {
   if (s.batch < 0 || s.steps < 0 || s.lanes < 0)
     return fail(KLA_ERR_INVALID_ARG, "%s: negative size (batch=%lld steps=%lld lanes=%lld)", fn,
@@ -128,19 +145,20 @@ Geom make_geom(Shape s) {
 
 // Workspace words of one tile shape: header, then K aggregate planes and one
 // carry plane, each n_chunks * plane words.
-size_t words_for(Shape s, int W, int S, int V, int K) {
+int64_t words_for(Shape s, int W, int S, int V, int K) {
   const Geom g = make_geom(s, W, S, V);
-  return static_cast<size_t>(kHeaderWords + (K + 1) * g.n_chunks * g.plane);
+  return sadd(kHeaderWords, smul(K + 1, smul(g.n_chunks, g.plane)));
 }
 
 template <class T>
-size_t words_for(Shape s, int K) {
+int64_t words_for(Shape s, int K) {
   return words_for(s, T::W, T::S, T::V, K);
 }
 
-// Bytes of workspace a scan kind needs: the largest over the shapes it may run.
+// Bytes of workspace a scan kind needs: the largest over the shapes it may run
+// (0 for an unknown kind or a size that saturates).
 size_t workspace_bytes_kind(int kind, Shape s) {
-  size_t w = 0;
+  int64_t w = 0;
   switch (kind) {
     case KLA_SCAN_MOBIUS_FWD:
       w = words_for<MobiusFwdTile>(s, 4);
@@ -159,7 +177,8 @@ size_t workspace_bytes_kind(int kind, Shape s) {
     default:
       return 0;
   }
-  return w * sizeof(uint64_t);
+  const int64_t bytes = smul(w, sizeof(uint64_t));
+  return bytes >= kHuge ? 0 : static_cast<size_t>(bytes);
 }
 
 bool empty(Shape s) { return s.batch == 0 || s.steps == 0 || s.lanes == 0; }
@@ -174,12 +193,13 @@ int check_launch(const char *fn, int kind, Shape s, void *ws, size_t ws_bytes) {
   // The largest grid any shape of this kind launches: the V = 1 shapes have
   // the most tiles, the shortest chunks the most chunks.
   const Geom g1 = make_geom(s, 8, 8, 1);
-  const int64_t blocks = g1.n_tiles * g1.n_chunks;
+  const int64_t blocks = smul(g1.n_tiles, g1.n_chunks);
   if (blocks >= (1ll << 31))
     return fail(KLA_ERR_INVALID_ARG, "%s: %lld workgroups exceed the grid limit", fn, (long long)blocks);
   if (ws == nullptr) return fail(KLA_ERR_WORKSPACE, "%s: workspace is NULL", fn);
   if (misaligned_bytes(ws, 256)) return fail(KLA_ERR_WORKSPACE, "%s: workspace not 256-byte aligned", fn);
   const size_t need = workspace_bytes_kind(kind, s);
+  if (need == 0) return fail(KLA_ERR_INVALID_ARG, "%s: problem too large", fn);
   if (ws_bytes < need)
     return fail(KLA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, ws_bytes, need);
   return KLA_OK;
@@ -240,9 +260,10 @@ FusedGeom fused_geom(int64_t batch, int64_t steps, int64_t M, int64_t S) {
   return g;
 }
 
-// Partials of the fused backward: part_k, part_q [B, L, G, S]; part_a, part_p [B, M, S].
-size_t fused_workspace_floats(const FusedGeom &g) {
-  return static_cast<size_t>(2 * g.batch * g.steps * g.groups * g.S + 2 * g.batch * g.M * g.S);
+// Partials of the fused backward: part_k, part_q [B, L, G, S]; part_a, part_p [B, M, S]
+// (kHuge when that saturates).
+int64_t fused_workspace_floats(const FusedGeom &g) {
+  return sadd(smul(2, smul(smul(g.batch, g.steps), smul(g.groups, g.S))), smul(2, smul(g.batch, smul(g.M, g.S))));
 }
 
 int check_fused_shape(const char *fn, int64_t batch, int64_t steps, int64_t M, int64_t S) {
@@ -289,21 +310,23 @@ int with_k(int64_t K, F &&f) {
   }
 }
 
+// Time chunks of the conv kernels (no overflow for any nonnegative L).
+int64_t conv_chunks(int64_t L) { return L / kConvT + (L % kConvT != 0); }
+
 int check_conv_shape(const char *fn, int dtype, int64_t B, int64_t L, int64_t D, int64_t K, int act) {
   if (dtype != KLA_DTYPE_F32 && dtype != KLA_DTYPE_BF16) return fail(KLA_ERR_DTYPE, "%s: unsupported dtype code %d", fn, dtype);
   if (B < 0 || L < 0 || D < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
   if (K < 1 || K > kConvMaxK) return fail(KLA_ERR_INVALID_ARG, "%s: kernel_size %lld outside [1, %d]", fn, (long long)K, kConvMaxK);
-  if (B > 65535 || (L + kConvT - 1) / kConvT > 65535 || D > (1ll << 31))
+  if (B > 65535 || conv_chunks(L) > 65535 || D > (1ll << 31))
     return fail(KLA_ERR_INVALID_ARG, "%s: batch, steps / %d or channels out of range", fn, kConvT);
   if (act < kActNone || act > kActRelu)
     return fail(KLA_ERR_INVALID_ARG, "%s: activation must be 0 (none), 1 (silu), 2 (gelu) or 3 (relu)", fn);
   return KLA_OK;
 }
 
-int64_t conv_chunks(int64_t L) { return (L + kConvT - 1) / kConvT; }
 
 // The row-block reduce for many short rows (outer large, inner a power of two up
-// to 64); false when the shape does not suit it.
+// to 256); false when the shape does not suit it.
 bool launch_reduce_rows(const float *in, float *out, int64_t outer, int64_t G, int64_t inner, hipStream_t stream) {
   if (outer == 1 && G >= 4 && inner < (1ll << 37)) {
     // One output row: split the rows across phases as well as the columns.
@@ -333,6 +356,8 @@ bool launch_reduce_rows(const float *in, float *out, int64_t outer, int64_t G, i
     case 16: hipLaunchKernelGGL(reduce_rows_kernel<16>, grid, dim3(256), 0, stream, in, out, G); return true;
     case 32: hipLaunchKernelGGL(reduce_rows_kernel<32>, grid, dim3(256), 0, stream, in, out, G); return true;
     case 64: hipLaunchKernelGGL(reduce_rows_kernel<64>, grid, dim3(256), 0, stream, in, out, G); return true;
+    case 128: hipLaunchKernelGGL(reduce_rows_kernel<128>, grid, dim3(256), 0, stream, in, out, G); return true;
+    case 256: hipLaunchKernelGGL(reduce_rows_kernel<256>, grid, dim3(256), 0, stream, in, out, G); return true;
     default: return false;
   }
 }
@@ -424,7 +449,9 @@ int fused_bwd(const char *fn, const float *dy, const float *dy_var, const float 
   const FusedGeom g = fused_geom(batch, steps, M, S);
   if (workspace == nullptr) return fail(KLA_ERR_WORKSPACE, "%s: workspace is NULL", fn);
   if (misaligned_bytes(workspace, 256)) return fail(KLA_ERR_WORKSPACE, "%s: workspace not 256-byte aligned", fn);
-  const size_t need = fused_workspace_floats(g) * sizeof(float);
+  const int64_t need_floats = fused_workspace_floats(g);
+  if (need_floats >= kHuge / 4) return fail(KLA_ERR_INVALID_ARG, "%s: problem too large", fn);
+  const size_t need = static_cast<size_t>(need_floats) * sizeof(float);
   if (workspace_bytes < need)
     return fail(KLA_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", fn, workspace_bytes, need);
   const int64_t grid = batch * g.groups;
@@ -582,8 +609,12 @@ const char *kla_hip_last_error(void) { return g_last_error; }
 size_t kla_scan_workspace_bytes(int kind, int64_t batch, int64_t steps, int64_t lanes) {
   const Shape s{batch, steps, lanes};
   if (check_shape("kla_scan_workspace_bytes", s) != KLA_OK) return 0;
+  if (kind < KLA_SCAN_MOBIUS_FWD || kind > KLA_SCAN_AFFINE_BWD) {
+    fail(KLA_ERR_INVALID_ARG, "kla_scan_workspace_bytes: unknown scan kind %d", kind);
+    return 0;
+  }
   const size_t bytes = workspace_bytes_kind(kind, s);
-  if (bytes == 0) fail(KLA_ERR_INVALID_ARG, "kla_scan_workspace_bytes: unknown scan kind %d", kind);
+  if (bytes == 0) fail(KLA_ERR_INVALID_ARG, "kla_scan_workspace_bytes: problem too large");
   return bytes;
 }
 
@@ -618,7 +649,7 @@ int kla_mobius_scan_fwd_noalloc(const float *A, const float *B, const float *C, 
   const char *fn = "kla_mobius_scan_fwd_noalloc";
   return mobius_fwd(fn, A, B, C, D, lam0, lam, batch, steps, lanes, stream, [&](void **ws, size_t *bytes) {
     const size_t need = workspace_bytes_kind(KLA_SCAN_MOBIUS_FWD, Shape{batch, steps, lanes});
-    if (need > kScratchBytes)
+    if (need == 0 || need > kScratchBytes)
       return fail(KLA_ERR_WORKSPACE, "%s: the look-back needs %zu bytes, the static scratch holds %zu", fn, need,
                   kScratchBytes);
     *bytes = kScratchBytes;
@@ -731,7 +762,12 @@ int64_t kla_fused_checkpoints(int64_t steps) { return steps < 0 ? 0 : (steps + k
 
 size_t kla_fused_workspace_bytes(int64_t batch, int64_t steps, int64_t M, int64_t S) {
   if (check_fused_shape("kla_fused_workspace_bytes", batch, steps, M, S) != KLA_OK) return 0;
-  return std::max<size_t>(256, fused_workspace_floats(fused_geom(batch, steps, M, S)) * sizeof(float));
+  const int64_t floats = fused_workspace_floats(fused_geom(batch, steps, M, S));
+  if (floats >= kHuge / 4) {
+    fail(KLA_ERR_INVALID_ARG, "kla_fused_workspace_bytes: problem too large");
+    return 0;
+  }
+  return std::max<size_t>(256, static_cast<size_t>(floats) * sizeof(float));
 }
 
 int kla_fused_scan_fwd(const float *v, const float *lambda_v, const float *k, const float *q,
@@ -951,7 +987,12 @@ size_t kla_causal_conv_workspace_bytes(int64_t batch, int64_t steps, int64_t cha
     fail(KLA_ERR_INVALID_ARG, "kla_causal_conv_workspace_bytes: bad size");
     return 0;
   }
-  return std::max<size_t>(256, static_cast<size_t>(batch * conv_chunks(steps) * channels * (kernel_size + 1)) * 4);
+  const int64_t bytes = smul(smul(smul(batch, conv_chunks(steps)), channels), smul(kernel_size + 1, 4));
+  if (bytes >= kHuge) {
+    fail(KLA_ERR_INVALID_ARG, "kla_causal_conv_workspace_bytes: problem too large");
+    return 0;
+  }
+  return std::max<size_t>(256, static_cast<size_t>(bytes));
 }
 
 int kla_causal_conv_bwd(int dtype, const void *dy, const void *x, int64_t ld_t, int64_t ld_b, const void *state,
@@ -1023,8 +1064,13 @@ int kla_causal_conv_bwd(int dtype, const void *dy, const void *x, int64_t ld_t, 
 
 size_t kla_gate_skip_workspace_bytes(int64_t rows, int64_t M) {
   if (rows < 0 || M < 0) return 0;
-  const int64_t nblk = (rows + kTailRows - 1) / kTailRows;
-  return std::max<size_t>(256, static_cast<size_t>(nblk * M + M + 1) * sizeof(float));
+  const int64_t nblk = rows / kTailRows + (rows % kTailRows != 0);
+  const int64_t bytes = smul(sadd(smul(nblk, M), sadd(M, 1)), sizeof(float));
+  if (bytes >= kHuge) {
+    fail(KLA_ERR_INVALID_ARG, "kla_gate_skip_workspace_bytes: problem too large");
+    return 0;
+  }
+  return std::max<size_t>(256, static_cast<size_t>(bytes));
 }
 
 int kla_gate_skip_fwd(int dtype, int out_dtype, const float *y, const void *residual, int64_t ld_res,
@@ -1270,15 +1316,15 @@ int rows_linear_launch(const char *fn, int epi, RowsLinearParams &p, hipStream_t
 // Parts per row of the split argmax: about 256 workgroups in all, chunks of at
 // least 2048 columns, at most 64 parts; 1 means the one-kernel path.
 int64_t argmax_parts(int64_t rows, int64_t n) {
-  int64_t parts = (256 + rows - 1) / rows;
+  int64_t parts = rows >= 256 ? 1 : (256 + rows - 1) / rows;
   if (parts > 64) parts = 64;
   while (parts > 1 && n / parts < 2048) --parts;
   return parts;
 }
 
 int64_t argmax_workspace_bytes(int64_t rows, int64_t n) {
-  const int64_t parts = argmax_parts(rows, n);
-  return ((rows * parts * 4 + 255) / 256) * 256 + rows * parts * 8;
+  const int64_t pairs = smul(rows, argmax_parts(rows, n));
+  return sadd(smul(sadd(smul(pairs, 4), 255) / 256, 256), smul(pairs, 8));
 }
 
 RowsLinearParams rows_params(const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
@@ -1365,7 +1411,9 @@ int kla_gather_rows(int dtype, const void *table, int64_t ld_table, int64_t voca
 }
 
 size_t kla_argmax_workspace_bytes(int64_t rows, int64_t n) {
-  return rows > 0 && n > 0 ? static_cast<size_t>(argmax_workspace_bytes(rows, n)) : 0;
+  if (rows <= 0 || n <= 0) return 0;
+  const int64_t bytes = argmax_workspace_bytes(rows, n);
+  return bytes >= kHuge ? 0 : static_cast<size_t>(bytes);
 }
 
 int kla_argmax_rows(const float *x, int64_t ldx, int64_t rows, int64_t n, int64_t *out, int64_t ld_out,

@@ -15,8 +15,10 @@ import threading
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
-                        "lib", "libkla_hip.so")
+# KLA_HIP_LIB names another build of the same library (e.g. the host-sanitised
+# one the ABI tests run against); by default the in-tree libkla_hip.so.
+LIB_PATH = os.environ.get("KLA_HIP_LIB") or os.path.join(
+    os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))), "lib", "libkla_hip.so")
 ABI_VERSION = 13
 
 KLA_OK = 0
