@@ -39,6 +39,7 @@ scan kernel, so one counter pass covers them all.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import platform
@@ -257,16 +258,34 @@ def time_kernels_in_step(kernels, steps, stream):
     return {name: statistics.mean(s.elapsed_time(e) for s, e in pairs) for name, pairs in ev.items()}
 
 
+class _NoGC:
+    """Python's cyclic garbage collector off for a timed region (collected just before).
+
+    A generation-2 collection is a host-side pause of tens of milliseconds (81 ms
+    measured in the C4 step's process) during which no kernel is launched and the
+    GPU runs dry; the step's kernels are the same either way."""
+
+    def __enter__(self):
+        gc.collect()
+        self.was = gc.isenabled()
+        gc.disable()
+
+    def __exit__(self, *exc):
+        if self.was:
+            gc.enable()
+
+
 def _timed(fn, steps, warmup, stream):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        fn()
-    end.record(stream)
-    torch.cuda.synchronize()
+    with _NoGC():
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        end.record(stream)
+        torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
 
 
@@ -459,13 +478,14 @@ def main(argv=None) -> int:
         step()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with _NoGC():
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(args.steps):
+            step()
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     ms_per_step = start.elapsed_time(end) / args.steps
 
     from kla.ops.hip import _lib
