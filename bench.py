@@ -205,7 +205,10 @@ def cpu_baseline(lanes_full: int, ops: str = "mobius+affine", budget_s: float = 
 # ----------------------------------------------------------------- GPU side
 
 
-def build_step(batch, steps, lanes, adt, device, ops="mobius+affine"):
+def build_step(batch, steps, lanes, adt, device, ops="mobius+affine", streams=1):
+    """(step, kernels): one fwd + bwd of the workload's scans, and each kernel alone.
+    With ``streams`` 2 the affine chain runs on a second stream beside the Moebius
+    chain (the two scans are independent); the same kernels, overlapped."""
     from kla.ops.hip import scans as hs
 
     if ops == "mobius+affine":
@@ -234,6 +237,19 @@ def build_step(batch, steps, lanes, adt, device, ops="mobius+affine"):
     def step():
         for fn in order:
             fn()
+
+    if streams == 2 and ops == "mobius+affine":
+        main = torch.cuda.current_stream(device)
+        side = torch.cuda.Stream(device)
+
+        def step():  # noqa: F811
+            side.wait_stream(main)
+            mobius_fwd()
+            mobius_bwd()
+            with torch.cuda.stream(side):
+                affine_fwd()
+                affine_bwd()
+            main.wait_stream(side)
 
     return step, kernels
 
@@ -414,6 +430,9 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default=None,
                     choices=["mobius_fwd", "mobius_bwd", "affine_fwd", "affine_bwd", "copy", "all"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--streams", type=int, default=1, choices=[1, 2],
+                    help="2: run the affine chain on a second stream beside the Moebius chain (the timed step "
+                         "only; the per-kernel timings and the roofline stay those of the serial step)")
     ap.add_argument("--layer", default=None, choices=["c1", "c4", "c5", "scan"],
                     help="measure a layer-level config instead of the headline scan step "
                          "(scan: kla_scan alone at --shape)")
@@ -456,7 +475,7 @@ def main(argv=None) -> int:
             return 0
 
     print(f"[bench] building inputs for {args.workload} ({batch}x{steps}x{lanes})", file=sys.stderr, flush=True)
-    step, kernels = build_step(batch, steps, lanes, adt, device, ops)
+    step, kernels = build_step(batch, steps, lanes, adt, device, ops, args.streams)
 
     if args.only:
         names = list(kernels) if args.only == "all" else [args.only]
@@ -490,7 +509,7 @@ def main(argv=None) -> int:
 
     from kla.ops.hip import _lib
 
-    failures = _lib.workspace_failures(device)
+    failures = _lib.workspace_failures_all(device)
     per_kernel_ms = time_kernels_in_step(kernels, args.steps, stream)
     per_kernel = {}
     for name, ms in per_kernel_ms.items():
@@ -533,6 +552,8 @@ def main(argv=None) -> int:
         "dtype": dtype,
         "data": "synthetic",
         "config": {"workload": args.workload, "batch": batch, "steps": steps, "lanes": lanes,
+                   "schedule": "one stream" if args.streams == 1 or ops != "mobius+affine" else
+                   "Moebius and affine chains on two streams",
                    "ops": ops_desc, "parallelism": "single GPU"},
         "achieved_GBps": round(achieved_step, 1),
         "alg_bytes_per_step": step_bytes,

@@ -499,7 +499,11 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
   // Wide channels stage shorter blocks: the [SP, TB] k and q tiles fill the LDS.
   constexpr int TB = SP >= 128 ? kCkpt : kFusedTB;
   __shared__ __align__(16) float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
-  __shared__ __align__(16) float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
+  // The [SP, TB] k and q tiles: double-buffered, except at 256 lanes per channel
+  // (40 KiB a buffer), where one buffer and a barrier before it is refilled let
+  // more than one workgroup share a CU.
+  constexpr int KQB = SP >= 256 ? 1 : 2;
+  __shared__ __align__(16) float s_k[KQB][SP][TB + kPad], s_q[KQB][SP][TB + kPad];
   __shared__ float s_y[2][WPC][CH][TB + kPad], s_yv[2][WPC][CH][TB + kPad];
 
   const FusedLane ln = fused_lane<SP>(g);
@@ -540,8 +544,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
     tile_to_lds<TB, CH>(rv, s_v[buf]);
     to_precision<TB, CH>(rl, sn);
     tile_to_lds<TB, CH>(rl, s_l[buf]);
-    tile_to_lds<TB, SP>(rk, s_k[buf]);
-    tile_to_lds<TB, SP>(rq, s_q[buf]);
+    tile_to_lds<TB, SP>(rk, s_k[KQB == 1 ? 0 : buf]);
+    tile_to_lds<TB, SP>(rq, s_q[KQB == 1 ? 0 : buf]);
   };
 
   // Checkpoint of the state entering step t: ck[((b * n_ck + t / kCkpt) * M + m) * S + s].
@@ -575,7 +579,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
       StepIO io;
       const float sig = x4 ? pick4(l4, j % 4) : s_l[cur][c][j];
       const float vv = x4 ? pick4(v4, j % 4) : s_v[cur][c][j];
-      const float kk = x4 ? pick4(k4, j % 4) : s_k[cur][ln.s][j];
+      const float kk = x4 ? pick4(k4, j % 4) : s_k[KQB == 1 ? 0 : cur][ln.s][j];
       lam = filter_step(lam, eta, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
       const float var = rcp(fmaxf(lam, kEps));
       float mean = eta * var, vo = var;
@@ -583,7 +587,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
         mean = a_s * mean;
         vo = a2 * var + pp;
       }
-      const float qq = x4 ? pick4(q4, j % 4) : s_q[cur][ln.s][j];
+      const float qq = x4 ? pick4(q4, j % 4) : s_q[KQB == 1 ? 0 : cur][ln.s][j];
       if constexpr (kTr) {
         yw[jj] = qq * mean;
         if constexpr (VAR) vw[jj] = (qq * qq) * vo;
@@ -613,8 +617,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
             if (kVecLds && jb % 4 == 0) {
               l4 = lds4(s_l[cur][c], jb);
               v4 = lds4(s_v[cur][c], jb);
-              k4 = lds4(s_k[cur][ln.s], jb);
-              q4 = lds4(s_q[cur][ln.s], jb);
+              k4 = lds4(s_k[KQB == 1 ? 0 : cur][ln.s], jb);
+              q4 = lds4(s_q[KQB == 1 ? 0 : cur][ln.s], jb);
             }
             step(jb, j, kVecLds);
           }
@@ -644,7 +648,10 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
         }
       }
     }
-    if (blk + 1 < nblk) stage(cur ^ 1);
+    if (blk + 1 < nblk) {
+      if constexpr (KQB == 1) __syncthreads();   // every wave is done with this block's k, q
+      stage(cur ^ 1);
+    }
     __syncthreads();
   }
   if (nblk > 0) {
@@ -672,10 +679,19 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
   constexpr int TB = kCkpt;
   __shared__ __align__(16) float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
   __shared__ __align__(16) float s_dy[2][CH][TB + kPad], s_dyv[2][CH][TB + kPad];
-  __shared__ __align__(16) float s_k[2][SP][TB + kPad], s_q[2][SP][TB + kPad];
+  // The [SP, TB] k and q tiles: double-buffered, except at 256 lanes per channel
+  // (40 KiB a buffer), where one buffer and a barrier before it is refilled let
+  // more than one workgroup share a CU.
+  constexpr int KQB = SP >= 256 ? 1 : 2;
+  __shared__ __align__(16) float s_k[KQB][SP][TB + kPad], s_q[KQB][SP][TB + kPad];
   __shared__ float s_dv[2][WPC][CH][TB + kPad], s_dl[2][WPC][CH][TB + kPad];
   __shared__ float s_lf[2][CH][TB + kPad];   // log sigma^2 gradient factors (log_var sensors)
-  __shared__ float s_red[2][2][TB][NW / WPC][SP];   // per-(step, s) sums of a channel slot
+  // Per-(step, s) sums of a channel slot, double-buffered like the tiles where
+  // it is small; from 64 lanes per channel on (64 KiB a buffer) one buffer and a
+  // barrier between the flush that reads it and the walk that refills it, which
+  // halves the backward's LDS and lets two workgroups share a CU.
+  constexpr int RB = SP >= kWave ? 1 : 2;
+  __shared__ float s_red[RB][2][TB][NW / WPC][SP];
 
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
@@ -724,8 +740,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     tile_to_lds<TB, CH>(rl, s_l[buf]);
     tile_to_lds<TB, CH>(rdy, s_dy[buf]);
     if constexpr (VAR) tile_to_lds<TB, CH>(rdyv, s_dyv[buf]);
-    tile_to_lds<TB, SP>(rk, s_k[buf]);
-    tile_to_lds<TB, SP>(rq, s_q[buf]);
+    tile_to_lds<TB, SP>(rk, s_k[KQB == 1 ? 0 : buf]);
+    tile_to_lds<TB, SP>(rq, s_q[KQB == 1 ? 0 : buf]);
   };
   // Outputs of block c (buffer `buf`): dv, dLv rows, and the workgroup's
   // partial sums of dk, dq (the waves' sums added here, in wave order).
@@ -749,7 +765,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       if (t < L && s < S) {
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW / WPC; ++w) sum += s_red[buf][which][j][w][s];
+        for (int w = 0; w < NW / WPC; ++w) sum += s_red[RB == 1 ? 0 : buf][which][j][w][s];
         float *part = which == 0 ? prm.part_k : prm.part_q;
         part[((ln.b * L + t) * g.groups + grp) * S + s] = sum;
       }
@@ -767,7 +783,10 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     const int64_t blk = n_ck - 1 - i;
     const int64_t t0 = blk * TB;
     if (i + 1 < n_ck) load(t0 - TB);
-    if (i > 0) flush(blk + 1, cur ^ 1);
+    if (i > 0) {
+      flush(blk + 1, cur ^ 1);
+      if constexpr (RB == 1) __syncthreads();   // the flush has read s_red before the walk refills it
+    }
 
     // Tile values four steps per LDS read, where the registers that hold them
     // do not cost occupancy (16 or more lanes per channel).
@@ -794,7 +813,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         if (kVecLds && j % 4 == 0) {
           l4 = lds4(s_l[cur][c], j);
           v4 = lds4(s_v[cur][c], j);
-          k4 = lds4(s_k[cur][ln.s], j);
+          k4 = lds4(s_k[KQB == 1 ? 0 : cur][ln.s], j);
         }
         lh[j] = lam;
         eh[j] = eta;
@@ -804,7 +823,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
           StepIO io;
           const float sig = kVecLds ? pick4(l4, j % 4) : s_l[cur][c][j];
           const float vv = kVecLds ? pick4(v4, j % 4) : s_v[cur][c][j];
-          const float kk = kVecLds ? pick4(k4, j % 4) : s_k[cur][ln.s][j];
+          const float kk = kVecLds ? pick4(k4, j % 4) : s_k[KQB == 1 ? 0 : cur][ln.s][j];
           lam = filter_step(lam, eta, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
           idn[j] = io.inv_den;
           vr[j] = rcp(fmaxf(lam, kEps));
@@ -828,8 +847,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         v4 = lds4(s_v[cur][c], j - 3);
         l4 = lds4(s_l[cur][c], j - 3);
         dy4 = lds4(s_dy[cur][c], j - 3);
-        k4 = lds4(s_k[cur][ln.s], j - 3);
-        q4 = lds4(s_q[cur][ln.s], j - 3);
+        k4 = lds4(s_k[KQB == 1 ? 0 : cur][ln.s], j - 3);
+        q4 = lds4(s_q[KQB == 1 ? 0 : cur][ln.s], j - 3);
       }
       float dk_c = 0.0f, dq_c = 0.0f;
       if constexpr (kTr) {
@@ -840,8 +859,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         const float vv = kVecLds ? pick4(v4, j % 4) : s_v[cur][c][j];
         const float sig = kVecLds ? pick4(l4, j % 4) : s_l[cur][c][j];
         const float dy = kVecLds ? pick4(dy4, j % 4) : s_dy[cur][c][j];
-        const float kk = kVecLds ? pick4(k4, j % 4) : s_k[cur][ln.s][j];
-        const float qq = kVecLds ? pick4(q4, j % 4) : s_q[cur][ln.s][j];
+        const float kk = kVecLds ? pick4(k4, j % 4) : s_k[KQB == 1 ? 0 : cur][ln.s][j];
+        const float qq = kVecLds ? pick4(q4, j % 4) : s_q[KQB == 1 ? 0 : cur][ln.s][j];
         const float lp = lh[j], ep = eh[j];
         const float lam_t = lh[j + 1], eta_t = eh[j + 1];
         const float inv_den = idn[j], var = vr[j];
@@ -930,8 +949,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
         dk_c = cross_group_sum<SP>(dk_c);
         dq_c = cross_group_sum<SP>(dq_c);
         if (SP >= kWave || lane < SP) {
-          s_red[cur][0][j][wave / WPC][ln.s] = dk_c;
-          s_red[cur][1][j][wave / WPC][ln.s] = dq_c;
+          s_red[RB == 1 ? 0 : cur][0][j][wave / WPC][ln.s] = dk_c;
+          s_red[RB == 1 ? 0 : cur][1][j][wave / WPC][ln.s] = dq_c;
         }
       }
     }
@@ -942,8 +961,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
 #pragma unroll
       for (int i = 0; i < TB / 4; ++i) {
         const int j = (TB / 2) * (row >> 1) + (TB / 4) * (row & 1) + i;
-        s_red[cur][0][j][wave][ln.s] = dk_w[i];
-        s_red[cur][1][j][wave][ln.s] = dq_w[i];
+        s_red[RB == 1 ? 0 : cur][0][j][wave][ln.s] = dk_w[i];
+        s_red[RB == 1 ? 0 : cur][1][j][wave][ln.s] = dq_w[i];
       }
     }
     if constexpr (kTr) {
@@ -958,7 +977,10 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     acc_a += blk_a;
     acc_a2 += fmaf(-fmaf(pp, blk_x, blk_y), inv_a2 * inv_a2, blk_a2);
     acc_p += fmaf(blk_x, inv_a2, blk_p);
-    if (i + 1 < n_ck) stage(cur ^ 1);
+    if (i + 1 < n_ck) {
+      if constexpr (KQB == 1) __syncthreads();   // every wave is done with this block's k, q
+      stage(cur ^ 1);
+    }
     __syncthreads();
   }
   if (n_ck > 0) flush(0, static_cast<int>((n_ck - 1) & 1));

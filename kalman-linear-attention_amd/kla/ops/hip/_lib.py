@@ -223,6 +223,18 @@ def workspace_failures(device: torch.device) -> int:
     return int(out.value)
 
 
+def workspace_failures_all(device: torch.device) -> int:
+    """Look-back waits that gave up on every stream's workspace of ``device``."""
+    total = 0
+    for (index, stream_handle), ws in list(_WORKSPACES.items()):
+        if index != device.index:
+            continue
+        out = ctypes.c_uint32(0)
+        check("kla_workspace_failures", lib().kla_workspace_failures(ws.data_ptr(), stream_handle, ctypes.byref(out)))
+        total += int(out.value)
+    return total
+
+
 def reset_workspaces() -> None:
     """Drop every cached workspace (the next call allocates a fresh zero-filled one)."""
     with _WS_LOCK:
