@@ -306,9 +306,11 @@ def _timed(fn, steps, warmup, stream):
 
 
 def bench_scan(args, device, stream) -> dict:
-    """The KLA scan alone (kla_scan fwd + bwd: y, y_var, every input gradient) at
-    ``--shape B,L,M,S`` on the chosen backend: the d_state > 64 case of the fused
-    kernels (hip_fused) against the composed path (hip_composed)."""
+    """The KLA scan alone (kla_scan fwd + bwd: y, y_var, every input gradient; or
+    with ``--scan-pass fwd`` the forward under no_grad, where small grids take the
+    time-split forward) at ``--shape B,L,M,S`` on the chosen backend: the d_state
+    > 64 case of the fused kernels (hip_fused) against the composed path
+    (hip_composed)."""
     from kla.ops import kla_scan
 
     B, L, M, S = (int(x) for x in args.shape.split(","))
@@ -317,7 +319,8 @@ def bench_scan(args, device, stream) -> dict:
            torch.randn(B, L, S, generator=g) * 0.3, torch.randn(B, L, S, generator=g) * 0.3,
            torch.rand(M, S, generator=g) * 0.5 + 0.45, torch.rand(M, S, generator=g) * 0.05 + 0.01]
     dy, dyv = torch.randn(B, L, M, generator=g).to(device), torch.randn(B, L, M, generator=g).to(device)
-    xs = [t.to(device).requires_grad_(True) for t in ins]
+    fwd_only = args.scan_pass == "fwd"
+    xs = [t.to(device).requires_grad_(not fwd_only) for t in ins]
 
     def step():
         y, y_var, _ = kla_scan(*xs, backend=args.backend)
@@ -325,8 +328,13 @@ def bench_scan(args, device, stream) -> dict:
         for x in xs:
             x.grad = None
 
-    ms = _timed(step, args.steps, args.warmup, stream)
-    return {"metric": f"kla_scan fwd+bwd tokens/s, (B, L, M, S) = ({B}, {L}, {M}, {S}), fp32",
+    @torch.no_grad()
+    def forward():
+        kla_scan(*xs, backend=args.backend)
+
+    ms = _timed(forward if fwd_only else step, args.steps, args.warmup, stream)
+    what = "forward (no_grad)" if fwd_only else "fwd+bwd"
+    return {"metric": f"kla_scan {what} tokens/s, (B, L, M, S) = ({B}, {L}, {M}, {S}), fp32",
             "value": B * L / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": round(ms, 4),
             "lane_steps_per_s": B * L * M * S / (ms * 1e-3), "backend": args.backend,
             "steps": args.steps, "warmup": args.warmup,
@@ -378,19 +386,20 @@ def bench_layer(args, device, stream) -> dict:
                 "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
     model = SequenceModel(ModelConfig(vocab_size=50304, d_model=512, n_layers=6),
                           KLAConfig(backend=args.backend)).to(device).eval()
-    ids = torch.randint(0, 50304, (16, 2048), generator=torch.Generator().manual_seed(0)).to(device)
+    nb = args.c5_batch
+    ids = torch.randint(0, 50304, (nb, 2048), generator=torch.Generator().manual_seed(0)).to(device)
     state = {}
 
     @torch.no_grad()
     def prefill():
-        st = model.init_state(16)
+        st = model.init_state(nb)
         logits, st = model(ids, state=st)
         state["s"], state["tok"] = st, model._sample(logits[:, -1], 0.0, None)   # greedy
 
     pre_ms = _timed(prefill, max(1, args.steps // 4), 1, stream)
     if args.c5_phase == "prefill":
-        return {"metric": "SequenceModel(d=512, 6 layers) prefill tokens/s (16x2048)",
-                "value": 16 * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
+        return {"metric": f"SequenceModel(d=512, 6 layers) prefill tokens/s ({nb}x2048)",
+                "value": nb * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
                 "backend": args.backend,
                 "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
 
@@ -402,8 +411,8 @@ def bench_layer(args, device, stream) -> dict:
             tok = model._sample(logits[:, -1], 0.0, None)
 
     dec_ms = _timed(decode256, 1, 1, stream)
-    out = {"metric": "SequenceModel(d=512, 6 layers) prefill tokens/s (16x2048) + decode ms/token (256 steps)",
-           "value": 16 * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
+    out = {"metric": f"SequenceModel(d=512, 6 layers) prefill tokens/s ({nb}x2048) + decode ms/token (256 steps)",
+           "value": nb * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
            "decode_ms_per_token": round(dec_ms / 256, 4), "backend": args.backend}
     if args.backend.startswith("hip"):
         from kla.models.decode_graph import DecodeGraph
@@ -437,6 +446,10 @@ def main(argv=None) -> int:
                     help="measure a layer-level config instead of the headline scan step "
                          "(scan: kla_scan alone at --shape)")
     ap.add_argument("--shape", default="2,2048,512,128", help="B,L,M,S for --layer scan")
+    ap.add_argument("--scan-pass", default="fwd+bwd", choices=["fwd+bwd", "fwd"],
+                    help="--layer scan: forward and backward, or the inference forward alone")
+    ap.add_argument("--c5-batch", type=int, default=16,
+                    help="--layer c5: sequences per prefill / decode batch (16 is the C5 config)")
     ap.add_argument("--c5-phase", default="all", choices=["all", "prefill"],
                     help="--layer c5: time the prefill and the decode (all) or the prefill only")
     ap.add_argument("--backend", default="hip", help="kla backend for --layer (hip, hip_composed, torch)")

@@ -243,6 +243,32 @@ int kla_fused_scan_sensors_bwd(const float *dy, const float *dy_var, const float
                                hipStream_t stream);
 
 /*
+ * The time-split forward of the fused scan (inference: no checkpoints, no
+ * backward), for problems with too few chains (batch * M * S) to fill the GPU.
+ * The sequence is cut into `chunks` equal pieces; a [B, L, .] tensor viewed as
+ * [B * chunks, L / chunks, .] is the same memory (sequence b's chunk c at
+ * b' = b * chunks + c). Three calls:
+ *   kla_fused_chunk_maps on the view (batch = B * chunks, steps = L / chunks):
+ *     each chunk's steps composed into one map of the state in homogeneous
+ *     coordinates (lam = N / D, eta = W / D, where a filter step is linear),
+ *     maps [B * chunks, M, S, 8] (n0 n1 d0 d1 w0 w1 w2, one word unused);
+ *   kla_chunk_starts (batch = B, chunks): the state entering each chunk,
+ *     lam_start, eta_start [B, chunks, M, S], from lam0 (NULL: 1) and eta0
+ *     (NULL: 0) through the maps in chunk order;
+ *   kla_fused_scan_sensors_fwd on the view with lam0 / eta0 = the starts: y,
+ *     y_var, and the final state in its chunk chunks - 1.
+ * The sensors are as for kla_fused_scan_sensors_fwd. The chunked forward of the
+ * reference's tiled Metal kernel (src/kla/ops/kernels/mps/tiled_kla_scan.metal:1-35,
+ * tiled_kla_scan.py:32-60), which composes the precision and the information
+ * leaves in two rounds; with kla_fused_scan_sensors_fwd it replaces
+ * kla_scan_torch's forward (src/kla/ops/kla_ops.py:188-290).
+ */
+int kla_fused_chunk_maps(const kla_sensors *sensors, const float *k, const float *a, const float *p, float *maps,
+                         int64_t batch, int64_t steps, int64_t M, int64_t S, hipStream_t stream);
+int kla_chunk_starts(const float *maps, const float *lam0, const float *eta0, float *lam_start, float *eta_start,
+                     int64_t batch, int64_t chunks, int64_t M, int64_t S, hipStream_t stream);
+
+/*
  * One O(1) decode step of the filter for every (b, m, s) lane: kla_step
  * (reference src/kla/ops/kla_ops.py:293-331), phi floored at 1e-12 as there.
  * v, lambda_v, y, y_var [batch, M]; k, q [batch, S]; a, p [M, S]; lam, eta,

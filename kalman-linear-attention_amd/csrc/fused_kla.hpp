@@ -1093,6 +1093,162 @@ __global__ void reduce_groups_kernel(const float *__restrict__ in, float *__rest
   out[idx] = sum;
 }
 
+// ============================================= time-split forward (inference)
+//
+// With few chains (batch * M * S) the lane-serial forward leaves CUs idle. For a
+// forward without a backward the sequence can be cut into `chunks` equal pieces
+// run side by side: a [B, L, .] tensor viewed as [B * chunks, L / chunks, .] is
+// the same memory, with sequence b's chunk c at b' = b * chunks + c.
+//
+// The state entering each chunk comes from one pass over the chunks and one
+// walk along them. In homogeneous coordinates lam = N / D, eta = W / D a step of
+// filter_step is linear:
+//   N' = A N + phi D,   D' = C N + D,   W' = g W + r D'      (g = a / a2)
+// since lam' = (A lam + phi) / (C lam + 1), alpha = g / (C lam + 1) = g D / D'
+// and eta' = alpha eta + r. So a chunk's steps compose to one 3x3 map
+//   [[n0, n1, 0], [d0, d1, 0], [w0, w1, w2]]
+// which needs no entering state, and the precision and information recurrences
+// are carried together. (The reference's tiled Metal kernel takes two rounds
+// here, composing the affine information leaves only once the precision is
+// known: src/kla/ops/kernels/mps/tiled_kla_scan.metal:26-35.) The map is scaled
+// after every step by the power of two that brings n0 + d1 into [0.5, 1), as
+// mobius_compose does: exact, and harmless because every read-out is a ratio.
+
+struct ChunkMapParams {
+  SensorIn sn;
+  const float *k, *a, *p;
+  float *maps;   // [B', M, S, 8]: n0 n1 d0 d1 w0 w1 w2 (and one unused word)
+};
+
+template <int SP, bool BF16>
+__global__ void __launch_bounds__(kFusedThreads) fused_chunk_map_kernel(ChunkMapParams prm, FusedGeom g) {
+  constexpr int CH = kFusedThreads / SP;
+  constexpr int TB = SP >= 128 ? kCkpt : kFusedTB;
+  constexpr int KQB = SP >= 256 ? 1 : 2;
+  constexpr bool kVecLds = SP >= 16;
+  __shared__ __align__(16) float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
+  __shared__ __align__(16) float s_k[KQB][SP][TB + kPad];
+
+  const FusedLane ln = fused_lane<SP>(g);
+  const int64_t M = g.M, S = g.S, L = g.steps;
+  const int64_t m0 = (xcd_block() % g.groups) * CH;
+  const int c = static_cast<int>(ln.m - m0);
+  const int64_t ms = ln.m * S + ln.s;
+  const int64_t bms = ln.b * M * S + ms;
+  const int64_t cols_m = M - m0 < CH ? M - m0 : CH;
+
+  const float a_s = ln.active ? prm.a[ms] : 1.0f;
+  const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
+  const float a2 = fmaxf(a_s * a_s, kEps);
+  const float inv_a2 = 1.0f / a2;
+  const float C = pp * inv_a2;
+  const float gain = a_s * inv_a2;
+
+  const SensorIn &sn = prm.sn;
+  const float *kbase = prm.k + ln.b * L * S;
+  TileRegs<TB, CH> rv, rl;
+  TileRegs<TB, SP> rk;
+  auto load = [&](int64_t t0) {
+    const int64_t rows = L - t0;
+    tile_load_sensor<TB, CH, BF16>(rv, sensor_at<BF16>(sn.v, ln.b * L + t0, m0, sn.ld_v), sn.ld_v, rows, cols_m);
+    tile_load_sensor<TB, CH, BF16>(rl, sensor_at<BF16>(sn.lv, ln.b * L + t0, m0, sn.ld_lv), sn.ld_lv, rows, cols_m);
+    tile_load<TB, SP>(rk, kbase + t0 * S, S, rows, S);
+  };
+  auto stage = [&](int buf) {
+    widen_sensor<TB, CH, BF16>(rv);
+    widen_sensor<TB, CH, BF16>(rl);
+    tile_to_lds<TB, CH>(rv, s_v[buf]);
+    to_precision<TB, CH>(rl, sn);
+    tile_to_lds<TB, CH>(rl, s_l[buf]);
+    tile_to_lds<TB, SP>(rk, s_k[KQB == 1 ? 0 : buf]);
+  };
+
+  float n0 = 1.0f, n1 = 0.0f, d0 = 0.0f, d1 = 1.0f, w0 = 0.0f, w1 = 0.0f, w2 = 1.0f;
+  auto step = [&](float sig, float vv, float kk) {
+    const float phi = sig * (kk * kk);
+    const float r = (vv * sig) * kk;
+    const float A = (1.0f + pp * phi) * inv_a2;
+    const float e0 = fmaf(C, n0, d0), e1 = fmaf(C, n1, d1);
+    const float m0_ = fmaf(A, n0, phi * d0), m1_ = fmaf(A, n1, phi * d1);
+    const float x0 = fmaf(gain, w0, r * e0), x1 = fmaf(gain, w1, r * e1), x2 = gain * w2;
+    const int e = __builtin_amdgcn_frexp_expf(m0_ + e1);
+    n0 = __builtin_amdgcn_ldexpf(m0_, -e);
+    n1 = __builtin_amdgcn_ldexpf(m1_, -e);
+    d0 = __builtin_amdgcn_ldexpf(e0, -e);
+    d1 = __builtin_amdgcn_ldexpf(e1, -e);
+    w0 = __builtin_amdgcn_ldexpf(x0, -e);
+    w1 = __builtin_amdgcn_ldexpf(x1, -e);
+    w2 = __builtin_amdgcn_ldexpf(x2, -e);
+  };
+
+  const int64_t nblk = (L + TB - 1) / TB;
+  if (nblk > 0) {
+    load(0);
+    stage(0);
+  }
+  __syncthreads();
+  for (int64_t blk = 0; blk < nblk; ++blk) {
+    const int cur = static_cast<int>(blk & 1);
+    const int kb = KQB == 1 ? 0 : cur;
+    const int64_t t0 = blk * TB;
+    if (blk + 1 < nblk) load(t0 + TB);
+    if (t0 + TB <= L) {
+#pragma unroll
+      for (int j = 0; j < TB; j += 4) {
+        if constexpr (kVecLds) {
+          const float4 l4 = lds4(s_l[cur][c], j), v4 = lds4(s_v[cur][c], j), k4 = lds4(s_k[kb][ln.s], j);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) step(pick4(l4, i), pick4(v4, i), pick4(k4, i));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) step(s_l[cur][c][j + i], s_v[cur][c][j + i], s_k[kb][ln.s][j + i]);
+        }
+      }
+    } else {
+      const int nv = static_cast<int>(L - t0);
+      for (int j = 0; j < nv; ++j) step(s_l[cur][c][j], s_v[cur][c][j], s_k[kb][ln.s][j]);
+    }
+    if (blk + 1 < nblk) {
+      if constexpr (KQB == 1) __syncthreads();   // every wave is done with this block's k
+      stage(cur ^ 1);
+    }
+    __syncthreads();
+  }
+  if (ln.active) {
+    float4 *out = reinterpret_cast<float4 *>(prm.maps + bms * 8);
+    out[0] = make_float4(n0, n1, d0, d1);
+    out[1] = make_float4(w0, w1, w2, 0.0f);
+  }
+}
+
+// The state entering each chunk, per (b, m, s) lane: from (lam0 or 1, eta0 or 0)
+// the chunk maps are applied in chunk order, lam' = (n0 lam + n1) / (d0 lam + d1)
+// and eta' = (w0 lam + w1 + w2 eta) / (d0 lam + d1) (denominator floored at EPS
+// like mobius_apply). maps [batch, chunks, n, 8]; lam0, eta0 [batch, n] or NULL;
+// lam_start, eta_start [batch, chunks, n].
+__global__ void __launch_bounds__(256) chunk_starts_kernel(const float *__restrict__ maps,
+                                                           const float *__restrict__ lam0,
+                                                           const float *__restrict__ eta0,
+                                                           float *__restrict__ lam_start, float *__restrict__ eta_start,
+                                                           int64_t batch, int64_t chunks, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= batch * n) return;
+  const int64_t b = i / n, e = i % n;
+  float lam = lam0 ? lam0[i] : 1.0f;
+  float eta = eta0 ? eta0[i] : 0.0f;
+  for (int64_t ch = 0; ch < chunks; ++ch) {
+    const int64_t row = (b * chunks + ch) * n + e;
+    lam_start[row] = lam;
+    eta_start[row] = eta;
+    const float4 *m = reinterpret_cast<const float4 *>(maps + row * 8);
+    const float4 nd = m[0], w = m[1];
+    const float den = fmaxf(fmaf(nd.z, lam, nd.w), kEps);
+    const float nl = fmaf(nd.x, lam, nd.y) / den;
+    eta = (fmaf(w.x, lam, w.y) + w.z * eta) / den;
+    lam = nl;
+  }
+}
+
 }  // namespace kla
 
 namespace kla {

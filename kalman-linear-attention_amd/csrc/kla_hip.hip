@@ -28,7 +28,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 13;
+constexpr int kAbiVersion = 14;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -821,6 +821,53 @@ int kla_fused_scan_sensors_bwd(const float *dy, const float *dy_var, const float
   if (rc != KLA_OK) return rc;
   return fused_bwd(fn, dy, dy_var, dlam_fin, deta_fin, sn, k, q, a, p, ck_lam, ck_eta, dv, dobs, dk, dq, da, dp,
                    dlam0, deta0, decode_from_prior, batch, steps, M, S, workspace, workspace_bytes, stream);
+}
+
+int kla_fused_chunk_maps(const kla_sensors *sensors, const float *k, const float *a, const float *p, float *maps,
+                         int64_t batch, int64_t steps, int64_t M, int64_t S, hipStream_t stream) {
+  const char *fn = "kla_fused_chunk_maps";
+  int rc = check_fused_shape(fn, batch, steps, M, S);
+  if (rc != KLA_OK) return rc;
+  SensorIn sn;
+  if ((rc = sensors_from(fn, sensors, M, &sn)) != KLA_OK) return rc;
+  if (batch == 0 || M == 0 || S == 0) return KLA_OK;
+  if (!a || !p || !maps) return fail(KLA_ERR_INVALID_ARG, "%s: a, p and maps must not be NULL", fn);
+  if (steps > 0 && (!sn.v || !sn.lv || !k))
+    return fail(KLA_ERR_INVALID_ARG, "%s: the sensors and k must not be NULL", fn);
+  if (!all_aligned(4, {k, a, p})) return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if (!all_aligned(16, {maps})) return fail(KLA_ERR_ALIGN, "%s: maps not 16-byte aligned", fn);
+  const FusedGeom g = fused_geom(batch, steps, M, S);
+  const int64_t grid = smul(batch, g.groups);
+  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+  const ChunkMapParams prm{sn, k, a, p, maps};
+  return with_sp(S, [&](auto sp) {
+    constexpr int SP = decltype(sp)::value;
+    if (sn.bf16)
+      hipLaunchKernelGGL((fused_chunk_map_kernel<SP, true>), dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads),
+                         0, stream, prm, g);
+    else
+      hipLaunchKernelGGL((fused_chunk_map_kernel<SP, false>), dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads),
+                         0, stream, prm, g);
+    return hip_status(fn, hipGetLastError());
+  });
+}
+
+int kla_chunk_starts(const float *maps, const float *lam0, const float *eta0, float *lam_start, float *eta_start,
+                     int64_t batch, int64_t chunks, int64_t M, int64_t S, hipStream_t stream) {
+  const char *fn = "kla_chunk_starts";
+  if (batch < 0 || chunks < 0 || M < 0 || S < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  const int64_t n = smul(M, S);
+  const int64_t lanes = smul(batch, n);
+  if (lanes >= (1ll << 40) || chunks > (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: problem too large", fn);
+  if (lanes == 0 || chunks == 0) return KLA_OK;
+  if (!maps || !lam_start || !eta_start)
+    return fail(KLA_ERR_INVALID_ARG, "%s: maps, lam_start and eta_start must not be NULL", fn);
+  if (!all_aligned(4, {lam0, eta0, lam_start, eta_start}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if (!all_aligned(16, {maps})) return fail(KLA_ERR_ALIGN, "%s: maps not 16-byte aligned", fn);
+  hipLaunchKernelGGL(chunk_starts_kernel, dim3(static_cast<uint32_t>((lanes + 255) / 256)), dim3(256), 0, stream, maps,
+                     lam0, eta0, lam_start, eta_start, batch, chunks, n);
+  return hip_status(fn, hipGetLastError());
 }
 
 int kla_step_fwd(const float *v, const float *lambda_v, const float *k, const float *q, const float *a,

@@ -18,6 +18,7 @@ lambda_v is formed inside the kernels.
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 from typing import Optional
 
@@ -29,6 +30,63 @@ from kla.ops.hip.scans import _require_device
 _F32 = torch.float32
 # d_state the fused kernels take: a channel's S lanes in one 256-thread workgroup.
 MAX_STATE = 256
+# The time-split forward (inference only): grids below SPLIT_BELOW workgroups
+# per CU are split, into chunks of at least MIN_CHUNK steps, up to about SPLIT_TO
+# workgroups per CU. Measured on MI355X: the chunk-map pass costs about what the
+# forward costs, so a split pays only where the whole grid leaves CUs or issue
+# slots idle -- below one workgroup per CU at d_state <= 16 (whose forward keeps
+# a CU busy with one workgroup), below two at wider states (whose per-step sums
+# over the channel's lanes leave a lone workgroup latency-bound); chunks shorter
+# than 128 steps lose to the map pass and the walk over chunks.
+SPLIT_TO, MIN_CHUNK = 8, 128
+
+
+def _split_below(sp: int) -> int:
+    return 1 if sp <= 16 else 2
+
+
+@functools.cache
+def _cus(index: int) -> int:
+    return torch.cuda.get_device_properties(index).multi_processor_count
+
+
+def time_chunks(B: int, L: int, M: int, S: int, cus: int) -> int:
+    """Chunks the time-split forward cuts each sequence into (1: no split). The
+    grid is B x channel groups (256 / SP channels a workgroup, SP = S rounded up
+    to a power of two, at least 4); below _split_below(SP) workgroups per CU the
+    chunk count doubles while the grid stays below SPLIT_TO per CU, the chunks
+    divide L evenly and stay MIN_CHUNK steps or longer."""
+    sp = 4
+    while sp < S:
+        sp *= 2
+    base = B * -(-M // (256 // sp))
+    if base >= _split_below(sp) * cus:
+        return 1
+    nc = 1
+    while base * nc * 2 <= SPLIT_TO * cus and L % (2 * nc) == 0 and L // (2 * nc) >= MIN_CHUNK:
+        nc *= 2
+    return nc
+
+
+def _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, decode_from_prior, B, L, M, S, nc, dev):
+    """The time-split forward: kla_fused_chunk_maps on the [B * nc, L / nc] view,
+    kla_chunk_starts, then the fused forward on the view from those starts.
+    Returns (lam_fin, eta_fin), the state leaving each sequence's last chunk."""
+    lib, pt = _lib.lib(), _lib.ptr
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    Bp, Lc = B * nc, L // nc
+    f32 = dict(dtype=_F32, device=dev)
+    maps = torch.empty(Bp, M, S, 8, **f32)
+    lam_st, eta_st = torch.empty(Bp, M, S, **f32), torch.empty(Bp, M, S, **f32)
+    _lib.check("kla_fused_chunk_maps", lib.kla_fused_chunk_maps(
+        ctypes.byref(sn), pt(k), pt(a), pt(p), pt(maps), Bp, Lc, M, S, stream))
+    _lib.check("kla_chunk_starts", lib.kla_chunk_starts(
+        pt(maps), pt(lam0), pt(eta0), pt(lam_st), pt(eta_st), B, nc, M, S, stream))
+    fin_l, fin_e = torch.empty(Bp, M, S, **f32), torch.empty(Bp, M, S, **f32)
+    _lib.check("kla_fused_scan_sensors_fwd", lib.kla_fused_scan_sensors_fwd(
+        ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam_st), pt(eta_st), pt(y), pt(y_var), pt(fin_l),
+        pt(fin_e), None, None, int(decode_from_prior), Bp, Lc, M, S, stream))
+    return fin_l.view(B, nc, M, S)[:, -1].contiguous(), fin_e.view(B, nc, M, S)[:, -1].contiguous()
 
 
 def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
@@ -68,6 +126,13 @@ def _fused_fwd_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: t
     ck_lam = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
     ck_eta = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
     if B * M * S == 0:
+        return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
+    nc = 1 if save else time_chunks(B, L, M, S, _cus(dev.index or 0))
+    if nc > 1:
+        sn = _lib.Sensors(v=_lib.ptr(v), ld_v=M, obs=_lib.ptr(lambda_v), ld_obs=M, dtype=_lib.KLA_DTYPE_F32,
+                          log_var=0, obs_var_min=0.0, obs_var_max=math.inf)
+        lam_fin, eta_fin = _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, decode_from_prior, B, L, M, S, nc,
+                                          dev)
         return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
     stream = torch.cuda.current_stream(dev).cuda_stream
     pt = _lib.ptr
@@ -229,6 +294,11 @@ def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torc
     if B * M * S == 0:
         return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
     sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
+    nc = 1 if save else time_chunks(B, L, M, S, _cus(dev.index or 0))
+    if nc > 1:
+        lam_fin, eta_fin = _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var if with_var else None,
+                                          decode_from_prior, B, L, M, S, nc, dev)
+        return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
     pt = _lib.ptr
     _lib.check("kla_fused_scan_sensors_fwd", _lib.lib().kla_fused_scan_sensors_fwd(
         ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam0), pt(eta0), pt(y), pt(y_var) if with_var else None,

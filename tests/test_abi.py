@@ -276,6 +276,73 @@ def test_fused_sensors_validation(lib):
     assert bwd(sensors(), nbytes=n - 4) == _lib.KLA_ERR_WORKSPACE
 
 
+def test_time_split_validation(lib):
+    """kla_fused_chunk_maps and kla_chunk_starts (the time-split forward's two
+    extra passes) check shape, sensors, NULL and alignment before launching."""
+    P = ALIGNED
+    P16 = ALIGNED + 16
+
+    def sensors(**kw):
+        a = dict(v=P, ld_v=6, obs=P, ld_obs=6, dtype=_lib.KLA_DTYPE_F32, log_var=0, obs_var_min=0.0,
+                 obs_var_max=float("inf"))
+        a.update(kw)
+        return _lib.Sensors(**a)
+
+    def maps(k=P, out=P, shape=(2, 5, 6, 16), s=None):
+        s = sensors() if s is None else s
+        return lib.kla_fused_chunk_maps(ctypes.byref(s), k, P, P, out, *shape, None)
+
+    assert maps(shape=(2, 5, 6, 257)) == _lib.KLA_ERR_INVALID_ARG
+    assert maps(shape=(2, -1, 6, 16)) == _lib.KLA_ERR_INVALID_ARG
+    assert maps(shape=(0, 5, 6, 16)) == _lib.KLA_OK
+    assert maps(out=None) == _lib.KLA_ERR_INVALID_ARG
+    assert "maps must not be NULL" in err(lib)
+    assert maps(k=None) == _lib.KLA_ERR_INVALID_ARG
+    assert maps(s=sensors(v=None)) == _lib.KLA_ERR_INVALID_ARG
+    assert maps(s=sensors(dtype=9)) == _lib.KLA_ERR_DTYPE
+    assert maps(k=ODD) == _lib.KLA_ERR_ALIGN
+    assert maps(out=P + 4) == _lib.KLA_ERR_ALIGN
+    assert "16-byte" in err(lib)
+    assert lib.kla_fused_chunk_maps(None, P, P, P, P, 2, 5, 6, 16, None) == _lib.KLA_ERR_INVALID_ARG
+
+    def starts(m=P16, lam0=None, eta0=None, ls=P, es=P, shape=(2, 4, 6, 16)):
+        return lib.kla_chunk_starts(m, lam0, eta0, ls, es, *shape, None)
+
+    assert starts(shape=(-2, 4, 6, 16)) == _lib.KLA_ERR_INVALID_ARG
+    assert starts(shape=(0, 4, 6, 16)) == _lib.KLA_OK
+    assert starts(shape=(2, 0, 6, 16)) == _lib.KLA_OK
+    assert starts(m=None) == _lib.KLA_ERR_INVALID_ARG
+    assert starts(es=None) == _lib.KLA_ERR_INVALID_ARG
+    assert starts(lam0=ODD) == _lib.KLA_ERR_ALIGN
+    assert starts(m=P + 8) == _lib.KLA_ERR_ALIGN
+    assert starts(shape=(2**31, 2**31, 2**31, 16)) == _lib.KLA_ERR_INVALID_ARG
+
+
+def test_time_chunks_plan():
+    """The time-split forward cuts only small grids (below one workgroup per CU at
+    d_state <= 16, two above), into up to eight workgroups per CU, with chunks
+    that divide L and last at least MIN_CHUNK steps."""
+    from kla.ops.hip.fused import MIN_CHUNK, time_chunks
+
+    assert MIN_CHUNK == 128
+    assert time_chunks(4, 4096, 2048, 16, 256) == 1       # C4: 512 workgroups already
+    assert time_chunks(16, 2048, 1024, 16, 256) == 1      # C5 prefill
+    assert time_chunks(2, 2048, 512, 128, 256) == 1       # 512 workgroups of 2 channels
+    assert time_chunks(4, 1024, 1024, 16, 256) == 1       # one workgroup per CU at d_state 16
+    assert time_chunks(1, 2048, 1024, 64, 256) == 8       # one per CU at d_state 64: split
+    assert time_chunks(2, 1024, 512, 16, 256) == 8        # C1: 64 workgroups, 128-step chunks
+    assert time_chunks(1, 2048, 1024, 16, 256) == 16
+    assert time_chunks(1, 4096, 2048, 16, 256) == 16      # 128 -> 2048 workgroups
+    assert time_chunks(1, 100, 1024, 16, 256) == 1
+    assert time_chunks(1, 255, 8, 16, 256) == 1           # odd
+    assert time_chunks(1, 2 * MIN_CHUNK, 8, 16, 256) == 2
+    assert time_chunks(1, 2500, 8, 16, 256) == 4          # 2500 = 4 * 625
+    assert time_chunks(1, 4096, 256, 256, 256) == 8       # 256 single-channel workgroups
+    for B, L, M, S in [(1, 4096, 64, 64), (3, 1000, 200, 32), (1, 65536, 1, 1), (2, 8192, 4096, 16)]:
+        nc = time_chunks(B, L, M, S, 256)
+        assert L % nc == 0 and (nc == 1 or L // nc >= MIN_CHUNK)
+
+
 def test_sensor_row_layouts():
     """Which [B, L, M] views the fused-sensor kernels read in place: rows of one
     stride ld >= M with element (b, t, m) at (b * L + t) * ld + m."""
