@@ -220,6 +220,31 @@ __device__ __forceinline__ void transpose_sum(float (&w)[N], int lane) {
   transpose_stage<0xB1, 0, N * 2 / SP>(w, lane);
 }
 
+// The sums over a channel's lanes in this wave of kCkpt per-step values at
+// once, stored to `row` (a channel's [TB + kPad] tile row in LDS) at steps
+// j0 + 0 .. kCkpt - 1. Up to 16 lanes per channel, transpose_sum leaves lane s
+// the sums of steps (kCkpt / SP) s + r. Wider channels take the 16-lane
+// transpose_sum within each row (lane l then holds its row's sum for step l % 16)
+// and add the row pair (32 lanes) and the wave halves (64 and more, where the
+// wave holds 64 of the channel's lanes): lanes 0-15 of the channel in the wave
+// store its 16 steps. s is the lane's state index, SG the channel's lanes in a
+// wave.
+template <int SP, int N>
+__device__ __forceinline__ void step_sums_to_lds(float (&w)[N], int lane, int s, float *row, int j0) {
+  static_assert(N == 16, "one checkpoint half of steps at a time");
+  if constexpr (SP <= 16) {
+    transpose_sum<SP, N>(w, lane);
+#pragma unroll
+    for (int r = 0; r < N / SP; ++r) row[j0 + (N / SP) * s + r] = w[r];
+  } else {
+    constexpr int SG = lanes_in_wave<SP>();
+    transpose_sum<16, N>(w, lane);
+    float x = row_pair_sum(w[0]);
+    if constexpr (SP >= 64) x = half_pair_sum(x);
+    if (s % SG < 16) row[j0 + s % 16] = x;
+  }
+}
+
 struct FusedLane {
   int64_t b, m;
   int s;
@@ -568,9 +593,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
       if constexpr (VAR) parts_to_global<TB, CH, WPC>(s_yv[cur ^ 1], yvbase + (t0 - TB) * M, M, TB, cols_m);
     }
     // The read-out terms of a kCkpt-step half of the block, summed over s after
-    // the half (transpose_sum) when a channel's lanes fit one 16-lane row.
-    constexpr bool kTr = SP <= 16;
-    float yw[kTr ? kCkpt : 1], vw[kTr ? kCkpt : 1];
+    // the half (step_sums_to_lds).
+    float yw[kCkpt], vw[kCkpt];
     constexpr bool kVecLds = SP >= 16;
     // One step at block position j (position jj within its half); with x4, the
     // step's tile values come from four-step LDS reads.
@@ -588,17 +612,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
         vo = a2 * var + pp;
       }
       const float qq = x4 ? pick4(q4, j % 4) : s_q[KQB == 1 ? 0 : cur][ln.s][j];
-      if constexpr (kTr) {
-        yw[jj] = qq * mean;
-        if constexpr (VAR) vw[jj] = (qq * qq) * vo;
-      } else {
-        const float ys = group_sum<SG>(qq * mean);
-        if (ln.s % SG == 0) s_y[cur][ln.s / SG][c][j] = ys;
-        if constexpr (VAR) {
-          const float vs = group_sum<SG>((qq * qq) * vo);
-          if (ln.s % SG == 0) s_yv[cur][ln.s / SG][c][j] = vs;
-        }
-      }
+      yw[jj] = qq * mean;
+      if constexpr (VAR) vw[jj] = (qq * qq) * vo;
     };
     // Checkpoints enter every kCkpt-step half of the block (TB is a multiple of kCkpt).
 #pragma unroll
@@ -622,7 +637,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
             }
             step(jb, j, kVecLds);
           }
-        } else if constexpr (kTr) {
+        } else {
           // Unrolled: the terms live in registers indexed by j.
 #pragma unroll
           for (int j = 0; j < kCkpt; ++j) {
@@ -633,19 +648,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
               if constexpr (VAR) vw[j] = 0.0f;
             }
           }
-        } else {
-          for (int j = 0; j < kCkpt; ++j)
-            if (th + j < L) step(h * kCkpt + j, j, false);
         }
-        if constexpr (kTr) {
-          transpose_sum<SP, kCkpt>(yw, lane);
-          if constexpr (VAR) transpose_sum<SP, kCkpt>(vw, lane);
-#pragma unroll
-          for (int r = 0; r < kCkpt / SP; ++r) {
-            s_y[cur][0][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = yw[r];
-            if constexpr (VAR) s_yv[cur][0][c][h * kCkpt + (kCkpt / SP) * ln.s + r] = vw[r];
-          }
-        }
+        step_sums_to_lds<SP>(yw, lane, ln.s, s_y[cur][ln.s / SG][c], h * kCkpt);
+        if constexpr (VAR) step_sums_to_lds<SP>(vw, lane, ln.s, s_yv[cur][ln.s / SG][c], h * kCkpt);
       }
     }
     if (blk + 1 < nblk) {
@@ -833,8 +838,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       eh[TB] = eta;
     }
     // dv, dLv contributions of the block's steps, summed over s after the walk
-    // (transpose_sum) when a channel's lanes fit one 16-lane row.
-    constexpr bool kTr = SP <= 16;
+    // (step_sums_to_lds) up to 64 lanes per channel; wider channels sum every
+    // step as it is walked (the 16 more registers would halve their occupancy).
+    constexpr bool kTr = SP <= kWave;
     float dv_w[kTr ? TB : 1], dl_w[kTr ? TB : 1];
     // dk, dq contributions, summed over the wave's four channel rows after the
     // walk (cross_row_transpose_sum) when SP = 16.
@@ -966,13 +972,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       }
     }
     if constexpr (kTr) {
-      transpose_sum<SP, TB>(dv_w, lane);
-      transpose_sum<SP, TB>(dl_w, lane);
-#pragma unroll
-      for (int r = 0; r < TB / SP; ++r) {
-        s_dv[cur][0][c][(TB / SP) * ln.s + r] = dv_w[r];
-        s_dl[cur][0][c][(TB / SP) * ln.s + r] = dl_w[r];
-      }
+      step_sums_to_lds<SP>(dv_w, lane, ln.s, s_dv[cur][ln.s / SG][c], 0);
+      step_sums_to_lds<SP>(dl_w, lane, ln.s, s_dl[cur][ln.s / SG][c], 0);
     }
     acc_a += blk_a;
     acc_a2 += fmaf(-fmaf(pp, blk_x, blk_y), inv_a2 * inv_a2, blk_a2);

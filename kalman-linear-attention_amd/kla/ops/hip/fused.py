@@ -30,19 +30,19 @@ from kla.ops.hip.scans import _require_device
 _F32 = torch.float32
 # d_state the fused kernels take: a channel's S lanes in one 256-thread workgroup.
 MAX_STATE = 256
-# The time-split forward (inference only): grids below SPLIT_BELOW workgroups
-# per CU are split, into chunks of at least MIN_CHUNK steps, up to about SPLIT_TO
-# workgroups per CU. Measured on MI355X: the chunk-map pass costs about what the
-# forward costs, so a split pays only where the whole grid leaves CUs or issue
-# slots idle -- below one workgroup per CU at d_state <= 16 (whose forward keeps
-# a CU busy with one workgroup), below two at wider states (whose per-step sums
-# over the channel's lanes leave a lone workgroup latency-bound); chunks shorter
-# than 128 steps lose to the map pass and the walk over chunks.
+# The time-split forward (inference only): grids below _split_below(SP)
+# workgroups per CU are split, into chunks of at least MIN_CHUNK steps, up to
+# about SPLIT_TO workgroups per CU. Measured on MI355X: the chunk-map pass costs
+# about what the forward costs, so a split pays only where the whole grid leaves
+# CUs or issue slots idle -- below one workgroup per CU up to 64 lanes per
+# channel (one workgroup keeps a CU busy), below two for 128 and 256 (whose
+# channels span several waves and wait on each other); chunks shorter than 128
+# steps lose to the map pass and the walk over chunks.
 SPLIT_TO, MIN_CHUNK = 8, 128
 
 
 def _split_below(sp: int) -> int:
-    return 1 if sp <= 16 else 2
+    return 1 if sp <= 64 else 2
 
 
 @functools.cache

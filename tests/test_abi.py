@@ -319,8 +319,8 @@ def test_time_split_validation(lib):
 
 
 def test_time_chunks_plan():
-    """The time-split forward cuts only small grids (below one workgroup per CU at
-    d_state <= 16, two above), into up to eight workgroups per CU, with chunks
+    """The time-split forward cuts only small grids (below one workgroup per CU up
+    to d_state 64, two above), into up to eight workgroups per CU, with chunks
     that divide L and last at least MIN_CHUNK steps."""
     from kla.ops.hip.fused import MIN_CHUNK, time_chunks
 
@@ -329,7 +329,9 @@ def test_time_chunks_plan():
     assert time_chunks(16, 2048, 1024, 16, 256) == 1      # C5 prefill
     assert time_chunks(2, 2048, 512, 128, 256) == 1       # 512 workgroups of 2 channels
     assert time_chunks(4, 1024, 1024, 16, 256) == 1       # one workgroup per CU at d_state 16
-    assert time_chunks(1, 2048, 1024, 64, 256) == 8       # one per CU at d_state 64: split
+    assert time_chunks(1, 2048, 1024, 64, 256) == 1       # and at d_state 64
+    assert time_chunks(1, 2048, 512, 64, 256) == 16       # half a workgroup per CU: split
+    assert time_chunks(1, 4096, 512, 128, 256) == 8       # one per CU at d_state 128: split
     assert time_chunks(2, 1024, 512, 16, 256) == 8        # C1: 64 workgroups, 128-step chunks
     assert time_chunks(1, 2048, 1024, 16, 256) == 16
     assert time_chunks(1, 4096, 2048, 16, 256) == 16      # 128 -> 2048 workgroups
