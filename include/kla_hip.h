@@ -254,9 +254,10 @@ int kla_fused_scan_sensors_bwd(const float *dy, const float *dy_var, const float
  *     maps [B * chunks, M, S, 8] (n0 n1 d0 d1 w0 w1 w2, one word unused);
  *   kla_chunk_starts (batch = B, chunks): the state entering each chunk,
  *     lam_start, eta_start [B, chunks, M, S], from lam0 (NULL: 1) and eta0
- *     (NULL: 0) through the maps in chunk order;
+ *     (NULL: 0) through the maps in chunk order, and (lam_end, eta_end, both
+ *     or neither) the state after the last chunk, [B, M, S];
  *   kla_fused_scan_sensors_fwd on the view with lam0 / eta0 = the starts: y,
- *     y_var, and the final state in its chunk chunks - 1.
+ *     y_var (its final-state outputs are those of every chunk, [B * chunks, M, S]).
  * The sensors are as for kla_fused_scan_sensors_fwd. The chunked forward of the
  * reference's tiled Metal kernel (src/kla/ops/kernels/mps/tiled_kla_scan.metal:1-35,
  * tiled_kla_scan.py:32-60), which composes the precision and the information
@@ -266,7 +267,8 @@ int kla_fused_scan_sensors_bwd(const float *dy, const float *dy_var, const float
 int kla_fused_chunk_maps(const kla_sensors *sensors, const float *k, const float *a, const float *p, float *maps,
                          int64_t batch, int64_t steps, int64_t M, int64_t S, hipStream_t stream);
 int kla_chunk_starts(const float *maps, const float *lam0, const float *eta0, float *lam_start, float *eta_start,
-                     int64_t batch, int64_t chunks, int64_t M, int64_t S, hipStream_t stream);
+                     float *lam_end, float *eta_end, int64_t batch, int64_t chunks, int64_t M, int64_t S,
+                     hipStream_t stream);
 
 /*
  * One O(1) decode step of the filter for every (b, m, s) lane: kla_step

@@ -66,6 +66,7 @@ struct ConvFwdParams {
   IO *state_out;               // [B, D, K-1] or NULL
   int64_t B, L, D;
   int act;
+  int T;                       // time steps per chunk (a workgroup's share of one sequence)
 };
 
 template <class IO>
@@ -83,14 +84,16 @@ struct ConvBwdParams {
   int act;
 };
 
-// Grid (ceil(D / 256), n_chunks, B); thread = channel d of chunk blockIdx.y.
+// Grid (ceil(D / 256), ceil(L / T), B); thread = channel d of chunk blockIdx.y.
+// The forward has no cross-chunk sums, so its chunk length T is free: the host
+// shortens it (64 down to 8 steps) until the grid has workgroups enough.
 template <class IO, int K>
 __global__ void __launch_bounds__(kConvThreads) causal_conv_fwd_kernel(ConvFwdParams<IO> p) {
   const int64_t d = static_cast<int64_t>(blockIdx.x) * kConvThreads + threadIdx.x;
   if (d >= p.D) return;
   const int64_t b = blockIdx.z;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kConvT;
-  const int64_t t1 = t0 + kConvT < p.L ? t0 + kConvT : p.L;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * p.T;
+  const int64_t t1 = t0 + p.T < p.L ? t0 + p.T : p.L;
   const IO *xb = p.x + b * p.ld_b + d;
   const IO *st = p.state ? p.state + (b * p.D + d) * (K - 1) : nullptr;
 
@@ -107,8 +110,7 @@ __global__ void __launch_bounds__(kConvThreads) causal_conv_fwd_kernel(ConvFwdPa
     win[j] = q < K - 1 ? (st ? io_load(st + q) : 0.0f) : io_load(xb + (q - (K - 1)) * p.ld_t);
   }
   IO *yb = p.y + b * p.L * p.D + d;
-  for (int64_t t = t0; t < t1; ++t) {
-    const float xt = io_load(xb + t * p.ld_t);
+  auto step = [&](int64_t t, float xt) {
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < K - 1; ++j) acc += w[j] * win[j];
@@ -118,7 +120,18 @@ __global__ void __launch_bounds__(kConvThreads) causal_conv_fwd_kernel(ConvFwdPa
 #pragma unroll
     for (int j = 0; j + 1 < K - 1; ++j) win[j] = win[j + 1];
     if (K > 1) win[K - 2] = xt;
+  };
+  // Four steps' loads in flight before their stores (y may not be assumed apart
+  // from x by the compiler, so it would not hoist them itself).
+  int64_t t = t0;
+  for (; t + 4 <= t1; t += 4) {
+    float xs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) xs[u] = io_load(xb + (t + u) * p.ld_t);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) step(t + u, xs[u]);
   }
+  for (; t < t1; ++t) step(t, io_load(xb + t * p.ld_t));
   // The chunk that ends the sequence holds xpad[L : L + K - 1] in its window.
   if (p.state_out && t1 == p.L) {
     IO *so = p.state_out + (b * p.D + d) * (K - 1);

@@ -1226,11 +1226,13 @@ __global__ void __launch_bounds__(kFusedThreads) fused_chunk_map_kernel(ChunkMap
 // the chunk maps are applied in chunk order, lam' = (n0 lam + n1) / (d0 lam + d1)
 // and eta' = (w0 lam + w1 + w2 eta) / (d0 lam + d1) (denominator floored at EPS
 // like mobius_apply). maps [batch, chunks, n, 8]; lam0, eta0 [batch, n] or NULL;
-// lam_start, eta_start [batch, chunks, n].
+// lam_start, eta_start [batch, chunks, n]; lam_end, eta_end [batch, n] (the state
+// after the last chunk) or NULL.
 __global__ void __launch_bounds__(256) chunk_starts_kernel(const float *__restrict__ maps,
                                                            const float *__restrict__ lam0,
                                                            const float *__restrict__ eta0,
                                                            float *__restrict__ lam_start, float *__restrict__ eta_start,
+                                                           float *__restrict__ lam_end, float *__restrict__ eta_end,
                                                            int64_t batch, int64_t chunks, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= batch * n) return;
@@ -1247,6 +1249,10 @@ __global__ void __launch_bounds__(256) chunk_starts_kernel(const float *__restri
     const float nl = fmaf(nd.x, lam, nd.y) / den;
     eta = (fmaf(w.x, lam, w.y) + w.z * eta) / den;
     lam = nl;
+  }
+  if (lam_end) {
+    lam_end[i] = lam;
+    eta_end[i] = eta;
   }
 }
 

@@ -41,6 +41,7 @@ struct TailParams {
   int64_t rows, M;
   // forward
   OUT *out;                      // [rows, M] dense
+  int64_t rows_per;              // rows per workgroup of the forward
   // backward
   const OUT *dout;               // [rows, M] dense
   float *dy;                     // [rows, M] dense
@@ -130,13 +131,15 @@ __device__ __forceinline__ void tail_values(const TailParams<IO, OUT> &p, int64_
   }
 }
 
-// Grid (ceil(rows / kTailRows), ceil(M / (256 V))); thread = V consecutive columns of a row block.
+// Grid (ceil(rows / rows_per), ceil(M / (256 V))); thread = V consecutive columns
+// of a row block. The forward sums nothing across rows, so its row blocks can be
+// short (the host picks rows_per, 16 down to 1, to give the grid workgroups enough).
 template <class IO, class OUT, int V>
 __global__ void __launch_bounds__(kTailThreads) gate_skip_fwd_kernel(TailParams<IO, OUT> p) {
   const int64_t m = (static_cast<int64_t>(blockIdx.y) * kTailThreads + threadIdx.x) * V;
   if (m >= p.M) return;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kTailRows;
-  const int64_t r1 = r0 + kTailRows < p.rows ? r0 + kTailRows : p.rows;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * p.rows_per;
+  const int64_t r1 = r0 + p.rows_per < p.rows ? r0 + p.rows_per : p.rows;
   for (int64_t r = r0; r < r1; ++r) {
     float y[V], t[V], gg[V], resv[V], gatev[V];
     vload<V>(p.y + r * p.M + m, y);

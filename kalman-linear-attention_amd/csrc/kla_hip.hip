@@ -853,7 +853,8 @@ int kla_fused_chunk_maps(const kla_sensors *sensors, const float *k, const float
 }
 
 int kla_chunk_starts(const float *maps, const float *lam0, const float *eta0, float *lam_start, float *eta_start,
-                     int64_t batch, int64_t chunks, int64_t M, int64_t S, hipStream_t stream) {
+                     float *lam_end, float *eta_end, int64_t batch, int64_t chunks, int64_t M, int64_t S,
+                     hipStream_t stream) {
   const char *fn = "kla_chunk_starts";
   if (batch < 0 || chunks < 0 || M < 0 || S < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
   const int64_t n = smul(M, S);
@@ -862,11 +863,12 @@ int kla_chunk_starts(const float *maps, const float *lam0, const float *eta0, fl
   if (lanes == 0 || chunks == 0) return KLA_OK;
   if (!maps || !lam_start || !eta_start)
     return fail(KLA_ERR_INVALID_ARG, "%s: maps, lam_start and eta_start must not be NULL", fn);
-  if (!all_aligned(4, {lam0, eta0, lam_start, eta_start}))
+  if (!lam_end != !eta_end) return fail(KLA_ERR_INVALID_ARG, "%s: lam_end and eta_end go together", fn);
+  if (!all_aligned(4, {lam0, eta0, lam_start, eta_start, lam_end, eta_end}))
     return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
   if (!all_aligned(16, {maps})) return fail(KLA_ERR_ALIGN, "%s: maps not 16-byte aligned", fn);
   hipLaunchKernelGGL(chunk_starts_kernel, dim3(static_cast<uint32_t>((lanes + 255) / 256)), dim3(256), 0, stream, maps,
-                     lam0, eta0, lam_start, eta_start, batch, chunks, n);
+                     lam0, eta0, lam_start, eta_start, lam_end, eta_end, batch, chunks, n);
   return hip_status(fn, hipGetLastError());
 }
 
@@ -1016,10 +1018,14 @@ int kla_causal_conv_fwd(int dtype, const void *x, int64_t ld_t, int64_t ld_b, co
                            stream, static_cast<const IO *>(state), static_cast<IO *>(state_out), n_state);
       return hip_status(fn, hipGetLastError());
     }
+    // Chunks of 64 steps, halved down to 8 while the grid is under 1024 workgroups.
+    const int64_t col_blocks = (channels + kConvThreads - 1) / kConvThreads;
+    int T = kConvT;
+    while (T > 8 && col_blocks * batch * ((steps + T - 1) / T) < 1024) T /= 2;
     ConvFwdParams<IO> p{static_cast<const IO *>(x), ld_t, ld_b, static_cast<const IO *>(state), weight, bias,
-                        static_cast<IO *>(y), static_cast<IO *>(state_out), batch, steps, channels, activation};
-    const dim3 grid(static_cast<uint32_t>((channels + kConvThreads - 1) / kConvThreads),
-                    static_cast<uint32_t>(conv_chunks(steps)), static_cast<uint32_t>(batch));
+                        static_cast<IO *>(y), static_cast<IO *>(state_out), batch, steps, channels, activation, T};
+    const dim3 grid(static_cast<uint32_t>(col_blocks), static_cast<uint32_t>((steps + T - 1) / T),
+                    static_cast<uint32_t>(batch));
     return with_k(kernel_size, [&](auto kc) {
       constexpr int K = decltype(kc)::value;
       hipLaunchKernelGGL((causal_conv_fwd_kernel<IO, K>), grid, dim3(kConvThreads), 0, stream, p);
@@ -1149,12 +1155,16 @@ int kla_gate_skip_fwd(int dtype, int out_dtype, const float *y, const void *resi
       p.rows = rows;
       p.M = M;
       p.out = static_cast<OUT *>(out);
-      if (tail_wide(M, ld_res, ld_gate, {y, residual, gate, lambda_vector ? lambda_skip : nullptr, out}))
-        hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, OUT, 8>), tail_grid(rows, M, 8), dim3(kTailThreads), 0, stream,
-                           p);
+      const int V = tail_wide(M, ld_res, ld_gate, {y, residual, gate, lambda_vector ? lambda_skip : nullptr, out}) ? 8 : 1;
+      // Row blocks of 16, halved down to 1 while the grid is under 1024 workgroups.
+      const int64_t col_blocks = (M + kTailThreads * V - 1) / (kTailThreads * V);
+      p.rows_per = kTailRows;
+      while (p.rows_per > 1 && col_blocks * ((rows + p.rows_per - 1) / p.rows_per) < 1024) p.rows_per /= 2;
+      const dim3 grid(static_cast<uint32_t>((rows + p.rows_per - 1) / p.rows_per), static_cast<uint32_t>(col_blocks));
+      if (V == 8)
+        hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, OUT, 8>), grid, dim3(kTailThreads), 0, stream, p);
       else
-        hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, OUT, 1>), tail_grid(rows, M, 1), dim3(kTailThreads), 0, stream,
-                           p);
+        hipLaunchKernelGGL((gate_skip_fwd_kernel<IO, OUT, 1>), grid, dim3(kTailThreads), 0, stream, p);
       return hip_status(fn, hipGetLastError());
     });
   });

@@ -60,7 +60,7 @@ _SIGNATURES = {
     "kla_fused_scan_sensors_bwd": (ctypes.c_int, [_p] * 19 + [ctypes.c_int] + [_i64] * 4
                                    + [_p, ctypes.c_size_t, _p]),
     "kla_fused_chunk_maps": (ctypes.c_int, [_p] * 5 + [_i64] * 4 + [_p]),
-    "kla_chunk_starts": (ctypes.c_int, [_p] * 5 + [_i64] * 4 + [_p]),
+    "kla_chunk_starts": (ctypes.c_int, [_p] * 7 + [_i64] * 4 + [_p]),
     "kla_step_fwd": (ctypes.c_int, [_p] * 12 + [ctypes.c_int] + [_i64] * 3 + [_p]),
     "kla_decode_step_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _p, _p, _i64] + [_p] * 10
                             + [_i64] * 3 + [_p]),

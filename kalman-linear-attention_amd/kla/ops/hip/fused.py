@@ -71,22 +71,25 @@ def time_chunks(B: int, L: int, M: int, S: int, cus: int) -> int:
 def _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, decode_from_prior, B, L, M, S, nc, dev):
     """The time-split forward: kla_fused_chunk_maps on the [B * nc, L / nc] view,
     kla_chunk_starts, then the fused forward on the view from those starts.
-    Returns (lam_fin, eta_fin), the state leaving each sequence's last chunk."""
+    Returns (lam_fin, eta_fin), the state after each sequence's last chunk (from
+    the chunk maps, written [B, M, S] by kla_chunk_starts)."""
     lib, pt = _lib.lib(), _lib.ptr
     stream = torch.cuda.current_stream(dev).cuda_stream
     Bp, Lc = B * nc, L // nc
     f32 = dict(dtype=_F32, device=dev)
     maps = torch.empty(Bp, M, S, 8, **f32)
     lam_st, eta_st = torch.empty(Bp, M, S, **f32), torch.empty(Bp, M, S, **f32)
+    lam_fin, eta_fin = torch.empty(B, M, S, **f32), torch.empty(B, M, S, **f32)
     _lib.check("kla_fused_chunk_maps", lib.kla_fused_chunk_maps(
         ctypes.byref(sn), pt(k), pt(a), pt(p), pt(maps), Bp, Lc, M, S, stream))
     _lib.check("kla_chunk_starts", lib.kla_chunk_starts(
-        pt(maps), pt(lam0), pt(eta0), pt(lam_st), pt(eta_st), B, nc, M, S, stream))
-    fin_l, fin_e = torch.empty(Bp, M, S, **f32), torch.empty(Bp, M, S, **f32)
+        pt(maps), pt(lam0), pt(eta0), pt(lam_st), pt(eta_st), pt(lam_fin), pt(eta_fin), B, nc, M, S, stream))
+    # Every chunk's final state (unused) lands in the maps' buffer, no longer read.
+    scratch = maps.view(-1)
     _lib.check("kla_fused_scan_sensors_fwd", lib.kla_fused_scan_sensors_fwd(
-        ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam_st), pt(eta_st), pt(y), pt(y_var), pt(fin_l),
-        pt(fin_e), None, None, int(decode_from_prior), Bp, Lc, M, S, stream))
-    return fin_l.view(B, nc, M, S)[:, -1].contiguous(), fin_e.view(B, nc, M, S)[:, -1].contiguous()
+        ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam_st), pt(eta_st), pt(y), pt(y_var), pt(scratch),
+        pt(scratch[Bp * M * S:]), None, None, int(decode_from_prior), Bp, Lc, M, S, stream))
+    return lam_fin, eta_fin
 
 
 def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:

@@ -305,8 +305,8 @@ def test_time_split_validation(lib):
     assert "16-byte" in err(lib)
     assert lib.kla_fused_chunk_maps(None, P, P, P, P, 2, 5, 6, 16, None) == _lib.KLA_ERR_INVALID_ARG
 
-    def starts(m=P16, lam0=None, eta0=None, ls=P, es=P, shape=(2, 4, 6, 16)):
-        return lib.kla_chunk_starts(m, lam0, eta0, ls, es, *shape, None)
+    def starts(m=P16, lam0=None, eta0=None, ls=P, es=P, le=None, ee=None, shape=(2, 4, 6, 16)):
+        return lib.kla_chunk_starts(m, lam0, eta0, ls, es, le, ee, *shape, None)
 
     assert starts(shape=(-2, 4, 6, 16)) == _lib.KLA_ERR_INVALID_ARG
     assert starts(shape=(0, 4, 6, 16)) == _lib.KLA_OK
@@ -315,6 +315,9 @@ def test_time_split_validation(lib):
     assert starts(es=None) == _lib.KLA_ERR_INVALID_ARG
     assert starts(lam0=ODD) == _lib.KLA_ERR_ALIGN
     assert starts(m=P + 8) == _lib.KLA_ERR_ALIGN
+    assert starts(le=P) == _lib.KLA_ERR_INVALID_ARG
+    assert "go together" in err(lib)
+    assert starts(le=P, ee=ODD) == _lib.KLA_ERR_ALIGN
     assert starts(shape=(2**31, 2**31, 2**31, 16)) == _lib.KLA_ERR_INVALID_ARG
 
 
