@@ -278,37 +278,30 @@ __device__ __forceinline__ FusedLane fused_lane(const FusedGeom &g) {
   return ln;
 }
 
-// One step of the filter; returns lam_t and leaves the intermediates the
-// backward needs in the out-parameters. The fused kernels are VALU-bound, so
-// quotients are formed with the hardware reciprocal (v_rcp_f32, 1 ulp) times the
-// numerator instead of the ~10-instruction IEEE division: a relative error of
-// ~2 ulp per step, which the contractive recurrence does not amplify.
-struct StepIO {
-  float phi, r, A, inv_den, alpha, inv_Da;
-};
-
+// One step of the filter (filter_step below). The fused kernels are VALU-bound,
+// so quotients are formed with the hardware reciprocal (v_rcp_f32, 1 ulp) times
+// the numerator instead of the ~10-instruction IEEE division: a relative error
+// of ~2 ulp per step, which the contractive recurrence does not amplify.
 constexpr float kInvEps = 1.0f / kEps;
-
-// 1 / max(a2 + p' lam, EPS) from 1 / den: den = C lam + 1 with C = p'/a2, so
-// a2 + p' lam = a2 den, and its reciprocal is inv_den / a2 (one multiply where
-// a second v_rcp would be). `ok` is the unclamped case a2 + p' lam >= EPS.
-__device__ __forceinline__ float inv_Da_of(float inv_den, float inv_a2, bool ok) {
-  return ok ? inv_den * inv_a2 : kInvEps;
-}
 
 __device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-__device__ __forceinline__ float filter_step(float lam, float &eta, float sig, float vv, float kk, float a_s,
-                                             float a2, float pp, float inv_a2, float C, StepIO &io) {
-  io.phi = sig * (kk * kk);
-  io.r = (vv * sig) * kk;
-  io.A = (1.0f + pp * io.phi) * inv_a2;
-  io.inv_den = rcp(C * lam + 1.0f);
-  const float lam_t = (io.A * lam + io.phi) * io.inv_den;
-  io.inv_Da = inv_Da_of(io.inv_den, inv_a2, a2 + pp * lam >= kEps);
-  io.alpha = a_s * io.inv_Da;
-  eta = io.alpha * eta + io.r;
-  return lam_t;
+// The precision update lam_t = (A lam + phi) / den, A = (1 + p' phi)/a2,
+// den = C lam + 1, C = p'/a2, in the form the kernels evaluate: A = 1/a2 + C phi
+// gives A lam + phi = lam/a2 + phi den, so
+//   lam_t = lam idn_a + phi,   idn_a = 1/(a2 den)
+// (one fma after the reciprocal; d lam_t / d phi = 1 exactly). The gain
+// alpha = a / max(a2 + p' lam, EPS) uses a2 + p' lam = a2 den: its reciprocal is
+// idn_a, and min(idn_a, 1/EPS) is the clamp for every den > 0 (the domain of the
+// filter: den = C lam + 1 is not clamped). phi = Lv k^2 and r = (v Lv) k come in
+// from the caller (from the k^2 and v Lv tiles the kernels stage per block).
+// Returns lam_t; inv_den = 1/den is left for the backward.
+__device__ __forceinline__ float filter_step(float lam, float &eta, float phi, float r, float a_s, float inv_a2,
+                                             float C, float &inv_den) {
+  inv_den = rcp(fmaf(C, lam, 1.0f));
+  const float idn_a = inv_den * inv_a2;
+  eta = fmaf(a_s * fminf(idn_a, kInvEps), eta, r);
+  return fmaf(lam, idn_a, phi);
 }
 
 // ------------------------------------------------------- block staging
@@ -359,6 +352,27 @@ __device__ __forceinline__ void tile_to_lds(const TileRegs<TB, W> &r, float (*ld
     const int e = tid + i * kFusedThreads;
     if (e < TB * W) lds[e % W][e / W] = r.x[i];
   }
+}
+
+// The elementwise product x * y of two staged tiles (y = x gives k^2 from k,
+// y = Lv gives v Lv from v), formed once per block for all the lanes that read
+// it, so the per-step work of a lane loses a multiply.
+template <int TB, int W>
+__device__ __forceinline__ void tile_mul_to_lds(const TileRegs<TB, W> &x, const TileRegs<TB, W> &y,
+                                                float (*lds)[TB + kPad]) {
+  TileRegs<TB, W> r;
+#pragma unroll
+  for (int i = 0; i < TileRegs<TB, W>::N; ++i) r.x[i] = x.x[i] * y.x[i];
+  tile_to_lds<TB, W>(r, lds);
+}
+
+// 2 x of a staged tile (exact).
+template <int TB, int W>
+__device__ __forceinline__ void tile_twice_to_lds(const TileRegs<TB, W> &x, float (*lds)[TB + kPad]) {
+  TileRegs<TB, W> r;
+#pragma unroll
+  for (int i = 0; i < TileRegs<TB, W>::N; ++i) r.x[i] = x.x[i] + x.x[i];
+  tile_to_lds<TB, W>(r, lds);
 }
 
 // LDS [W][TB + 4] -> global rows `row0 + t * ld`, columns c < cols.
@@ -516,19 +530,27 @@ __device__ __forceinline__ void to_precision(TileRegs<TB, W> &r, const SensorIn 
 
 // VAR: y_var is produced (prm.yvar non-NULL); without it the variance read-out
 // is skipped altogether.
+// 8 to 32 lanes per channel: held to three waves per SIMD (their registers fit
+// 168 with at most a couple of spilled words).
 template <int SP, bool PRIOR, bool BF16, bool VAR>
-__global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdParams prm, FusedGeom g) {
+__global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(SP >= 8 && SP <= 32 ? 3 : 1)))
+    fused_kla_fwd_kernel(FusedFwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int WPC = waves_per_channel<SP>();
   constexpr int SG = lanes_in_wave<SP>();
   // Wide channels stage shorter blocks: the [SP, TB] k and q tiles fill the LDS.
   constexpr int TB = SP >= 128 ? kCkpt : kFusedTB;
-  __shared__ __align__(16) float s_v[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
+  // s_sv holds v Lv (the information statistic's channel factor), s_l Lv.
+  __shared__ __align__(16) float s_sv[2][CH][TB + kPad], s_l[2][CH][TB + kPad];
   // The [SP, TB] k and q tiles: double-buffered, except at 256 lanes per channel
   // (40 KiB a buffer), where one buffer and a barrier before it is refilled let
   // more than one workgroup share a CU.
   constexpr int KQB = SP >= 256 ? 1 : 2;
   __shared__ __align__(16) float s_k[KQB][SP][TB + kPad], s_q[KQB][SP][TB + kPad];
+  // k^2 staged beside k up to 64 lanes per channel (wider channels square k per
+  // step: their k tiles already fill the LDS).
+  constexpr bool kK2 = SP <= kWave;
+  __shared__ __align__(16) float s_k2[kK2 ? KQB : 1][kK2 ? SP : 1][TB + kPad];
   __shared__ float s_y[2][WPC][CH][TB + kPad], s_yv[2][WPC][CH][TB + kPad];
 
   const FusedLane ln = fused_lane<SP>(g);
@@ -566,10 +588,11 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
   auto stage = [&](int buf) {
     widen_sensor<TB, CH, BF16>(rv);
     widen_sensor<TB, CH, BF16>(rl);
-    tile_to_lds<TB, CH>(rv, s_v[buf]);
     to_precision<TB, CH>(rl, sn);
+    tile_mul_to_lds<TB, CH>(rv, rl, s_sv[buf]);
     tile_to_lds<TB, CH>(rl, s_l[buf]);
     tile_to_lds<TB, SP>(rk, s_k[KQB == 1 ? 0 : buf]);
+    if constexpr (kK2) tile_mul_to_lds<TB, SP>(rk, rk, s_k2[KQB == 1 ? 0 : buf]);
     tile_to_lds<TB, SP>(rq, s_q[KQB == 1 ? 0 : buf]);
   };
 
@@ -598,13 +621,15 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
     constexpr bool kVecLds = SP >= 16;
     // One step at block position j (position jj within its half); with x4, the
     // step's tile values come from four-step LDS reads.
-    float4 l4{}, v4{}, k4{}, q4{};
+    float4 l4{}, v4{}, k4{}, q4{}, k24{};
     auto step = [&](int j, int jj, bool x4) {
-      StepIO io;
+      const int kb = KQB == 1 ? 0 : cur;
       const float sig = x4 ? pick4(l4, j % 4) : s_l[cur][c][j];
-      const float vv = x4 ? pick4(v4, j % 4) : s_v[cur][c][j];
-      const float kk = x4 ? pick4(k4, j % 4) : s_k[KQB == 1 ? 0 : cur][ln.s][j];
-      lam = filter_step(lam, eta, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
+      const float sv = x4 ? pick4(v4, j % 4) : s_sv[cur][c][j];
+      const float kk = x4 ? pick4(k4, j % 4) : s_k[kb][ln.s][j];
+      const float k2 = !kK2 ? kk * kk : x4 ? pick4(k24, j % 4) : s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0][j];
+      float inv_den;
+      lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, inv_a2, C, inv_den);
       const float var = rcp(fmaxf(lam, kEps));
       float mean = eta * var, vo = var;
       if (PRIOR) {
@@ -631,8 +656,9 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
             const int jb = h * kCkpt + j;
             if (kVecLds && jb % 4 == 0) {
               l4 = lds4(s_l[cur][c], jb);
-              v4 = lds4(s_v[cur][c], jb);
+              v4 = lds4(s_sv[cur][c], jb);
               k4 = lds4(s_k[KQB == 1 ? 0 : cur][ln.s], jb);
+              if constexpr (kK2) k24 = lds4(s_k2[kK2 && KQB == 2 ? cur : 0][kK2 ? ln.s : 0], jb);
               q4 = lds4(s_q[KQB == 1 ? 0 : cur][ln.s], jb);
             }
             step(jb, j, kVecLds);
@@ -676,7 +702,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_fwd_kernel(FusedFwdPa
 // VAR: a y_var gradient is given (prm.dyvar non-NULL); without it the
 // variance read-out's adjoint is skipped (a zero gradient).
 template <int SP, bool PRIOR, bool BF16, bool VAR>
-__global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdParams prm, FusedGeom g) {
+__global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(SP >= 8 ? 2 : 1)))
+    fused_kla_bwd_kernel(FusedBwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int NW = kFusedThreads / kWave;
   constexpr int WPC = waves_per_channel<SP>();
@@ -691,12 +718,25 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
   __shared__ __align__(16) float s_k[KQB][SP][TB + kPad], s_q[KQB][SP][TB + kPad];
   __shared__ float s_dv[2][WPC][CH][TB + kPad], s_dl[2][WPC][CH][TB + kPad];
   __shared__ float s_lf[2][CH][TB + kPad];   // log sigma^2 gradient factors (log_var sensors)
+  // Per-block products of the staged tiles: v Lv and 2 Lv per channel, k^2 per
+  // state lane (up to 64 lanes per channel; wider channels square k per step).
+  // At 4 lanes per channel (64 channels a workgroup) 2 Lv is formed per step
+  // instead, which keeps the LDS at two workgroups per CU.
+  constexpr bool kK2 = SP <= kWave;
+  constexpr bool kS2 = SP >= 8;
+  __shared__ __align__(16) float s_sv[2][CH][TB + kPad], s_s2[kS2 ? 2 : 1][kS2 ? CH : 1][TB + kPad];
+  __shared__ __align__(16) float s_k2[kK2 ? KQB : 1][kK2 ? SP : 1][TB + kPad];
   // Per-(step, s) sums of a channel slot, double-buffered like the tiles where
   // it is small; from 64 lanes per channel on (64 KiB a buffer) one buffer and a
   // barrier between the flush that reads it and the walk that refills it, which
   // halves the backward's LDS and lets two workgroups share a CU.
   constexpr int RB = SP >= kWave ? 1 : 2;
   __shared__ float s_red[RB][2][TB][NW / WPC][SP];
+  // Blocks wholly inside the sequence run as one straight block of code (no
+  // per-step bound) where that code still fits two waves per SIMD without
+  // spills; elsewhere (4, 8 or 256 lanes per channel, the prior's read-out, the
+  // variance's adjoint) every block keeps the per-step bound.
+  constexpr bool kFullBlocks = SP >= 16 && SP <= 128 && !PRIOR && !VAR;
 
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
@@ -743,9 +783,12 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
       tile_to_lds<TB, CH>(rf, s_lf[buf]);
     }
     tile_to_lds<TB, CH>(rl, s_l[buf]);
+    tile_mul_to_lds<TB, CH>(rv, rl, s_sv[buf]);
+    if constexpr (kS2) tile_twice_to_lds<TB, CH>(rl, s_s2[kS2 ? buf : 0]);
     tile_to_lds<TB, CH>(rdy, s_dy[buf]);
     if constexpr (VAR) tile_to_lds<TB, CH>(rdyv, s_dyv[buf]);
     tile_to_lds<TB, SP>(rk, s_k[KQB == 1 ? 0 : buf]);
+    if constexpr (kK2) tile_mul_to_lds<TB, SP>(rk, rk, s_k2[KQB == 1 ? 0 : buf]);
     tile_to_lds<TB, SP>(rq, s_q[KQB == 1 ? 0 : buf]);
   };
   // Outputs of block c (buffer `buf`): dv, dLv rows, and the workgroup's
@@ -800,43 +843,57 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     // bound is then a scalar compare (there is no 64-bit scalar less-than).
     const int nv = static_cast<int>(L - t0 < TB ? L - t0 : TB);
     // Over the block: lam_{t-1}, eta_{t-1} (lh[TB], eh[TB]: the state after the
-    // block), and each step's 1/den and posterior variance, kept from the replay.
-    float lh[TB + 1], eh[TB + 1], idn[TB], vr[TB];
+    // block), and each step's 1/den, kept from the replay (the posterior variance
+    // 1/lam_t is formed again in the walk: 16 registers fewer).
+    float lh[TB + 1], eh[TB + 1], idn[TB];
     // da, dp sum over all steps: accumulate each block apart and add the block
     // totals (two-level summation keeps fp32 rounding at ~(TB + L/TB) ulp).
     // The terms through A = (1 + p' phi)/a2 and C = p'/a2 are gathered as
     // X = sum (dA phi + dC) and Y = sum dA and applied once per block:
     // dp += X/a2, d(a2) -= (Y + p' X)/a2^2.
     float blk_a = 0.0f, blk_a2 = 0.0f, blk_p = 0.0f, blk_x = 0.0f, blk_y = 0.0f;
-    {
-      const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
+    const int kb = KQB == 1 ? 0 : cur;
+    // Whether no clamp acts in the block: every lam of the block (the checkpoint
+    // and each step's lam_t) >= EPS. Then var = 1/lam_t has its plain derivative,
+    // and lam' >= 0 makes a2 + p' lam' >= a2 >= EPS, so alpha's clamp is idle too.
+    bool unclamped = true;
+    const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
+    // The replay from the block's checkpoint. FULL: every step of the block lies
+    // inside the sequence (all blocks but the sequence's last partial one), so
+    // the steps need no bound and the block is one straight run of code.
+    auto replay = [&](auto full_c) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_c)::value;
       float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
       float eta = ln.active ? prm.ck_eta[ci] : 0.0f;
-      float4 l4{}, v4{}, k4{};
+      unclamped = lam >= kEps;
+      float4 l4{}, v4{}, k4{}, k24{};
 #pragma unroll
       for (int j = 0; j < TB; ++j) {
         if (kVecLds && j % 4 == 0) {
+          // (A compiler barrier: the next four steps' LDS reads are not hoisted
+          // into earlier steps, which would hold more registers than two waves
+          // per SIMD allow.)
+          asm volatile("" ::: "memory");
           l4 = lds4(s_l[cur][c], j);
-          v4 = lds4(s_v[cur][c], j);
-          k4 = lds4(s_k[KQB == 1 ? 0 : cur][ln.s], j);
+          v4 = lds4(s_sv[cur][c], j);
+          k4 = lds4(s_k[kb][ln.s], j);
+          if constexpr (kK2) k24 = lds4(s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0], j);
         }
         lh[j] = lam;
         eh[j] = eta;
-        idn[j] = 0.0f;
-        vr[j] = 0.0f;
-        if (j < nv) {
-          StepIO io;
+        if (!FULL) idn[j] = 0.0f;
+        if (FULL || j < nv) {
           const float sig = kVecLds ? pick4(l4, j % 4) : s_l[cur][c][j];
-          const float vv = kVecLds ? pick4(v4, j % 4) : s_v[cur][c][j];
-          const float kk = kVecLds ? pick4(k4, j % 4) : s_k[KQB == 1 ? 0 : cur][ln.s][j];
-          lam = filter_step(lam, eta, sig, vv, kk, a_s, a2, pp, inv_a2, C, io);
-          idn[j] = io.inv_den;
-          vr[j] = rcp(fmaxf(lam, kEps));
+          const float sv = kVecLds ? pick4(v4, j % 4) : s_sv[cur][c][j];
+          const float kk = kVecLds ? pick4(k4, j % 4) : s_k[kb][ln.s][j];
+          const float k2 = !kK2 ? kk * kk : kVecLds ? pick4(k24, j % 4) : s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0][j];
+          lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, inv_a2, C, idn[j]);
+          if (FULL) unclamped = unclamped && lam >= kEps;
         }
       }
       lh[TB] = lam;
       eh[TB] = eta;
-    }
+    };
     // dv, dLv contributions of the block's steps, summed over s after the walk
     // (step_sums_to_lds) up to 64 lanes per channel; wider channels sum every
     // step as it is walked (the 16 more registers would halve their occupancy).
@@ -846,119 +903,143 @@ __global__ void __launch_bounds__(kFusedThreads) fused_kla_bwd_kernel(FusedBwdPa
     // walk (cross_row_transpose_sum) when SP = 16.
     constexpr bool kRows = SP == 16;
     float dk_w[kRows ? TB : 1], dq_w[kRows ? TB : 1];
-    float4 v4{}, l4{}, dy4{}, k4{}, q4{};
+    // The adjoint walk over the block. CLAMPS: with the clamps' branches (the
+    // general case); without, for a block where no clamp acts (the same values).
+    // FULL as for the replay.
+    // No implicit contraction in the walk: every fused multiply-add is written
+    // as fmaf, so the four copies (with or without clamps, guarded or full)
+    // round alike wherever their code differs only by a select or a branch.
+    auto walk = [&](auto clamps_c, auto full_c) __attribute__((always_inline)) {
+#pragma clang fp contract(off)
+      constexpr bool CLAMPS = decltype(clamps_c)::value;
+      constexpr bool FULL = decltype(full_c)::value;
+      float4 sv4{}, s24{}, dy4{}, k4{}, q4{};
 #pragma unroll
-    for (int j = TB - 1; j >= 0; --j) {
-      if (kVecLds && j % 4 == 3) {
-        v4 = lds4(s_v[cur][c], j - 3);
-        l4 = lds4(s_l[cur][c], j - 3);
-        dy4 = lds4(s_dy[cur][c], j - 3);
-        k4 = lds4(s_k[KQB == 1 ? 0 : cur][ln.s], j - 3);
-        q4 = lds4(s_q[KQB == 1 ? 0 : cur][ln.s], j - 3);
-      }
-      float dk_c = 0.0f, dq_c = 0.0f;
-      if constexpr (kTr) {
-        dv_w[j] = 0.0f;
-        dl_w[j] = 0.0f;
-      }
-      if (j < nv) {
-        const float vv = kVecLds ? pick4(v4, j % 4) : s_v[cur][c][j];
-        const float sig = kVecLds ? pick4(l4, j % 4) : s_l[cur][c][j];
-        const float dy = kVecLds ? pick4(dy4, j % 4) : s_dy[cur][c][j];
-        const float kk = kVecLds ? pick4(k4, j % 4) : s_k[KQB == 1 ? 0 : cur][ln.s][j];
-        const float qq = kVecLds ? pick4(q4, j % 4) : s_q[KQB == 1 ? 0 : cur][ln.s][j];
-        const float lp = lh[j], ep = eh[j];
-        const float lam_t = lh[j + 1], eta_t = eh[j + 1];
-        const float inv_den = idn[j], var = vr[j];
-        // The step's intermediates (filter_step) from the kept 1/den.
-        const float kk2 = kk * kk;
-        const float phi = sig * kk2;
-        const float idn_a = inv_den * inv_a2;   // d lam_t / d lam' = 1/(a2 den^2) = idn_a / den
-        const bool da_ok = a2 + pp * lp >= kEps;
-        const float inv_Da = da_ok ? idn_a : kInvEps;
-        const float alpha = a_s * inv_Da;
-        const float mean = eta_t * var;
-        const float mean_o = PRIOR ? a_s * mean : mean;
-        const float var_o = PRIOR ? a2 * var + pp : var;
+      for (int j = TB - 1; j >= 0; --j) {
+        if (kVecLds && j % 4 == 3) {
+          asm volatile("" ::: "memory");   // (as in the replay)
+          sv4 = lds4(s_sv[cur][c], j - 3);
+          if constexpr (kS2) s24 = lds4(s_s2[kS2 ? cur : 0][kS2 ? c : 0], j - 3);
+          dy4 = lds4(s_dy[cur][c], j - 3);
+          k4 = lds4(s_k[kb][ln.s], j - 3);
+          q4 = lds4(s_q[kb][ln.s], j - 3);
+        }
+        float dk_c = 0.0f, dq_c = 0.0f;
+        if constexpr (kTr && !FULL) {
+          dv_w[j] = 0.0f;
+          dl_w[j] = 0.0f;
+        }
+        if (FULL || j < nv) {
+          const float sv = kVecLds ? pick4(sv4, j % 4) : s_sv[cur][c][j];
+          const float s2 = !kS2 ? 2.0f * s_l[cur][c][j] : kVecLds ? pick4(s24, j % 4) : s_s2[kS2 ? cur : 0][kS2 ? c : 0][j];
+          const float dy = kVecLds ? pick4(dy4, j % 4) : s_dy[cur][c][j];
+          const float kk = kVecLds ? pick4(k4, j % 4) : s_k[kb][ln.s][j];
+          const float qq = kVecLds ? pick4(q4, j % 4) : s_q[kb][ln.s][j];
+          const float lp = lh[j], ep = eh[j];
+          const float lam_t = lh[j + 1], eta_t = eh[j + 1];
+          const float inv_den = idn[j], var = rcp(fmaxf(lam_t, kEps));
+          // The step's intermediates (filter_step) from the kept 1/den.
+          const float idn_a = inv_den * inv_a2;   // d lam_t / d lam' = 1/(a2 den^2) = idn_a / den
+          // alpha = a / max(a2 + p' lam', EPS) = a min(idn_a, 1/EPS)
+          const bool da_ok = !CLAMPS || idn_a <= kInvEps;
+          const float inv_Da = CLAMPS ? fminf(idn_a, kInvEps) : idn_a;
+          const float alpha = a_s * inv_Da;
+          const float mean = eta_t * var;
+          const float mean_o = PRIOR ? a_s * mean : mean;
+          const float var_o = PRIOR ? fmaf(a2, var, pp) : var;
 
-        // read-out
-        const float dmo = dy * qq;
-        float dmean = dmo;
-        if (PRIOR) {
-          dmean = dmo * a_s;
-          blk_a += dmo * mean;
-        }
-        float dvar_tot;
-        if constexpr (VAR) {
-          const float dyv = s_dyv[cur][c][j];
-          const float dvo = dyv * (qq * qq);
-          dq_c = dy * mean_o + dyv * 2.0f * qq * var_o;
-          float dvar = dvo;
+          // read-out
+          const float dmo = dy * qq;
+          float dmean = dmo;
           if (PRIOR) {
-            dvar = dvo * a2;
-            blk_a2 += dvo * var;
-            blk_p += dvo;
+            dmean = dmo * a_s;
+            blk_a = fmaf(dmo, mean, blk_a);
           }
-          dvar_tot = dvar + dmean * eta_t;
-        } else {
-          dq_c = dy * mean_o;
-          dvar_tot = dmean * eta_t;
+          float dvar_tot;
+          if constexpr (VAR) {
+            const float dyv = s_dyv[cur][c][j];
+            const float dvo = dyv * (qq * qq);
+            dq_c = fmaf(dy, mean_o, ((dyv * 2.0f) * qq) * var_o);
+            float dvar = dvo;
+            if (PRIOR) {
+              dvar = dvo * a2;
+              blk_a2 = fmaf(dvo, var, blk_a2);
+              blk_p += dvo;
+            }
+            dvar_tot = fmaf(dmean, eta_t, dvar);
+          } else {
+            dq_c = dy * mean_o;
+            dvar_tot = dmean * eta_t;
+          }
+          // mean = eta var, var = 1/max(lam, EPS)
+          const float ge_t = fmaf(dmean, var, ge);
+          float gl_t = fmaf(-(dvar_tot * var), var, gl);
+          if constexpr (CLAMPS) gl_t = lam_t >= kEps ? gl_t : gl;
+          // eta_t = alpha eta' + r
+          const float dalpha = ge_t * ep;
+          ge = ge_t * alpha;
+          // alpha = a / Da, Da = max(a2 + p' lam', EPS): d a += dalpha / Da, d Da = -dalpha alpha / Da
+          const float w = dalpha * inv_Da;
+          blk_a += w;
+          float dDa = -(w * alpha);
+          if constexpr (CLAMPS) dDa = da_ok ? dDa : 0.0f;
+          blk_a2 += dDa;
+          blk_p = fmaf(dDa, lp, blk_p);
+          // lam_t = (A lam' + phi) / den, den = C lam' + 1: dA = u lam', dC = -u lam_t lam'
+          const float u = gl_t * inv_den;
+          const float dA = u * lp;
+          // (Explicit fmaf where a sum of two products could be contracted either
+          // way, so every kernel variant rounds alike.)
+          blk_x = fmaf(-dA, lp * idn_a, blk_x);   // dA phi + dC = dA (phi - lam_t), lam_t - phi = lam' idn_a
+          blk_y += dA;
+          gl = fmaf(u, idn_a, dDa * pp);
+          // phi = Lv k^2, r = (v Lv) k, d phi = gl_t (d lam_t / d phi = 1), d r = ge_t.
+          // Per lane the s-sums need only dr k and d phi k^2: dv = Lv sum(dr k),
+          // dLv = sum(d phi k^2) + v sum(dr k), formed once per (step, channel)
+          // when the block is flushed; d k = 2 Lv k d phi + (v Lv) d r.
+          const float pk = ge_t * kk;
+          const float gk = gl_t * kk;
+          const float qk = gk * kk;
+          dk_c = fmaf(gk, s2, ge_t * sv);
+          if constexpr (kTr) {
+            dv_w[j] = pk;
+            dl_w[j] = qk;
+          } else {
+            const float dv_s = group_sum<SG>(pk);
+            const float dl_s = group_sum<SG>(qk);
+            if (ln.s % SG == 0) {
+              s_dv[cur][ln.s / SG][c][j] = dv_s;
+              s_dl[cur][ln.s / SG][c][j] = dl_s;
+            }
+          }
         }
-        // mean = eta var, var = 1/max(lam, EPS)
-        const float ge_t = ge + dmean * var;
-        const float gl_t = gl + ((lam_t >= kEps) ? -dvar_tot * var * var : 0.0f);
-        // eta_t = alpha eta' + r
-        const float dalpha = ge_t * ep;
-        const float dr = ge_t;
-        ge = ge_t * alpha;
-        // alpha = a / Da, Da = max(a2 + p' lam', EPS)
-        blk_a += dalpha * inv_Da;
-        const float dDa = da_ok ? -dalpha * alpha * inv_Da : 0.0f;
-        blk_a2 += dDa;
-        blk_p += dDa * lp;
-        // lam_t = (A lam' + phi) / den, den = C lam' + 1: dA = u lam', dC = -u lam_t lam'
-        const float u = gl_t * inv_den;
-        const float dA = u * lp;
-        // (Explicit fmaf where a sum of two products could be contracted either
-        // way, so every kernel variant rounds alike.)
-        blk_x = fmaf(dA, phi - lam_t, blk_x);   // dA phi + dC
-        blk_y += dA;
-        gl = fmaf(u, idn_a, dDa * pp);
-        // A = (1 + p' phi)/a2: d phi = u + dA p'/a2 = u + dA C
-        const float dphi = fmaf(dA, C, u);
-        // phi = Lv k^2, r = (v Lv) k. Per lane the s-sums need only dr k and
-        // d phi k^2: dv = Lv sum(dr k), dLv = sum(d phi k^2) + v sum(dr k), formed
-        // once per (step, channel) when the block is flushed.
-        const float pk = dr * kk;
-        const float qk = dphi * kk2;
-        dk_c = sig * fmaf(2.0f * dphi, kk, dr * vv);
-        if constexpr (kTr) {
-          dv_w[j] = pk;
-          dl_w[j] = qk;
+        // Sum over this wave's channels (now, or after the walk), over the waves
+        // at the flush.
+        if constexpr (kRows) {
+          dk_w[j] = dk_c;
+          dq_w[j] = dq_c;
         } else {
-          const float dv_s = group_sum<SG>(pk);
-          const float dl_s = group_sum<SG>(qk);
-          if (ln.s % SG == 0) {
-            s_dv[cur][ln.s / SG][c][j] = dv_s;
-            s_dl[cur][ln.s / SG][c][j] = dl_s;
+          // (For SP >= 64 a wave holds one channel's lanes or part of them:
+          // nothing to add within the wave, and every lane stores its s.)
+          dk_c = cross_group_sum<SP>(dk_c);
+          dq_c = cross_group_sum<SP>(dq_c);
+          if (SP >= kWave || lane < SP) {
+            s_red[RB == 1 ? 0 : cur][0][j][wave / WPC][ln.s] = dk_c;
+            s_red[RB == 1 ? 0 : cur][1][j][wave / WPC][ln.s] = dq_c;
           }
         }
       }
-      // Sum over this wave's channels (now, or after the walk), over the waves
-      // at the flush.
-      if constexpr (kRows) {
-        dk_w[j] = dk_c;
-        dq_w[j] = dq_c;
-      } else {
-        // (For SP >= 64 a wave holds one channel's lanes or part of them:
-        // nothing to add within the wave, and every lane stores its s.)
-        dk_c = cross_group_sum<SP>(dk_c);
-        dq_c = cross_group_sum<SP>(dq_c);
-        if (SP >= kWave || lane < SP) {
-          s_red[RB == 1 ? 0 : cur][0][j][wave / WPC][ln.s] = dk_c;
-          s_red[RB == 1 ? 0 : cur][1][j][wave / WPC][ln.s] = dq_c;
-        }
-      }
+    };
+    // (Wave-uniform branches: neither the replay nor the walk holds a barrier.)
+    if (kFullBlocks && nv == TB) {
+      replay(std::true_type{});
+      if (__all(unclamped))
+        walk(std::false_type{}, std::true_type{});
+      else
+        walk(std::true_type{}, std::true_type{});
+    } else {
+      replay(std::false_type{});
+      walk(std::true_type{}, std::false_type{});
     }
     if constexpr (kRows) {
       cross_row_transpose_sum<TB>(dk_w);

@@ -44,11 +44,14 @@ def make_inputs(B=2, L=64, M=16, S=8, seed=0):
 
 
 # Gradients that contract over many terms: dk, dq sum over the M channels, da, dp
-# over batch and time (B*L terms). Their fp32 rounding grows with the magnitude
-# of the terms, not of the (possibly cancelled) result, so their atol is taken
-# relative to the tensor's scale; every other output of the scan meets the
-# absolute rtol 1e-5 / atol 1e-6.
-CONTRACTIONS = ("dk", "dq", "da", "dp")
+# over batch and time (B*L terms), dv and dlambda_v (and dproj, the projection
+# gradient that carries them) over the S state lanes of a channel. Their fp32
+# rounding grows with the magnitude of the terms, not of the (possibly
+# cancelled) result, so their atol is taken relative to the tensor's scale (the
+# reference's rel_err, tests/test_backends.py:161-168); every other output of
+# the scan -- y, y_var, the final state and the initial-state gradients --
+# meets the absolute rtol 1e-5 / atol 1e-6.
+CONTRACTIONS = ("dk", "dq", "da", "dp", "dv", "dlambda_v", "dproj")
 
 
 def check_scan(name, got, want):
