@@ -937,7 +937,7 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
           const float qq = kVecLds ? pick4(q4, j % 4) : s_q[kb][ln.s][j];
           const float lp = lh[j], ep = eh[j];
           const float lam_t = lh[j + 1], eta_t = eh[j + 1];
-          const float inv_den = idn[j], var = rcp(fmaxf(lam_t, kEps));
+          const float inv_den = idn[j], var = rcp(CLAMPS ? fmaxf(lam_t, kEps) : lam_t);
           // The step's intermediates (filter_step) from the kept 1/den.
           const float idn_a = inv_den * inv_a2;   // d lam_t / d lam' = 1/(a2 den^2) = idn_a / den
           // alpha = a / max(a2 + p' lam', EPS) = a min(idn_a, 1/EPS)
@@ -955,7 +955,8 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
             dmean = dmo * a_s;
             blk_a = fmaf(dmo, mean, blk_a);
           }
-          float dvar_tot;
+          // t = d(loss)/d(var) var = (dvar + dmean eta_t) var = dvar var + dmean mean.
+          float t;
           if constexpr (VAR) {
             const float dyv = s_dyv[cur][c][j];
             const float dvo = dyv * (qq * qq);
@@ -966,14 +967,14 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
               blk_a2 = fmaf(dvo, var, blk_a2);
               blk_p += dvo;
             }
-            dvar_tot = fmaf(dmean, eta_t, dvar);
+            t = fmaf(dmean, mean, dvar * var);
           } else {
             dq_c = dy * mean_o;
-            dvar_tot = dmean * eta_t;
+            t = dmean * mean;
           }
-          // mean = eta var, var = 1/max(lam, EPS)
+          // mean = eta var, var = 1/max(lam, EPS): d lam = -d(var) var^2 = -t var
           const float ge_t = fmaf(dmean, var, ge);
-          float gl_t = fmaf(-(dvar_tot * var), var, gl);
+          float gl_t = fmaf(-t, var, gl);
           if constexpr (CLAMPS) gl_t = lam_t >= kEps ? gl_t : gl;
           // eta_t = alpha eta' + r
           const float dalpha = ge_t * ep;
