@@ -10,6 +10,8 @@ Uses:
 * parity reference for the GPU kernels in fp32 (same algorithm, same dtype as
   the reference CPU path) and, in float64, a second opinion beside
   :mod:`oracle.scans`;
+* :func:`kla_scan_stepwise`, the same filter one step at a time: the float64
+  reference where the prefix form loses precision (a precision near zero);
 * the timed ``cpu_baseline`` of ``bench.py`` (kind "port").
 """
 
@@ -150,3 +152,39 @@ def kla_scan_torch(v, lambda_v, k, q, a, p, lam0=None, eta0=None, decode_from_pr
     y = torch.einsum("blms,bls->blm", mean, q)
     y_var = torch.einsum("blms,bls->blm", var, q * q)
     return y, y_var, lam[:, -1], eta[:, -1]
+
+
+def kla_scan_stepwise(v, lambda_v, k, q, a, p, lam0=None, eta0=None, decode_from_prior=False):
+    """kla_scan_torch's filter (kla_ops.py:188-290) applied one step at a time:
+    the same leaves, guards and read-out (phi not floored, p at P_MIN, a^2 at
+    EPS, every denominator at EPS), each Moebius leaf and affine leaf applied to
+    the running state instead of composed into prefixes. Differentiable through
+    autograd. Where the trace-normalised prefixes lose precision (a state near
+    zero under strong decay: the normalised D entry of a prefix falls toward or
+    below EPS, and the prefix read-out's max(C lam0 + D, EPS) departs from the
+    filter) this form stays exact; elsewhere the two agree to rounding."""
+    Bn, L, M = v.shape
+    S = k.shape[2]
+    dt = v.dtype
+    lam = torch.ones(Bn, M, S, dtype=dt) if lam0 is None else lam0
+    eta = torch.zeros(Bn, M, S, dtype=dt) if eta0 is None else eta0
+    a_ = a.view(1, M, S).to(dt)
+    p_ = p.view(1, M, S).clamp_min(P_MIN).to(dt)
+    a2 = (a_ * a_).clamp_min(EPS)
+    ys, yvs = [], []
+    for t in range(L):
+        phi = lambda_v[:, t].unsqueeze(-1) * (k[:, t] * k[:, t]).unsqueeze(-2)
+        r = (v[:, t] * lambda_v[:, t]).unsqueeze(-1) * k[:, t].unsqueeze(-2)
+        A = (1.0 + p_ * phi) / a2
+        C = p_ / a2
+        alpha = a_ / (a2 + p_ * lam).clamp_min(EPS)
+        lam = (A * lam + phi) / (C * lam + 1.0).clamp_min(EPS)
+        eta = alpha * eta + r
+        var = 1.0 / lam.clamp_min(EPS)
+        mean = eta * var
+        if decode_from_prior:
+            mean = a_ * mean
+            var = a2 * var + p_
+        ys.append(torch.einsum("bms,bs->bm", mean, q[:, t]))
+        yvs.append(torch.einsum("bms,bs->bm", var, q[:, t] * q[:, t]))
+    return torch.stack(ys, 1), torch.stack(yvs, 1), lam, eta

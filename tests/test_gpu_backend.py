@@ -176,6 +176,52 @@ def test_gradients_match_float64_autograd(cuda, backend, decode_from_prior, shap
         check_scan("d" + name, got.grad, want.grad.numpy())
 
 
+@pytest.mark.parametrize("shape", [(2, 64, 16, 16), (1, 70, 8, 32), (2, 48, 4, 64), (1, 40, 3, 8)])
+def test_clamped_blocks_match_float64_autograd(cuda, shape):
+    """A precision that sits at zero for 20 steps (lam0 = 0 and k = q = 0 on some
+    state lanes, so lam_t stays 0 and var = 1/max(lam, EPS) is clamped): the
+    fused backward walks those 16-step blocks with the clamps' branches and the
+    later blocks without, and its outputs and gradients match float64 autograd
+    of the reference's filter applied step by step (oracle.torch_ref.
+    kla_scan_stepwise). The doubling-scan form (kla_scan_torch) is no reference
+    here: from lam0 = 0 under decay its trace-normalised prefixes lose up to 6e-5
+    of relative precision in float64 (their D entry shrinks toward EPS)."""
+    B, L, M, S = shape
+    v, lv, k, q, _, p = make_inputs(B, L, M, S, seed=21)
+    # Decay close to 1: near zero precision the predict step scales lam by 1/a^2
+    # per step, so d lam_20 / d lam0 ~ (1/a^2)^20 (1e16 at a = 0.4, ~100 here).
+    a = torch.rand(M, S, generator=torch.Generator().manual_seed(24)) * 0.1 + 0.89
+    st = random_state(B, M, S, seed=22)
+    cold = torch.arange(S) % 3 == 0
+    k[:, :20, cold] = 0.0
+    q[:, :20, cold] = 0.0
+    # The first informative step after the cold run sets lam = Lv k^2 from zero;
+    # |k| = 1 there keeps var = 1/lam moderate (a tiny k would make the eta0
+    # gradient a large cancelled sum, ill-conditioned in any fp32 arithmetic).
+    k[:, 20, cold] = 1.0
+    st.lam[:, :, cold] = 0.0
+    st.eta[:, :, cold] = 0.0
+    g = torch.Generator().manual_seed(23)
+    wy, wv = torch.randn(B, L, M, generator=g), torch.randn(B, L, M, generator=g)
+    wl, we = torch.randn(B, M, S, generator=g), torch.randn(B, M, S, generator=g)
+
+    def loss(y, y_var, lam, eta):
+        w = [t.to(device=y.device, dtype=y.dtype) for t in (wy, wv, wl, we)]
+        return (w[0] * y).sum() + (w[1] * y_var).sum() + (w[2] * lam).sum() + (w[3] * eta).sum()
+
+    ins = (v, lv, k, q, a, p, st.lam, st.eta)
+    xs = [t.double().requires_grad_(True) for t in ins]
+    ref = torch_ref.kla_scan_stepwise(*xs)
+    loss(*ref).backward()
+    gs = [t.to(cuda).requires_grad_(True) for t in ins]
+    y, y_var, fin = kla_scan(*gs[:6], backend="hip_fused", initial_state=KLAState(gs[6], gs[7]))
+    for name, got, want in zip(("y", "y_var", "lam", "eta"), (y, y_var, fin.lam, fin.eta), ref):
+        check_scan(name, got, want.detach().numpy())
+    loss(y, y_var, fin.lam, fin.eta).backward()
+    for name, got, want in zip(("v", "lambda_v", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
+        check_scan("d" + name, got.grad, want.grad.numpy())
+
+
 @pytest.mark.parametrize("backend", BACKENDS)
 def test_non_positive_noise_and_near_zero_decay_stay_finite(cuda, backend):
     """Reference tests/test_backends.py:421-493."""

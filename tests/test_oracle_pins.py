@@ -13,7 +13,9 @@ function is pinned here by something independent of its own formula:
 * affine backward    finite differences; the g = 1 closed form (reverse cumsum).
 * KLA scan           sequential information form vs covariance-form filter; the scalar
                      steady state (closed-form root of the stationary Riccati equation);
-                     the torch doubling restatement vs the sequential one; gradcheck.
+                     the torch doubling restatement vs the sequential one; gradcheck;
+                     the torch stepwise restatement vs the sequential one, gradcheck,
+                     and a held zero precision.
 * trace-norm combine the invariants of reference tests/test_mobius_impl.py:116-146.
 
 Each pin is a function returning an error measure, and ``test_planted_mistakes``
@@ -284,6 +286,50 @@ def test_torch_restatement_matches_sequential(decode_from_prior):
                                        decode_from_prior=decode_from_prior, mobius_impl=impl)
         for x, w in zip(got, want):
             assert _rel(x.numpy(), w) < 1e-9, impl
+
+
+@pytest.mark.parametrize("decode_from_prior", [False, True])
+def test_stepwise_restatement_matches_sequential(decode_from_prior):
+    """oracle.torch_ref.kla_scan_stepwise (kla_scan_torch's leaves applied one step
+    at a time, in torch) against the sequential float64 filter, with k away from
+    zero so that filter's phi floor never acts; and its gradients by central
+    differences."""
+    args = _kla_inputs(2, 64, 5, 3, seed=43)
+    lam0 = np.full((2, 5, 3), 0.9)
+    eta0 = np.random.default_rng(44).standard_normal((2, 5, 3))
+    want = okla.kla_scan_sequential(*args, lam0, eta0, decode_from_prior=decode_from_prior)
+    got = torch_ref.kla_scan_stepwise(*(torch.tensor(x) for x in args), torch.tensor(lam0), torch.tensor(eta0),
+                                      decode_from_prior=decode_from_prior)
+    for x, w in zip(got, want):
+        assert _rel(x.numpy(), w) < 1e-12
+    r = np.random.default_rng(52)
+    B, L, M, S = 1, 6, 2, 2
+    ins = (r.standard_normal((B, L, M)), r.random((B, L, M)) + 0.5, r.standard_normal((B, L, S)) * 0.5,
+           r.standard_normal((B, L, S)) * 0.5, r.random((M, S)) * 0.4 + 0.5, r.random((M, S)) * 0.04 + 0.02,
+           r.random((B, M, S)) + 0.5, r.standard_normal((B, M, S)))
+    ts = tuple(torch.tensor(x, requires_grad=True) for x in ins)
+    assert torch.autograd.gradcheck(
+        lambda *a: torch_ref.kla_scan_stepwise(*a, decode_from_prior=decode_from_prior), ts,
+        eps=1e-6, atol=1e-5, rtol=1e-3)
+
+
+def test_stepwise_holds_a_zero_precision():
+    """From lam0 = 0 with k = 0 the precision stays exactly 0 (phi = 0, lam idn = 0)
+    and var = 1/max(lam, EPS) is clamped; the first step with k != 0 gives
+    lam = phi = lambda_v k^2 exactly, the filter's update from an uninformative
+    prior."""
+    B, L, M, S = 1, 5, 2, 3
+    r = np.random.default_rng(53)
+    v, lv = torch.tensor(r.standard_normal((B, L, M))), torch.tensor(r.random((B, L, M)) + 0.5)
+    k = torch.zeros(B, L, S, dtype=torch.float64)
+    k[:, 3:] = torch.tensor(r.standard_normal((B, 2, S)))
+    q = torch.tensor(r.standard_normal((B, L, S)))
+    a, p = torch.tensor(r.random((M, S)) * 0.4 + 0.5), torch.tensor(r.random((M, S)) * 0.04 + 0.02)
+    zero = torch.zeros(B, M, S, dtype=torch.float64)
+    _, y_var, _, _ = torch_ref.kla_scan_stepwise(v, lv, k, q, a, p, zero, zero.clone())
+    assert torch.allclose(y_var[:, :3], (q[:, :3] ** 2).sum(-1).unsqueeze(-1).expand(B, 3, M) / torch_ref.EPS)
+    _, _, lam, _ = torch_ref.kla_scan_stepwise(v[:, :4], lv[:, :4], k[:, :4], q[:, :4], a, p, zero, zero.clone())
+    assert torch.equal(lam, lv[:, 3].unsqueeze(-1) * (k[:, 3] ** 2).unsqueeze(-2))
 
 
 def test_doubling_matches_sequential_scan():
