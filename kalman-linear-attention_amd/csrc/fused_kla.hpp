@@ -1114,7 +1114,7 @@ __global__ void __launch_bounds__(256) reduce_rows_kernel(const float *__restric
 template <int INNER>
 __global__ void __launch_bounds__(256) reduce_rows_wave_kernel(const float *__restrict__ in, float *__restrict__ out,
                                                                int64_t outer, int64_t G) {
-  static_assert(INNER >= 4 && INNER <= 64 && 256 % INNER == 0, "INNER must be 4 to 64, a power of two");
+  static_assert(INNER >= 4 && INNER <= 256 && 256 % INNER == 0, "INNER must be 4 to 256, a power of two");
   constexpr int Q = INNER / 4;
   constexpr int R = kWave / Q;
   typedef float f32x4v __attribute__((ext_vector_type(4)));

@@ -335,7 +335,7 @@ bool launch_reduce_rows(const float *in, float *out, int64_t outer, int64_t G, i
     return true;
   }
   if (outer < 256 || outer >= (1ll << 31)) return false;
-  if (inner >= 4 && inner <= 64 && all_aligned(16, {in, out})) {
+  if (inner >= 4 && inner <= 256 && all_aligned(16, {in, out})) {
     // The same sums with one wave per row block (reduce_rows_wave_kernel).
     const dim3 wgrid(static_cast<uint32_t>((outer + 3) / 4));
     switch (inner) {
@@ -344,6 +344,8 @@ bool launch_reduce_rows(const float *in, float *out, int64_t outer, int64_t G, i
       case 16: hipLaunchKernelGGL(reduce_rows_wave_kernel<16>, wgrid, dim3(256), 0, stream, in, out, outer, G); return true;
       case 32: hipLaunchKernelGGL(reduce_rows_wave_kernel<32>, wgrid, dim3(256), 0, stream, in, out, outer, G); return true;
       case 64: hipLaunchKernelGGL(reduce_rows_wave_kernel<64>, wgrid, dim3(256), 0, stream, in, out, outer, G); return true;
+      case 128: hipLaunchKernelGGL(reduce_rows_wave_kernel<128>, wgrid, dim3(256), 0, stream, in, out, outer, G); return true;
+      case 256: hipLaunchKernelGGL(reduce_rows_wave_kernel<256>, wgrid, dim3(256), 0, stream, in, out, outer, G); return true;
       default: break;
     }
   }

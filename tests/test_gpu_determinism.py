@@ -56,7 +56,7 @@ def test_fused_backward_is_bitwise_repeatable(cuda, shape):
             assert torch.equal(a, b), name
 
 
-@pytest.mark.parametrize("S", [4, 16, 64])
+@pytest.mark.parametrize("S", [4, 16, 64, 128, 256])
 def test_reduce_kernels_give_identical_sums(cuda, S):
     """dk and dq through the wave reduce (16-byte aligned outputs) and through the
     LDS reduce (outputs at a 4-byte offset) are bit-identical, with B * L >= 256
