@@ -271,6 +271,37 @@ int kla_chunk_starts(const float *maps, const float *lam0, const float *eta0, fl
                      hipStream_t stream);
 
 /*
+ * The time-split backward of the fused scan (training at small batch), the
+ * adjoint of the time-split forward: the forward's checkpoints are the same
+ * memory on the [B * chunks, L / chunks] view (chunks of a multiple of 16
+ * steps). The adjoint of the state (lam_t, eta_t) walks back through an affine
+ * map with an upper-triangular linear part per step, so each chunk's steps
+ * compose into five numbers per lane. Three calls:
+ *   kla_fused_adjoint_maps on the view (batch = B * chunks, steps = L / chunks),
+ *     with the backward's dy, dy_var (NULL: no y_var gradient), sensors, k, q,
+ *     a, p and checkpoints: maps [B * chunks, M, S, 8] (P Q A u_l u_e, three words
+ *     unused), x -> [[P, Q], [0, A]] x + (u_l, u_e) for the adjoint x entering a
+ *     chunk from its end;
+ *   kla_adjoint_ends (batch = B, chunks): from dlam_fin, deta_fin (NULL: 0)
+ *     through the maps in reverse chunk order, the adjoint entering each chunk
+ *     from its end, gl_end, ge_end [B, chunks, M, S];
+ *   kla_fused_scan_sensors_bwd (or kla_fused_scan_bwd) on the view with
+ *     dlam_fin, deta_fin = gl_end, ge_end: every gradient; da, dp summed over
+ *     all chunks; the initial-state gradients are chunk 0's, [B * chunks, M, S]
+ *     rows b * chunks.
+ * The chunked backward of the reference's tiled Metal kernel has no
+ * counterpart here (its backward runs through torch autograd,
+ * src/kla/ops/mps_backend.py:10-16); with kla_fused_scan_sensors_bwd these
+ * replace kla_scan_torch's backward (src/kla/ops/kla_ops.py:188-290).
+ */
+int kla_fused_adjoint_maps(const float *dy, const float *dy_var, const kla_sensors *sensors, const float *k,
+                           const float *q, const float *a, const float *p, const float *ck_lam, const float *ck_eta,
+                           float *maps, int decode_from_prior, int64_t batch, int64_t steps, int64_t M, int64_t S,
+                           hipStream_t stream);
+int kla_adjoint_ends(const float *maps, const float *dlam_fin, const float *deta_fin, float *gl_end, float *ge_end,
+                     int64_t batch, int64_t chunks, int64_t M, int64_t S, hipStream_t stream);
+
+/*
  * One O(1) decode step of the filter for every (b, m, s) lane: kla_step
  * (reference src/kla/ops/kla_ops.py:293-331), phi floored at 1e-12 as there.
  * v, lambda_v, y, y_var [batch, M]; k, q [batch, S]; a, p [M, S]; lam, eta,

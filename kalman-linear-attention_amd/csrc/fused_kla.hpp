@@ -1338,6 +1338,200 @@ __global__ void __launch_bounds__(256) chunk_starts_kernel(const float *__restri
   }
 }
 
+// ============================================== time-split backward (training)
+//
+// The backward's reverse walk carries the adjoint (gl, ge) of the state
+// (lam_t, eta_t). Step t of fused_kla_bwd_kernel maps it, with the forward's
+// trajectory fixed, as
+//   ge_t = ge + c_e,   gl_t = gl + c_l        (the step's read-out terms:
+//                                              c_e = dmean var, c_l = -T var, or 0
+//                                              where var's clamp acts)
+//   ge' = alpha ge_t,  gl' = p gl_t + q ge_t   (p = 1/(a2 den^2) = inv_den idn_a,
+//                                              q = -eta' inv_Da alpha p' where the
+//                                              gain's clamp is idle, else 0)
+// an affine map with an upper-triangular linear part, so a chunk's steps compose
+// into five numbers per lane, x -> [[P, Q], [0, A]] x + (u_l, u_e), whatever
+// adjoint enters the chunk from the right. fused_adjoint_map_kernel composes
+// them per chunk (replaying each 16-step block from the forward's checkpoints,
+// like the backward), adjoint_ends_kernel walks the maps from the end of each
+// sequence and leaves every chunk the adjoint entering it from the right, and
+// fused_kla_bwd_kernel then runs on the [B * chunks, L / chunks] view with those
+// as its dlam_fin, deta_fin: the view's checkpoints, sensors, gradients and
+// partial sums are the same memory as the whole sequence's.
+
+struct AdjointMapParams {
+  const float *dy, *dyvar;   // dyvar NULL: no y_var gradient (VAR false)
+  SensorIn sn;
+  const float *k, *q, *a, *p, *ck_lam, *ck_eta;
+  float *maps;   // [B', M, S, 8]: P Q A u_l u_e (and three unused words)
+};
+
+template <int SP, bool PRIOR, bool BF16, bool VAR>
+__global__ void __launch_bounds__(kFusedThreads) fused_adjoint_map_kernel(AdjointMapParams prm, FusedGeom g) {
+  constexpr int CH = kFusedThreads / SP;
+  constexpr int TB = kCkpt;
+  constexpr int KQB = SP >= 256 ? 1 : 2;
+  constexpr bool kK2 = SP <= kWave;
+  __shared__ __align__(16) float s_l[2][CH][TB + kPad], s_sv[2][CH][TB + kPad];
+  __shared__ __align__(16) float s_dy[2][CH][TB + kPad], s_dyv[VAR ? 2 : 1][VAR ? CH : 1][TB + kPad];
+  __shared__ __align__(16) float s_k[KQB][SP][TB + kPad], s_q[KQB][SP][TB + kPad];
+  __shared__ __align__(16) float s_k2[kK2 ? KQB : 1][kK2 ? SP : 1][TB + kPad];
+
+  const FusedLane ln = fused_lane<SP>(g);
+  const int64_t M = g.M, S = g.S, L = g.steps;
+  const int64_t m0 = (xcd_block() % g.groups) * CH;
+  const int c = static_cast<int>(ln.m - m0);
+  const int64_t ms = ln.m * S + ln.s;
+  const int64_t bms = ln.b * M * S + ms;
+  const int64_t cols_m = M - m0 < CH ? M - m0 : CH;
+
+  const float a_s = ln.active ? prm.a[ms] : 1.0f;
+  const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
+  const float a2 = fmaxf(a_s * a_s, kEps);
+  const float inv_a2 = 1.0f / a2;
+  const float C = pp * inv_a2;
+
+  const int64_t offM = ln.b * L * M + m0, offS = ln.b * L * S;
+  const SensorIn &sn = prm.sn;
+  TileRegs<TB, CH> rv, rl, rdy, rdyv;
+  TileRegs<TB, SP> rk, rq;
+  auto load = [&](int64_t t0) {
+    const int64_t rows = L - t0;
+    tile_load_sensor<TB, CH, BF16>(rv, sensor_at<BF16>(sn.v, ln.b * L + t0, m0, sn.ld_v), sn.ld_v, rows, cols_m);
+    tile_load_sensor<TB, CH, BF16>(rl, sensor_at<BF16>(sn.lv, ln.b * L + t0, m0, sn.ld_lv), sn.ld_lv, rows, cols_m);
+    tile_load<TB, CH>(rdy, prm.dy + offM + t0 * M, M, rows, cols_m);
+    if constexpr (VAR) tile_load<TB, CH>(rdyv, prm.dyvar + offM + t0 * M, M, rows, cols_m);
+    tile_load<TB, SP>(rk, prm.k + offS + t0 * S, S, rows, S);
+    tile_load<TB, SP>(rq, prm.q + offS + t0 * S, S, rows, S);
+  };
+  auto stage = [&](int buf) {
+    const int kb = KQB == 1 ? 0 : buf;
+    widen_sensor<TB, CH, BF16>(rv);
+    widen_sensor<TB, CH, BF16>(rl);
+    to_precision<TB, CH>(rl, sn);
+    tile_mul_to_lds<TB, CH>(rv, rl, s_sv[buf]);
+    tile_to_lds<TB, CH>(rl, s_l[buf]);
+    tile_to_lds<TB, CH>(rdy, s_dy[buf]);
+    if constexpr (VAR) tile_to_lds<TB, CH>(rdyv, s_dyv[VAR ? buf : 0]);
+    tile_to_lds<TB, SP>(rk, s_k[kb]);
+    if constexpr (kK2) tile_mul_to_lds<TB, SP>(rk, rk, s_k2[kK2 ? kb : 0]);
+    tile_to_lds<TB, SP>(rq, s_q[kb]);
+  };
+
+  // The chunk's map so far (identity): the adjoint entering the chunk from the
+  // right, x, becomes [[P, Q], [0, A]] x + (ul, ue) before the steps walked.
+  float P = 1.0f, Q = 0.0f, A = 1.0f, ul = 0.0f, ue = 0.0f;
+  const int64_t n_ck = g.n_ck;
+  if (n_ck > 0) {
+    load((n_ck - 1) * TB);
+    stage(0);
+  }
+  __syncthreads();
+  for (int64_t i = 0; i < n_ck; ++i) {
+    const int cur = static_cast<int>(i & 1);
+    const int kb = KQB == 1 ? 0 : cur;
+    const int64_t blk = n_ck - 1 - i;
+    const int64_t t0 = blk * TB;
+    if (i + 1 < n_ck) load(t0 - TB);
+    const int nv = static_cast<int>(L - t0 < TB ? L - t0 : TB);
+    // The block's replay, as in fused_kla_bwd_kernel.
+    float lh[TB + 1], eh[TB + 1], idn[TB];
+    {
+      const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
+      float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
+      float eta = ln.active ? prm.ck_eta[ci] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < TB; ++j) {
+        lh[j] = lam;
+        eh[j] = eta;
+        idn[j] = 0.0f;
+        if (j < nv) {
+          const float sig = s_l[cur][c][j];
+          const float sv = s_sv[cur][c][j];
+          const float kk = s_k[kb][ln.s][j];
+          const float k2 = kK2 ? s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0][j] : kk * kk;
+          lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, inv_a2, C, idn[j]);
+        }
+      }
+      lh[TB] = lam;
+      eh[TB] = eta;
+    }
+    // Compose the block's steps in reverse (the read-out terms as the backward
+    // forms them: dmean, t = d(loss)/d(var) var).
+#pragma unroll
+    for (int j = TB - 1; j >= 0; --j) {
+      if (j < nv) {
+        const float dy = s_dy[cur][c][j];
+        const float qq = s_q[kb][ln.s][j];
+        const float ep = eh[j];
+        const float lam_t = lh[j + 1], eta_t = eh[j + 1];
+        const float inv_den = idn[j];
+        const float idn_a = inv_den * inv_a2;
+        const bool da_ok = idn_a <= kInvEps;
+        const float inv_Da = fminf(idn_a, kInvEps);
+        const float alpha = a_s * inv_Da;
+        const float var = rcp(fmaxf(lam_t, kEps));
+        const float mean = eta_t * var;
+        const float dmo = dy * qq;
+        const float dmean = PRIOR ? dmo * a_s : dmo;
+        float t;
+        if constexpr (VAR) {
+          const float dvo = s_dyv[VAR ? cur : 0][VAR ? c : 0][j] * (qq * qq);
+          t = fmaf(dmean, mean, (PRIOR ? dvo * a2 : dvo) * var);
+        } else {
+          t = dmean * mean;
+        }
+        const float c_e = dmean * var;
+        const float c_l = lam_t >= kEps ? -(t * var) : 0.0f;
+        const float p_t = inv_den * idn_a;
+        const float q_t = da_ok ? -((ep * inv_Da) * alpha) * pp : 0.0f;
+        const float vl = ul + c_l, ve = ue + c_e;
+        Q = fmaf(p_t, Q, q_t * A);
+        P = p_t * P;
+        A = alpha * A;
+        ul = fmaf(p_t, vl, q_t * ve);
+        ue = alpha * ve;
+      }
+    }
+    if (i + 1 < n_ck) {
+      if constexpr (KQB == 1) __syncthreads();   // every wave is done with this block's k, q
+      stage(cur ^ 1);
+    }
+    __syncthreads();
+  }
+  if (ln.active) {
+    float4 *out = reinterpret_cast<float4 *>(prm.maps + bms * 8);
+    out[0] = make_float4(P, Q, A, ul);
+    out[1] = make_float4(ue, 0.0f, 0.0f, 0.0f);
+  }
+}
+
+// The adjoint entering each chunk from the right, per (b, m, s) lane: from
+// (dlam_fin or 0, deta_fin or 0) at the end of the sequence the chunk maps are
+// applied from the last chunk to the first. maps [batch, chunks, n, 8]; dlam_fin,
+// deta_fin [batch, n] or NULL; gl_end, ge_end [batch, chunks, n].
+__global__ void __launch_bounds__(256) adjoint_ends_kernel(const float *__restrict__ maps,
+                                                           const float *__restrict__ dlam_fin,
+                                                           const float *__restrict__ deta_fin,
+                                                           float *__restrict__ gl_end, float *__restrict__ ge_end,
+                                                           int64_t batch, int64_t chunks, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= batch * n) return;
+  const int64_t b = i / n, e = i % n;
+  float gl = dlam_fin ? dlam_fin[i] : 0.0f;
+  float ge = deta_fin ? deta_fin[i] : 0.0f;
+  for (int64_t ch = chunks - 1; ch >= 0; --ch) {
+    const int64_t row = (b * chunks + ch) * n + e;
+    gl_end[row] = gl;
+    ge_end[row] = ge;
+    const float4 *m = reinterpret_cast<const float4 *>(maps + row * 8);
+    const float4 pqa = m[0], rest = m[1];
+    const float gl_new = fmaf(pqa.x, gl, fmaf(pqa.y, ge, pqa.w));
+    ge = fmaf(pqa.z, ge, rest.x);
+    gl = gl_new;
+  }
+}
+
 }  // namespace kla
 
 namespace kla {

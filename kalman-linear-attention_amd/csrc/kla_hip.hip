@@ -28,7 +28,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 14;
+constexpr int kAbiVersion = 15;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -871,6 +871,56 @@ int kla_chunk_starts(const float *maps, const float *lam0, const float *eta0, fl
   if (!all_aligned(16, {maps})) return fail(KLA_ERR_ALIGN, "%s: maps not 16-byte aligned", fn);
   hipLaunchKernelGGL(chunk_starts_kernel, dim3(static_cast<uint32_t>((lanes + 255) / 256)), dim3(256), 0, stream, maps,
                      lam0, eta0, lam_start, eta_start, lam_end, eta_end, batch, chunks, n);
+  return hip_status(fn, hipGetLastError());
+}
+
+int kla_fused_adjoint_maps(const float *dy, const float *dy_var, const kla_sensors *sensors, const float *k,
+                           const float *q, const float *a, const float *p, const float *ck_lam, const float *ck_eta,
+                           float *maps, int decode_from_prior, int64_t batch, int64_t steps, int64_t M, int64_t S,
+                           hipStream_t stream) {
+  const char *fn = "kla_fused_adjoint_maps";
+  int rc = check_fused_shape(fn, batch, steps, M, S);
+  if (rc != KLA_OK) return rc;
+  SensorIn sn;
+  if ((rc = sensors_from(fn, sensors, M, &sn)) != KLA_OK) return rc;
+  if (batch == 0 || M == 0 || S == 0) return KLA_OK;
+  if (!a || !p || !maps) return fail(KLA_ERR_INVALID_ARG, "%s: a, p and maps must not be NULL", fn);
+  if (steps > 0 && (!dy || !sn.v || !sn.lv || !k || !q || !ck_lam || !ck_eta))
+    return fail(KLA_ERR_INVALID_ARG, "%s: dy, the sensors, k, q and the checkpoints must not be NULL", fn);
+  if (!all_aligned(4, {dy, dy_var, k, q, a, p, ck_lam, ck_eta}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if (!all_aligned(16, {maps})) return fail(KLA_ERR_ALIGN, "%s: maps not 16-byte aligned", fn);
+  const FusedGeom g = fused_geom(batch, steps, M, S);
+  const int64_t grid = smul(batch, g.groups);
+  if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
+  const AdjointMapParams prm{dy, dy_var, sn, k, q, a, p, ck_lam, ck_eta, maps};
+  return with_sp(S, [&](auto sp) {
+    constexpr int SP = decltype(sp)::value;
+    auto run = [&](auto prior, auto bf16, auto var) {
+      hipLaunchKernelGGL(
+          (fused_adjoint_map_kernel<SP, decltype(prior)::value, decltype(bf16)::value, decltype(var)::value>),
+          dim3(static_cast<uint32_t>(grid)), dim3(kFusedThreads), 0, stream, prm, g);
+    };
+    with_flags(run, decode_from_prior != 0, sn.bf16 != 0, dy_var != nullptr);
+    return hip_status(fn, hipGetLastError());
+  });
+}
+
+int kla_adjoint_ends(const float *maps, const float *dlam_fin, const float *deta_fin, float *gl_end, float *ge_end,
+                     int64_t batch, int64_t chunks, int64_t M, int64_t S, hipStream_t stream) {
+  const char *fn = "kla_adjoint_ends";
+  if (batch < 0 || chunks < 0 || M < 0 || S < 0) return fail(KLA_ERR_INVALID_ARG, "%s: negative size", fn);
+  const int64_t n = smul(M, S);
+  const int64_t lanes = smul(batch, n);
+  if (lanes >= (1ll << 40) || chunks > (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: problem too large", fn);
+  if (lanes == 0 || chunks == 0) return KLA_OK;
+  if (!maps || !gl_end || !ge_end)
+    return fail(KLA_ERR_INVALID_ARG, "%s: maps, gl_end and ge_end must not be NULL", fn);
+  if (!all_aligned(4, {dlam_fin, deta_fin, gl_end, ge_end}))
+    return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  if (!all_aligned(16, {maps})) return fail(KLA_ERR_ALIGN, "%s: maps not 16-byte aligned", fn);
+  hipLaunchKernelGGL(adjoint_ends_kernel, dim3(static_cast<uint32_t>((lanes + 255) / 256)), dim3(256), 0, stream, maps,
+                     dlam_fin, deta_fin, gl_end, ge_end, batch, chunks, n);
   return hip_status(fn, hipGetLastError());
 }
 

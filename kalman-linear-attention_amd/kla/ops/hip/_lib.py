@@ -19,7 +19,7 @@ import torch
 # one the ABI tests run against); by default the in-tree libkla_hip.so.
 LIB_PATH = os.environ.get("KLA_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))), "lib", "libkla_hip.so")
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -61,6 +61,8 @@ _SIGNATURES = {
                                    + [_p, ctypes.c_size_t, _p]),
     "kla_fused_chunk_maps": (ctypes.c_int, [_p] * 5 + [_i64] * 4 + [_p]),
     "kla_chunk_starts": (ctypes.c_int, [_p] * 7 + [_i64] * 4 + [_p]),
+    "kla_fused_adjoint_maps": (ctypes.c_int, [_p] * 10 + [ctypes.c_int] + [_i64] * 4 + [_p]),
+    "kla_adjoint_ends": (ctypes.c_int, [_p] * 5 + [_i64] * 4 + [_p]),
     "kla_step_fwd": (ctypes.c_int, [_p] * 12 + [ctypes.c_int] + [_i64] * 3 + [_p]),
     "kla_decode_step_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _p, _p, _i64] + [_p] * 10
                             + [_i64] * 3 + [_p]),

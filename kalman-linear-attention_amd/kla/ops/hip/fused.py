@@ -56,10 +56,7 @@ def time_chunks(B: int, L: int, M: int, S: int, cus: int) -> int:
     to a power of two, at least 4); below _split_below(SP) workgroups per CU the
     chunk count doubles while the grid stays below SPLIT_TO per CU, the chunks
     divide L evenly and stay MIN_CHUNK steps or longer."""
-    sp = 4
-    while sp < S:
-        sp *= 2
-    base = B * -(-M // (256 // sp))
+    sp, base = _grid(B, M, S)
     if base >= _split_below(sp) * cus:
         return 1
     nc = 1
@@ -68,11 +65,41 @@ def time_chunks(B: int, L: int, M: int, S: int, cus: int) -> int:
     return nc
 
 
-def _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, decode_from_prior, B, L, M, S, nc, dev):
+def _grid(B: int, M: int, S: int) -> tuple[int, int]:
+    """(SP, workgroups) of the fused kernels' plain grid: SP = S rounded up to a
+    power of two (at least 4), 256 / SP channels a workgroup, B x channel groups."""
+    sp = 4
+    while sp < S:
+        sp *= 2
+    return sp, B * -(-M // (256 // sp))
+
+
+def train_chunks(B: int, L: int, M: int, S: int, cus: int) -> int:
+    """Chunks the time-split training pair (the forward that keeps checkpoints and
+    the backward) cuts each sequence into (1: no split). The backward holds two
+    workgroups per CU and the split costs about 1.7 backwards of work (the chunk
+    maps' replay and composition, then the backward itself), so it pays below one
+    workgroup per CU: the chunk count doubles while the grid stays below two per
+    CU, the chunks divide L into whole 16-step checkpoint blocks (the forward's
+    checkpoints are then the same memory on the chunk view) and last at least
+    MIN_CHUNK steps."""
+    _, base = _grid(B, M, S)
+    if base >= cus:
+        return 1
+    nc = 1
+    while base * nc < 2 * cus and L % (32 * nc) == 0 and L // (2 * nc) >= MIN_CHUNK:
+        nc *= 2
+    return nc
+
+
+def _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, decode_from_prior, B, L, M, S, nc, dev,
+                   ck_lam=None, ck_eta=None):
     """The time-split forward: kla_fused_chunk_maps on the [B * nc, L / nc] view,
-    kla_chunk_starts, then the fused forward on the view from those starts.
-    Returns (lam_fin, eta_fin), the state after each sequence's last chunk (from
-    the chunk maps, written [B, M, S] by kla_chunk_starts)."""
+    kla_chunk_starts, then the fused forward on the view from those starts (with
+    the checkpoints when given: [B, n_ck, M, S] is the view's [B * nc, n_ck / nc,
+    M, S] when L / nc is a multiple of 16). Returns (lam_fin, eta_fin), the state
+    after each sequence's last chunk (from the chunk maps, written [B, M, S] by
+    kla_chunk_starts)."""
     lib, pt = _lib.lib(), _lib.ptr
     stream = torch.cuda.current_stream(dev).cuda_stream
     Bp, Lc = B * nc, L // nc
@@ -88,8 +115,40 @@ def _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, decode_from_prior, B, L
     scratch = maps.view(-1)
     _lib.check("kla_fused_scan_sensors_fwd", lib.kla_fused_scan_sensors_fwd(
         ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam_st), pt(eta_st), pt(y), pt(y_var), pt(scratch),
-        pt(scratch[Bp * M * S:]), None, None, int(decode_from_prior), Bp, Lc, M, S, stream))
+        pt(scratch[Bp * M * S:]), pt(ck_lam), pt(ck_eta), int(decode_from_prior), Bp, Lc, M, S, stream))
     return lam_fin, eta_fin
+
+
+def _split_backward(bwd, dy, dy_var, dlam_fin, deta_fin, sn, k, q, a, p, ck_lam, ck_eta, decode_from_prior,
+                    B, L, M, S, nc, dev):
+    """The time-split backward: kla_fused_adjoint_maps on the [B * nc, L / nc]
+    view, kla_adjoint_ends, then ``bwd(batch, steps, dlam_fin, deta_fin, dlam0,
+    deta0, workspace, nbytes)`` -- the backward entry point on the view, with every
+    chunk's adjoint entering from its end. Returns (dlam0, deta0) [B, M, S], the
+    first chunks' initial-state gradients."""
+    lib, pt = _lib.lib(), _lib.ptr
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    Bp, Lc = B * nc, L // nc
+    f32 = dict(dtype=_F32, device=dev)
+    maps = torch.empty(Bp, M, S, 8, **f32)
+    _lib.check("kla_fused_adjoint_maps", lib.kla_fused_adjoint_maps(
+        pt(dy), pt(dy_var), ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(ck_lam), pt(ck_eta), pt(maps),
+        int(decode_from_prior), Bp, Lc, M, S, stream))
+    gl_end, ge_end = torch.empty(B, nc, M, S, **f32), torch.empty(B, nc, M, S, **f32)
+    _lib.check("kla_adjoint_ends", lib.kla_adjoint_ends(
+        pt(maps), pt(dlam_fin), pt(deta_fin), pt(gl_end), pt(ge_end), B, nc, M, S, stream))
+    dlam0, deta0 = torch.empty(B, nc, M, S, **f32), torch.empty(B, nc, M, S, **f32)
+    nbytes = int(lib.kla_fused_workspace_bytes(Bp, Lc, M, S))
+    ws, _ = _lib.scratch(nbytes, dev)
+    bwd(Bp, Lc, gl_end, ge_end, dlam0, deta0, ws, nbytes)
+    return dlam0[:, 0].contiguous(), deta0[:, 0].contiguous()
+
+
+def _dense_sensors(v: torch.Tensor, lambda_v: torch.Tensor) -> "_lib.Sensors":
+    """Dense fp32 [B, L, M] v and lambda_v as a sensor descriptor."""
+    M = v.shape[2]
+    return _lib.Sensors(v=_lib.ptr(v), ld_v=M, obs=_lib.ptr(lambda_v), ld_obs=M, dtype=_lib.KLA_DTYPE_F32,
+                        log_var=0, obs_var_min=0.0, obs_var_max=math.inf)
 
 
 def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
@@ -130,12 +189,12 @@ def _fused_fwd_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: t
     ck_eta = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
     if B * M * S == 0:
         return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
-    nc = 1 if save else time_chunks(B, L, M, S, _cus(dev.index or 0))
+    cus = _cus(dev.index or 0)
+    nc = train_chunks(B, L, M, S, cus) if save else time_chunks(B, L, M, S, cus)
     if nc > 1:
-        sn = _lib.Sensors(v=_lib.ptr(v), ld_v=M, obs=_lib.ptr(lambda_v), ld_obs=M, dtype=_lib.KLA_DTYPE_F32,
-                          log_var=0, obs_var_min=0.0, obs_var_max=math.inf)
-        lam_fin, eta_fin = _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, decode_from_prior, B, L, M, S, nc,
-                                          dev)
+        lam_fin, eta_fin = _split_forward(_dense_sensors(v, lambda_v), k, q, a, p, lam0, eta0, y, y_var,
+                                          decode_from_prior, B, L, M, S, nc, dev,
+                                          ck_lam=ck_lam if save else None, ck_eta=ck_eta if save else None)
         return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
     stream = torch.cuda.current_stream(dev).cuda_stream
     pt = _lib.ptr
@@ -174,13 +233,23 @@ def _fused_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: Op
     dlam0, deta0 = v.new_empty(B, M, S), v.new_empty(B, M, S)
     if M * S == 0:
         return dv, dlv, dk, dq, da, dp, dlam0, deta0
-    nbytes = int(_lib.lib().kla_fused_workspace_bytes(B, L, M, S))
-    ws, stream = _lib.scratch(nbytes, dev)
     pt = _lib.ptr
-    _lib.check("kla_fused_scan_bwd", _lib.lib().kla_fused_scan_bwd(
-        pt(dy), pt(dy_var), pt(dlam_fin), pt(deta_fin), pt(v), pt(lambda_v), pt(k), pt(q), pt(a), pt(p),
-        pt(ck_lam), pt(ck_eta), pt(dv), pt(dlv), pt(dk), pt(dq), pt(da), pt(dp), pt(dlam0), pt(deta0),
-        int(decode_from_prior), B, L, M, S, pt(ws), ws.numel(), stream))
+
+    def bwd(batch, steps, lam_fin_grad, eta_fin_grad, lam0_grad, eta0_grad, ws, nbytes):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check("kla_fused_scan_bwd", _lib.lib().kla_fused_scan_bwd(
+            pt(dy), pt(dy_var), pt(lam_fin_grad), pt(eta_fin_grad), pt(v), pt(lambda_v), pt(k), pt(q), pt(a),
+            pt(p), pt(ck_lam), pt(ck_eta), pt(dv), pt(dlv), pt(dk), pt(dq), pt(da), pt(dp), pt(lam0_grad),
+            pt(eta0_grad), int(decode_from_prior), batch, steps, M, S, pt(ws), nbytes, stream))
+
+    nc = train_chunks(B, L, M, S, _cus(dev.index or 0))
+    if nc > 1:
+        dlam0, deta0 = _split_backward(bwd, dy, dy_var, dlam_fin, deta_fin, _dense_sensors(v, lambda_v), k, q, a,
+                                       p, ck_lam, ck_eta, decode_from_prior, B, L, M, S, nc, dev)
+        return dv, dlv, dk, dq, da, dp, dlam0, deta0
+    nbytes = int(_lib.lib().kla_fused_workspace_bytes(B, L, M, S))
+    ws, _ = _lib.scratch(nbytes, dev)
+    bwd(B, L, dlam_fin, deta_fin, dlam0, deta0, ws, ws.numel())
     return dv, dlv, dk, dq, da, dp, dlam0, deta0
 
 
@@ -297,10 +366,12 @@ def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torc
     if B * M * S == 0:
         return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
     sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
-    nc = 1 if save else time_chunks(B, L, M, S, _cus(dev.index or 0))
+    cus = _cus(dev.index or 0)
+    nc = train_chunks(B, L, M, S, cus) if save else time_chunks(B, L, M, S, cus)
     if nc > 1:
         lam_fin, eta_fin = _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var if with_var else None,
-                                          decode_from_prior, B, L, M, S, nc, dev)
+                                          decode_from_prior, B, L, M, S, nc, dev,
+                                          ck_lam=ck_lam if save else None, ck_eta=ck_eta if save else None)
         return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
     pt = _lib.ptr
     _lib.check("kla_fused_scan_sensors_fwd", _lib.lib().kla_fused_scan_sensors_fwd(
@@ -344,14 +415,24 @@ def _sensors_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: 
     dlam0, deta0 = k.new_empty(B, M, S), k.new_empty(B, M, S)
     if M * S == 0:
         return dv, dobs, dk, dq, da, dp, dlam0, deta0
-    nbytes = int(_lib.lib().kla_fused_workspace_bytes(B, L, M, S))
-    ws, stream = _lib.scratch(nbytes, dev)
     sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
     pt = _lib.ptr
-    _lib.check("kla_fused_scan_sensors_bwd", _lib.lib().kla_fused_scan_sensors_bwd(
-        pt(dy), pt(dy_var), pt(dlam_fin), pt(deta_fin), ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p),
-        pt(ck_lam), pt(ck_eta), pt(dv), pt(dobs), pt(dk), pt(dq), pt(da), pt(dp), pt(dlam0), pt(deta0),
-        int(decode_from_prior), B, L, M, S, pt(ws), ws.numel(), stream))
+
+    def bwd(batch, steps, lam_fin_grad, eta_fin_grad, lam0_grad, eta0_grad, ws, nbytes):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        _lib.check("kla_fused_scan_sensors_bwd", _lib.lib().kla_fused_scan_sensors_bwd(
+            pt(dy), pt(dy_var), pt(lam_fin_grad), pt(eta_fin_grad), ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p),
+            pt(ck_lam), pt(ck_eta), pt(dv), pt(dobs), pt(dk), pt(dq), pt(da), pt(dp), pt(lam0_grad),
+            pt(eta0_grad), int(decode_from_prior), batch, steps, M, S, pt(ws), nbytes, stream))
+
+    nc = train_chunks(B, L, M, S, _cus(dev.index or 0))
+    if nc > 1:
+        dlam0, deta0 = _split_backward(bwd, dy, dy_var, dlam_fin, deta_fin, sn, k, q, a, p, ck_lam, ck_eta,
+                                       decode_from_prior, B, L, M, S, nc, dev)
+        return dv, dobs, dk, dq, da, dp, dlam0, deta0
+    nbytes = int(_lib.lib().kla_fused_workspace_bytes(B, L, M, S))
+    ws, _ = _lib.scratch(nbytes, dev)
+    bwd(B, L, dlam_fin, deta_fin, dlam0, deta0, ws, ws.numel())
     return dv, dobs, dk, dq, da, dp, dlam0, deta0
 
 

@@ -321,6 +321,72 @@ def test_time_split_validation(lib):
     assert starts(shape=(2**31, 2**31, 2**31, 16)) == _lib.KLA_ERR_INVALID_ARG
 
 
+def test_time_split_backward_validation(lib):
+    """kla_fused_adjoint_maps and kla_adjoint_ends (the time-split backward's two
+    extra passes) check shape, sensors, NULL and alignment before launching."""
+    P = ALIGNED
+    P16 = ALIGNED + 16
+
+    def sensors(**kw):
+        a = dict(v=P, ld_v=6, obs=P, ld_obs=6, dtype=_lib.KLA_DTYPE_F32, log_var=0, obs_var_min=0.0,
+                 obs_var_max=float("inf"))
+        a.update(kw)
+        return _lib.Sensors(**a)
+
+    def maps(dy=P, dyv=None, k=P, q=P, ck=P, out=P, shape=(2, 32, 6, 16), s=None):
+        s = sensors() if s is None else s
+        return lib.kla_fused_adjoint_maps(dy, dyv, ctypes.byref(s), k, q, P, P, ck, ck, out, 0, *shape, None)
+
+    assert maps(shape=(2, 32, 6, 257)) == _lib.KLA_ERR_INVALID_ARG
+    assert maps(shape=(2, -1, 6, 16)) == _lib.KLA_ERR_INVALID_ARG
+    assert maps(shape=(0, 32, 6, 16)) == _lib.KLA_OK
+    assert maps(out=None) == _lib.KLA_ERR_INVALID_ARG
+    assert "maps must not be NULL" in err(lib)
+    assert maps(dy=None) == _lib.KLA_ERR_INVALID_ARG
+    assert maps(ck=None) == _lib.KLA_ERR_INVALID_ARG
+    assert "checkpoints" in err(lib)
+    assert maps(s=sensors(obs=None)) == _lib.KLA_ERR_INVALID_ARG
+    assert maps(s=sensors(dtype=9)) == _lib.KLA_ERR_DTYPE
+    assert maps(dyv=ODD) == _lib.KLA_ERR_ALIGN
+    assert maps(out=P + 4) == _lib.KLA_ERR_ALIGN
+    assert "16-byte" in err(lib)
+    assert lib.kla_fused_adjoint_maps(P, None, None, P, P, P, P, P, P, P, 0, 2, 32, 6, 16,
+                                      None) == _lib.KLA_ERR_INVALID_ARG
+
+    def ends(m=P16, dl=None, de=None, gl=P, ge=P, shape=(2, 4, 6, 16)):
+        return lib.kla_adjoint_ends(m, dl, de, gl, ge, *shape, None)
+
+    assert ends(shape=(-2, 4, 6, 16)) == _lib.KLA_ERR_INVALID_ARG
+    assert ends(shape=(0, 4, 6, 16)) == _lib.KLA_OK
+    assert ends(shape=(2, 0, 6, 16)) == _lib.KLA_OK
+    assert ends(m=None) == _lib.KLA_ERR_INVALID_ARG
+    assert ends(ge=None) == _lib.KLA_ERR_INVALID_ARG
+    assert ends(dl=ODD) == _lib.KLA_ERR_ALIGN
+    assert ends(m=P + 8) == _lib.KLA_ERR_ALIGN
+    assert ends(shape=(2**31, 2**31, 2**31, 16)) == _lib.KLA_ERR_INVALID_ARG
+
+
+def test_train_chunks_plan():
+    """The time-split training pair cuts grids below one workgroup per CU, doubling
+    the chunk count while the grid stays below two per CU, with chunks that divide
+    L into whole 16-step checkpoint blocks and last at least MIN_CHUNK steps."""
+    from kla.ops.hip.fused import MIN_CHUNK, train_chunks
+
+    assert train_chunks(4, 4096, 1024 * 2, 16, 256) == 1   # C4: 512 workgroups
+    assert train_chunks(4, 1024, 1024, 16, 256) == 1       # one workgroup per CU
+    assert train_chunks(2, 1024, 1024, 16, 256) == 4       # C1's shape with gradients: 128 -> 512
+    assert train_chunks(1, 2048, 1024, 16, 256) == 8       # 64 -> 512
+    assert train_chunks(2, 2048, 512, 64, 256) == 1        # 256 workgroups of 4 channels
+    assert train_chunks(1, 2048, 512, 64, 256) == 4        # 128 -> 512
+    assert train_chunks(1, 4096, 128, 256, 256) == 4       # 128 single-channel workgroups -> 512
+    assert train_chunks(1, 256, 64, 16, 256) == 2          # 128-step chunks at least
+    assert train_chunks(1, 100, 64, 16, 256) == 1          # not whole 16-step blocks
+    assert train_chunks(1, 2 * MIN_CHUNK + 16, 8, 16, 256) == 1
+    for B, L, M, S in [(1, 4096, 64, 64), (3, 1024, 200, 32), (1, 65536, 1, 1), (2, 8192, 4096, 16)]:
+        nc = train_chunks(B, L, M, S, 256)
+        assert nc >= 1 and L % (16 * nc) == 0 and (nc == 1 or L // nc >= MIN_CHUNK)
+
+
 def test_time_chunks_plan():
     """The time-split forward cuts only small grids (below one workgroup per CU up
     to d_state 64, two above), into up to eight workgroups per CU, with chunks

@@ -96,12 +96,15 @@ def test_forced_split_of_bf16_sensors_matches_oracle(cuda, chunks, nc, with_var)
 def test_planner_splits_c1_and_matches_oracle(cuda, monkeypatch):
     """At C1's scan shape (B=2, L=1024, M=1024, S=16) the planner cuts 8 chunks
     (128 workgroups -> 1024); split outputs against the float64 filter on whole tensors,
-    and the whole forward (taken when a gradient is to be saved for) to the same bar."""
+    and the forward that saves checkpoints for a gradient (cut by the training
+    planner, into 4) to the same bar."""
     B, L, M, S = 2, 1024, 1024, 16
-    assert fused.time_chunks(B, L, M, S, fused._cus(cuda.index or 0)) == 8
+    cus = fused._cus(cuda.index or 0)
+    assert fused.time_chunks(B, L, M, S, cus) == 8
+    assert fused.train_chunks(B, L, M, S, cus) == 4
     calls = []
     split = fused._split_forward
-    monkeypatch.setattr(fused, "_split_forward", lambda *a: calls.append(a[-2]) or split(*a))
+    monkeypatch.setattr(fused, "_split_forward", lambda *a, **kw: calls.append(a[-2]) or split(*a, **kw))
     ins = make_inputs(B, L, M, S, seed=24)
     xs = [t.to(cuda) for t in ins]
     y, y_var, fin = kla_scan(*xs, backend="hip_fused")
@@ -109,12 +112,12 @@ def test_planner_splits_c1_and_matches_oracle(cuda, monkeypatch):
     wy, wv, wl, we = oracle(ins)
     for name, got, want in (("y", y, wy), ("y_var", y_var, wv), ("lam", fin.lam, wl), ("eta", fin.eta, we)):
         check_scan(name, got, want)
-    # With a gradient to save for, the forward runs whole: the same numbers to the same bar.
+    # With a gradient to save for, the training planner's 4 chunks: the same numbers to the same bar.
     ws = [t.clone().requires_grad_(True) for t in xs]
     y2, y_var2, fin2 = kla_scan(*ws, backend="hip_fused")
     for name, got, want in (("y", y2, wy), ("y_var", y_var2, wv), ("lam", fin2.lam, wl), ("eta", fin2.eta, we)):
         check_scan(name, got, want)
-    assert calls == [8], "a forward that saves checkpoints runs whole"
+    assert calls == [8, 4]
 
 
 def test_split_chunked_prefill_carries_state(cuda):
@@ -129,3 +132,132 @@ def test_split_chunked_prefill_carries_state(cuda):
     check_scan("y", torch.cat([y1, y2], 1), wy)
     check_scan("lam", st2.lam, wl)
     check_scan("eta", st2.eta, we)
+
+
+# ------------------------------------------------------------ training (backward)
+#
+# With a gradient to save for, small grids split as well (kla.ops.hip.fused.
+# train_chunks): the forward keeps its checkpoints on the chunk view (the same
+# memory as the whole sequence's), a pass composes each chunk's adjoint steps
+# into an affine map with an upper-triangular linear part, a walk over the maps
+# from the end of each sequence gives every chunk the adjoint entering it from
+# the right, and the fused backward runs on the view from those. Parity bar: the
+# fused scan's against float64 autograd of the reference's torch path.
+
+
+@pytest.fixture
+def train_chunks(monkeypatch):
+    """force(nc) makes the training planner return nc for every call in the test."""
+
+    def force(nc):
+        monkeypatch.setattr(fused, "train_chunks", lambda B, L, M, S, cus: nc)
+
+    return force
+
+
+@pytest.mark.parametrize("shape", [(2, 256, 9, 16), (1, 128, 3, 128), (3, 320, 70, 4), (1, 256, 2, 256),
+                                   (2, 192, 5, 32)])
+@pytest.mark.parametrize("nc", [2, 4, 8])
+@pytest.mark.parametrize("with_state", [False, True])
+@pytest.mark.parametrize("decode_from_prior", [False, True])
+@pytest.mark.parametrize("with_var", [True, False])
+def test_forced_training_split_matches_float64_autograd(cuda, train_chunks, shape, nc, with_state,
+                                                        decode_from_prior, with_var):
+    from oracle import torch_ref
+
+    B, L, M, S = shape
+    if L % (16 * nc):
+        pytest.skip("chunks must hold whole 16-step checkpoint blocks")
+    print(f"[training split] shape={shape} nc={nc} state={with_state} prior={decode_from_prior} "
+          f"var={with_var}", flush=True)
+    train_chunks(nc)
+    ins = make_inputs(B, L, M, S, seed=31)
+    st = random_state(B, M, S, seed=32)
+    g = torch.Generator().manual_seed(33)
+    wy, wv = torch.randn(B, L, M, generator=g), torch.randn(B, L, M, generator=g)
+    wl, we = torch.randn(B, M, S, generator=g), torch.randn(B, M, S, generator=g)
+
+    def loss(y, y_var, lam, eta):
+        w = [t.to(device=y.device, dtype=y.dtype) for t in (wy, wv, wl, we)]
+        var_term = (w[1] * y_var).sum() if with_var else 0.0
+        return (w[0] * y).sum() + var_term + (w[2] * lam).sum() + (w[3] * eta).sum()
+
+    extra = (st.lam, st.eta) if with_state else ()
+    xs = [t.double().requires_grad_(True) for t in ins + extra]
+    ref = torch_ref.kla_scan_torch(*xs, decode_from_prior=decode_from_prior)
+    loss(*ref).backward()
+    gs = [t.to(cuda).requires_grad_(True) for t in ins + extra]
+    state = KLAState(gs[6], gs[7]) if with_state else None
+    y, y_var, fin = kla_scan(*gs[:6], backend="hip_fused", initial_state=state, decode_from_prior=decode_from_prior)
+    for name, got, want in zip(("y", "y_var", "lam", "eta"), (y, y_var, fin.lam, fin.eta), ref):
+        check_scan(name, got, want.detach().numpy())
+    loss(y, y_var, fin.lam, fin.eta).backward()
+    for name, got, want in zip(("v", "lambda_v", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
+        check_scan("d" + name, got.grad, want.grad.numpy())
+
+
+@pytest.mark.parametrize("nc", [2, 4])
+def test_forced_training_split_of_sensors(cuda, train_chunks, nc):
+    """The layer's training path (kla_scan_fused_sensors on projection columns):
+    fp32 columns against float64 autograd of the read-out tail and the reference's
+    filter, and bf16 columns equal to the fp32 run on the widened values bit for
+    bit, as for the whole sequence (dv, d log sigma^2 rounded to bf16)."""
+    import torch.nn.functional as F
+
+    from kla.ops.hip.fused import kla_scan_fused_sensors
+    from oracle import torch_ref
+
+    B, L, M, S = 2, 256, 20, 16
+    train_chunks(nc)
+    _, _, k, q, a, p = make_inputs(B, L, M, S, seed=34)
+    g = torch.Generator().manual_seed(35)
+    proj16 = (torch.randn(B, L, 2 * M + 3, generator=g) * 1.5).to(torch.bfloat16)
+    proj = proj16.float()
+    st = random_state(B, M, S, seed=36)
+    wy, wl = torch.randn(B, L, M, generator=g), torch.randn(B, M, S, generator=g)
+
+    def views(t):
+        return t[..., :M], t[..., M + 1:2 * M + 1]
+
+    xs = [t.double().requires_grad_(True) for t in (proj, k, q, a, p, st.lam, st.eta)]
+    v64, lv64 = views(xs[0])
+    ref = torch_ref.kla_scan_torch(v64, 1.0 / (F.softplus(lv64) + 1e-4), *xs[1:])
+    ((wy.double() * ref[0]).sum() + (wl.double() * ref[2]).sum()).backward()
+    runs = []
+    for pj in (proj, proj16):
+        gs = [t.to(cuda).requires_grad_(True) for t in (pj, k, q, a, p, st.lam, st.eta)]
+        y, _, lam, _ = kla_scan_fused_sensors(*views(gs[0]), *gs[1:], with_var=False)
+        ((wy.to(cuda) * y).sum() + (wl.to(cuda) * lam).sum()).backward()
+        runs.append([y, lam] + [t.grad for t in gs])
+    check_scan("y", runs[0][0], ref[0].detach().numpy())
+    check_scan("lam", runs[0][1], ref[2].detach().numpy())
+    for name, got, want in zip(("dproj", "dk", "dq", "da", "dp", "dlam0", "deta0"), runs[0][2:], xs):
+        check_scan(name, got, want.grad.numpy())
+    f32, b16 = runs
+    for i, name in enumerate(("y", "lam", "dproj", "dk", "dq", "da", "dp", "dlam0", "deta0")):
+        want = f32[i].to(torch.bfloat16) if name == "dproj" else f32[i]
+        assert torch.equal(b16[i], want), name
+
+
+def test_training_planner_at_c1_matches_whole_backward(cuda, monkeypatch):
+    """At C1's shape with gradients (B=2, L=1024, M=1024, S=16: 128 workgroups) the
+    training planner cuts 4 chunks; every output and gradient of the split pair
+    against the whole pair (the training planner forced to 1), at the scan's bar
+    relative to the whole run."""
+    B, L, M, S = 2, 1024, 1024, 16
+    assert fused.train_chunks(B, L, M, S, fused._cus(cuda.index or 0)) == 4
+    ins = [t.to(cuda) for t in make_inputs(B, L, M, S, seed=37)]
+    st = random_state(B, M, S, seed=38)
+    g = torch.Generator(device="cpu").manual_seed(39)
+    wy, wv = torch.randn(B, L, M, generator=g).to(cuda), torch.randn(B, L, M, generator=g).to(cuda)
+    runs = []
+    for force in (None, 1):
+        if force is not None:
+            monkeypatch.setattr(fused, "train_chunks", lambda *a: 1)
+        gs = [t.clone().requires_grad_(True) for t in ins + [st.lam.to(cuda), st.eta.to(cuda)]]
+        y, y_var, fin = kla_scan(*gs[:6], backend="hip_fused", initial_state=KLAState(gs[6], gs[7]))
+        ((wy * y).sum() + (wv * y_var).sum() + fin.lam.sum() + fin.eta.square().sum()).backward()
+        runs.append([y, y_var, fin.lam, fin.eta] + [t.grad for t in gs])
+    names = ("y", "y_var", "lam", "eta", "dv", "dlambda_v", "dk", "dq", "da", "dp", "dlam0", "deta0")
+    for name, got, want in zip(names, *runs):
+        check_scan(name, got, want.detach().double().cpu().numpy())
