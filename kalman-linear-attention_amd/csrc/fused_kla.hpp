@@ -1434,65 +1434,90 @@ __global__ void __launch_bounds__(kFusedThreads) fused_adjoint_map_kernel(Adjoin
     const int64_t t0 = blk * TB;
     if (i + 1 < n_ck) load(t0 - TB);
     const int nv = static_cast<int>(L - t0 < TB ? L - t0 : TB);
-    // The block's replay, as in fused_kla_bwd_kernel.
-    float lh[TB + 1], eh[TB + 1], idn[TB];
-    {
-      const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
-      float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
-      float eta = ln.active ? prm.ck_eta[ci] : 0.0f;
+    const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
+    // The block's replay and its steps composed in reverse, as the backward's
+    // replay and walk (FULL: every step of the block lies inside the sequence;
+    // tile values four steps per LDS read from 16 lanes per channel on).
+    auto block = [&](auto full_c) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_c)::value;
+      constexpr bool X4 = SP >= 16;
+      float lh[TB + 1], eh[TB + 1], idn[TB];
+      {
+        float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
+        float eta = ln.active ? prm.ck_eta[ci] : 0.0f;
+        float4 l4{}, v4{}, k4{}, k24{};
 #pragma unroll
-      for (int j = 0; j < TB; ++j) {
-        lh[j] = lam;
-        eh[j] = eta;
-        idn[j] = 0.0f;
-        if (j < nv) {
-          const float sig = s_l[cur][c][j];
-          const float sv = s_sv[cur][c][j];
-          const float kk = s_k[kb][ln.s][j];
-          const float k2 = kK2 ? s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0][j] : kk * kk;
-          lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, inv_a2, C, idn[j]);
+        for (int j = 0; j < TB; ++j) {
+          if (X4 && j % 4 == 0) {
+            asm volatile("" ::: "memory");
+            l4 = lds4(s_l[cur][c], j);
+            v4 = lds4(s_sv[cur][c], j);
+            k4 = lds4(s_k[kb][ln.s], j);
+            if constexpr (kK2) k24 = lds4(s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0], j);
+          }
+          lh[j] = lam;
+          eh[j] = eta;
+          if (!FULL) idn[j] = 0.0f;
+          if (FULL || j < nv) {
+            const float sig = X4 ? pick4(l4, j % 4) : s_l[cur][c][j];
+            const float sv = X4 ? pick4(v4, j % 4) : s_sv[cur][c][j];
+            const float kk = X4 ? pick4(k4, j % 4) : s_k[kb][ln.s][j];
+            const float k2 = !kK2 ? kk * kk : X4 ? pick4(k24, j % 4) : s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0][j];
+            lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, inv_a2, C, idn[j]);
+          }
+        }
+        lh[TB] = lam;
+        eh[TB] = eta;
+      }
+      // The read-out terms as the backward forms them: dmean, t = d(loss)/d(var) var.
+      float4 dy4{}, q4{}, dyv4{};
+#pragma unroll
+      for (int j = TB - 1; j >= 0; --j) {
+        if (X4 && j % 4 == 3) {
+          asm volatile("" ::: "memory");
+          dy4 = lds4(s_dy[cur][c], j - 3);
+          q4 = lds4(s_q[kb][ln.s], j - 3);
+          if constexpr (VAR) dyv4 = lds4(s_dyv[VAR ? cur : 0][VAR ? c : 0], j - 3);
+        }
+        if (FULL || j < nv) {
+          const float dy = X4 ? pick4(dy4, j % 4) : s_dy[cur][c][j];
+          const float qq = X4 ? pick4(q4, j % 4) : s_q[kb][ln.s][j];
+          const float ep = eh[j];
+          const float lam_t = lh[j + 1], eta_t = eh[j + 1];
+          const float inv_den = idn[j];
+          const float idn_a = inv_den * inv_a2;
+          const bool da_ok = idn_a <= kInvEps;
+          const float inv_Da = fminf(idn_a, kInvEps);
+          const float alpha = a_s * inv_Da;
+          const float var = rcp(fmaxf(lam_t, kEps));
+          const float mean = eta_t * var;
+          const float dmo = dy * qq;
+          const float dmean = PRIOR ? dmo * a_s : dmo;
+          float t;
+          if constexpr (VAR) {
+            const float dyv = X4 ? pick4(dyv4, j % 4) : s_dyv[VAR ? cur : 0][VAR ? c : 0][j];
+            const float dvo = dyv * (qq * qq);
+            t = fmaf(dmean, mean, (PRIOR ? dvo * a2 : dvo) * var);
+          } else {
+            t = dmean * mean;
+          }
+          const float c_e = dmean * var;
+          const float c_l = lam_t >= kEps ? -(t * var) : 0.0f;
+          const float p_t = inv_den * idn_a;
+          const float q_t = da_ok ? -((ep * inv_Da) * alpha) * pp : 0.0f;
+          const float vl = ul + c_l, ve = ue + c_e;
+          Q = fmaf(p_t, Q, q_t * A);
+          P = p_t * P;
+          A = alpha * A;
+          ul = fmaf(p_t, vl, q_t * ve);
+          ue = alpha * ve;
         }
       }
-      lh[TB] = lam;
-      eh[TB] = eta;
-    }
-    // Compose the block's steps in reverse (the read-out terms as the backward
-    // forms them: dmean, t = d(loss)/d(var) var).
-#pragma unroll
-    for (int j = TB - 1; j >= 0; --j) {
-      if (j < nv) {
-        const float dy = s_dy[cur][c][j];
-        const float qq = s_q[kb][ln.s][j];
-        const float ep = eh[j];
-        const float lam_t = lh[j + 1], eta_t = eh[j + 1];
-        const float inv_den = idn[j];
-        const float idn_a = inv_den * inv_a2;
-        const bool da_ok = idn_a <= kInvEps;
-        const float inv_Da = fminf(idn_a, kInvEps);
-        const float alpha = a_s * inv_Da;
-        const float var = rcp(fmaxf(lam_t, kEps));
-        const float mean = eta_t * var;
-        const float dmo = dy * qq;
-        const float dmean = PRIOR ? dmo * a_s : dmo;
-        float t;
-        if constexpr (VAR) {
-          const float dvo = s_dyv[VAR ? cur : 0][VAR ? c : 0][j] * (qq * qq);
-          t = fmaf(dmean, mean, (PRIOR ? dvo * a2 : dvo) * var);
-        } else {
-          t = dmean * mean;
-        }
-        const float c_e = dmean * var;
-        const float c_l = lam_t >= kEps ? -(t * var) : 0.0f;
-        const float p_t = inv_den * idn_a;
-        const float q_t = da_ok ? -((ep * inv_Da) * alpha) * pp : 0.0f;
-        const float vl = ul + c_l, ve = ue + c_e;
-        Q = fmaf(p_t, Q, q_t * A);
-        P = p_t * P;
-        A = alpha * A;
-        ul = fmaf(p_t, vl, q_t * ve);
-        ue = alpha * ve;
-      }
-    }
+    };
+    if (nv == TB)
+      block(std::true_type{});
+    else
+      block(std::false_type{});
     if (i + 1 < n_ck) {
       if constexpr (KQB == 1) __syncthreads();   // every wave is done with this block's k, q
       stage(cur ^ 1);
