@@ -112,6 +112,7 @@ Geom make_geom(Shape s, int W, int S, int V) {
   g.n_chunks = (s.steps + chunk - 1) / chunk;
   g.plane = g.n_tiles * tile;
   g.max_spin = kMaxSpin;
+  g.carry_only = 0;
   return g;
 }
 
@@ -210,9 +211,20 @@ int hip_status(const char *fn, hipError_t e) {
   return KLA_OK;
 }
 
+// Look-back records: carries only (no chunk aggregates) when one chunk of every
+// tile together moves at least this many HBM bytes, i.e. several microseconds
+// of streaming per hop of the carry chain (about 0.5 us). Measured per kernel
+// (us, aggregates -> carries only): (8, 4096, 2048) Moebius fwd 197 -> 190, bwd
+// 366 -> 361, affine fwd 140 -> 137, bwd 215 -> 213; (1, 65536, 64) Moebius
+// fwd 152 -> 577 and (4, 4096, 256) 33 -> 56, where the chain is the critical
+// path (there one chunk row is under 2 MiB).
+constexpr int64_t kCarryOnlyRowBytes = 16ll << 20;
+
 template <class P, class T>
 int launch(const char *fn, const typename P::Params &prm, Shape s, void *ws, hipStream_t stream) {
-  const Geom g = make_geom<T>(s);
+  Geom g = make_geom<T>(s);
+  const int64_t row_bytes = smul(smul(g.plane, T::W * T::S), P::BYTES);
+  g.carry_only = row_bytes >= kCarryOnlyRowBytes ? 1 : 0;
   const int64_t grid = g.n_tiles * g.n_chunks;
   hipLaunchKernelGGL((lookback_scan_kernel<P, T::W, T::S, T::V>), dim3(static_cast<uint32_t>(grid)),
                      dim3(kWave * T::W), 0, stream, prm, g, static_cast<uint64_t *>(ws));

@@ -22,6 +22,14 @@
 // HBM traffic is therefore the compulsory one (inputs read once, outputs
 // written once) plus 8-byte records per lane per chunk.
 //
+// Carry-only launches (Geom::carry_only) publish no aggregates: a chunk waits
+// for its predecessor's carry alone, so the carries travel the chain one chunk
+// at a time (about half a microsecond a hop). That pays where one chunk of every
+// tile together is many microseconds of HBM traffic, so the chain hides under
+// the streaming (the headline shapes: 2-4% faster, 1 record word per lane and
+// chunk instead of K + 1); with few tiles along a long sequence the hop latency
+// is the critical path and the aggregates let a chunk skip ahead instead.
+//
 // Records. Each published float travels in one 64-bit word, (tag << 32) | bits,
 // written and read with relaxed agent-scope atomics: a word is valid iff its tag
 // equals the launch's tag, so no fence orders a payload against a flag, and the
@@ -67,8 +75,8 @@ __device__ __forceinline__ float word_val(uint64_t w) { return __uint_as_float(s
 // Carry entering `chunk` along one lane chain (see "Determinism" above).
 //
 // Polls the nearest unresolved predecessor's carry word (one load per poll
-// while it waits); when only its aggregate is out, the search passes on to the
-// chunk before. The aggregates between the carry found and `chunk` are then
+// while it waits); when only its aggregate is out (never in a carry-only
+// launch), the search passes on to the chunk before. The aggregates between the carry found and `chunk` are then
 // applied one by one in chain order. Each chunk's K aggregate words are read
 // with their loads in flight together.
 template <class P>
@@ -86,7 +94,7 @@ __device__ __forceinline__ float look_back(uint64_t *rec, uint64_t *ctl, const G
       break;
     }
     // Chunk 0 publishes only its carry, never an aggregate.
-    bool ready = j > 0;
+    bool ready = !g.carry_only && j > 0;
     if (ready) {
       uint64_t aw[K];
 #pragma unroll
@@ -199,7 +207,7 @@ __global__ void __launch_bounds__(kWave * W)
       if (q.ok) {
         if (chunk == 0) {
           carry = P::initial(prm, g, q, v);
-        } else {
+        } else if (!g.carry_only) {
 #pragma unroll
           for (int k = 0; k < K; ++k) put_word(rec + (k * g.n_chunks + chunk) * g.plane + slot, tot.v[k], tag);
         }

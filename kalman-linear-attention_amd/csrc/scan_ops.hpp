@@ -55,6 +55,7 @@ struct Geom {
   int64_t n_chunks;          // look-back kernel: ceil(steps / (W * S))
   int64_t plane;             // look-back kernel: record words per (plane, chunk) = n_tiles * 64 V
   uint32_t max_spin;         // look-back kernel: polls before a wait gives up
+  int carry_only;            // look-back kernel: publish carries only, no chunk aggregates
 };
 
 template <int K>
@@ -389,6 +390,7 @@ __device__ __forceinline__ float mobius_next(float a, float b, float x, float de
 template <bool HAS_D>
 struct MobiusFwd {
   static constexpr int AGG = 4;
+  static constexpr int BYTES = HAS_D ? 20 : 16;   // HBM bytes per element: A, B, C (D) in, lam out
   using IO = float;
   struct Params {
     const float *A, *B, *C, *D, *lam0;
@@ -511,6 +513,7 @@ struct MobiusFwd {
 template <bool HAS_D>
 struct MobiusBwd {
   static constexpr int AGG = 2;
+  static constexpr int BYTES = HAS_D ? 36 : 28;   // dlam, A, B, C (D) in, dA, dB, dC (dD) out
   using IO = float;
   struct Params {
     const float *dlam, *A, *B, *C, *D, *lam0, *lam;
@@ -629,6 +632,7 @@ struct MobiusBwd {
 template <class IOT, bool CACHED = false>
 struct AffineFwd {
   static constexpr int AGG = 2;
+  static constexpr int BYTES = 3 * static_cast<int>(sizeof(IOT));   // g, u in, h out
   using IO = IOT;
   struct Params {
     const IO *g, *u;
@@ -706,6 +710,7 @@ struct AffineFwd {
 template <class IOT>
 struct AffineBwd {
   static constexpr int AGG = 2;
+  static constexpr int BYTES = 5 * static_cast<int>(sizeof(IOT));   // dh, g, h in, dg, du out
   using IO = IOT;
   struct Params {
     const IO *dh, *g, *h;

@@ -15,6 +15,9 @@ the workgroups at every memory operation on the shared workspace:
   predecessor's aggregate is out it passes on to the chunk before, then
   re-applies the aggregates it skipped in chain order -- which computes the same
   float32 chain as the sequential carry, whatever the schedule;
+* carry-only launches publish no aggregates: a chunk waits on its
+  predecessor's carry alone (the chain then advances one chunk per hop), which
+  computes the same chain;
 * give-up: a wait that exceeds the spin limit yields NaN and counts a failure
   in the header (instead of hanging); a header left in a state no launch leaves
   (a workspace that was not zero-filled) makes every workgroup count a failure
@@ -62,8 +65,9 @@ def word_val(w):
 class Launch:
     """One launch of the look-back scan over g, u [batch, steps, lanes] (float32)."""
 
-    def __init__(self, ws, g, u, h0, W, S, tile, max_spin):
+    def __init__(self, ws, g, u, h0, W, S, tile, max_spin, carry_only=False):
         self.ws, self.g, self.u, self.h0 = ws, g, u, h0
+        self.carry_only = carry_only
         self.batch, self.steps, self.lanes = g.shape
         self.W, self.S, self.tile, self.max_spin = W, S, tile, max_spin
         self.tiles_per_batch = -(-self.lanes // tile)
@@ -116,7 +120,7 @@ class Launch:
             if chunk == 0:
                 carry = F(self.h0[b, n])
             else:
-                for k in range(K):
+                for k in range(0 if self.carry_only else K):
                     yield
                     ws[self.rec(k, chunk, slot)] = word(tag, tot[k])
                 carry = yield from self.look_back(chunk, slot, tag)
@@ -142,7 +146,7 @@ class Launch:
             if word_ok(cw, tag):
                 x = word_val(cw)
                 break
-            ready = j > 0
+            ready = not self.carry_only and j > 0
             if ready:
                 aw = []
                 for k in range(K):
@@ -231,16 +235,19 @@ GEOM = dict(W=3, S=4, tile=4, max_spin=10**9)
 
 @pytest.mark.parametrize("policy", ["in_order", "reverse", "random", "round_robin", "lifo"])
 @pytest.mark.parametrize("resident", [None, 3])
-def test_every_schedule_gives_the_sequential_chain_bit_for_bit(policy, resident):
+@pytest.mark.parametrize("modes", ["aggregates", "carry_only", "alternating"])
+def test_every_schedule_gives_the_sequential_chain_bit_for_bit(policy, resident, modes):
     """Three launches on one workspace, never re-zeroed, with new inputs each time
-    (a stale record of the previous launch read as valid would show): every
-    schedule gives the value of the in-order run, and that is the per-step chain
-    up to the reassociation inside a chunk."""
+    (a stale record of the previous launch read as valid would show; with
+    alternating modes a carry-only launch finds the aggregates of the launch
+    before it): every schedule gives the value of the in-order run, and that is
+    the per-step chain up to the reassociation inside a chunk."""
     rng = random.Random(7)
     ws = None
     for rep in range(3):
         g, u, h0 = inputs(2, 61, 7, seed=10 + rep)
-        la = Launch(ws, g, u, h0, **GEOM)
+        co = modes == "carry_only" or (modes == "alternating" and rep % 2 == 1)
+        la = Launch(ws, g, u, h0, **GEOM, carry_only=co)
         if ws is None:
             ws = la.ws = new_workspace(la)
         run(la, policy, rng, resident=resident)
@@ -253,11 +260,12 @@ def test_every_schedule_gives_the_sequential_chain_bit_for_bit(policy, resident)
         np.testing.assert_allclose(la.h, sequential(g, u, h0), rtol=1e-5, atol=1e-6)
 
 
-def test_results_do_not_depend_on_the_schedule():
+@pytest.mark.parametrize("carry_only", [False, True])
+def test_results_do_not_depend_on_the_schedule(carry_only):
     g, u, h0 = inputs(1, 97, 5, seed=2)
     base = None
     for seed in range(12):
-        la = Launch(None, g, u, h0, **GEOM)
+        la = Launch(None, g, u, h0, **GEOM, carry_only=carry_only)
         la.ws = new_workspace(la)
         run(la, "random", random.Random(seed), resident=1 + seed % 4)
         if base is None:
@@ -280,10 +288,11 @@ def test_epoch_wraps_without_a_zero_tag():
     assert all(np.array_equal(h, outs[0]) for h in outs)
 
 
-def test_a_starved_predecessor_makes_the_wait_give_up_with_nan():
+@pytest.mark.parametrize("carry_only", [False, True])
+def test_a_starved_predecessor_makes_the_wait_give_up_with_nan(carry_only):
     g, u, h0 = inputs(1, 48, 1, seed=4)
     geom = dict(GEOM, max_spin=20)
-    la = Launch(None, g, u, h0, **geom)
+    la = Launch(None, g, u, h0, **geom, carry_only=carry_only)
     la.ws = new_workspace(la)
     # The workgroup holding ticket 0 (chunk 0, which publishes the first carry) stalls
     # after drawing it, for longer than its successors' spin limit.
