@@ -47,8 +47,7 @@ def _state(st, cuda):
 @pytest.mark.parametrize("decode_from_prior", [False, True])
 def test_forced_split_matches_oracle(cuda, chunks, shape, nc, with_state, decode_from_prior):
     B, L, M, S = shape
-    if L % nc:
-        pytest.skip("chunks must divide L")
+    assert L % nc == 0, "chunks must divide L"
     print(f"[time split] shape={shape} nc={nc} state={with_state} prior={decode_from_prior}", flush=True)
     chunks(nc)
     ins = make_inputs(B, L, M, S, seed=21)
@@ -155,9 +154,13 @@ def train_chunks(monkeypatch):
     return force
 
 
-@pytest.mark.parametrize("shape", [(2, 256, 9, 16), (1, 128, 3, 128), (3, 320, 70, 4), (1, 256, 2, 256),
-                                   (2, 192, 5, 32)])
-@pytest.mark.parametrize("nc", [2, 4, 8])
+# (shape, chunk count) pairs whose chunks hold whole 16-step checkpoint blocks.
+_TRAIN_SPLITS = [(shape, nc)
+                 for shape in [(2, 256, 9, 16), (1, 128, 3, 128), (3, 320, 70, 4), (1, 256, 2, 256), (2, 192, 5, 32)]
+                 for nc in (2, 4, 8) if shape[1] % (16 * nc) == 0]
+
+
+@pytest.mark.parametrize("shape,nc", _TRAIN_SPLITS)
 @pytest.mark.parametrize("with_state", [False, True])
 @pytest.mark.parametrize("decode_from_prior", [False, True])
 @pytest.mark.parametrize("with_var", [True, False])
@@ -166,8 +169,6 @@ def test_forced_training_split_matches_float64_autograd(cuda, train_chunks, shap
     from oracle import torch_ref
 
     B, L, M, S = shape
-    if L % (16 * nc):
-        pytest.skip("chunks must hold whole 16-step checkpoint blocks")
     print(f"[training split] shape={shape} nc={nc} state={with_state} prior={decode_from_prior} "
           f"var={with_var}", flush=True)
     train_chunks(nc)
