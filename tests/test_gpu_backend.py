@@ -483,6 +483,60 @@ def test_fused_at_c4_size(cuda):
     check_scan("dq", fused[5], xs[3].grad.numpy())
 
 
+def test_fused_past_2_31_elements(cuda):
+    """The fused kernels' element offsets are 64-bit: (B, L, M, S) = (1, 2048,
+    2^20 + 1, 16) has 2^31 + 2048 elements per [B, L, M] tensor (8.6 GB in fp32),
+    and the last channel -- a ragged channel group of one -- lies past 2^31 from
+    step 2047 on. Inputs are drawn on the GPU; dy, dy_var are zero outside five
+    channels (first, second, middle, the last full group's last, and the ragged
+    last), so dk and dq come from those alone. y, y_var, dv, dLv, da, dp on those
+    channels and the whole of dk, dq against float64 autograd through the
+    reference's torch path; dv and dLv are zero on every other channel."""
+    import torch.nn.functional as F
+
+    B, L, S = 1, 2048, 16
+    M = 2 ** 20 + 1
+    assert B * L * M > 2 ** 31 and (L - 1) * M + (M - 1) >= 2 ** 31
+    gen = torch.Generator(device=cuda).manual_seed(41)
+    print("[2^31 fused] drawing inputs", flush=True)
+    v = torch.randn(B, L, M, device=cuda, generator=gen)
+    lv = torch.rand(B, L, M, device=cuda, generator=gen) + 0.5
+    k = torch.randn(B, L, S, device=cuda, generator=gen) * 0.3
+    q = torch.randn(B, L, S, device=cuda, generator=gen) * 0.3
+    a = torch.rand(M, S, device=cuda, generator=gen) * 0.5 + 0.45
+    p = torch.rand(M, S, device=cuda, generator=gen) * 0.05 + 0.01
+    chans = torch.tensor([0, 1, 2 ** 19 + 7, 2 ** 20 - 1, 2 ** 20], device=cuda)
+    dy = torch.zeros(B, L, M, device=cuda)
+    dyv = torch.zeros(B, L, M, device=cuda)
+    dy[..., chans] = torch.randn(B, L, len(chans), device=cuda, generator=gen)
+    dyv[..., chans] = torch.randn(B, L, len(chans), device=cuda, generator=gen)
+    xs = [t.requires_grad_(True) for t in (v, lv, k, q, a, p)]
+    print("[2^31 fused] forward + backward", flush=True)
+    y, y_var, _ = kla_scan(*xs, backend="hip_fused")
+    torch.autograd.backward((y, y_var), (dy, dyv))
+    torch.cuda.synchronize()
+    got = {"y": y.detach()[..., chans].cpu(), "y_var": y_var.detach()[..., chans].cpu(),
+           "dv": v.grad[..., chans].cpu(), "dlambda_v": lv.grad[..., chans].cpu(),
+           "da": a.grad[chans].cpu(), "dp": p.grad[chans].cpu(), "dk": k.grad.cpu(), "dq": q.grad.cpu()}
+    for name, g_ in (("dv", v.grad), ("dlambda_v", lv.grad)):
+        nz = (g_ != 0).sum(dim=(0, 1))
+        nz[chans] = 0
+        assert int(nz.sum()) == 0, f"{name} nonzero outside the checked channels"
+    sub = [t.detach()[..., chans].cpu() for t in (v, lv)] + [k.detach().cpu(), q.detach().cpu()]
+    sub += [a.detach()[chans].cpu(), p.detach()[chans].cpu()]
+    dys, dyvs = dy[..., chans].cpu(), dyv[..., chans].cpu()
+    del xs, v, lv, k, q, a, p, y, y_var, dy, dyv
+    torch.cuda.empty_cache()
+    print("[2^31 fused] float64 reference", flush=True)
+    ref = [t.double().requires_grad_(True) for t in sub]
+    yr, yvr, _, _ = torch_ref.kla_scan_torch(*ref)
+    ((dys.double() * yr).sum() + (dyvs.double() * yvr).sum()).backward()
+    check_scan("y", got["y"], yr.detach().numpy())
+    check_scan("y_var", got["y_var"], yvr.detach().numpy())
+    for name, i in (("dv", 0), ("dlambda_v", 1), ("dk", 2), ("dq", 3), ("da", 4), ("dp", 5)):
+        check_scan(name, got[name], ref[i].grad.numpy())
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_affine_scan_at_c3_size(cuda, dtype):
     """C3 (B=8, T=8192, L=2048), fp32 and bf16 I/O: every element of h, dg and du
