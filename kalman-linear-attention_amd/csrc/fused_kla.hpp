@@ -734,9 +734,9 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
   __shared__ float s_red[RB][2][TB][NW / WPC][SP];
   // Blocks wholly inside the sequence run as one straight block of code (no
   // per-step bound) where that code still fits two waves per SIMD without
-  // spills; elsewhere (4, 8 or 256 lanes per channel, the prior's read-out, the
-  // variance's adjoint) every block keeps the per-step bound.
-  constexpr bool kFullBlocks = SP >= 16 && SP <= 128 && !PRIOR && !VAR;
+  // spills; elsewhere (4, 8, 128 or 256 lanes per channel, the prior's
+  // read-out, the variance's adjoint) every block keeps the per-step bound.
+  constexpr bool kFullBlocks = SP >= 16 && SP <= 64 && !PRIOR && !VAR;
 
   const FusedLane ln = fused_lane<SP>(g);
   const int64_t M = g.M, S = g.S, L = g.steps;
@@ -895,10 +895,9 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
       eh[TB] = eta;
     };
     // dv, dLv contributions of the block's steps, summed over s after the walk
-    // (step_sums_to_lds) up to 64 lanes per channel; wider channels sum every
-    // step as it is walked (the 16 more registers would halve their occupancy).
-    constexpr bool kTr = SP <= kWave;
-    float dv_w[kTr ? TB : 1], dl_w[kTr ? TB : 1];
+    // (step_sums_to_lds: within the wave; from 128 lanes per channel each wave
+    // writes its partial slot, which the flush adds in wave order).
+    float dv_w[TB], dl_w[TB];
     // dk, dq contributions, summed over the wave's four channel rows after the
     // walk (cross_row_transpose_sum) when SP = 16.
     constexpr bool kRows = SP == 16;
@@ -925,7 +924,7 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
           q4 = lds4(s_q[kb][ln.s], j - 3);
         }
         float dk_c = 0.0f, dq_c = 0.0f;
-        if constexpr (kTr && !FULL) {
+        if constexpr (!FULL) {
           dv_w[j] = 0.0f;
           dl_w[j] = 0.0f;
         }
@@ -1002,17 +1001,8 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
           const float gk = gl_t * kk;
           const float qk = gk * kk;
           dk_c = fmaf(gk, s2, ge_t * sv);
-          if constexpr (kTr) {
-            dv_w[j] = pk;
-            dl_w[j] = qk;
-          } else {
-            const float dv_s = group_sum<SG>(pk);
-            const float dl_s = group_sum<SG>(qk);
-            if (ln.s % SG == 0) {
-              s_dv[cur][ln.s / SG][c][j] = dv_s;
-              s_dl[cur][ln.s / SG][c][j] = dl_s;
-            }
-          }
+          dv_w[j] = pk;
+          dl_w[j] = qk;
         }
         // Sum over this wave's channels (now, or after the walk), over the waves
         // at the flush.
@@ -1053,10 +1043,8 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
         s_red[RB == 1 ? 0 : cur][1][j][wave][ln.s] = dq_w[i];
       }
     }
-    if constexpr (kTr) {
-      step_sums_to_lds<SP>(dv_w, lane, ln.s, s_dv[cur][ln.s / SG][c], 0);
-      step_sums_to_lds<SP>(dl_w, lane, ln.s, s_dl[cur][ln.s / SG][c], 0);
-    }
+    step_sums_to_lds<SP>(dv_w, lane, ln.s, s_dv[cur][ln.s / SG][c], 0);
+    step_sums_to_lds<SP>(dl_w, lane, ln.s, s_dl[cur][ln.s / SG][c], 0);
     acc_a += blk_a;
     acc_a2 += fmaf(-fmaf(pp, blk_x, blk_y), inv_a2 * inv_a2, blk_a2);
     acc_p += fmaf(blk_x, inv_a2, blk_p);
