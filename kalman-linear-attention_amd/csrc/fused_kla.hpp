@@ -530,10 +530,13 @@ __device__ __forceinline__ void to_precision(TileRegs<TB, W> &r, const SensorIn 
 
 // VAR: y_var is produced (prm.yvar non-NULL); without it the variance read-out
 // is skipped altogether.
-// 8 to 32 lanes per channel: held to three waves per SIMD (their registers fit
-// 168 with at most a couple of spilled words).
+// 8 to 32 lanes per channel, and 128 with bf16 sensors and no y_var (the
+// training layer's case): held to three waves per SIMD (their registers fit 168
+// with at most a few spilled words; measured at (4, 2048, 1024, 128) 1.08 ->
+// 0.95 ms, while the fp32 y_var variant at 128 lost 2-3% to its spills).
 template <int SP, bool PRIOR, bool BF16, bool VAR>
-__global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(SP >= 8 && SP <= 32 ? 3 : 1)))
+__global__ void __launch_bounds__(kFusedThreads)
+    __attribute__((amdgpu_waves_per_eu((SP >= 8 && SP <= 32) || (SP == 128 && BF16 && !VAR && !PRIOR) ? 3 : 1)))
     fused_kla_fwd_kernel(FusedFwdParams prm, FusedGeom g) {
   constexpr int CH = kFusedThreads / SP;
   constexpr int WPC = waves_per_channel<SP>();
