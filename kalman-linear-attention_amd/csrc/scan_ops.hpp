@@ -1,5 +1,5 @@
-// scan_ops.hpp -- the four scan policies run by the scan kernels
-// (lookback_scan_kernel, stripe_scan_kernel):
+// scan_ops.hpp -- the four scan policies run by the look-back scan kernel
+// (lookback_scan_kernel):
 //
 //   MobiusFwd   lam_t = (A lam_{t-1} + B) / max(C lam_{t-1} + D, EPS)
 //   MobiusBwd   exact scalar adjoint of MobiusFwd (reverse in time)
