@@ -231,6 +231,12 @@ def test_deterministic_bitwise(cuda):
     g, u, dh = (t.to(cuda) for t in affine_inputs(4, 2048, 512, seed=12))
     hs = [affine_scan(g, u) for _ in range(3)]
     assert torch.equal(hs[0], hs[1]) and torch.equal(hs[0], hs[2])
+    # A fresh (zero-filled) workspace after reset_workspaces gives the same bits.
+    from kla.ops.hip import _lib
+
+    _lib.reset_workspaces()
+    assert torch.equal(affine_scan(g, u), hs[0])
+    assert torch.equal(mobius_scan(A, Bm, C, None, lam0), runs[0][0])
 
 
 def test_headline_shape_whole_tensors(cuda):
