@@ -109,10 +109,12 @@ __device__ __forceinline__ f32x4_t load4(const float *p, int64_t lim) {
 // PIPE: one pass of IT steps covers each wave's k range. The lane's slice of x
 // then stays in registers for every column tile the workgroup takes, and the
 // next tile's weights are loaded while the current tile's products run.
-template <int EPI, bool NORM, bool VEC, bool PIPE>
+// ITS (nonzero): IT steps a pass instead of rows_lin_steps, for short k: fewer
+// registers, so that two workgroups share a CU (the LM head's many tiles).
+template <int EPI, bool NORM, bool VEC, bool PIPE, int ITS = 0>
 __global__ void __launch_bounds__(kRowsLinThreads) rows_linear_kernel(RowsLinearParams p) {
   constexpr int NT = EPI == kEpiSwiglu ? 2 : 1;   // weight tiles per output tile
-  constexpr int IT = rows_lin_steps(EPI, NORM);    // 16-wide k steps with all their loads in flight
+  constexpr int IT = ITS ? ITS : rows_lin_steps(EPI, NORM);   // 16-wide k steps with all their loads in flight
   __shared__ f32x4_t s_part[2][NT][kRowsLinWaves][kWave];
   __shared__ float s_ss[kRowsLinWaves][kRowsLinTile];
 
