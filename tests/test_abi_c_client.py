@@ -28,3 +28,22 @@ def test_c_client_uses_the_abi(tmp_path):
     out = subprocess.run([str(exe), str(_lib.ABI_VERSION)], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr + out.stdout
     assert "abi client ok" in out.stdout
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="no C compiler")
+def test_c_client_runs_the_scans_on_the_gpu(tmp_path):
+    """tests/abi_gpu_client.c: the Moebius and affine forward scans from plain C
+    (hipMalloc / hipMemcpy / a hipStream_t and the C ABI), against a float64
+    per-step loop at rtol 1e-5 / atol 1e-6, no look-back wait given up."""
+    lib = _lib.LIB_PATH
+    exe = tmp_path / "abi_gpu_client"
+    cmd = ["gcc", "-std=c11", "-O2", "-Wall", "-Werror", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(REPO, "include"),
+           "-I", "/opt/rocm/include", os.path.join(HERE, "abi_gpu_client.c"), "-o", str(exe), lib,
+           "-L/opt/rocm/lib", "-lamdhip64", "-lm", f"-Wl,-rpath,{os.path.dirname(lib)}", "-Wl,-rpath,/opt/rocm/lib"]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    print("[c client] running the scans from C", flush=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    print(out.stdout, flush=True)
+    assert out.returncode == 0, out.stderr + out.stdout
+    assert "gpu abi client ok" in out.stdout
