@@ -79,11 +79,15 @@ def alg_bytes_per_elem(kernel: str, affine_dtype: torch.dtype) -> int:
 
 
 # Bytes per element the kernels themselves must move: the same, except that the
-# Moebius backward reads the saved lam once per 16 steps and recomputes the rest
-# from A, B, C (so 28 + 4/16 instead of 32).
+# Moebius backward reads the saved lam once per thread's run of steps (24, the
+# backward tile's steps per wave) and recomputes the rest from A, B, C (so
+# 28 + 4/24 instead of 32).
+MOBIUS_BWD_STEPS = 24
+
+
 def kernel_bytes_per_elem(kernel: str, affine_dtype: torch.dtype) -> float:
     if kernel == "mobius_bwd":
-        return 28 + 4 / 16
+        return 28 + 4 / MOBIUS_BWD_STEPS
     return float(alg_bytes_per_elem(kernel, affine_dtype))
 
 

@@ -98,9 +98,9 @@ def test_mobius_bwd_recomputes_lam_bitwise(cuda, shape, with_D):
     """The backward reads the saved lam only where a thread's steps begin and
     recomputes the rest with the forward's own step, so the recomputed values
     are the stored ones bit for bit: poisoning every other row of lam (with NaN)
-    leaves every gradient bitwise unchanged. Threads hold 16 consecutive steps
-    in reverse time (a multiple of 16 also passes), so the rows read are
-    t = T-1-16m, m >= 1."""
+    leaves every gradient bitwise unchanged. Threads hold MOBIUS_BWD_STEPS (24)
+    consecutive steps in reverse time, so the rows read are t = T-1-24m, m >= 1."""
+    from bench import MOBIUS_BWD_STEPS
     from kla.ops.hip import scans as hs
 
     B, T, N = shape
@@ -109,7 +109,7 @@ def test_mobius_bwd_recomputes_lam_bitwise(cuda, shape, with_D):
     lam = hs._mobius_scan_op(A, Bm, C, D, lam0)
     ref_grads = hs._mobius_scan_bwd_op(dlam, A, Bm, C, D, lam0, lam)
     t = torch.arange(T, device=cuda)
-    keep = ((T - 1 - t) % 16 == 0) & (t != T - 1)
+    keep = ((T - 1 - t) % MOBIUS_BWD_STEPS == 0) & (t != T - 1)
     poisoned = torch.where(keep[None, :, None], lam, torch.full_like(lam, float("nan")))
     got = hs._mobius_scan_bwd_op(dlam, A, Bm, C, D, lam0, poisoned)
     names = ("dA", "dB", "dC", "dD", "dlam0")
