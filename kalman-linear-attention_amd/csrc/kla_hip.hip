@@ -219,10 +219,12 @@ int hip_status(const char *fn, hipError_t e) {
 // tile together moves at least this many HBM bytes, i.e. several microseconds
 // of streaming per hop of the carry chain (about 0.5 us). Measured per kernel
 // (us, aggregates -> carries only): (8, 4096, 2048) Moebius fwd 197 -> 190, bwd
-// 366 -> 361, affine fwd 140 -> 137, bwd 215 -> 213; (1, 65536, 64) Moebius
-// fwd 152 -> 577 and (4, 4096, 256) 33 -> 56, where the chain is the critical
-// path (there one chunk row is under 2 MiB).
-constexpr int64_t kCarryOnlyRowBytes = 16ll << 20;
+// 366 -> 361, affine fwd 140 -> 137, bwd 215 -> 213; at 12.6 MB per chunk row
+// ((4, 4096, 2048), (8, 4096, 1024), (16, 4096, 512)) Moebius fwd 100-104 ->
+// 97-99; at 6.3 MB ((2, 4096, 2048), (2, 8192, 2048)) 57-58 -> 62 and 105 -> 114,
+// and (1, 65536, 64) Moebius fwd 152 -> 577, (4, 4096, 256) 33 -> 56, where the
+// chain is the critical path.
+constexpr int64_t kCarryOnlyRowBytes = 8ll << 20;
 
 template <class P, class T>
 int launch(const char *fn, const typename P::Params &prm, Shape s, void *ws, hipStream_t stream) {

@@ -25,10 +25,10 @@
 // Carry-only launches (Geom::carry_only) publish no aggregates: a chunk waits
 // for its predecessor's carry alone, so the carries travel the chain one chunk
 // at a time (about half a microsecond a hop). That pays where one chunk of every
-// tile together is many microseconds of HBM traffic, so the chain hides under
-// the streaming (the headline shapes: 2-4% faster, 1 record word per lane and
-// chunk instead of K + 1); with few tiles along a long sequence the hop latency
-// is the critical path and the aggregates let a chunk skip ahead instead.
+// tile together is a few microseconds of HBM traffic or more, so the chain hides
+// under the streaming (the headline shapes: 2-4% faster, 1 record word per lane
+// and chunk instead of K + 1); with few tiles along a long sequence the hop
+// latency is the critical path and the aggregates let a chunk skip ahead instead.
 //
 // Records. Each published float travels in one 64-bit word, (tag << 32) | bits,
 // written and read with relaxed agent-scope atomics: a word is valid iff its tag
