@@ -373,10 +373,20 @@ __device__ __forceinline__ float mobius_apply(const Agg<4> &m, float x) {
 
 // One step of the recurrence, lam_t = (A lam_{t-1} + B) / den_t with
 // den_t = max(C lam_{t-1} + D, EPS), as the forward walk computes it. The
-// backward recomputes lam_t with these same two functions (explicit fmaf, one
-// IEEE division), so its values equal the forward's stored lam bit for bit.
+// quotient is the numerator times the hardware reciprocal (v_rcp_f32, 1 ulp):
+// ~2 ulp per step, which the contractive recurrence does not amplify, for a
+// tenth of the IEEE division's instructions (the backward forms three quotients
+// per step from one reciprocal). The reciprocal stays a normal float for den up
+// to 2^126, within a factor 4 of float overflow. The backward recomputes lam_t
+// with these same functions (explicit fmaf, the same reciprocal), so its values
+// equal the forward's stored lam bit for bit.
 __device__ __forceinline__ float mobius_den(float c, float d, float x) { return fmaxf(fmaf(c, x, d), kEps); }
-__device__ __forceinline__ float mobius_next(float a, float b, float x, float den) { return fmaf(a, x, b) / den; }
+__device__ __forceinline__ float mobius_next_inv(float a, float b, float x, float inv_den) {
+  return fmaf(a, x, b) * inv_den;
+}
+__device__ __forceinline__ float mobius_next(float a, float b, float x, float den) {
+  return mobius_next_inv(a, b, x, __builtin_amdgcn_rcpf(den));
+}
 
 // ================================================================ MobiusFwd
 // The backward (MobiusBwd) walks time in reverse right after this kernel and
@@ -505,8 +515,8 @@ struct MobiusFwd {
 // The saved lam is read once per thread: the value entering the thread's S
 // steps (lam at time T-1-s0-nvalid, or lam0 once the scan has passed time 0).
 // The thread recomputes lam over its steps from A, B, C, D, which it loads for
-// the adjoint anyway, with the forward walk's own step (mobius_den /
-// mobius_next), so the values are the forward's bit for bit. That takes the
+// the adjoint anyway, with the forward walk's own step (mobius_den, the
+// reciprocal, mobius_next_inv), so the values are the forward's bit for bit. That takes the
 // per-element traffic from 32 to 28 bytes plus 4 / S (dlam, A, B, C in;
 // dA, dB, dC out) for D = 1.
 
@@ -527,7 +537,7 @@ struct MobiusBwd {
   template <int S, int V>
   struct Regs {
     // lv[j] = lam at step j's time t, lv[j+1] = lam_{t-1}.
-    float dl[S][V], den[S][V], gain[S][V], lv[S + 1][V];
+    float dl[S][V], inv[S][V], gain[S][V], lv[S + 1][V];   // inv = 1 / den
   };
 
   template <int S, int V>
@@ -574,11 +584,11 @@ struct MobiusBwd {
 #pragma unroll
       for (int v = 0; v < V; ++v) {
         const float D = HAS_D ? raw.d[HAS_D ? j : 0][v] : 1.0f;
-        const float den = mobius_den(raw.c[j][v], D, r.lv[j + 1][v]);
-        r.lv[j][v] = mobius_next(raw.a[j][v], raw.b[j][v], r.lv[j + 1][v], den);
+        const float inv = __builtin_amdgcn_rcpf(mobius_den(raw.c[j][v], D, r.lv[j + 1][v]));
+        r.lv[j][v] = mobius_next_inv(raw.a[j][v], raw.b[j][v], r.lv[j + 1][v], inv);
         r.dl[j][v] = raw.dl[j][v];
-        r.den[j][v] = den;
-        r.gain[j][v] = (raw.a[j][v] * D - raw.b[j][v] * raw.c[j][v]) / (den * den);
+        r.inv[j][v] = inv;
+        r.gain[j][v] = (raw.a[j][v] * D - raw.b[j][v] * raw.c[j][v]) * (inv * inv);
       }
     }
   }
@@ -605,7 +615,7 @@ struct MobiusBwd {
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           const float nu = r.dl[j][v] + x[v];
-          const float qv = nu / r.den[j][v];
+          const float qv = nu * r.inv[j][v];
           const float lt = r.lv[j][v], lp = r.lv[j + 1][v];
           da[v] = qv * lp;
           db[v] = qv;
