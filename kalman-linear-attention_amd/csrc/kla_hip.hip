@@ -48,7 +48,9 @@ using MobiusFwdTile = Shape3<void, 8, 12, 1>;
 // Moebius backward: 12 waves of 24 steps. Re-swept once the look-back published
 // carries only (headline step, kernel in the step, three rounds on one box):
 // 12 x 24 336-337 us against 340-342 for 16 x 16, 16 x 20 341, 12 x 20 343,
-// 12 x 28 341, 12 x 32 343, 8 x 24 348, 8 x 16 356.
+// 12 x 28 341, 12 x 32 343, 8 x 24 348, 8 x 16 356. Again once the quotients
+// used the reciprocal (two rounds): 12 x 24 324-325 us, 8 x 32 322, 12 x 32 327,
+// 16 x 24 330, 12 x 20 330-331, 16 x 16 336-337, 8 x 24 343-344.
 using MobiusBwdTile = Shape3<void, 12, 24, 1>;
 using AffineFwdTile = Shape3<void, 16, 24, 1>;
 using AffineBwdTile = Shape3<void, 12, 32, 1>;
