@@ -156,8 +156,10 @@ __global__ void __launch_bounds__(kWave * W)
     s_tag = epoch + 1;
   }
   __syncthreads();
-  const uint32_t ticket = s_ticket;
-  const uint32_t tag = s_tag;
+  // Uniform by construction (one thread wrote them before the barrier); read
+  // back from LDS the compiler cannot know that, so say it.
+  const uint32_t ticket = __builtin_amdgcn_readfirstlane(s_ticket);
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(s_tag);
   if (ticket >= gridDim.x) {
     // Header not in the state a previous launch leaves it in (e.g. a workspace
     // that was not zero-filled): count it and touch nothing else.
@@ -174,7 +176,7 @@ __global__ void __launch_bounds__(kWave * W)
   q.ok = q.n0 + q.off < g.lanes;
   const int64_t s0 = chunk * (W * S) + static_cast<int64_t>(w) * S;
   const int64_t rem = g.steps - s0;
-  const int nvalid = rem <= 0 ? 0 : (rem >= S ? S : static_cast<int>(rem));
+  const int nvalid = __builtin_amdgcn_readfirstlane(rem <= 0 ? 0 : (rem >= S ? S : static_cast<int>(rem)));
 
   typename P::template Regs<S, V> r;
   {

@@ -107,16 +107,42 @@ struct Pos {
   bool ok;        // n0 + off < lanes (lanes is a multiple of V, so all V lanes are valid)
 };
 
-// Element index of (b, t, n0): the start of a tile's row at time t (wave-uniform).
-__device__ __forceinline__ int64_t row_index(const Geom &g, const Pos &q, int64_t t) {
+// Element index of (b, t, n0): the start of a tile's row at time t, for a time
+// that is wave-uniform at every call. row_index pins the result to scalar
+// registers (readfirstlane of both halves: exact for a uniform value, and free
+// once the value is already scalar), so that the per-step row offsets and the
+// access addresses below stay scalar arithmetic; without it the compiler keeps
+// the row in vector registers in some kernels (the Moebius forward).
+// row_index_vreg is the plain form, for the policy that measured faster with it.
+__device__ __forceinline__ int64_t row_index_vreg(const Geom &g, const Pos &q, int64_t t) {
   return (q.b * g.steps + t) * g.lanes + q.n0;
 }
+__device__ __forceinline__ int64_t row_index(const Geom &g, const Pos &q, int64_t t) {
+  const uint64_t r = static_cast<uint64_t>(row_index_vreg(g, q, t));
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(r));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(r >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 
-// The thread's first element in the row starting at `row`: uniform base plus a
-// 32-bit lane offset, which the compiler turns into SGPR-base addressing.
+// The thread's first element in the row starting at `row` (wave-uniform at
+// every call). at() makes the row start an explicit wave-uniform global
+// pointer, so each access takes the scalar-base plus 32-bit lane-offset form
+// (global_load v, v_off, s[base]) with no vector address arithmetic. Written as
+// plain (p + row) + off -- at_vreg -- the compiler hoists p + off into a vector
+// register pair per array and adds each row with a 64-bit vector add, one per
+// access (194 of the Moebius backward's 1070 VALU instructions).
+template <class T>
+__device__ __forceinline__ T *at_vreg(T *p, int64_t row, const Pos &q) {
+  return (p + row) + q.off;
+}
 template <class T>
 __device__ __forceinline__ T *at(T *p, int64_t row, const Pos &q) {
-  return (p + row) + q.off;
+  using Global = __attribute__((address_space(1))) T;
+  const uint64_t u = reinterpret_cast<uint64_t>(p + row);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  Global *base = (Global *)((static_cast<uint64_t>(hi) << 32) | lo);
+  return (T *)(base + q.off);
 }
 
 __device__ __forceinline__ int64_t state_index(const Geom &g, const Pos &q) {
@@ -516,9 +542,13 @@ struct MobiusFwd {
 // steps (lam at time T-1-s0-nvalid, or lam0 once the scan has passed time 0).
 // The thread recomputes lam over its steps from A, B, C, D, which it loads for
 // the adjoint anyway, with the forward walk's own step (mobius_den, the
-// reciprocal, mobius_next_inv), so the values are the forward's bit for bit. That takes the
-// per-element traffic from 32 to 28 bytes plus 4 / S (dlam, A, B, C in;
-// dA, dB, dC out) for D = 1.
+// reciprocal, mobius_next_inv), so the values are the forward's bit for bit.
+// That takes the per-element traffic from 32 to 28 bytes plus 4 / S (dlam, A,
+// B, C in; dA, dB, dC out) for D = 1.
+//
+// Its accesses keep the compiler's vector-register addressing (at_vreg,
+// row_index_vreg): with the scalar-base form it measured 325-326 us in the
+// headline step against 323-324.
 
 template <bool HAS_D>
 struct MobiusBwd {
@@ -543,7 +573,7 @@ struct MobiusBwd {
   template <int S, int V>
   __device__ __forceinline__ static void fetch(const Params &p, const Geom &g, Raw<S, V> &r, const Pos &q, int64_t s0,
                                int nvalid) {
-    const int64_t row = row_index(g, q, g.steps - 1 - s0);
+    const int64_t row = row_index_vreg(g, q, g.steps - 1 - s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       fill_v(r.dl[j], 0.0f);
@@ -555,7 +585,7 @@ struct MobiusBwd {
     fill_v(r.lin, 1.0f);
     if (!q.ok) return;
     if (s0 + nvalid < g.steps) {
-      load_v<V>(at(p.lam, row - static_cast<int64_t>(nvalid) * g.lanes, q), r.lin);
+      load_v<V>(at_vreg(p.lam, row - static_cast<int64_t>(nvalid) * g.lanes, q), r.lin);
     } else if (p.lam0) {
       load_state_v<V>(p.lam0 + state_index(g, q), r.lin);
     }
@@ -563,11 +593,11 @@ struct MobiusBwd {
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
         const int64_t rj = row - j * g.lanes;
-        load_v<V>(at(p.dlam, rj, q), r.dl[j]);
-        load_v<V>(at(p.A, rj, q), r.a[j]);
-        load_v<V>(at(p.B, rj, q), r.b[j]);
-        load_v<V>(at(p.C, rj, q), r.c[j]);
-        if (HAS_D) load_v<V>(at(p.D, rj, q), r.d[HAS_D ? j : 0]);
+        load_v<V>(at_vreg(p.dlam, rj, q), r.dl[j]);
+        load_v<V>(at_vreg(p.A, rj, q), r.a[j]);
+        load_v<V>(at_vreg(p.B, rj, q), r.b[j]);
+        load_v<V>(at_vreg(p.C, rj, q), r.c[j]);
+        if (HAS_D) load_v<V>(at_vreg(p.D, rj, q), r.d[HAS_D ? j : 0]);
       }
     }
   }
@@ -606,7 +636,7 @@ struct MobiusBwd {
   template <int S, int V>
   __device__ __forceinline__ static void walk(const Params &p, const Geom &g, const Regs<S, V> &r, const Pos &q,
                               int64_t s0, int nvalid, float (&x)[V]) {
-    const int64_t row = row_index(g, q, g.steps - 1 - s0);
+    const int64_t row = row_index_vreg(g, q, g.steps - 1 - s0);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
@@ -624,10 +654,10 @@ struct MobiusBwd {
           x[v] = r.gain[j][v] * nu;
         }
         if (q.ok) {
-          if (p.dA) store_v<V>(at(p.dA, rj, q), da);
-          if (p.dB) store_v<V>(at(p.dB, rj, q), db);
-          if (p.dC) store_v<V>(at(p.dC, rj, q), dc);
-          if (HAS_D && p.dD) store_v<V>(at(p.dD, rj, q), dd);
+          if (p.dA) store_v<V>(at_vreg(p.dA, rj, q), da);
+          if (p.dB) store_v<V>(at_vreg(p.dB, rj, q), db);
+          if (p.dC) store_v<V>(at_vreg(p.dC, rj, q), dc);
+          if (HAS_D && p.dD) store_v<V>(at_vreg(p.dD, rj, q), dd);
         }
       }
     }
