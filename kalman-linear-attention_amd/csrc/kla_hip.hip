@@ -137,7 +137,10 @@ bool output_fits_cache(Shape s, int64_t elem) { return s.batch * s.steps * s.lan
 // finds them there. Measured in the headline fwd + bwd step (8 x 4096 x 2048,
 // 768 MiB of A, B, C, the last third cached): Moebius bwd 350 -> 332 us and the
 // affine forward that follows 149 -> 139 us, for 197 -> 220 us in the Moebius
-// forward; caching the last sixth or all of the inputs gains less.
+// forward; caching the last sixth or all of the inputs gains less. Re-checked
+// with scalar-base addressing (three rounds): no tail / last sixth / last third
+// give Moebius bwd 346 / 336 / 324 us, fwd 196 / 197 / 199 us, step 0.913-0.917
+// / 0.905-0.907 / 0.896-0.897 ms.
 int64_t cached_tail_from(Shape s, int64_t tensors) {
   const int64_t per_step = s.batch * s.lanes * tensors * 4;
   if (per_step <= 0) return 0;
