@@ -59,12 +59,15 @@ def test_every_declared_function_is_exported_and_bound(lib):
     assert sorted(_lib._SIGNATURES) == declared, "ctypes binding and header disagree"
 
 
+GUIDE = os.path.join(REPO, "INTEGRATION.md")   # the maintainers' integration guide
+
+
 def test_every_declared_function_has_a_row_in_integration():
-    """INTEGRATION.md's ABI table names every entry point of kla_hip.h, with the
-    reference code it replaces (or why it has none)."""
-    text = open(os.path.join(REPO, "INTEGRATION.md")).read()
+    """The integration guide's ABI table names every entry point of kla_hip.h,
+    with the reference code it replaces (or why it has none)."""
+    text = open(GUIDE).read()
     missing = [name for name in header_functions() if f"`{name}`" not in text]
-    assert not missing, f"not in INTEGRATION.md: {missing}"
+    assert not missing, f"entry points without a row in the integration guide: {missing}"
 
 
 def test_workspace_bytes(lib):
