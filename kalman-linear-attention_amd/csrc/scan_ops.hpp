@@ -773,13 +773,27 @@ struct AffineBwd {
   __device__ __forceinline__ static void fetch(const Params &p, const Geom &gm, Raw<S, V> &r, const Pos &q, int64_t s0,
                                int nvalid) {
     const int64_t row = row_index(gm, q, gm.steps - 1 - s0);
+    fill_v(r.h_init, 0.0f);
+    if (nvalid == S && s0 + S < gm.steps && q.n0 + kWave * V <= gm.lanes) {
+      // Wave-uniform fast path: a full chunk away from time 0 with every lane
+      // of the wave valid needs none of the fill values below. At C3 with bf16
+      // I/O (8 x 8192 x 2048) the kernel went 285-288 -> 270-271 us (the fills
+      // were 308 of its 2405 VALU instructions); fp32 is unchanged.
+#pragma unroll
+      for (int j = 0; j < S; ++j) {
+        const int64_t rj = row - j * gm.lanes;
+        r.dh[j].load(at(p.dh, rj, q));
+        r.g[j].load(at(p.g, rj, q));
+        r.hp[j].load(at(p.h, rj - gm.lanes, q));
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       r.dh[j].fill(0.0f);
       r.g[j].fill(1.0f);
       r.hp[j].fill(0.0f);
     }
-    fill_v(r.h_init, 0.0f);
     if (!q.ok) return;
 #pragma unroll
     for (int j = 0; j < S; ++j) {
