@@ -53,6 +53,13 @@ using MobiusFwdTile = Shape3<void, 8, 12, 1>;
 // 16 x 24 330, 12 x 20 330-331, 16 x 16 336-337, 8 x 24 343-344.
 using MobiusBwdTile = Shape3<void, 12, 24, 1>;
 using AffineFwdTile = Shape3<void, 16, 24, 1>;
+// fp32 affine forward whose output is stored cached (it fits the memory-side
+// cache): 12 waves of 24 steps. In the headline step (three rounds, one box)
+// the kernel ran 133-134 us against 140-141 for 16 x 24 (and the affine
+// backward after it 231 against 226), the step 0.890-0.895 ms against
+// 0.897-0.900; 8 x 32 135 us. The streaming form (C3 fp32) keeps 16 x 24, where
+// 12 x 24 ran 277-280 us against 273.
+using AffineFwdCachedTile = Shape3<void, 12, 24, 1>;
 using AffineBwdTile = Shape3<void, 12, 32, 1>;
 using AffineFwdBf16Tile = Shape3<void, 8, 24, 2>;
 using AffineBwdBf16Tile = Shape3<void, 16, 16, 4>;
@@ -177,7 +184,7 @@ size_t workspace_bytes_kind(int kind, Shape s) {
       w = words_for<MobiusBwdTile>(s, 2);
       break;
     case KLA_SCAN_AFFINE_FWD:
-      w = std::max(words_for<AffineFwdTile>(s, 2),
+      w = std::max(std::max(words_for<AffineFwdTile>(s, 2), words_for<AffineFwdCachedTile>(s, 2)),
                    std::max(words_for<AffineFwdBf16Tile>(s, 2), words_for<AffineBf16Fallback>(s, 2)));
       break;
     case KLA_SCAN_AFFINE_BWD:
@@ -734,7 +741,8 @@ int kla_affine_scan_fwd(int dtype, const void *g, const void *u, const float *h0
       using P = AffineFwd<float, CACHED>;
       const typename P::Params prm{static_cast<const float *>(g), static_cast<const float *>(u), h0,
                                    static_cast<float *>(h)};
-      return launch<P, AffineFwdTile>(fn, prm, s, workspace, stream);
+      using Tile = std::conditional_t<CACHED, AffineFwdCachedTile, AffineFwdTile>;
+      return launch<P, Tile>(fn, prm, s, workspace, stream);
     }
     using P = AffineFwd<bf16_t, CACHED>;
     const typename P::Params prm{static_cast<const bf16_t *>(g), static_cast<const bf16_t *>(u), h0,
