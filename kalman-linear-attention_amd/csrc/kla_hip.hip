@@ -44,6 +44,9 @@ struct Shape3 {
   using Policy = P;
   static constexpr int W = W_, S = S_, V = V_;
 };
+// Moebius forward: 8 waves of 12 steps. Re-swept with scalar-base addressing
+// (headline step, two rounds): 8 x 12 199 us, 12 x 12 200, 16 x 8 209, 8 x 16
+// 211-212, 8 x 8 244.
 using MobiusFwdTile = Shape3<void, 8, 12, 1>;
 // Moebius backward: 12 waves of 24 steps. Re-swept once the look-back published
 // carries only (headline step, kernel in the step, three rounds on one box):
@@ -60,6 +63,10 @@ using AffineFwdTile = Shape3<void, 16, 24, 1>;
 // 0.897-0.900; 8 x 32 135 us. The streaming form (C3 fp32) keeps 16 x 24, where
 // 12 x 24 ran 277-280 us against 273.
 using AffineFwdCachedTile = Shape3<void, 12, 24, 1>;
+// fp32 affine backward: 12 waves of 32 steps. Re-swept after the cached-output
+// forward moved to 12 x 24 (headline step, two rounds): 12 x 32 232-233 us,
+// 16 x 24 230-231, 12 x 24 231, 12 x 40 232-233, 16 x 32 233, 8 x 32 248;
+// steps within noise of each other but for 8 x 32.
 using AffineBwdTile = Shape3<void, 12, 32, 1>;
 using AffineFwdBf16Tile = Shape3<void, 8, 24, 2>;
 using AffineBwdBf16Tile = Shape3<void, 16, 16, 4>;
