@@ -68,7 +68,11 @@ using AffineFwdCachedTile = Shape3<void, 12, 24, 1>;
 // 16 x 24 230-231, 12 x 24 231, 12 x 40 232-233, 16 x 32 233, 8 x 32 248;
 // steps within noise of each other but for 8 x 32.
 using AffineBwdTile = Shape3<void, 12, 32, 1>;
-using AffineFwdBf16Tile = Shape3<void, 8, 24, 2>;
+// bf16 affine forward: 12 waves of 24 steps, two lanes per thread. Re-swept
+// at C3 (8 x 8192 x 2048, three rounds, one box): 12 x 24 144 us, step
+// 0.426-0.435 ms, against 8 x 24 (the earlier choice) 146-147 us and
+// 0.435-0.438 ms; 8 x 32 148-149, 12 x 16 147, 16 x 16 169.
+using AffineFwdBf16Tile = Shape3<void, 12, 24, 2>;
 using AffineBwdBf16Tile = Shape3<void, 16, 16, 4>;
 using AffineBf16Fallback = Shape3<void, 8, 32, 1>;
 
