@@ -15,7 +15,15 @@ launch stream) and a CPU baseline: the reference's pure-PyTorch CPU algorithm
 Inputs are drawn on the CPU with torch.Generator(seed 0) in a fixed order and
 copied to the GPU, so the CPU and GPU sides see the same bytes.
 
-``--layer c1|c4|c5`` measures the layer-level BASELINE configs instead of the
+After the headline the same JSON line carries ``configs``: every other BASELINE
+config (``--configs``, default all), each with its GPU time and rate, a roofline
+for what bounds it and a bounded CPU baseline of the reference's algorithm on
+this host: c1 the KLALayer(512) forward, c3 the standalone affine scan at
+(8, 8192, 2048) fp32 and bf16 I/O, c4 the KLALayer(1024) training step (its fused
+scan kernels timed inside the step and priced on VALU issue), c5 the
+SequenceModel prefill (fp32 matrix flops) and one-token decode (weight bytes).
+
+``--layer c1|c4|c5`` measures one layer-level BASELINE config instead of the
 headline (its own JSON line; ``--backend`` picks the kla backend): c1 is a
 KLALayer(512, d_state=16) forward on x (2, 1024, 512), timed on the GPU and, on
 backend "torch", on this host's CPU; c4 is a
@@ -345,52 +353,254 @@ def bench_scan(args, device, stream) -> dict:
             "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
 
 
-def bench_layer(args, device, stream) -> dict:
-    """Layer-level BASELINE configs c1 / c4 / c5 on the chosen kla backend."""
-    from kla import KLAConfig, KLALayer, ModelConfig, SequenceModel
+# ------------------------------------------------------- BASELINE configs 1-5
+#
+# Each config entry carries the GPU time and rate, a roofline for what bounds it
+# and a CPU baseline: the same workload's reference algorithm (the kla package's
+# restated torch backend, reference kla_ops.py:188-290 and the layer and model
+# around it) on a bounded sample on this host.
+
+PEAK_FP32_MATRIX_TFLOPS = 157.3
+# VALU issue: 256 CUs x 4 SIMDs, one wave64 VALU instruction per SIMD every 4
+# cycles (16 lanes wide) at 2.4 GHz = 614.4 G wave-instructions/s. SQ_INSTS_VALU
+# counts wave-instructions; transcendentals issue at a quarter of this rate, so
+# the fraction of a kernel that uses them is a lower bound on its issue use.
+VALU_ISSUE_PEAK_G = 256 * 4 * 2.4 / 4
+
+
+def linear_flops_per_token(module) -> int:
+    """Multiply-add flops per token of every nn.Linear in ``module`` (2 in out)."""
+    import torch.nn as nn
+
+    return sum(2 * m.in_features * m.out_features for m in module.modules() if isinstance(m, nn.Linear))
+
+
+def _mfma_roofline(what: str, flops: float, ms: float) -> dict:
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"kernel": what, "bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_FP32_MATRIX_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tflops / PEAK_FP32_MATRIX_TFLOPS, 4), "traffic": None,
+            "flops": int(flops)}
+
+
+def _hbm_roofline(what: str, nbytes: float, ms: float, traffic=None, traffic_source=None) -> dict:
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"kernel": what, "bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": traffic, "traffic_source": traffic_source,
+            "alg_bytes": int(nbytes)}
+
+
+def _host() -> dict:
+    return {"cpu": cpu_model_name(), "affinity_cores": len(os.sched_getaffinity(0)),
+            "torch_threads": torch.get_num_threads()}
+
+
+def _cpu_once(fn, warm=None):
+    """One untimed call of ``warm`` (or ``fn``), then one timed call of ``fn``; seconds."""
+    (warm or fn)()
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
+
+
+def config_c1(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
+    """KLALayer(512, d_state=16) forward, x (2, 1024, 512) fp32."""
+    from kla import KLAConfig, KLALayer
 
     torch.manual_seed(0)
-    if args.layer == "c1":
-        # BASELINE config 1: the reference's CPU-runnable case, forward only.
-        layer = KLALayer(512, KLAConfig(d_state=16, backend=args.backend))
-        x_cpu = torch.randn(2, 1024, 512, generator=torch.Generator().manual_seed(0))
-        with torch.no_grad():
-            layer.config.backend = "torch"
-            cpu_s, cpu_reps = _median_time(lambda: layer(x_cpu), 10.0, max_reps=30)
-            y_cpu = layer(x_cpu)
-            layer.config.backend = args.backend
-            layer.to(device)
-            x = x_cpu.to(device)
-            ms = _timed(lambda: layer(x), args.steps, args.warmup, stream)
-            y = layer(x).float().cpu()
-        err = ((y - y_cpu).abs().max() / (y_cpu.abs().max() + 1e-12)).item()
-        return {"metric": "KLALayer(512, d_state=16) forward tokens/s, x (2,1024,512) fp32",
-                "value": 2 * 1024 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": round(ms, 4),
-                "backend": args.backend, "steps": args.steps, "warmup": args.warmup,
-                "max_rel_err_vs_cpu": err,
-                "cpu_baseline": {"value": 2 * 1024 / cpu_s, "unit": "tokens/s", "cores": torch.get_num_threads(),
-                                 "kind": "port",
-                                 "sample": (f"the same layer and input on backend='torch' (reference kla_scan_torch, "
-                                            f"doubling scan under no_grad), median of {cpu_reps} reps = "
-                                            f"{cpu_s * 1e3:.1f} ms")}}
-    if args.layer == "c4":
-        layer = KLALayer(1024, KLAConfig(d_state=16, backend=args.backend)).to(device)
-        x = torch.randn(4, 4096, 1024, generator=torch.Generator().manual_seed(0)).to(device)
+    layer = KLALayer(512, KLAConfig(d_state=16, backend=backend))
+    x_cpu = torch.randn(2, 1024, 512, generator=torch.Generator().manual_seed(0))
+    out = {}
+    with torch.no_grad():
+        layer.config.backend = "torch"
+        y_cpu = layer(x_cpu)
+        if cpu:
+            cpu_s, reps = _median_time(lambda: layer(x_cpu), 6.0, max_reps=5)
+            out["cpu_baseline"] = {
+                "value": 2 * 1024 / cpu_s, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+                "sample": (f"the whole config (same layer and input) on backend 'torch' on the host CPU (reference "
+                           f"kla_scan_torch, doubling scan under no_grad); median of {reps} reps = {cpu_s:.2f} s"),
+                "host": _host()}
+        layer.config.backend = backend
+        layer.to(device)
+        x = x_cpu.to(device)
+        ms = _timed(lambda: layer(x), steps, warmup, stream)
+        y = layer(x).float().cpu()
+    err = ((y - y_cpu).abs().max() / (y_cpu.abs().max() + 1e-12)).item()
+    flops = linear_flops_per_token(layer) * 2 * 1024
+    out.update({"metric": "KLALayer(512, d_state=16) forward tokens/s, x (2,1024,512) fp32",
+                "value": 2 * 1024 / (ms * 1e-3), "unit": "tokens/s", "ms": round(ms, 4), "backend": backend,
+                "dtype": "f32", "max_rel_err_vs_cpu": err,
+                "roofline": _mfma_roofline("whole forward: fp32 projections (hipBLASLt) + HIP scan and glue, "
+                                           "priced on the projections' flops", flops, ms)})
+    return out
 
-        def step():
-            with torch.autocast("cuda", dtype=torch.bfloat16):
+
+def config_c3(device, stream, steps, warmup, adt, cpu=True) -> dict:
+    """the standalone affine scan fwd + bwd at (8, 8192, 2048), fp32 or bf16 I/O."""
+    name = "affine_b8_t8192_l2048" + ("_bf16" if adt == torch.bfloat16 else "")
+    batch, steps_t, lanes, _, ops = WORKLOADS[name]
+    elems = batch * steps_t * lanes
+    step, kernels = build_step(batch, steps_t, lanes, adt, device, ops)
+    ms = _timed(step, steps, warmup, stream)
+    per = time_kernels_in_step(kernels, steps, stream)
+    kern = {}
+    for k, kms in per.items():
+        nbytes = alg_bytes_per_elem(k, adt) * elems
+        kern[k] = {"ms": round(kms, 4), "alg_bytes": nbytes, "GBps": round(nbytes / (kms * 1e-3) / 1e9, 1)}
+    dom = max(kern, key=lambda k: kern[k]["ms"])
+    traffic, src = None, None
+    tfile = os.path.join(REPO, "profiles", f"traffic_{name}.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            traffic, src = json.load(f).get(dom), os.path.relpath(tfile, REPO)
+    step_bytes = sum(v["alg_bytes"] for v in kern.values())
+    out = {"metric": f"Affine scan fwd+bwd tokens/s, B=8 T=8192 L=2048 {'bf16 I/O' if adt == torch.bfloat16 else 'fp32'}",
+           "value": batch * steps_t / (ms * 1e-3), "unit": "tokens/s", "ms": round(ms, 4),
+           "dtype": "f32" if adt == torch.float32 else "bf16 I/O, f32 arithmetic",
+           "achieved_GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1), "alg_bytes_per_step": step_bytes,
+           "roofline": _hbm_roofline(dom, kern[dom]["alg_bytes"], kern[dom]["ms"], traffic, src),
+           "kernels": kern, "workload": name}
+    del step, kernels
+    torch.cuda.empty_cache()
+    if cpu:
+        cb = cpu_baseline(lanes, "affine", budget_s=5.0, seq_budget_s=3.0)
+        cb["sample"] += " (the reference widens bf16 to fp32, so the CPU side is fp32)" if adt == torch.bfloat16 else ""
+        out["cpu_baseline"] = cb
+    return out
+
+
+def _fused_kernel_bytes(B, L, M, S, sensor_bytes, var=False):
+    """Bytes the fused scan kernels of a KLALayer training step must move: the
+    forward reads v and log sigma^2 (sensor dtype), k, q and writes y (and y_var)
+    and the (lam, eta) checkpoints every 16 steps; the backward reads dy (and
+    dy_var), v, log sigma^2, k, q, the checkpoints and writes dv, d log sigma^2
+    (sensor dtype) and the per-channel-group dk, dq partials ([B, L, M / (256 /
+    S), S] fp32, which the backward's fixed-order reductions then sum: the one
+    part of these bytes that the reference algorithm does not move)."""
+    seq, st = B * L * M, B * L * S
+    ck = 2 * B * -(-L // 16) * M * S * 4
+    groups = -(-M // (256 // S))
+    fwd = 2 * seq * sensor_bytes + 2 * st * 4 + seq * 4 * (2 if var else 1) + ck
+    bwd = seq * 4 * (2 if var else 1) + 2 * seq * sensor_bytes + 2 * st * 4 + ck + 2 * seq * sensor_bytes \
+        + 2 * B * L * groups * S * 4
+    return {"fused_fwd": fwd, "fused_bwd": bwd}
+
+
+def config_c4(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
+    """KLALayer(1024, d_state=16) training step, x (4, 4096, 1024),
+    bf16 autocast, loss = mean(out^2). The fused scan kernels are timed inside the
+    step with HIP events that the library records around each launch
+    (kla_set_kernel_events) and priced on their VALU issue (SQ_INSTS_VALU of a
+    committed rocprofv3 counter run) and on their compulsory HBM bytes."""
+    from kla import KLAConfig, KLALayer
+    from kla.ops.hip import _lib
+
+    torch.manual_seed(0)
+    layer = KLALayer(1024, KLAConfig(d_state=16, backend=backend))
+    out = {}
+    if cpu:
+        L = 128
+
+        def cpu_step(x):
+            with torch.autocast("cpu", dtype=torch.bfloat16):
                 y = layer(x)
             y.float().square().mean().backward()
             layer.zero_grad(set_to_none=True)
 
-        ms = _timed(step, args.steps, args.warmup, stream)
-        return {"metric": "KLALayer(1024, d_state=16) train step tokens/s, x (4,4096,1024), bf16 autocast",
-                "value": 4 * 4096 / (ms * 1e-3), "unit": "tokens/s", "ms_per_step": round(ms, 3),
-                "backend": args.backend, "steps": args.steps, "warmup": args.warmup,
-                "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
+        layer.config.backend = "torch"
+        xs = torch.randn(1, L, 1024, generator=torch.Generator().manual_seed(1))
+        cpu_s = _cpu_once(lambda: cpu_step(xs), warm=lambda: cpu_step(xs[:, :16]))
+        layer.config.backend = backend
+        out["cpu_baseline"] = {
+            "value": L / cpu_s, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"the same layer's training step on backend 'torch' on the host CPU under bf16 autocast, "
+                       f"x (1, {L}, 1024) (the reference's associative scan under grad; its cost grows faster than "
+                       f"linearly in L, so the full 4096-step rate is lower); one rep after a 16-step warm-up = "
+                       f"{cpu_s:.2f} s"),
+            "host": _host()}
+    layer.to(device)
+    x = torch.randn(4, 4096, 1024, generator=torch.Generator().manual_seed(0)).to(device)
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = layer(x)
+        y.float().square().mean().backward()
+        layer.zero_grad(set_to_none=True)
+
+    ms = _timed(step, steps, warmup, stream)
+    out.update({"metric": "KLALayer(1024, d_state=16) train step tokens/s, x (4,4096,1024), bf16 autocast",
+                "value": 4 * 4096 / (ms * 1e-3), "unit": "tokens/s", "ms": round(ms, 4), "backend": backend,
+                "dtype": "bf16 activations, f32 scan state",
+                "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)})
+    if not backend.startswith("hip"):
+        return out
+    with _lib.KernelTimer(_lib.KLA_KERNEL_FUSED_FWD, device) as tf, \
+            _lib.KernelTimer(_lib.KLA_KERNEL_FUSED_BWD, device) as tb:
+        for _ in range(steps):
+            tf.arm()
+            tb.arm()
+            step()
+    kms = {"fused_fwd": statistics.mean(tf.times_ms()), "fused_bwd": statistics.mean(tb.times_ms())}
+    kb = _fused_kernel_bytes(4, 4096, layer.d_inner, 16, sensor_bytes=2)
+    valu = {}
+    vfile = os.path.join(REPO, "profiles", "valu_fused_kla_c4_layer_train_step.json")
+    if os.path.exists(vfile):
+        with open(vfile) as f:
+            valu = json.load(f)
+    kern = {}
+    for k in ("fused_fwd", "fused_bwd"):
+        e = {"ms": round(kms[k], 4), "kernel_bytes": kb[k], "GBps": round(kb[k] / (kms[k] * 1e-3) / 1e9, 1)}
+        if k in valu:
+            rate = valu[k]["SQ_INSTS_VALU"] / (kms[k] * 1e-3) / 1e9
+            e.update({"valu_wave_instructions": valu[k]["SQ_INSTS_VALU"], "valu_G_per_s": round(rate, 1),
+                      "valu_frac": round(rate / VALU_ISSUE_PEAK_G, 4)})
+        kern[k] = e
+    bwd = kern["fused_bwd"]
+    out["kernels"] = kern
+    out["roofline"] = {"kernel": "fused_kla_bwd_kernel<16, false, true, false>", "bound": "valu",
+                       "achieved": bwd.get("valu_G_per_s"), "peak": VALU_ISSUE_PEAK_G,
+                       "unit": "G VALU wave-instructions/s", "frac": bwd.get("valu_frac"), "traffic": None,
+                       "valu_source": os.path.relpath(vfile, REPO) if valu else None,
+                       "hbm_GBps": bwd["GBps"], "hbm_frac": round(bwd["GBps"] / PEAK_HBM_GBPS, 4)}
+    return out
+
+
+def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "decode"), cpu=True) -> dict:
+    """SequenceModel(vocab 50304, d_model 512, 6 layers) stateful
+    prefill of (nb, 2048) random ids, then 256 greedy one-token decode steps."""
+    from kla import KLAConfig, ModelConfig, SequenceModel
+
+    torch.manual_seed(0)
     model = SequenceModel(ModelConfig(vocab_size=50304, d_model=512, n_layers=6),
-                          KLAConfig(backend=args.backend)).to(device).eval()
-    nb = args.c5_batch
+                          KLAConfig(backend=backend)).eval()
+    weight_bytes = sum(p.numel() * p.element_size() for n, p in model.named_parameters() if n != "embedding.weight")
+    flops_tok = linear_flops_per_token(model)
+    out = {}
+    cpu_pre = cpu_dec = None
+    if cpu:
+        for blk in model.blocks:
+            blk.mixer.config.backend = "torch"
+        Lp = 128
+        ids_c = torch.randint(0, 50304, (1, Lp), generator=torch.Generator().manual_seed(1))
+        with torch.no_grad():
+            pre_s = _cpu_once(lambda: model(ids_c, state=model.init_state(1)), warm=lambda: model(ids_c[:, :8]))
+            ids16 = torch.randint(0, 50304, (nb, 16), generator=torch.Generator().manual_seed(2))
+            lg, st = model(ids16, state=model.init_state(nb))
+            tok = lg[:, -1].argmax(-1, keepdim=True)
+            t0 = time.perf_counter()
+            for _ in range(4):
+                lg, st = model(tok, state=st)
+                tok = lg[:, -1].argmax(-1, keepdim=True)
+            dec_s = (time.perf_counter() - t0) / 4
+        for blk in model.blocks:
+            blk.mixer.config.backend = backend
+        cpu_pre = {"value": Lp / pre_s, "unit": "prefill tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+                   "sample": (f"the same model on backend 'torch' on the host CPU, stateful prefill of (1, {Lp}) ids; "
+                              f"one rep after a warm-up = {pre_s:.2f} s"), "host": _host()}
+        cpu_dec = {"value": dec_s * 1e3, "unit": "ms/token", "cores": torch.get_num_threads(), "kind": "port",
+                   "sample": (f"the same model on backend 'torch' on the host CPU: 4 one-token decode steps at batch "
+                              f"{nb} after a 16-token prefill; mean {dec_s * 1e3:.1f} ms per step"), "host": _host()}
+    model.to(device)
     ids = torch.randint(0, 50304, (nb, 2048), generator=torch.Generator().manual_seed(0)).to(device)
     state = {}
 
@@ -400,12 +610,16 @@ def bench_layer(args, device, stream) -> dict:
         logits, st = model(ids, state=st)
         state["s"], state["tok"] = st, model._sample(logits[:, -1], 0.0, None)   # greedy
 
-    pre_ms = _timed(prefill, max(1, args.steps // 4), 1, stream)
-    if args.c5_phase == "prefill":
-        return {"metric": f"SequenceModel(d=512, 6 layers) prefill tokens/s ({nb}x2048)",
-                "value": nb * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
-                "backend": args.backend,
-                "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)}
+    pre_ms = _timed(prefill, max(1, steps), 1, stream)
+    out["prefill"] = {"metric": f"SequenceModel(d=512, 6 layers) stateful prefill tokens/s ({nb}x2048)",
+                      "value": nb * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "ms": round(pre_ms, 3),
+                      "backend": backend, "dtype": "f32",
+                      "roofline": _mfma_roofline("whole prefill: fp32 projections and LM head (hipBLASLt) + HIP "
+                                                 "scan and glue, priced on the projections' flops",
+                                                 flops_tok * nb * 2048, pre_ms),
+                      "cpu_baseline": cpu_pre}
+    if "decode" not in phases:
+        return out
 
     @torch.no_grad()
     def decode256():
@@ -414,11 +628,12 @@ def bench_layer(args, device, stream) -> dict:
             logits, st = model(tok, state=st)
             tok = model._sample(logits[:, -1], 0.0, None)
 
-    dec_ms = _timed(decode256, 1, 1, stream)
-    out = {"metric": f"SequenceModel(d=512, 6 layers) prefill tokens/s ({nb}x2048) + decode ms/token (256 steps)",
-           "value": nb * 2048 / (pre_ms * 1e-3), "unit": "prefill tokens/s", "prefill_ms": round(pre_ms, 3),
-           "decode_ms_per_token": round(dec_ms / 256, 4), "backend": args.backend}
-    if args.backend.startswith("hip"):
+    eager_ms = _timed(decode256, 1, 1, stream) / 256
+    dec = {"metric": f"SequenceModel(d=512, 6 layers) one-token decode ms/token (batch {nb}, 256 greedy steps)",
+           "unit": "ms/token", "higher_is_better": False, "eager_ms": round(eager_ms, 4), "backend": backend,
+           "dtype": "f32", "weight_bytes_per_token": weight_bytes, "cpu_baseline": cpu_dec}
+    graph_ms = None
+    if backend.startswith("hip"):
         from kla.models.decode_graph import DecodeGraph
 
         graph = DecodeGraph(model, state["s"])
@@ -429,9 +644,54 @@ def bench_layer(args, device, stream) -> dict:
             for _ in range(256):
                 tok = model._sample(graph.step(tok)[:, -1], 0.0, None)
 
-        out["decode_graph_ms_per_token"] = round(_timed(decode256_graph, 1, 1, stream) / 256, 4)
+        graph_ms = _timed(decode256_graph, 1, 1, stream) / 256
+        dec["graph_ms"] = round(graph_ms, 4)
+    best = graph_ms if graph_ms is not None else eager_ms
+    dec["value"] = round(best, 4)
+    dec["ms"] = round(best, 4)
+    dec["roofline"] = _hbm_roofline("one decode step (every weight but the embedding table streamed once)",
+                                    weight_bytes, best)
+    out["decode"] = dec
     out["peak_mem_GiB"] = round(torch.cuda.max_memory_allocated(device) / 2**30, 2)
     return out
+
+
+CONFIG_NAMES = ("c1", "c3_fp32", "c3_bf16", "c4", "c5")
+
+
+def run_configs(names, device, stream, steps, warmup, cpu=True) -> dict:
+    """The BASELINE configs named in ``names``, each in its own entry."""
+    out = {}
+    for name in names:
+        print(f"[bench] config {name}", file=sys.stderr, flush=True)
+        t0 = time.perf_counter()
+        if name == "c1":
+            out["c1_layer_forward"] = config_c1(device, stream, steps, warmup, cpu=cpu)
+        elif name == "c3_fp32":
+            out["c3_affine_fp32"] = config_c3(device, stream, steps, warmup, torch.float32, cpu=cpu)
+        elif name == "c3_bf16":
+            out["c3_affine_bf16"] = config_c3(device, stream, steps, warmup, torch.bfloat16, cpu=cpu)
+        elif name == "c4":
+            out["c4_layer_train_step"] = config_c4(device, stream, steps, max(3, warmup // 4), cpu=cpu)
+        elif name == "c5":
+            c5 = config_c5(device, stream, max(1, steps // 4), cpu=cpu)
+            out["c5_prefill"] = c5["prefill"]
+            out["c5_decode"] = c5["decode"]
+        gc.collect()
+        torch.cuda.empty_cache()
+        print(f"[bench] config {name} done in {time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    return out
+
+
+def bench_layer(args, device, stream) -> dict:
+    """One layer-level BASELINE config (c1 / c4 / c5) on the chosen kla backend, on its own line."""
+    cpu = not args.no_cpu_baseline
+    if args.layer == "c1":
+        return config_c1(device, stream, args.steps, args.warmup, args.backend, cpu=cpu)
+    if args.layer == "c4":
+        return config_c4(device, stream, args.steps, args.warmup, args.backend, cpu=cpu)
+    phases = ("prefill",) if args.c5_phase == "prefill" else ("prefill", "decode")
+    return config_c5(device, stream, max(1, args.steps // 4), args.backend, args.c5_batch, phases, cpu=cpu)
 
 
 def main(argv=None) -> int:
@@ -457,7 +717,19 @@ def main(argv=None) -> int:
     ap.add_argument("--c5-phase", default="all", choices=["all", "prefill"],
                     help="--layer c5: time the prefill and the decode (all) or the prefill only")
     ap.add_argument("--backend", default="hip", help="kla backend for --layer (hip, hip_composed, torch)")
+    ap.add_argument("--configs", default="all",
+                    help="BASELINE configs measured after the headline, in the same JSON line's 'configs': 'all', "
+                         "'none' or a comma list of " + ", ".join(CONFIG_NAMES))
     args = ap.parse_args(argv)
+    if args.configs == "all":
+        config_names = list(CONFIG_NAMES)
+    elif args.configs == "none":
+        config_names = []
+    else:
+        config_names = [c for c in args.configs.split(",") if c]
+        bad = [c for c in config_names if c not in CONFIG_NAMES]
+        if bad:
+            ap.error(f"unknown config(s) {bad}; choose from {', '.join(CONFIG_NAMES)}")
 
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build runs the scan on one GPU "
@@ -597,6 +869,12 @@ def main(argv=None) -> int:
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(lanes, ops)
+    if config_names and args.workload == DEFAULT_WORKLOAD:
+        del step, kernels
+        gc.collect()
+        torch.cuda.empty_cache()
+        result["configs"] = run_configs(config_names, device, stream, args.steps, args.warmup,
+                                        cpu=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
 

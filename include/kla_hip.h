@@ -70,8 +70,23 @@ const char *kla_hip_last_error(void);
 /* Bytes of workspace a scan of this kind and size needs (0 on bad arguments). */
 size_t kla_scan_workspace_bytes(int kind, int64_t batch, int64_t steps, int64_t lanes);
 
+/* Kernels kla_set_kernel_events can bracket. */
+#define KLA_KERNEL_FUSED_FWD 0 /* fused_kla_fwd_kernel (kla_fused_scan*_fwd)  */
+#define KLA_KERNEL_FUSED_BWD 1 /* fused_kla_bwd_kernel (kla_fused_scan*_bwd)  */
+
+/* Timing hook, no counterpart in the reference: for a benchmark that times one
+ * kernel inside a larger step (the fused backward launches its scan kernel and
+ * then the partial-sum reductions). Until called again with NULL events, every
+ * launch of `kernel` from the calling host thread records `start` on its stream
+ * right before that kernel and `stop` right after it; hipEventElapsedTime of
+ * the pair is then that kernel's duration. Events are the caller's; the hook
+ * holds no reference to them beyond the handles. */
+int kla_set_kernel_events(int kernel, hipEvent_t start, hipEvent_t stop);
+
 /* Number of look-back waits that gave up since the workspace was zero-filled
- * (0 in every correct run). Reads the workspace header: synchronises `stream`. */
+ * (0 in every correct run). Reads the workspace header: synchronises `stream`.
+ * workspace NULL: the current device's static scratch of
+ * kla_mobius_scan_fwd_noalloc (0 if no such call has run on the device). */
 int kla_workspace_failures(const void *workspace, hipStream_t stream, uint32_t *failures);
 
 /*
@@ -93,11 +108,14 @@ int kla_mobius_scan_fwd(const float *A, const float *B, const float *C, const fl
  * records live in a static 32 MiB device array (one per GPU, held until the
  * process ends), which fits the scan up to (8, 4096, 2048); a larger call
  * returns KLA_ERR_WORKSPACE and launches nothing. The first call on a device
- * looks the array up and zero-fills it on `stream` (so make that first call
- * outside a graph capture); the call itself allocates nothing. Every call on
- * one GPU shares that GPU's array: calls that overlap in time on one GPU race
- * (their results are undefined; the bounded look-back waits still end).
- * Results are bit-identical to kla_mobius_scan_fwd's.
+ * looks the array up, zero-fills it on `stream` and waits for the fill (so make
+ * that first call outside a graph capture); the call itself allocates nothing.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on
+ * one GPU race. Their results are undefined: the bounded look-back waits still
+ * end, but a workgroup whose ticket falls outside its own launch writes nothing,
+ * so parts of lam can be left unwritten rather than NaN. A look-back wait that
+ * gives up writes NaN and is counted: kla_workspace_failures(NULL, ...) reads the
+ * count. Results are bit-identical to kla_mobius_scan_fwd's.
  */
 int kla_mobius_scan_fwd_noalloc(const float *A, const float *B, const float *C, const float *D,
                                 const float *lam0, float *lam, int64_t batch, int64_t steps,
@@ -110,7 +128,7 @@ int kla_mobius_scan_fwd_noalloc(const float *A, const float *B, const float *C, 
  *   dA = nu*l_{t-1}/den, dB = nu/den, dC = -nu*l_t*l_{t-1}/den, dD = -nu*l_t/den
  *   dlam0 = nu_0*gain_0
  * lam: the forward's output. It is read only where a thread's block of steps
- * begins (one row in 16); the values in between are recomputed from A, B, C, D
+ * begins (one row in 24); the values in between are recomputed from A, B, C, D
  * with the forward's own step, which reproduces the forward's lam bit for bit,
  * so lam must be exactly what kla_mobius_scan_fwd wrote for these inputs.
  * D, dD, lam0, dlam0 may be NULL (dD is written only

@@ -1297,10 +1297,17 @@ __global__ void __launch_bounds__(kFusedThreads) fused_chunk_map_kernel(ChunkMap
 
 // The state entering each chunk, per (b, m, s) lane: from (lam0 or 1, eta0 or 0)
 // the chunk maps are applied in chunk order, lam' = (n0 lam + n1) / (d0 lam + d1)
-// and eta' = (w0 lam + w1 + w2 eta) / (d0 lam + d1) (denominator floored at EPS
-// like mobius_apply). maps [batch, chunks, n, 8]; lam0, eta0 [batch, n] or NULL;
-// lam_start, eta_start [batch, chunks, n]; lam_end, eta_end [batch, n] (the state
-// after the last chunk) or NULL.
+// and eta' = (w0 lam + w1 + w2 eta) / (d0 lam + d1). maps [batch, chunks, n, 8];
+// lam0, eta0 [batch, n] or NULL; lam_start, eta_start [batch, chunks, n]; lam_end,
+// eta_end [batch, n] (the state after the last chunk) or NULL.
+//
+// A step's denominator (p/a2) lam + 1 is at least 1, so the sequential filter never
+// floors it and the composed map is exact. A map rescaled to a trace in [0.5, 1)
+// can still carry a normal d1 far below EPS (lam0 = 0 under decay: d1 ~ a^(2 steps)
+// relative to n0), so only a zero or subnormal denominator is guarded (FLT_MIN);
+// an EPS floor here would replace such a d1 and lose the chunk's state.
+constexpr float kMapDenMin = __FLT_MIN__;
+
 __global__ void __launch_bounds__(256) chunk_starts_kernel(const float *__restrict__ maps,
                                                            const float *__restrict__ lam0,
                                                            const float *__restrict__ eta0,
@@ -1318,7 +1325,7 @@ __global__ void __launch_bounds__(256) chunk_starts_kernel(const float *__restri
     eta_start[row] = eta;
     const float4 *m = reinterpret_cast<const float4 *>(maps + row * 8);
     const float4 nd = m[0], w = m[1];
-    const float den = fmaxf(fmaf(nd.z, lam, nd.w), kEps);
+    const float den = fmaxf(fmaf(nd.z, lam, nd.w), kMapDenMin);
     const float nl = fmaf(nd.x, lam, nd.y) / den;
     eta = (fmaf(w.x, lam, w.y) + w.z * eta) / den;
     lam = nl;

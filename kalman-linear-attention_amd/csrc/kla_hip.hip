@@ -28,7 +28,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 15;
+constexpr int kAbiVersion = 16;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
@@ -442,6 +442,17 @@ int sensors_from(const char *fn, const kla_sensors *in, int64_t M, SensorIn *out
   return KLA_OK;
 }
 
+// Timing events of the fused kernels (kla_set_kernel_events), per host thread:
+// [KLA_KERNEL_FUSED_FWD / _BWD][start, stop]. When set, the fused forward or
+// backward records `start` on its stream right before its scan kernel and
+// `stop` right after it, so that the pair brackets that kernel alone.
+thread_local hipEvent_t t_kernel_events[2][2] = {};
+
+int record_kernel_event(const char *fn, int kernel, int which, hipStream_t stream) {
+  hipEvent_t ev = t_kernel_events[kernel][which];
+  return ev ? hip_status(fn, hipEventRecord(ev, stream)) : KLA_OK;
+}
+
 int fused_fwd(const char *fn, const SensorIn &sn, const float *k, const float *q, const float *a, const float *p,
               const float *lam0, const float *eta0, float *y, float *y_var, float *lam_fin, float *eta_fin,
               float *ck_lam, float *ck_eta, int decode_from_prior, int64_t batch, int64_t steps, int64_t M,
@@ -461,7 +472,8 @@ int fused_fwd(const char *fn, const SensorIn &sn, const float *k, const float *q
   const int64_t grid = batch * g.groups;
   if (grid >= (1ll << 31)) return fail(KLA_ERR_INVALID_ARG, "%s: grid too large", fn);
   const FusedFwdParams prm{sn, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, ck_lam, ck_eta};
-  return with_sp(S, [&](auto sp) {
+  if ((rc = record_kernel_event(fn, KLA_KERNEL_FUSED_FWD, 0, stream)) != KLA_OK) return rc;
+  rc = with_sp(S, [&](auto sp) {
     constexpr int SP = decltype(sp)::value;
     auto run = [&](auto prior, auto bf16, auto var) {
       hipLaunchKernelGGL(
@@ -471,6 +483,8 @@ int fused_fwd(const char *fn, const SensorIn &sn, const float *k, const float *q
     with_flags(run, decode_from_prior != 0, sn.bf16 != 0, y_var != nullptr);
     return hip_status(fn, hipGetLastError());
   });
+  if (rc != KLA_OK) return rc;
+  return record_kernel_event(fn, KLA_KERNEL_FUSED_FWD, 1, stream);
 }
 
 int fused_bwd(const char *fn, const float *dy, const float *dy_var, const float *dlam_fin, const float *deta_fin,
@@ -508,6 +522,7 @@ int fused_bwd(const char *fn, const float *dy, const float *dy_var, const float 
   if (batch > 0) {
     const FusedBwdParams prm{dy, dy_var, dlam_fin, deta_fin, sn, k, q, a, p, ck_lam, ck_eta,
                              dv, dlambda_v, dlam0, deta0, part_k, part_q, part_a, part_p};
+    if ((rc = record_kernel_event(fn, KLA_KERNEL_FUSED_BWD, 0, stream)) != KLA_OK) return rc;
     rc = with_sp(S, [&](auto sp) {
       constexpr int SP = decltype(sp)::value;
       auto run = [&](auto prior, auto bf16, auto var) {
@@ -519,6 +534,7 @@ int fused_bwd(const char *fn, const float *dy, const float *dy_var, const float 
       return hip_status(fn, hipGetLastError());
     });
     if (rc != KLA_OK) return rc;
+    if ((rc = record_kernel_event(fn, KLA_KERNEL_FUSED_BWD, 1, stream)) != KLA_OK) return rc;
   }
   // Fixed-order sums of the partials: dk, dq over channel groups; da, dp over batch.
   auto reduce = [&](const float *in, float *out, int64_t outer, int64_t G, int64_t inner) {
@@ -617,8 +633,10 @@ std::mutex g_scratch_mu;
 void *g_scratch_addr[kMaxDevices] = {};
 
 // The current device's scratch address. The first call on a device looks the
-// symbol up and zero-fills the array on `stream` (the look-back records' start
-// state; the kernels keep it consistent from launch to launch afterwards).
+// symbol up, zero-fills the array on `stream` (the look-back records' start
+// state; the kernels keep it consistent from launch to launch afterwards) and
+// waits for the fill, so that no later call, on any stream, can see the array
+// before it is filled. Later calls only read the address.
 int scratch_address(const char *fn, hipStream_t stream, void **out) {
   int dev = -1;
   int rc = hip_status(fn, hipGetDevice(&dev));
@@ -635,10 +653,25 @@ int scratch_address(const char *fn, hipStream_t stream, void **out) {
                        static_cast<float *>(p), count);
     rc = hip_status(fn, hipGetLastError());
     if (rc != KLA_OK) return rc;
+    rc = hip_status(fn, hipStreamSynchronize(stream));
+    if (rc != KLA_OK) return rc;
     g_scratch_addr[dev] = p;
   }
   *out = g_scratch_addr[dev];
   return KLA_OK;
+}
+
+// The current device's scratch address if a no-alloc call has set it up, else NULL.
+void *scratch_address_if_set(const char *fn, int *rc) {
+  int dev = -1;
+  *rc = hip_status(fn, hipGetDevice(&dev));
+  if (*rc != KLA_OK) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *rc = fail(KLA_ERR_INVALID_ARG, "%s: device %d beyond %d", fn, dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_addr[dev];
 }
 
 }  // namespace
@@ -661,9 +694,28 @@ size_t kla_scan_workspace_bytes(int kind, int64_t batch, int64_t steps, int64_t 
   return bytes;
 }
 
+int kla_set_kernel_events(int kernel, hipEvent_t start, hipEvent_t stop) {
+  if (kernel != KLA_KERNEL_FUSED_FWD && kernel != KLA_KERNEL_FUSED_BWD)
+    return fail(KLA_ERR_INVALID_ARG, "kla_set_kernel_events: unknown kernel %d", kernel);
+  if ((start == nullptr) != (stop == nullptr))
+    return fail(KLA_ERR_INVALID_ARG, "kla_set_kernel_events: pass both events or neither");
+  t_kernel_events[kernel][0] = start;
+  t_kernel_events[kernel][1] = stop;
+  return KLA_OK;
+}
+
 int kla_workspace_failures(const void *workspace, hipStream_t stream, uint32_t *failures) {
   const char *fn = "kla_workspace_failures";
-  if (workspace == nullptr || failures == nullptr) return fail(KLA_ERR_INVALID_ARG, "%s: NULL argument", fn);
+  if (failures == nullptr) return fail(KLA_ERR_INVALID_ARG, "%s: NULL argument", fn);
+  if (workspace == nullptr) {   // the current device's static scratch (kla_mobius_scan_fwd_noalloc)
+    int rc = KLA_OK;
+    workspace = scratch_address_if_set(fn, &rc);
+    if (rc != KLA_OK) return rc;
+    if (workspace == nullptr) {   // no allocation-free call has run on this device
+      *failures = 0;
+      return KLA_OK;
+    }
+  }
   uint64_t word = 0;
   int rc = hip_status(fn, hipMemcpyAsync(&word, static_cast<const uint64_t *>(workspace) + 1, sizeof(word),
                                          hipMemcpyDeviceToHost, stream));

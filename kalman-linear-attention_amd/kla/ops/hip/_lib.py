@@ -19,7 +19,7 @@ import torch
 # one the ABI tests run against); by default the in-tree libkla_hip.so.
 LIB_PATH = os.environ.get("KLA_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))), "lib", "libkla_hip.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -40,6 +40,9 @@ KLA_SCAN_MOBIUS_BWD = 1
 KLA_SCAN_AFFINE_FWD = 2
 KLA_SCAN_AFFINE_BWD = 3
 
+KLA_KERNEL_FUSED_FWD = 0
+KLA_KERNEL_FUSED_BWD = 1
+
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _SIGNATURES = {
@@ -47,6 +50,7 @@ _SIGNATURES = {
     "kla_hip_last_error": (ctypes.c_char_p, []),
     "kla_scan_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, _i64, _i64, _i64]),
     "kla_workspace_failures": (ctypes.c_int, [_p, _p, ctypes.POINTER(ctypes.c_uint32)]),
+    "kla_set_kernel_events": (ctypes.c_int, [ctypes.c_int, _p, _p]),
     "kla_mobius_scan_fwd": (ctypes.c_int, [_p] * 6 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
     "kla_mobius_scan_fwd_noalloc": (ctypes.c_int, [_p] * 6 + [_i64] * 3 + [_p]),
     "kla_mobius_scan_bwd": (ctypes.c_int, [_p] * 12 + [_i64] * 3 + [_p, ctypes.c_size_t, _p]),
@@ -224,6 +228,45 @@ def workspace_failures(device: torch.device) -> int:
         return 0
     out = ctypes.c_uint32(0)
     check("kla_workspace_failures", lib().kla_workspace_failures(ws.data_ptr(), stream.cuda_stream, ctypes.byref(out)))
+    return int(out.value)
+
+
+class KernelTimer:
+    """Brackets every launch of one fused kernel from this thread with HIP events
+    (kla_set_kernel_events) while the context is open; ``times_ms()`` are the
+    launches' durations, in launch order. Each launch gets its own event pair."""
+
+    def __init__(self, kernel: int, device: torch.device):
+        self.kernel, self.device = kernel, device
+        self.pairs = []
+
+    def arm(self):
+        """Hand the library a fresh event pair for the next launch."""
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        stream = torch.cuda.current_stream(self.device)
+        s.record(stream)   # creates the events; the library records them again at the launch
+        e.record(stream)
+        self.pairs.append((s, e))
+        check("kla_set_kernel_events", lib().kla_set_kernel_events(self.kernel, s.cuda_event, e.cuda_event))
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        check("kla_set_kernel_events", lib().kla_set_kernel_events(self.kernel, None, None))
+
+    def times_ms(self) -> list:
+        torch.cuda.synchronize(self.device)
+        return [s.elapsed_time(e) for s, e in self.pairs]
+
+
+def noalloc_failures(device: torch.device) -> int:
+    """Look-back waits that gave up in the static scratch of kla_mobius_scan_fwd_noalloc
+    on ``device`` (kla_workspace_failures with a NULL workspace; 0 if never used)."""
+    stream = torch.cuda.current_stream(device)
+    out = ctypes.c_uint32(0)
+    with torch.cuda.device(device):
+        check("kla_workspace_failures", lib().kla_workspace_failures(None, stream.cuda_stream, ctypes.byref(out)))
     return int(out.value)
 
 

@@ -20,6 +20,7 @@ import re
 import threading
 
 import pytest
+import torch
 
 from kla.ops.hip import _lib
 
@@ -156,9 +157,28 @@ def test_affine_validation(lib):
 
 
 def test_workspace_failures_validation(lib):
-    out = ctypes.c_uint32(0)
-    assert lib.kla_workspace_failures(None, None, ctypes.byref(out)) == _lib.KLA_ERR_INVALID_ARG
+    out = ctypes.c_uint32(7)
     assert lib.kla_workspace_failures(WS, None, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_workspace_failures(None, None, None) == _lib.KLA_ERR_INVALID_ARG
+    # NULL workspace: the current device's static scratch (the allocation-free
+    # entry point's). Without a GPU there is no current device: a HIP error, and
+    # nothing is written; with one (and no allocation-free call yet) the count is 0.
+    rc = lib.kla_workspace_failures(None, None, ctypes.byref(out))
+    if torch.cuda.is_available():
+        assert rc == _lib.KLA_OK and out.value in (0, 7)
+    else:
+        assert rc == _lib.KLA_ERR_HIP and out.value == 7
+        assert "kla_workspace_failures" in err(lib)
+
+
+def test_set_kernel_events_validation(lib):
+    E = ctypes.c_void_p(0x1000)
+    assert lib.kla_set_kernel_events(2, None, None) == _lib.KLA_ERR_INVALID_ARG
+    assert "unknown kernel 2" in err(lib)
+    assert lib.kla_set_kernel_events(_lib.KLA_KERNEL_FUSED_BWD, E, None) == _lib.KLA_ERR_INVALID_ARG
+    assert lib.kla_set_kernel_events(_lib.KLA_KERNEL_FUSED_FWD, None, E) == _lib.KLA_ERR_INVALID_ARG
+    for kernel in (_lib.KLA_KERNEL_FUSED_FWD, _lib.KLA_KERNEL_FUSED_BWD):
+        assert lib.kla_set_kernel_events(kernel, None, None) == _lib.KLA_OK
 
 
 def test_last_error_is_per_thread(lib):

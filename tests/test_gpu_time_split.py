@@ -262,3 +262,58 @@ def test_training_planner_at_c1_matches_whole_backward(cuda, monkeypatch):
     names = ("y", "y_var", "lam", "eta", "dv", "dlambda_v", "dk", "dq", "da", "dp", "dlam0", "deta0")
     for name, got, want in zip(names, *runs):
         check_scan(name, got, want.detach().double().cpu().numpy())
+
+
+def _cold_start_inputs():
+    """lam0 = 0, eta0 = 0 under decay (a = 0.8, p = 0.03) with state lane s = 0 of
+    every channel nearly unobserved (phi = 4e-12, above the filter's EPS floor) for
+    the whole first chunk of 128 steps: the chunk's composed map carries a
+    denominator entry d1 below 1e-12, which chunk_starts_kernel must not floor at
+    EPS (the map algebra of this case is pinned in tests/test_time_split_algebra.py)."""
+    B, L, M, S = 1, 256, 8, 16
+    v, lv, k, q, _, _ = make_inputs(B, L, M, S, seed=41)
+    lv[:, :128] = 1.0
+    k[:, :128, 0] = 2e-6
+    a, p = torch.full((M, S), 0.8), torch.full((M, S), 0.03)
+    return (v, lv, k, q, a, p), KLAState(torch.zeros(B, M, S), torch.zeros(B, M, S))
+
+
+def test_forced_split_from_a_cold_start_matches_oracle(cuda, chunks):
+    ins, st = _cold_start_inputs()
+    print("[time split] cold start, nc=2", flush=True)
+    chunks(2)
+    y, y_var, fin = kla_scan(*(t.to(cuda) for t in ins), backend="hip_fused", initial_state=_state(st, cuda))
+    wy, wv, wl, we = oracle(ins, st)
+    assert wl.min() > 0
+    for name, got, want in (("y", y, wy), ("y_var", y_var, wv), ("lam", fin.lam, wl), ("eta", fin.eta, we)):
+        check_scan(name, got, want)
+
+
+def test_forced_training_split_from_a_cold_start_matches_float64_autograd(cuda, train_chunks):
+    """The same inputs with gradients (2 training chunks) against float64 autograd of
+    the step-by-step form of the reference's scan (torch_ref.kla_scan_stepwise: no
+    phi floor, exact from lam0 = 0, where the doubling form's trace-normalised
+    prefixes lose precision)."""
+    from oracle import torch_ref
+
+    ins, st = _cold_start_inputs()
+    print("[training split] cold start, nc=2", flush=True)
+    train_chunks(2)
+    B, L, M, S = ins[2].shape[0], ins[2].shape[1], ins[0].shape[2], ins[2].shape[2]
+    g = torch.Generator().manual_seed(42)
+    wy, wl, we = torch.randn(B, L, M, generator=g), torch.randn(B, M, S, generator=g), torch.randn(B, M, S, generator=g)
+
+    def loss(y, lam, eta):
+        w = [t.to(device=y.device, dtype=y.dtype) for t in (wy, wl, we)]
+        return (w[0] * y).sum() + (w[1] * lam).sum() + (w[2] * eta).sum()
+
+    xs = [t.double().requires_grad_(True) for t in ins + (st.lam, st.eta)]
+    ref = torch_ref.kla_scan_stepwise(*xs)
+    loss(ref[0], ref[2], ref[3]).backward()
+    gs = [t.to(cuda).requires_grad_(True) for t in ins + (st.lam, st.eta)]
+    y, _, fin = kla_scan(*gs[:6], backend="hip_fused", initial_state=KLAState(gs[6], gs[7]))
+    for name, got, want in zip(("y", "lam", "eta"), (y, fin.lam, fin.eta), (ref[0], ref[2], ref[3])):
+        check_scan(name, got, want.detach().numpy())
+    loss(y, fin.lam, fin.eta).backward()
+    for name, got, want in zip(("v", "lambda_v", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
+        check_scan("d" + name, got.grad, want.grad.numpy())

@@ -51,7 +51,12 @@ def chunk_maps(v, lv, k, a, p):
     return np.stack([n0, n1, d0, d1, w0, w1, w2], -1)
 
 
-def chain(maps, lam0, eta0):
+# chunk_starts_kernel guards a map's denominator against zero and subnormals only
+# (FLT_MIN): a rescaled map's d1 can be a normal number far below EPS.
+DEN_MIN = float(np.finfo(np.float32).tiny)
+
+
+def chain(maps, lam0, eta0, den_min=DEN_MIN):
     """States entering each chunk: maps [B, nc, M, S, 7] -> lam, eta [B, nc, M, S]."""
     nc = maps.shape[1]
     lam, eta = lam0.copy(), eta0.copy()
@@ -60,7 +65,7 @@ def chain(maps, lam0, eta0):
         lams.append(lam)
         etas.append(eta)
         n0, n1, d0, d1, w0, w1, w2 = np.moveaxis(maps[:, c], -1, 0)
-        den = np.maximum(d0 * lam + d1, okla.EPS)
+        den = np.maximum(d0 * lam + d1, den_min)
         lam, eta = (n0 * lam + n1) / den, (w0 * lam + w1 + w2 * eta) / den
     return np.stack(lams, 1), np.stack(etas, 1), lam, eta
 
@@ -105,3 +110,31 @@ def test_dropping_the_coupling_term_is_caught():
         A = (1 + np.maximum(p, okla.P_MIN) * phi) / a2
         n, d, w = A * n + phi * d, C * n + d, g * w + r * d
     assert np.abs(w / d - want_e).max() > 1e-3
+
+
+def test_cold_lane_over_a_whole_chunk_keeps_its_state():
+    """lam0 = 0 under decay (a = 0.8, p = 0.03) with a lane whose phi is 4e-12 for the
+    whole first chunk of 128 steps: the chunk's map, rescaled to a trace in
+    [0.5, 1), has d1 below 1e-12 (a normal float32), and the state entering chunk 1
+    is lam = n1 / d1 ~ 12. The chain follows the sequential filter (whose phi
+    floor stays idle at this k); the same chain with its denominator floored at
+    EPS (the slip this guards against) leaves lam far lower."""
+    B, L, M, S, Lc = 1, 256, 2, 3, 128
+    v, lv, k, q, _, _ = _inputs(B, L, M, S, seed=9)
+    lv[:, :Lc] = 1.0
+    k[:, :Lc, 0] = 2e-6   # phi = 4e-12: above the sequential filter's EPS floor
+    a, p = np.full((M, S), 0.8), np.full((M, S), 0.03)
+    lam0, eta0 = np.zeros((B, M, S)), np.zeros((B, M, S))
+    maps = np.stack([chunk_maps(v[:, c * Lc:(c + 1) * Lc], lv[:, c * Lc:(c + 1) * Lc], k[:, c * Lc:(c + 1) * Lc],
+                                a, p) for c in range(2)], 1)
+    assert maps[0, 0, :, 0, 3].max() < 1e-12 < maps[0, 0, :, 0, 3].min() * 1e6, "d1 of the cold lane's map"
+    _, _, want_l, want_e = okla.kla_scan_sequential(v[:, :Lc], lv[:, :Lc], k[:, :Lc], q[:, :Lc], a, p, lam0, eta0)
+    _, _, fin_l, fin_e = okla.kla_scan_sequential(v, lv, k, q, a, p, lam0, eta0)
+    assert want_l[0, 0, 0] > 1.0
+    lams, etas, lam_fin, eta_fin = chain(maps, lam0, eta0)
+    np.testing.assert_allclose(lams[:, 1], want_l, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(etas[:, 1], want_e, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(lam_fin, fin_l, rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(eta_fin, fin_e, rtol=1e-9, atol=1e-12)
+    bad = chain(maps, lam0, eta0, den_min=okla.EPS)[0][:, 1]
+    assert abs(bad[0, 0, 0] - want_l[0, 0, 0]) > 0.5 * want_l[0, 0, 0]
