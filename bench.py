@@ -499,7 +499,7 @@ def config_c4(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
     layer = KLALayer(1024, KLAConfig(d_state=16, backend=backend))
     out = {}
     if cpu:
-        L = 128
+        L = 1024
 
         def cpu_step(x):
             with torch.autocast("cpu", dtype=torch.bfloat16):
@@ -580,7 +580,7 @@ def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "d
     if cpu:
         for blk in model.blocks:
             blk.mixer.config.backend = "torch"
-        Lp = 128
+        Lp = 1024
         ids_c = torch.randint(0, 50304, (1, Lp), generator=torch.Generator().manual_seed(1))
         with torch.no_grad():
             pre_s = _cpu_once(lambda: model(ids_c, state=model.init_state(1)), warm=lambda: model(ids_c[:, :8]))
@@ -588,17 +588,17 @@ def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "d
             lg, st = model(ids16, state=model.init_state(nb))
             tok = lg[:, -1].argmax(-1, keepdim=True)
             t0 = time.perf_counter()
-            for _ in range(4):
+            for _ in range(16):
                 lg, st = model(tok, state=st)
                 tok = lg[:, -1].argmax(-1, keepdim=True)
-            dec_s = (time.perf_counter() - t0) / 4
+            dec_s = (time.perf_counter() - t0) / 16
         for blk in model.blocks:
             blk.mixer.config.backend = backend
         cpu_pre = {"value": Lp / pre_s, "unit": "prefill tokens/s", "cores": torch.get_num_threads(), "kind": "port",
                    "sample": (f"the same model on backend 'torch' on the host CPU, stateful prefill of (1, {Lp}) ids; "
                               f"one rep after a warm-up = {pre_s:.2f} s"), "host": _host()}
         cpu_dec = {"value": dec_s * 1e3, "unit": "ms/token", "cores": torch.get_num_threads(), "kind": "port",
-                   "sample": (f"the same model on backend 'torch' on the host CPU: 4 one-token decode steps at batch "
+                   "sample": (f"the same model on backend 'torch' on the host CPU: 16 one-token decode steps at batch "
                               f"{nb} after a 16-token prefill; mean {dec_s * 1e3:.1f} ms per step"), "host": _host()}
     model.to(device)
     ids = torch.randint(0, 50304, (nb, 2048), generator=torch.Generator().manual_seed(0)).to(device)
@@ -717,6 +717,8 @@ def main(argv=None) -> int:
     ap.add_argument("--c5-phase", default="all", choices=["all", "prefill"],
                     help="--layer c5: time the prefill and the decode (all) or the prefill only")
     ap.add_argument("--backend", default="hip", help="kla backend for --layer (hip, hip_composed, torch)")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="skip the headline step: print the configs alone (for per-config rocprofv3 runs)")
     ap.add_argument("--configs", default="all",
                     help="BASELINE configs measured after the headline, in the same JSON line's 'configs': 'all', "
                          "'none' or a comma list of " + ", ".join(CONFIG_NAMES))
@@ -746,6 +748,10 @@ def main(argv=None) -> int:
         return 0
     if args.layer:
         print(json.dumps(bench_layer(args, device, stream)), flush=True)
+        return 0
+    if args.configs_only:
+        print(json.dumps({"configs": run_configs(config_names, device, stream, args.steps, args.warmup,
+                                                 cpu=not args.no_cpu_baseline)}), flush=True)
         return 0
     batch, steps, lanes, adt, ops = WORKLOADS[args.workload]
     elems = batch * steps * lanes

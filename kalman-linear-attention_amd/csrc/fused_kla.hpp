@@ -281,25 +281,53 @@ __device__ __forceinline__ FusedLane fused_lane(const FusedGeom &g) {
 // One step of the filter (filter_step below). The fused kernels are VALU-bound,
 // so quotients are formed with the hardware reciprocal (v_rcp_f32, 1 ulp) times
 // the numerator instead of the ~10-instruction IEEE division: a relative error
-// of ~2 ulp per step, which the contractive recurrence does not amplify.
+// of ~2 ulp per step, different from step to step, which the contractive
+// recurrence does not amplify.
 constexpr float kInvEps = 1.0f / kEps;
 
 __device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
-// The precision update lam_t = (A lam + phi) / den, A = (1 + p' phi)/a2,
-// den = C lam + 1, C = p'/a2, in the form the kernels evaluate: A = 1/a2 + C phi
-// gives A lam + phi = lam/a2 + phi den, so
-//   lam_t = lam idn_a + phi,   idn_a = 1/(a2 den)
-// (one fma after the reciprocal; d lam_t / d phi = 1 exactly). The gain
-// alpha = a / max(a2 + p' lam, EPS) uses a2 + p' lam = a2 den: its reciprocal is
-// idn_a, and min(idn_a, 1/EPS) is the clamp for every den > 0 (the domain of the
-// filter: den = C lam + 1 is not clamped). phi = Lv k^2 and r = (v Lv) k come in
-// from the caller (from the k^2 and v Lv tiles the kernels stage per block).
-// Returns lam_t; inv_den = 1/den is left for the backward.
-__device__ __forceinline__ float filter_step(float lam, float &eta, float phi, float r, float a_s, float inv_a2,
-                                             float C, float &inv_den) {
-  inv_den = rcp(fmaf(C, lam, 1.0f));
-  const float idn_a = inv_den * inv_a2;
+// a2 = max(a^2, EPS) as an unevaluated sum hi + lo: hi = fl(a a) and lo = a a - hi
+// exactly (one fma), or (EPS, 0) where the clamp acts. Every step of the filter
+// divides by a2 + p' lam; a2 rounded once and reused for every step would bias
+// each step's decay by the same half ulp, and where the filter forgets slowly
+// (a close to 1, small p', a time constant of ~1 / (1 - a^2 / (a2 + p' lam))
+// steps) that bias adds up over the time constant instead of averaging out:
+// with a ~ 0.999 the final state of a 1024-step sequence moved by ~3e-5
+// relative. With lo folded in, each step's denominator is rounded once, afresh.
+struct A2 {
+  float hi, lo;
+};
+
+__device__ __forceinline__ A2 split_a2(float a) {
+  const float hi = a * a;
+  if (hi < kEps) return A2{kEps, 0.0f};
+  return A2{hi, fmaf(a, a, -hi)};
+}
+
+// 1 / (a2 + p' lam), the quotient every filter step needs.
+__device__ __forceinline__ float inv_den_a(const A2 &a2, float pp, float lam) {
+  return rcp(fmaf(pp, lam, a2.lo) + a2.hi);
+}
+
+// 1 / den = a2 / (a2 + p' lam) from idn_a = 1 / (a2 + p' lam), with a2's low part.
+__device__ __forceinline__ float inv_den_from(const A2 &a2, float idn_a) {
+  return fmaf(a2.hi, idn_a, a2.lo * idn_a);
+}
+
+// One step of the filter (reference kla_step, kla_ops.py:293-331, phi not floored
+// as in the scan): with idn_a = 1 / (a2 + p' lam),
+//   lam_t = lam / (a2 + p' lam) + phi = lam idn_a + phi       (d lam_t / d phi = 1)
+//   eta_t = alpha eta + r,  alpha = a / max(a2 + p' lam, EPS) = a min(idn_a, 1/EPS)
+// which is lam_t = (A lam + phi) / den with A = (1 + p' phi)/a2, den = C lam + 1,
+// C = p'/a2 (the Moebius leaf), and the gain clamp. The fused kernels are
+// VALU-bound, so the quotient is the hardware reciprocal (v_rcp_f32, 1 ulp) of
+// the one denominator. phi = Lv k^2 and r = (v Lv) k come in from the caller
+// (from the k^2 and v Lv tiles the kernels stage per block). Returns lam_t;
+// idn_a is left for the backward.
+__device__ __forceinline__ float filter_step(float lam, float &eta, float phi, float r, float a_s, const A2 &a2,
+                                             float pp, float &idn_a) {
+  idn_a = inv_den_a(a2, pp, lam);
   eta = fmaf(a_s * fminf(idn_a, kInvEps), eta, r);
   return fmaf(lam, idn_a, phi);
 }
@@ -567,9 +595,7 @@ __global__ void __launch_bounds__(kFusedThreads)
 
   const float a_s = ln.active ? prm.a[ms] : 1.0f;
   const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
-  const float a2 = fmaxf(a_s * a_s, kEps);
-  const float inv_a2 = 1.0f / a2;
-  const float C = pp * inv_a2;
+  const A2 a2 = split_a2(a_s);
   float lam = (ln.active && prm.lam0) ? prm.lam0[bms] : 1.0f;
   float eta = (ln.active && prm.eta0) ? prm.eta0[bms] : 0.0f;
 
@@ -631,13 +657,13 @@ __global__ void __launch_bounds__(kFusedThreads)
       const float sv = x4 ? pick4(v4, j % 4) : s_sv[cur][c][j];
       const float kk = x4 ? pick4(k4, j % 4) : s_k[kb][ln.s][j];
       const float k2 = !kK2 ? kk * kk : x4 ? pick4(k24, j % 4) : s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0][j];
-      float inv_den;
-      lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, inv_a2, C, inv_den);
+      float idn_a;
+      lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, a2, pp, idn_a);
       const float var = rcp(fmaxf(lam, kEps));
       float mean = eta * var, vo = var;
       if (PRIOR) {
         mean = a_s * mean;
-        vo = a2 * var + pp;
+        vo = a2.hi * var + pp;
       }
       const float qq = x4 ? pick4(q4, j % 4) : s_q[KQB == 1 ? 0 : cur][ln.s][j];
       yw[jj] = qq * mean;
@@ -755,9 +781,9 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
   const float a_s = ln.active ? prm.a[ms] : 1.0f;
   const float p_raw = ln.active ? prm.p[ms] : 0.0f;
   const float pp = fmaxf(p_raw, kEps);
-  const float a2 = fmaxf(a_s * a_s, kEps);
+  const A2 a2s = split_a2(a_s);
+  const float a2 = a2s.hi;
   const float inv_a2 = 1.0f / a2;
-  const float C = pp * inv_a2;
 
   float gl = (ln.active && prm.dlam_fin) ? prm.dlam_fin[bms] : 0.0f;   // adjoint of lam_t
   float ge = (ln.active && prm.deta_fin) ? prm.deta_fin[bms] : 0.0f;   // adjoint of eta_t
@@ -846,8 +872,8 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
     // bound is then a scalar compare (there is no 64-bit scalar less-than).
     const int nv = static_cast<int>(L - t0 < TB ? L - t0 : TB);
     // Over the block: lam_{t-1}, eta_{t-1} (lh[TB], eh[TB]: the state after the
-    // block), and each step's 1/den, kept from the replay (the posterior variance
-    // 1/lam_t is formed again in the walk: 16 registers fewer).
+    // block), and each step's 1/(a2 den), kept from the replay (the posterior
+    // variance 1/lam_t is formed again in the walk: 16 registers fewer).
     float lh[TB + 1], eh[TB + 1], idn[TB];
     // da, dp sum over all steps: accumulate each block apart and add the block
     // totals (two-level summation keeps fp32 rounding at ~(TB + L/TB) ulp).
@@ -890,7 +916,7 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
           const float sv = kVecLds ? pick4(v4, j % 4) : s_sv[cur][c][j];
           const float kk = kVecLds ? pick4(k4, j % 4) : s_k[kb][ln.s][j];
           const float k2 = !kK2 ? kk * kk : kVecLds ? pick4(k24, j % 4) : s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0][j];
-          lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, inv_a2, C, idn[j]);
+          lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, a2s, pp, idn[j]);
           if (FULL) unclamped = unclamped && lam >= kEps;
         }
       }
@@ -939,9 +965,10 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
           const float qq = kVecLds ? pick4(q4, j % 4) : s_q[kb][ln.s][j];
           const float lp = lh[j], ep = eh[j];
           const float lam_t = lh[j + 1], eta_t = eh[j + 1];
-          const float inv_den = idn[j], var = rcp(CLAMPS ? fmaxf(lam_t, kEps) : lam_t);
-          // The step's intermediates (filter_step) from the kept 1/den.
-          const float idn_a = inv_den * inv_a2;   // d lam_t / d lam' = 1/(a2 den^2) = idn_a / den
+          const float idn_a = idn[j], var = rcp(CLAMPS ? fmaxf(lam_t, kEps) : lam_t);
+          // The step's intermediates (filter_step) from the kept 1/(a2 den):
+          // 1/den = a2 idn_a, and d lam_t / d lam' = 1/(a2 den^2) = idn_a / den.
+          const float inv_den = inv_den_from(a2s, idn_a);
           // alpha = a / max(a2 + p' lam', EPS) = a min(idn_a, 1/EPS)
           const bool da_ok = !CLAMPS || idn_a <= kInvEps;
           const float inv_Da = CLAMPS ? fminf(idn_a, kInvEps) : idn_a;
@@ -1213,10 +1240,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_chunk_map_kernel(ChunkMap
 
   const float a_s = ln.active ? prm.a[ms] : 1.0f;
   const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
-  const float a2 = fmaxf(a_s * a_s, kEps);
-  const float inv_a2 = 1.0f / a2;
-  const float C = pp * inv_a2;
-  const float gain = a_s * inv_a2;
+  const A2 a2 = split_a2(a_s);
 
   const SensorIn &sn = prm.sn;
   const float *kbase = prm.k + ln.b * L * S;
@@ -1238,13 +1262,17 @@ __global__ void __launch_bounds__(kFusedThreads) fused_chunk_map_kernel(ChunkMap
   };
 
   float n0 = 1.0f, n1 = 0.0f, d0 = 0.0f, d1 = 1.0f, w0 = 0.0f, w1 = 0.0f, w2 = 1.0f;
+  // The step's leaf scaled by a2 (the map is projective, so any common factor
+  // is free): N' = (1 + p' phi) N + a2 phi D, D' = p' N + a2 D, W' = a W + r D'.
+  // No quotient, and the decay a2 enters D' with its low part (split_a2), so
+  // no rounding of a2 repeats from step to step.
   auto step = [&](float sig, float vv, float kk) {
     const float phi = sig * (kk * kk);
     const float r = (vv * sig) * kk;
-    const float A = (1.0f + pp * phi) * inv_a2;
-    const float e0 = fmaf(C, n0, d0), e1 = fmaf(C, n1, d1);
-    const float m0_ = fmaf(A, n0, phi * d0), m1_ = fmaf(A, n1, phi * d1);
-    const float x0 = fmaf(gain, w0, r * e0), x1 = fmaf(gain, w1, r * e1), x2 = gain * w2;
+    const float pphi = pp * phi, a2phi = a2.hi * phi;
+    const float e0 = fmaf(a2.hi, d0, fmaf(pp, n0, a2.lo * d0)), e1 = fmaf(a2.hi, d1, fmaf(pp, n1, a2.lo * d1));
+    const float m0_ = fmaf(a2phi, d0, fmaf(pphi, n0, n0)), m1_ = fmaf(a2phi, d1, fmaf(pphi, n1, n1));
+    const float x0 = fmaf(a_s, w0, r * e0), x1 = fmaf(a_s, w1, r * e1), x2 = a_s * w2;
     const int e = __builtin_amdgcn_frexp_expf(m0_ + e1);
     n0 = __builtin_amdgcn_ldexpf(m0_, -e);
     n1 = __builtin_amdgcn_ldexpf(m1_, -e);
@@ -1385,9 +1413,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_adjoint_map_kernel(Adjoin
 
   const float a_s = ln.active ? prm.a[ms] : 1.0f;
   const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
-  const float a2 = fmaxf(a_s * a_s, kEps);
-  const float inv_a2 = 1.0f / a2;
-  const float C = pp * inv_a2;
+  const A2 a2s = split_a2(a_s);
+  const float a2 = a2s.hi;
 
   const int64_t offM = ln.b * L * M + m0, offS = ln.b * L * S;
   const SensorIn &sn = prm.sn;
@@ -1461,7 +1488,7 @@ __global__ void __launch_bounds__(kFusedThreads) fused_adjoint_map_kernel(Adjoin
             const float sv = X4 ? pick4(v4, j % 4) : s_sv[cur][c][j];
             const float kk = X4 ? pick4(k4, j % 4) : s_k[kb][ln.s][j];
             const float k2 = !kK2 ? kk * kk : X4 ? pick4(k24, j % 4) : s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0][j];
-            lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, inv_a2, C, idn[j]);
+            lam = filter_step(lam, eta, sig * k2, sv * kk, a_s, a2s, pp, idn[j]);
           }
         }
         lh[TB] = lam;
@@ -1482,8 +1509,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_adjoint_map_kernel(Adjoin
           const float qq = X4 ? pick4(q4, j % 4) : s_q[kb][ln.s][j];
           const float ep = eh[j];
           const float lam_t = lh[j + 1], eta_t = eh[j + 1];
-          const float inv_den = idn[j];
-          const float idn_a = inv_den * inv_a2;
+          const float idn_a = idn[j];
+          const float inv_den = inv_den_from(a2s, idn_a);
           const bool da_ok = idn_a <= kInvEps;
           const float inv_Da = fminf(idn_a, kInvEps);
           const float alpha = a_s * inv_Da;
@@ -1585,7 +1612,8 @@ __global__ void __launch_bounds__(kFusedThreads) kla_step_kernel(StepParams prm,
   const int64_t bms = ln.b * M * S + ms;
   const float a_s = ln.active ? prm.a[ms] : 1.0f;
   const float pp = fmaxf(ln.active ? prm.p[ms] : 0.0f, kEps);
-  const float a2 = fmaxf(a_s * a_s, kEps);
+  const A2 a2s = split_a2(a_s);   // a2 + p' lam rounded once per step, as in the scan
+  const float a2 = a2s.hi;
   const float vv = mok ? prm.v[ln.b * M + ln.m] : 0.0f;
   const float sig = mok ? prm.lv[ln.b * M + ln.m] : 0.0f;
   const float kk = sok ? prm.k[ln.b * S + ln.s] : 0.0f;
@@ -1595,7 +1623,7 @@ __global__ void __launch_bounds__(kFusedThreads) kla_step_kernel(StepParams prm,
 
   const float phi = fmaxf(sig * (kk * kk), kEps);
   const float r = (vv * sig) * kk;
-  const float denom = fmaxf(a2 + pp * lam, kEps);
+  const float denom = fmaxf(fmaf(pp, lam, a2s.lo) + a2s.hi, kEps);
   lam = lam / denom + phi;
   eta = (a_s / denom) * eta + r;
   const float var = 1.0f / fmaxf(lam, kEps);
@@ -1687,7 +1715,8 @@ __global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodePa
   }
   const float a_s = a_bar;
   const float pp = fmaxf(p_bar, kEps);
-  const float a2 = fmaxf(a_s * a_s, kEps);
+  const A2 a2s = split_a2(a_s);   // a2 + p' lam rounded once per step, as in the scan
+  const float a2 = a2s.hi;
 
 #pragma unroll
   for (int bb = 0; bb < BB; ++bb) {
@@ -1715,7 +1744,7 @@ __global__ void __launch_bounds__(kFusedThreads) kla_decode_step_kernel(DecodePa
     float eta = active ? prm.eta[bms] : 0.0f;
     const float phi = fmaxf(sig * (kk * kk), kEps);
     const float r = (vv * sig) * kk;
-    const float denom = fmaxf(a2 + pp * lam, kEps);
+    const float denom = fmaxf(fmaf(pp, lam, a2s.lo) + a2s.hi, kEps);
     lam = lam / denom + phi;
     eta = (a_s / denom) * eta + r;
     const float var = 1.0f / fmaxf(lam, kEps);

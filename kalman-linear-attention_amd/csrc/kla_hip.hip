@@ -31,56 +31,33 @@ using namespace kla;
 constexpr int kAbiVersion = 16;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
-// thread (tile = 64 V lanes). Chosen by measurement on MI355X, each kernel
-// timed inside the fwd+bwd step: fp32 at (batch 8, steps 4096, lanes 2048),
-// bf16 at (8, 8192, 2048). The forward scans want a short register footprint
+// thread (tile = 64 V lanes), each chosen by timing the kernel inside the
+// fwd+bwd step on MI355X (fp32 at batch 8, 4096 steps, 2048 lanes; bf16 at
+// 8 x 8192 x 2048). The forward scans want a short register footprint
 // (occupancy hides the look-back), the backward scans long chunks; bf16 holds
 // two elements per register, so its tiles run wider (V = 2, 4) for the same
-// footprint.
-// A V > 1 shape needs lanes % V == 0 and operands aligned to V elements; the
-// V = 1 shape of the same kind serves every other call.
+// footprint. A V > 1 shape needs lanes % V == 0 and operands aligned to V
+// elements; the V = 1 shape of the same kind serves every other call.
 template <class P, int W_, int S_, int V_>
 struct Shape3 {
   using Policy = P;
   static constexpr int W = W_, S = S_, V = V_;
 };
-// Moebius forward: 8 waves of 12 steps. Re-swept with scalar-base addressing
-// (headline step, two rounds): 8 x 12 199 us, 12 x 12 200, 16 x 8 209, 8 x 16
-// 211-212, 8 x 8 244.
 using MobiusFwdTile = Shape3<void, 8, 12, 1>;
-// Moebius backward: 12 waves of 24 steps. Re-swept once the look-back published
-// carries only (headline step, kernel in the step, three rounds on one box):
-// 12 x 24 336-337 us against 340-342 for 16 x 16, 16 x 20 341, 12 x 20 343,
-// 12 x 28 341, 12 x 32 343, 8 x 24 348, 8 x 16 356. Again once the quotients
-// used the reciprocal (two rounds): 12 x 24 324-325 us, 8 x 32 322, 12 x 32 327,
-// 16 x 24 330, 12 x 20 330-331, 16 x 16 336-337, 8 x 24 343-344.
+// 24 steps per wave: the backward reads the saved lam once per 24 steps.
 using MobiusBwdTile = Shape3<void, 12, 24, 1>;
 using AffineFwdTile = Shape3<void, 16, 24, 1>;
-// fp32 affine forward whose output is stored cached (it fits the memory-side
-// cache): 12 waves of 24 steps. In the headline step (three rounds, one box)
-// the kernel ran 133-134 us against 140-141 for 16 x 24 (and the affine
-// backward after it 231 against 226), the step 0.890-0.895 ms against
-// 0.897-0.900; 8 x 32 135 us. The streaming form (C3 fp32) keeps 16 x 24, where
-// 12 x 24 ran 277-280 us against 273.
+// fp32 affine forward whose output is stored cached (it fits the memory-side cache).
 using AffineFwdCachedTile = Shape3<void, 12, 24, 1>;
-// fp32 affine backward: 12 waves of 32 steps. Re-swept after the cached-output
-// forward moved to 12 x 24 (headline step, two rounds): 12 x 32 232-233 us,
-// 16 x 24 230-231, 12 x 24 231, 12 x 40 232-233, 16 x 32 233, 8 x 32 248;
-// steps within noise of each other but for 8 x 32.
 using AffineBwdTile = Shape3<void, 12, 32, 1>;
-// bf16 affine forward: 12 waves of 24 steps, two lanes per thread. Re-swept
-// at C3 (8 x 8192 x 2048, three rounds, one box): 12 x 24 144 us, step
-// 0.426-0.435 ms, against 8 x 24 (the earlier choice) 146-147 us and
-// 0.435-0.438 ms; 8 x 32 148-149, 12 x 16 147, 16 x 16 169.
 using AffineFwdBf16Tile = Shape3<void, 12, 24, 2>;
 using AffineBwdBf16Tile = Shape3<void, 16, 16, 4>;
 using AffineBf16Fallback = Shape3<void, 8, 32, 1>;
 
 constexpr uint32_t kMaxSpin = 1u << 20;   // ~1 s of polling before a look-back wait gives up
 
-// Batch rows per thread of the one-token SSM step (kla_decode_step_kernel).
-// Measured in C5 graph decode (batch 16): 1 row 0.298 ms/token, 2 rows 0.305,
-// 4 rows 0.326, 8 rows 0.377 -- more workgroups beat discretising fewer times.
+// Batch rows per thread of the one-token SSM step (kla_decode_step_kernel): one
+// (more workgroups beat discretising the dynamics fewer times, in C5 decode).
 constexpr int kDecodeRows = 1;
 
 thread_local char g_last_error[512] = "";

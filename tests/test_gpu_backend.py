@@ -7,8 +7,9 @@ torch autograd through oracle.torch_ref for every gradient -- including the
 initial-state gradients the stateful prefill needs. The scan's bar is the
 path's fp32 tolerance, |got - want| <= atol + rtol |want| with rtol 1e-5 and an
 absolute atol 1e-6 (check_scan), except for the gradients that contract over
-many terms (dk, dq over channels; da, dp over batch and time), whose atol is
-1e-6 * max|want|, as the reference's tests/test_backends.py rel_err scales it.
+many terms of mixed sign (dk, dq over channels; da, dp over batch and time),
+whose atol is 1e-6 * max|want|, as the reference's tests/test_backends.py rel_err
+scales it; their ratio under the literal bar is printed beside it.
 The layer kernels around the scan are checked against torch's own operations
 relative to each tensor's scale (check), and the layer-level checks reuse the
 reference's golden vectors (tests/golden/layer_golden.npz).
@@ -43,28 +44,51 @@ def make_inputs(B=2, L=64, M=16, S=8, seed=0):
     )
 
 
-# Gradients that contract over many terms: dk, dq sum over the M channels, da, dp
-# over batch and time (B*L terms), dv and dlambda_v (and dproj, the projection
-# gradient that carries them) over the S state lanes of a channel. Their fp32
-# rounding grows with the magnitude of the terms, not of the (possibly
-# cancelled) result, so their atol is taken relative to the tensor's scale (the
-# reference's rel_err, tests/test_backends.py:161-168); every other output of
-# the scan -- y, y_var, the final state and the initial-state gradients --
-# meets the absolute rtol 1e-5 / atol 1e-6.
-CONTRACTIONS = ("dk", "dq", "da", "dp", "dv", "dlambda_v", "dproj")
+# Gradients that contract over many terms of mixed sign: dk and dq sum over the
+# M channels, da and dp over batch and time (B*L terms). Their fp32 rounding
+# grows with the magnitude of the terms, not of the (possibly cancelled)
+# result, so their atol is taken relative to the tensor's scale (the
+# reference's rel_err, tests/test_backends.py:161-168); the ratio under the
+# literal bar is printed beside it. Every other output and gradient of the scan
+# -- y, y_var, the final state, dv, dlambda_v, dproj and the initial-state
+# gradients -- meets the literal rtol 1e-5 / atol 1e-6.
+CONTRACTIONS = ("dk", "dq", "da", "dp")
+
+
+# KLA_TOL_LOG=path appends one line per check_scan call (test, tensor, the ratio
+# under the literal rtol 1e-5 / atol 1e-6 bar, the ratio under the bar applied,
+# the share of elements outside the literal bar): the record behind the
+# tolerance table of the design notes.
+TOL_LOG = os.environ.get("KLA_TOL_LOG")
+
+
+def literal_ratio(got, want):
+    """(worst |d| / (1e-6 + 1e-5 |want|), share of elements above 1) under the literal bar."""
+    if not got.size:
+        return 0.0, 0.0
+    r = np.abs(got - want) / (ATOL + RTOL * np.abs(want))
+    return float(r.max()), float((r > 1.0).mean())
 
 
 def check_scan(name, got, want):
     """The KLA scan's tolerance: |got - want| <= 1e-6 + 1e-5 |want| for outputs,
-    state and elementwise gradients; atol 1e-6 * max|want| for CONTRACTIONS."""
+    state and elementwise gradients; atol 1e-6 * max|want| for CONTRACTIONS.
+    The ratio under the literal bar is printed (and logged) beside it for every
+    tensor, contractions included."""
     got = got.detach().double().cpu().numpy()
     want = np.asarray(want, dtype=np.float64).reshape(got.shape)
     assert np.isfinite(got).all(), f"{name}: non-finite values"
     err = np.abs(got - want)
     atol = ATOL * max(float(np.abs(want).max()), 1e-30) if name in CONTRACTIONS else ATOL
     worst = float((err / (atol + RTOL * np.abs(want))).max()) if err.size else 0.0
+    lit, share = literal_ratio(got, want)
     kind = "atol 1e-6*max|ref|" if name in CONTRACTIONS else "atol 1e-6"
-    print(f"  {name:10s} worst |d|/(atol+rtol|ref|) = {worst:.3f}  [rtol 1e-5, {kind}]", flush=True)
+    print(f"  {name:10s} worst |d|/(atol+rtol|ref|) = {worst:.3f}  [rtol 1e-5, {kind}]; "
+          f"literal atol 1e-6: {lit:.3f} ({share:.2e} of elements above 1)", flush=True)
+    if TOL_LOG:
+        with open(TOL_LOG, "a") as f:
+            test = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+            f.write(f"{test}\t{name}\t{lit:.4g}\t{worst:.4g}\t{share:.3g}\t{kind}\n")
     assert worst <= 1.0, f"{name}: outside rtol={RTOL}, {kind} (ratio {worst:.3f})"
 
 
@@ -481,6 +505,40 @@ def test_fused_at_c4_size(cuda):
         assert torch.equal(fused[2 + i][rest], torch.zeros_like(fused[2 + i][rest])), name
     check_scan("dk", fused[4], xs[2].grad.numpy())
     check_scan("dq", fused[5], xs[3].grad.numpy())
+
+
+def test_fused_at_c4_size_whole_tensors(cuda):
+    """C4's scan shape (B=4, L=4096, M=2048, S=16), forward + backward on the fused
+    kernels with output gradients on every channel: every element of y, y_var,
+    the final state and all six input gradients against float64 autograd of the
+    reference's filter applied step by step (torch_ref.kla_scan_stepwise, the
+    leaves and guards of kla_ops.py:188-290), run in float64 on the GPU."""
+    B, L, M, S = 4, 4096, 2048, 16
+    g = torch.Generator().manual_seed(22)
+    v = torch.randn(B, L, M, generator=g)
+    lv = torch.rand(B, L, M, generator=g) + 0.5
+    k = torch.randn(B, L, S, generator=g) * 0.3
+    q = torch.randn(B, L, S, generator=g) * 0.3
+    a = torch.rand(M, S, generator=g) * 0.5 + 0.45
+    p = torch.rand(M, S, generator=g) * 0.05 + 0.01
+    dy = torch.randn(B, L, M, generator=g).to(cuda)
+    dyv = torch.randn(B, L, M, generator=g).to(cuda)
+    print("[c4 scan] hip", flush=True)
+    xs = [t.to(cuda).requires_grad_(True) for t in (v, lv, k, q, a, p)]
+    y, y_var, fin = kla_scan(*xs, backend="hip_fused")
+    ((dy * y).sum() + (dyv * y_var).sum()).backward()
+    got = [y.detach(), y_var.detach(), fin.lam, fin.eta] + [x.grad for x in xs]
+    del xs, y, y_var, fin
+    print("[c4 scan] float64 reference on the GPU", flush=True)
+    xd = [t.to(cuda).double().requires_grad_(True) for t in (v, lv, k, q, a, p)]
+    ones = torch.ones(B, M, S, dtype=torch.float64, device=cuda)
+    wy, wv, wl, we = torch_ref.kla_scan_stepwise(*xd, ones, torch.zeros_like(ones))
+    ((dy.double() * wy).sum() + (dyv.double() * wv).sum()).backward()
+    want = [wy.detach(), wv.detach(), wl.detach(), we.detach()] + [x.grad for x in xd]
+    del wy, wv, wl, we
+    names = ("y", "y_var", "lam", "eta", "dv", "dlambda_v", "dk", "dq", "da", "dp")
+    for name, gt, wt in zip(names, got, want):
+        check_scan(name, gt, wt.cpu().numpy())
 
 
 def test_fused_past_2_31_elements(cuda):

@@ -169,3 +169,40 @@ def test_c5_full_size_prefill_and_decode(cuda):
         assert torch.equal(eager[:, :C5_PREFILL], ids)
         assert torch.equal(eager, graph)
         assert int(eager.min()) >= 0 and int(eager.max()) < C5_VOCAB
+
+
+@pytest.mark.parametrize("mc_samples", [8])
+def test_mc_readout_matches_torch_backend(cuda, mc_samples):
+    """SequenceModel.logprobs with a Monte-Carlo read-out (reference
+    src/kla/models/readout.py:34-89, sequence_model.py:175): the model's mixers
+    emit their variance (KLAConfig(return_variance=True)), so on "hip" the fused
+    scan's y_var feeds the sampled read-out. The deterministic and MC
+    log-probabilities against the same weights on backend "torch" on the same
+    GPU, with the same seeded generator (the same eps draws), at rtol 1e-5 /
+    atol 1e-6; and both against float64 on the CPU for the deterministic part."""
+    torch.manual_seed(3)
+    cfg = ModelConfig(vocab_size=128, d_model=64, n_layers=2)
+    hip = SequenceModel(cfg, KLAConfig(d_state=8, return_variance=True, backend="hip")).to(cuda).eval()
+    ref = copy.deepcopy(hip)
+    for layer in ref.modules():
+        if isinstance(layer, KLALayer):
+            layer.config = KLAConfig(d_state=8, return_variance=True, backend="torch")
+        if hasattr(layer, "backend"):
+            layer.backend = "torch"
+    ref.norm_f.backend = "torch"
+    ids = torch.randint(0, 128, (2, 48), generator=torch.Generator().manual_seed(4)).to(cuda)
+    outs = []
+    with torch.no_grad():
+        for model in (hip, ref):
+            gen = torch.Generator(device=cuda).manual_seed(5)
+            det, mc = model.logprobs(ids, mc_samples=mc_samples, generator=gen)
+            assert mc is not None and mc.shape == det.shape == (2, 48, 128)
+            outs.append((det, mc))
+        det64, _ = copy.deepcopy(ref).double().cpu().logprobs(ids.cpu(), mc_samples=0)
+    (dh, mh), (dr, mr) = outs
+    # The MC mixture differs from the deterministic read-out (the variance is used).
+    assert float((mh - dh).abs().max()) > 1e-4
+    _close("det vs torch", dh, dr.cpu().numpy())
+    _close("mc vs torch", mh, mr.cpu().numpy())
+    _close("det vs float64", dh, det64.numpy())
+    _close("det torch vs f64", dr, det64.numpy())

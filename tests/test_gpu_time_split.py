@@ -269,11 +269,16 @@ def _cold_start_inputs():
     every channel nearly unobserved (phi = 4e-12, above the filter's EPS floor) for
     the whole first chunk of 128 steps: the chunk's composed map carries a
     denominator entry d1 below 1e-12, which chunk_starts_kernel must not floor at
-    EPS (the map algebra of this case is pinned in tests/test_time_split_algebra.py)."""
+    EPS (the map algebra of this case is pinned in tests/test_time_split_algebra.py).
+    An EPS floor there leaves that lane's lam entering chunk 1 about 3x too low,
+    which y, lam and eta of the second chunk show."""
     B, L, M, S = 1, 256, 8, 16
     v, lv, k, q, _, _ = make_inputs(B, L, M, S, seed=41)
     lv[:, :128] = 1.0
     k[:, :128, 0] = 2e-6
+    # The cold lane is not read out while cold (its mean eta / lam ~ 1e5 would make
+    # y ill-conditioned in fp32 over the first chunk); its state still enters chunk 1.
+    q[:, :128, 0] = 0.0
     a, p = torch.full((M, S), 0.8), torch.full((M, S), 0.03)
     return (v, lv, k, q, a, p), KLAState(torch.zeros(B, M, S), torch.zeros(B, M, S))
 
