@@ -410,7 +410,14 @@ def config_c1(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
     layer = KLALayer(512, KLAConfig(d_state=16, backend=backend))
     x_cpu = torch.randn(2, 1024, 512, generator=torch.Generator().manual_seed(0))
     out = {}
+    # The GPU first: CPU worker threads still spinning after a large CPU run slow
+    # the thread that launches the GPU kernels.
     with torch.no_grad():
+        layer.to(device)
+        x = x_cpu.to(device)
+        ms = _timed(lambda: layer(x), steps, warmup, stream)
+        y = layer(x).float().cpu()
+        layer.cpu()
         layer.config.backend = "torch"
         y_cpu = layer(x_cpu)
         if cpu:
@@ -421,10 +428,6 @@ def config_c1(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
                            f"kla_scan_torch, doubling scan under no_grad); median of {reps} reps = {cpu_s:.2f} s"),
                 "host": _host()}
         layer.config.backend = backend
-        layer.to(device)
-        x = x_cpu.to(device)
-        ms = _timed(lambda: layer(x), steps, warmup, stream)
-        y = layer(x).float().cpu()
     err = ((y - y_cpu).abs().max() / (y_cpu.abs().max() + 1e-12)).item()
     flops = linear_flops_per_token(layer) * 2 * 1024
     out.update({"metric": "KLALayer(512, d_state=16) forward tokens/s, x (2,1024,512) fp32",
@@ -493,31 +496,10 @@ def config_c4(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
     (kla_set_kernel_events) and priced on their VALU issue (SQ_INSTS_VALU of a
     committed rocprofv3 counter run) and on their compulsory HBM bytes."""
     from kla import KLAConfig, KLALayer
-    from kla.ops.hip import _lib
 
     torch.manual_seed(0)
     layer = KLALayer(1024, KLAConfig(d_state=16, backend=backend))
     out = {}
-    if cpu:
-        L = 1024
-
-        def cpu_step(x):
-            with torch.autocast("cpu", dtype=torch.bfloat16):
-                y = layer(x)
-            y.float().square().mean().backward()
-            layer.zero_grad(set_to_none=True)
-
-        layer.config.backend = "torch"
-        xs = torch.randn(1, L, 1024, generator=torch.Generator().manual_seed(1))
-        cpu_s = _cpu_once(lambda: cpu_step(xs), warm=lambda: cpu_step(xs[:, :16]))
-        layer.config.backend = backend
-        out["cpu_baseline"] = {
-            "value": L / cpu_s, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": (f"the same layer's training step on backend 'torch' on the host CPU under bf16 autocast, "
-                       f"x (1, {L}, 1024) (the reference's associative scan under grad; its cost grows faster than "
-                       f"linearly in L, so the full 4096-step rate is lower); one rep after a 16-step warm-up = "
-                       f"{cpu_s:.2f} s"),
-            "host": _host()}
     layer.to(device)
     x = torch.randn(4, 4096, 1024, generator=torch.Generator().manual_seed(0)).to(device)
 
@@ -532,8 +514,20 @@ def config_c4(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
                 "value": 4 * 4096 / (ms * 1e-3), "unit": "tokens/s", "ms": round(ms, 4), "backend": backend,
                 "dtype": "bf16 activations, f32 scan state",
                 "peak_mem_GiB": round(torch.cuda.max_memory_allocated(device) / 2**30, 2)})
-    if not backend.startswith("hip"):
-        return out
+    if backend.startswith("hip"):
+        out.update(_c4_kernel_rooflines(layer, step, steps, device))
+    if cpu:
+        layer.cpu()
+        torch.cuda.empty_cache()
+        out["cpu_baseline"] = _c4_cpu_baseline(layer, backend)
+    return out
+
+
+def _c4_kernel_rooflines(layer, step, steps, device) -> dict:
+    """The fused scan kernels of the C4 step, timed inside it (HIP events the
+    library records around each launch) and priced on VALU issue and bytes."""
+    from kla.ops.hip import _lib
+
     with _lib.KernelTimer(_lib.KLA_KERNEL_FUSED_FWD, device) as tf, \
             _lib.KernelTimer(_lib.KLA_KERNEL_FUSED_BWD, device) as tb:
         for _ in range(steps):
@@ -556,13 +550,36 @@ def config_c4(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
                       "valu_frac": round(rate / VALU_ISSUE_PEAK_G, 4)})
         kern[k] = e
     bwd = kern["fused_bwd"]
-    out["kernels"] = kern
+    out = {"kernels": kern}
     out["roofline"] = {"kernel": "fused_kla_bwd_kernel<16, false, true, false>", "bound": "valu",
                        "achieved": bwd.get("valu_G_per_s"), "peak": VALU_ISSUE_PEAK_G,
                        "unit": "G VALU wave-instructions/s", "frac": bwd.get("valu_frac"), "traffic": None,
                        "valu_source": os.path.relpath(vfile, REPO) if valu else None,
                        "hbm_GBps": bwd["GBps"], "hbm_frac": round(bwd["GBps"] / PEAK_HBM_GBPS, 4)}
     return out
+
+
+def _c4_cpu_baseline(layer, backend) -> dict:
+    """The same layer's training step on backend 'torch' on the host CPU."""
+    L = 1024
+
+    def cpu_step(x):
+        with torch.autocast("cpu", dtype=torch.bfloat16):
+            y = layer(x)
+        y.float().square().mean().backward()
+        layer.zero_grad(set_to_none=True)
+
+    layer.config.backend = "torch"
+    xs = torch.randn(1, L, 1024, generator=torch.Generator().manual_seed(1))
+    cpu_s = _cpu_once(lambda: cpu_step(xs), warm=lambda: cpu_step(xs[:, :16]))
+    layer.config.backend = backend
+    return {
+        "value": L / cpu_s, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+        "sample": (f"the same layer's training step on backend 'torch' on the host CPU under bf16 autocast, "
+                   f"x (1, {L}, 1024) (the reference's associative scan under grad; its cost grows faster than "
+                   f"linearly in L, so the full 4096-step rate is lower); one rep after a 16-step warm-up = "
+                   f"{cpu_s:.2f} s"),
+        "host": _host()}
 
 
 def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "decode"), cpu=True) -> dict:
@@ -576,30 +593,6 @@ def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "d
     weight_bytes = sum(p.numel() * p.element_size() for n, p in model.named_parameters() if n != "embedding.weight")
     flops_tok = linear_flops_per_token(model)
     out = {}
-    cpu_pre = cpu_dec = None
-    if cpu:
-        for blk in model.blocks:
-            blk.mixer.config.backend = "torch"
-        Lp = 1024
-        ids_c = torch.randint(0, 50304, (1, Lp), generator=torch.Generator().manual_seed(1))
-        with torch.no_grad():
-            pre_s = _cpu_once(lambda: model(ids_c, state=model.init_state(1)), warm=lambda: model(ids_c[:, :8]))
-            ids16 = torch.randint(0, 50304, (nb, 16), generator=torch.Generator().manual_seed(2))
-            lg, st = model(ids16, state=model.init_state(nb))
-            tok = lg[:, -1].argmax(-1, keepdim=True)
-            t0 = time.perf_counter()
-            for _ in range(16):
-                lg, st = model(tok, state=st)
-                tok = lg[:, -1].argmax(-1, keepdim=True)
-            dec_s = (time.perf_counter() - t0) / 16
-        for blk in model.blocks:
-            blk.mixer.config.backend = backend
-        cpu_pre = {"value": Lp / pre_s, "unit": "prefill tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-                   "sample": (f"the same model on backend 'torch' on the host CPU, stateful prefill of (1, {Lp}) ids; "
-                              f"one rep after a warm-up = {pre_s:.2f} s"), "host": _host()}
-        cpu_dec = {"value": dec_s * 1e3, "unit": "ms/token", "cores": torch.get_num_threads(), "kind": "port",
-                   "sample": (f"the same model on backend 'torch' on the host CPU: 16 one-token decode steps at batch "
-                              f"{nb} after a 16-token prefill; mean {dec_s * 1e3:.1f} ms per step"), "host": _host()}
     model.to(device)
     ids = torch.randint(0, 50304, (nb, 2048), generator=torch.Generator().manual_seed(0)).to(device)
     state = {}
@@ -617,9 +610,9 @@ def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "d
                       "roofline": _mfma_roofline("whole prefill: fp32 projections and LM head (hipBLASLt) + HIP "
                                                  "scan and glue, priced on the projections' flops",
                                                  flops_tok * nb * 2048, pre_ms),
-                      "cpu_baseline": cpu_pre}
+                      "cpu_baseline": None}
     if "decode" not in phases:
-        return out
+        return _c5_finish(out, model, backend, nb, cpu)
 
     @torch.no_grad()
     def decode256():
@@ -631,7 +624,7 @@ def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "d
     eager_ms = _timed(decode256, 1, 1, stream) / 256
     dec = {"metric": f"SequenceModel(d=512, 6 layers) one-token decode ms/token (batch {nb}, 256 greedy steps)",
            "unit": "ms/token", "higher_is_better": False, "eager_ms": round(eager_ms, 4), "backend": backend,
-           "dtype": "f32", "weight_bytes_per_token": weight_bytes, "cpu_baseline": cpu_dec}
+           "dtype": "f32", "weight_bytes_per_token": weight_bytes, "cpu_baseline": None}
     graph_ms = None
     if backend.startswith("hip"):
         from kla.models.decode_graph import DecodeGraph
@@ -653,7 +646,47 @@ def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "d
                                     weight_bytes, best)
     out["decode"] = dec
     out["peak_mem_GiB"] = round(torch.cuda.max_memory_allocated(device) / 2**30, 2)
+    return _c5_finish(out, model, backend, nb, cpu)
+
+
+def _c5_finish(out, model, backend, nb, cpu) -> dict:
+    """The CPU baselines, after the GPU timings (GPU first: CPU worker threads
+    still spinning after a large CPU run slow the thread that launches kernels)."""
+    if cpu:
+        model.cpu()
+        torch.cuda.empty_cache()
+        pre, dec = _c5_cpu_baselines(model, backend, nb)
+        out["prefill"]["cpu_baseline"] = pre
+        if "decode" in out:
+            out["decode"]["cpu_baseline"] = dec
     return out
+
+
+def _c5_cpu_baselines(model, backend, nb) -> tuple:
+    """The same model on backend 'torch' on the host CPU: prefill and one-token decode."""
+    for blk in model.blocks:
+        blk.mixer.config.backend = "torch"
+    Lp = 1024
+    ids_c = torch.randint(0, 50304, (1, Lp), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        pre_s = _cpu_once(lambda: model(ids_c, state=model.init_state(1)), warm=lambda: model(ids_c[:, :8]))
+        ids16 = torch.randint(0, 50304, (nb, 16), generator=torch.Generator().manual_seed(2))
+        lg, st = model(ids16, state=model.init_state(nb))
+        tok = lg[:, -1].argmax(-1, keepdim=True)
+        t0 = time.perf_counter()
+        for _ in range(16):
+            lg, st = model(tok, state=st)
+            tok = lg[:, -1].argmax(-1, keepdim=True)
+        dec_s = (time.perf_counter() - t0) / 16
+    for blk in model.blocks:
+        blk.mixer.config.backend = backend
+    pre = {"value": Lp / pre_s, "unit": "prefill tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+           "sample": (f"the same model on backend 'torch' on the host CPU, stateful prefill of (1, {Lp}) ids; "
+                      f"one rep after a warm-up = {pre_s:.2f} s"), "host": _host()}
+    dec = {"value": dec_s * 1e3, "unit": "ms/token", "cores": torch.get_num_threads(), "kind": "port",
+           "sample": (f"the same model on backend 'torch' on the host CPU: 16 one-token decode steps at batch "
+                      f"{nb} after a 16-token prefill; mean {dec_s * 1e3:.1f} ms per step"), "host": _host()}
+    return pre, dec
 
 
 CONFIG_NAMES = ("c1", "c3_fp32", "c3_bf16", "c4", "c5")
@@ -664,6 +697,7 @@ def run_configs(names, device, stream, steps, warmup, cpu=True) -> dict:
     out = {}
     for name in names:
         print(f"[bench] config {name}", file=sys.stderr, flush=True)
+        time.sleep(0.5)   # let the CPU worker threads of the previous config's CPU baseline go idle
         t0 = time.perf_counter()
         if name == "c1":
             out["c1_layer_forward"] = config_c1(device, stream, steps, warmup, cpu=cpu)

@@ -77,10 +77,11 @@ size_t kla_scan_workspace_bytes(int kind, int64_t batch, int64_t steps, int64_t 
 /* Timing hook, no counterpart in the reference: for a benchmark that times one
  * kernel inside a larger step (the fused backward launches its scan kernel and
  * then the partial-sum reductions). Until called again with NULL events, every
- * launch of `kernel` from the calling host thread records `start` on its stream
+ * launch of `kernel` in the process (from any host thread: torch's autograd
+ * launches backwards from a thread of its own) records `start` on its stream
  * right before that kernel and `stop` right after it; hipEventElapsedTime of
- * the pair is then that kernel's duration. Events are the caller's; the hook
- * holds no reference to them beyond the handles. */
+ * the pair is then that kernel's duration (of the last launch recorded). Events
+ * are the caller's; the hook holds no reference to them beyond the handles. */
 int kla_set_kernel_events(int kernel, hipEvent_t start, hipEvent_t stop);
 
 /* Number of look-back waits that gave up since the workspace was zero-filled

@@ -419,14 +419,21 @@ int sensors_from(const char *fn, const kla_sensors *in, int64_t M, SensorIn *out
   return KLA_OK;
 }
 
-// Timing events of the fused kernels (kla_set_kernel_events), per host thread:
-// [KLA_KERNEL_FUSED_FWD / _BWD][start, stop]. When set, the fused forward or
-// backward records `start` on its stream right before its scan kernel and
-// `stop` right after it, so that the pair brackets that kernel alone.
-thread_local hipEvent_t t_kernel_events[2][2] = {};
+// Timing events of the fused kernels (kla_set_kernel_events), for the whole
+// process: [KLA_KERNEL_FUSED_FWD / _BWD][start, stop]. When set, the fused
+// forward or backward records `start` on its stream right before its scan
+// kernel and `stop` right after it, so that the pair brackets that kernel
+// alone, whichever host thread launches it (torch's autograd launches the
+// backward from its own thread).
+std::mutex g_events_mu;
+hipEvent_t g_kernel_events[2][2] = {};
 
 int record_kernel_event(const char *fn, int kernel, int which, hipStream_t stream) {
-  hipEvent_t ev = t_kernel_events[kernel][which];
+  hipEvent_t ev;
+  {
+    std::lock_guard<std::mutex> lock(g_events_mu);
+    ev = g_kernel_events[kernel][which];
+  }
   return ev ? hip_status(fn, hipEventRecord(ev, stream)) : KLA_OK;
 }
 
@@ -676,8 +683,9 @@ int kla_set_kernel_events(int kernel, hipEvent_t start, hipEvent_t stop) {
     return fail(KLA_ERR_INVALID_ARG, "kla_set_kernel_events: unknown kernel %d", kernel);
   if ((start == nullptr) != (stop == nullptr))
     return fail(KLA_ERR_INVALID_ARG, "kla_set_kernel_events: pass both events or neither");
-  t_kernel_events[kernel][0] = start;
-  t_kernel_events[kernel][1] = stop;
+  std::lock_guard<std::mutex> lock(g_events_mu);
+  g_kernel_events[kernel][0] = start;
+  g_kernel_events[kernel][1] = stop;
   return KLA_OK;
 }
 

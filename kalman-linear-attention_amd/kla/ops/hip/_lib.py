@@ -232,9 +232,11 @@ def workspace_failures(device: torch.device) -> int:
 
 
 class KernelTimer:
-    """Brackets every launch of one fused kernel from this thread with HIP events
-    (kla_set_kernel_events) while the context is open; ``times_ms()`` are the
-    launches' durations, in launch order. Each launch gets its own event pair."""
+    """Brackets launches of one fused kernel with HIP events (kla_set_kernel_events,
+    process-wide, so the backward that torch's autograd launches from its own
+    thread is seen too) while the context is open: ``arm()`` before each step
+    hands the library a fresh event pair, and ``times_ms()`` are the durations
+    of the last launch in each armed step, in order."""
 
     def __init__(self, kernel: int, device: torch.device):
         self.kernel, self.device = kernel, device

@@ -145,3 +145,33 @@ def test_gate_skip_backward_is_bitwise_repeatable(cuda, lambda_vector):
     for other in runs[1:]:
         for name, a_, b_ in zip(("out", "dy", "dz", "dlambda"), runs[0], other):
             assert torch.equal(a_, b_), name
+
+
+def test_kernel_timer_brackets_the_fused_kernels(cuda):
+    """kla_set_kernel_events (the bench's in-step kernel timing): the event pairs
+    bracket the fused forward and the fused backward -- the latter launched from
+    torch's autograd thread -- with positive durations, and arming them changes
+    no result bit."""
+    from kla.ops.hip import _lib
+
+    ins = [t.to(cuda) for t in _inputs(2, 1024, 256, 16, seed=7)[:6]]
+
+    def run():
+        xs = [t.clone().requires_grad_(True) for t in ins]
+        y, y_var, _ = kla_scan(*xs, backend="hip_fused")
+        (y.square().sum() + y_var.sum()).backward()
+        return [y.detach(), y_var.detach()] + [x.grad for x in xs]
+
+    plain = run()
+    with _lib.KernelTimer(_lib.KLA_KERNEL_FUSED_FWD, cuda) as tf, \
+            _lib.KernelTimer(_lib.KLA_KERNEL_FUSED_BWD, cuda) as tb:
+        for _ in range(3):
+            tf.arm()
+            tb.arm()
+            timed = run()
+    fwd, bwd = tf.times_ms(), tb.times_ms()
+    print(f"[timer] fused fwd {fwd} ms, bwd {bwd} ms", flush=True)
+    assert len(fwd) == len(bwd) == 3
+    assert min(fwd) > 0.005 and min(bwd) > 0.005
+    for a, b in zip(plain, timed):
+        assert torch.equal(a, b)
