@@ -206,3 +206,50 @@ def test_mc_readout_matches_torch_backend(cuda, mc_samples):
     _close("mc vs torch", mh, mr.cpu().numpy())
     _close("det vs float64", dh, det64.numpy())
     _close("det torch vs f64", dr, det64.numpy())
+
+
+def test_c5_prefill_logits_against_float64(cuda, monkeypatch):
+    """C5's prefill on hip (fp32 GEMMs through torch, the fused scan and HIP glue)
+    against the same model evaluated in float64 on the GPU: float64 GEMMs, and the
+    reference layer's float32 scan inputs (kla_layer.py:224-231) evaluated by the
+    scan in float64, on the same static dynamics (a_bar, p_bar) as the hip layers.
+    The logits of the last position of every sequence, elementwise: the literal
+    ratio under rtol 1e-5 / atol 1e-6 is printed; the bar is rtol 1e-5 with atol
+    1e-5 max|logit| (six blocks of fp32 products over k = 512 to 1365 round at
+    ~1e-6 of their terms)."""
+    import kla.layers.kla_layer as kl
+    from kla.ops import kla_scan as real_scan
+
+    torch.manual_seed(0)
+    model = SequenceModel(ModelConfig(vocab_size=C5_VOCAB, d_model=C5_D, n_layers=C5_LAYERS),
+                          KLAConfig(backend="hip")).to(cuda).eval()
+    ids = torch.randint(0, C5_VOCAB, (C5_BATCH, C5_PREFILL), generator=torch.Generator().manual_seed(5)).to(cuda)
+    with torch.no_grad():
+        print("[c5 f64] hip prefill", flush=True)
+        got = model(ids)[:, -1].double()
+        aq = [blk.mixer._compute_aq() for blk in model.blocks]
+        ref = copy.deepcopy(model).double()
+        for layer in ref.modules():
+            if isinstance(layer, KLALayer):
+                layer.config = KLAConfig(backend="torch")
+            if hasattr(layer, "backend"):
+                layer.backend = "torch"
+        ref.norm_f.backend = "torch"
+        calls = []
+
+        def scan64(v, lv, k, q, a, p, **kw):
+            a_h, p_h = aq[len(calls)]
+            calls.append(1)
+            return real_scan(v.double(), lv.double(), k.double(), q.double(), a_h.double(), p_h.double(), **kw)
+
+        monkeypatch.setattr(kl, "kla_scan", scan64)
+        print("[c5 f64] float64 prefill", flush=True)
+        want = ref(ids)[:, -1]
+        assert len(calls) == C5_LAYERS
+    scale = float(want.abs().max())
+    err = (got - want).abs()
+    lit = float((err / (1e-6 + 1e-5 * want.abs())).max())
+    bar = float((err / (1e-5 * scale + 1e-5 * want.abs())).max())
+    print(f"  last-position logits vs float64: max |d| {float(err.max()):.3e} (scale {scale:.3e}); "
+          f"literal rtol 1e-5 / atol 1e-6 ratio {lit:.3f}, rtol 1e-5 / atol 1e-5 max ratio {bar:.3f}", flush=True)
+    assert bar <= 1.0
