@@ -28,3 +28,23 @@ def test_synthetic_inputs_follow_the_recipes():
     assert bool(((g > 0) & (g < 1)).all()) and g.shape == u.shape == dh.shape == (2, 5, 7)
     # Seeded on the CPU: the same draw twice.
     assert torch.equal(bench.mobius_inputs(2, 5, 7, seed=0)[0], A)
+
+
+def test_config_rooflines_price_the_documented_work():
+    """The configs' roofline numerators: the projections' multiply-add flops per
+    token (2 in out of every nn.Linear: C1's KLALayer(512) has in_proj 512 -> 2048,
+    sensor_proj 1024 -> 2080, out_proj 1024 -> 512), and the bytes the fused scan
+    kernels of C4 must move (514 MiB forward, 898 MiB backward with bf16 sensors)."""
+    from kla import KLAConfig, KLALayer
+
+    layer = KLALayer(512, KLAConfig(d_state=16))
+    assert bench.linear_flops_per_token(layer) == 2 * (512 * 2048 + 1024 * 2080 + 1024 * 512)
+    b = bench._fused_kernel_bytes(4, 4096, 2048, 16, sensor_bytes=2)
+    assert b == {"fused_fwd": 514 * 2**20, "fused_bwd": 898 * 2**20}
+    assert bench.VALU_ISSUE_PEAK_G == 614.4
+
+
+def test_unknown_config_is_refused(capsys):
+    with pytest.raises(SystemExit):
+        bench.main(["--configs", "c9"])
+    assert "unknown config" in capsys.readouterr().err
