@@ -28,6 +28,10 @@ namespace kla {
 constexpr int kConvThreads = 256;
 constexpr int kConvT = 64;   // time steps per thread (one chunk)
 constexpr int kConvMaxK = 8;
+// Steps whose loads a thread issues together (one thread walks one channel, so
+// a load moves 2 or 4 bytes a lane and one step's loads alone leave the stream
+// latency-bound).
+constexpr int kConvU = 8;
 
 __device__ __forceinline__ float io_load(const float *p) { return *p; }
 __device__ __forceinline__ float io_load(const bf16_t *p) { return to_f32(*p); }
@@ -121,15 +125,15 @@ __global__ void __launch_bounds__(kConvThreads) causal_conv_fwd_kernel(ConvFwdPa
     for (int j = 0; j + 1 < K - 1; ++j) win[j] = win[j + 1];
     if (K > 1) win[K - 2] = xt;
   };
-  // Four steps' loads in flight before their stores (y may not be assumed apart
+  // kConvU steps' loads in flight before their stores (y may not be assumed apart
   // from x by the compiler, so it would not hoist them itself).
   int64_t t = t0;
-  for (; t + 4 <= t1; t += 4) {
-    float xs[4];
+  for (; t + kConvU <= t1; t += kConvU) {
+    float xs[kConvU];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) xs[u] = io_load(xb + (t + u) * p.ld_t);
+    for (int u = 0; u < kConvU; ++u) xs[u] = io_load(xb + (t + u) * p.ld_t);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) step(t + u, xs[u]);
+    for (int u = 0; u < kConvU; ++u) step(t + u, xs[u]);
   }
   for (; t < t1; ++t) step(t, io_load(xb + t * p.ld_t));
   // The chunk that ends the sequence holds xpad[L : L + K - 1] in its window.
@@ -177,18 +181,17 @@ __global__ void __launch_bounds__(kConvThreads) causal_conv_bwd_kernel(ConvBwdPa
 
   IO *dxb = p.dx + b * p.L * p.D + d;
   IO *dsb = p.dstate ? p.dstate + (b * p.D + d) * (K - 1) : nullptr;
-  // Steps s in [t0, t1 + K - 1): g[s] for s < L; position s of xpad completes at step s.
-  const int64_t s_end = t1 + K - 1;
-  for (int64_t s = t0; s < s_end; ++s) {
+  // Steps s in [t0, t1 + K - 1): g[s] for s < L; position s of xpad completes at
+  // step s. xs = x[s], dys = dy[s] (both 0 past L, where they are not read).
+  auto step = [&](int64_t s, float xs, float dys) {
     float g = 0.0f;
     if (s < p.L) {
-      const float xs = io_load(xb + s * p.ld_t);
       float a = 0.0f;
 #pragma unroll
       for (int j = 0; j < K - 1; ++j) a += w[j] * win[j];
       a += w[K - 1] * xs;
       const float pre = io_round<IO>(a + bias);
-      g = io_load(dyb + s * p.D) * activation_grad(p.act, pre);
+      g = dys * activation_grad(p.act, pre);
       if (s < t1) {
 #pragma unroll
         for (int j = 0; j < K - 1; ++j) dw[j] += g * win[j];
@@ -214,6 +217,30 @@ __global__ void __launch_bounds__(kConvThreads) causal_conv_bwd_kernel(ConvBwdPa
 #pragma unroll
     for (int i = 0; i + 1 < K; ++i) acc[i] = acc[i + 1];
     acc[K - 1] = 0.0f;
+  };
+  // Groups of kConvU steps wholly inside the sequence load their x and dy first,
+  // unconditionally (the stores of dx may not be assumed apart from x and dy by
+  // the compiler, so it would not hoist the loads itself); the rest step by step.
+  const int64_t s_end = t1 + K - 1;
+  const int64_t s_in = s_end < p.L ? s_end : p.L;
+  int64_t s = t0;
+  for (; s + kConvU <= s_in; s += kConvU) {
+    float xs[kConvU], dys[kConvU];
+#pragma unroll
+    for (int u = 0; u < kConvU; ++u) {
+      xs[u] = io_load(xb + (s + u) * p.ld_t);
+      dys[u] = io_load(dyb + (s + u) * p.D);
+    }
+#pragma unroll
+    for (int u = 0; u < kConvU; ++u) step(s + u, xs[u], dys[u]);
+  }
+  for (; s < s_end; ++s) {
+    float xs = 0.0f, dys = 0.0f;
+    if (s < p.L) {
+      xs = io_load(xb + s * p.ld_t);
+      dys = io_load(dyb + s * p.D);
+    }
+    step(s, xs, dys);
   }
   const int64_t row = b * n_chunks + chunk;
 #pragma unroll
