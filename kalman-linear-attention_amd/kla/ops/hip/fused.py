@@ -28,7 +28,9 @@ from kla.ops.hip import _lib
 from kla.ops.hip.scans import _require_device
 
 _F32 = torch.float32
-# d_state the fused kernels take: a channel's S lanes in one 256-thread workgroup.
+# d_state one fused launch takes: a channel's S lanes in one 256-thread
+# workgroup. kla_scan_fused runs a larger d_state as groups of this many lanes
+# (state_groups); the sensor-fed variant and the decode steps stop here.
 MAX_STATE = 256
 # The time-split forward (inference only): grids below _split_below(SP)
 # workgroups per CU are split, into chunks of at least MIN_CHUNK steps, up to
@@ -155,13 +157,13 @@ def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     return None if t is None else t.to(_F32).contiguous()
 
 
-def _check(v, lambda_v, k, q, a, p, lam0, eta0):
+def _check(v, lambda_v, k, q, a, p, lam0, eta0, max_state: Optional[int] = MAX_STATE):
     if v.dim() != 3 or k.dim() != 3:
         raise ValueError(f"v must be [B, L, M] and k [B, L, S]; got {tuple(v.shape)} and {tuple(k.shape)}")
     B, L, M = v.shape
     S = k.shape[2]
-    if S > MAX_STATE:
-        raise NotImplementedError(f"the fused hip kernel supports d_state <= {MAX_STATE} (got {S}); "
+    if max_state is not None and S > max_state:
+        raise NotImplementedError(f"the fused hip kernel supports d_state <= {max_state} (got {S}); "
                                   "use backend='hip_composed'")
     for name, t, shape in (("lambda_v", lambda_v, (B, L, M)), ("k", k, (B, L, S)), ("q", q, (B, L, S)),
                            ("a", a, (M, S)), ("p", p, (M, S)), ("lam0", lam0, (B, M, S)),
@@ -171,37 +173,80 @@ def _check(v, lambda_v, k, q, a, p, lam0, eta0):
     return B, L, M, S
 
 
-@torch.library.custom_op("kla_hip::kla_scan_fused", mutates_args=())
-def _fused_fwd_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
-                  p: torch.Tensor, lam0: Optional[torch.Tensor], eta0: Optional[torch.Tensor],
-                  decode_from_prior: bool, save: bool
-                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Returns (y, y_var, lam_fin, eta_fin, ck_lam, ck_eta); the checkpoints are
-    empty unless ``save``."""
-    dev = _require_device(v, lambda_v, k, q, a, p, lam0, eta0)
-    B, L, M, S = _check(v, lambda_v, k, q, a, p, lam0, eta0)
+def state_groups(S: int) -> list[tuple[int, int]]:
+    """(first lane, lanes) of the state groups a d_state above MAX_STATE runs as:
+    MAX_STATE lanes each, the remainder last. The filter's lanes are independent
+    but for the read-out's sum over s, so each group is a whole fused scan of its
+    own lanes (k, q, a, p and the state sliced along s) and y, y_var -- and in the
+    backward dv, dlambda_v -- are the groups' sums, added in group order."""
+    return [(s0, min(MAX_STATE, S - s0)) for s0 in range(0, S, MAX_STATE)]
+
+
+def _lanes(t: Optional[torch.Tensor], s0: int, n: int) -> Optional[torch.Tensor]:
+    return None if t is None else t[..., s0:s0 + n].contiguous()
+
+
+def _ck_group(ck: torch.Tensor, B: int, n_ck: int, M: int, s0: int, n: int) -> torch.Tensor:
+    """Group (s0, n)'s checkpoints: the grouped forward keeps each group's [B, n_ck,
+    M, n] checkpoints as one contiguous block of the [B, n_ck, M, S] buffer, in
+    group order (the buffer is opaque to everything but the backward)."""
+    unit = B * n_ck * M
+    return ck.view(-1)[unit * s0:unit * (s0 + n)].view(B, n_ck, M, n)
+
+
+def _fwd_one(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save, dev, ck_lam, ck_eta):
+    """One fused forward over d_state <= MAX_STATE into the given checkpoint
+    buffers (used when ``save``); returns (y, y_var, lam_fin, eta_fin)."""
+    B, L, M = v.shape
+    S = k.shape[2]
     y = v.new_empty(B, L, M)
     y_var = v.new_empty(B, L, M)
     lam_fin = v.new_empty(B, M, S)
     eta_fin = v.new_empty(B, M, S)
-    n_ck = int(_lib.lib().kla_fused_checkpoints(L))
-    ck_lam = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
-    ck_eta = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
     if B * M * S == 0:
-        return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
+        return y, y_var, lam_fin, eta_fin
     cus = _cus(dev.index or 0)
     nc = train_chunks(B, L, M, S, cus) if save else time_chunks(B, L, M, S, cus)
     if nc > 1:
         lam_fin, eta_fin = _split_forward(_dense_sensors(v, lambda_v), k, q, a, p, lam0, eta0, y, y_var,
                                           decode_from_prior, B, L, M, S, nc, dev,
                                           ck_lam=ck_lam if save else None, ck_eta=ck_eta if save else None)
-        return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
+        return y, y_var, lam_fin, eta_fin
     stream = torch.cuda.current_stream(dev).cuda_stream
     pt = _lib.ptr
     _lib.check("kla_fused_scan_fwd", _lib.lib().kla_fused_scan_fwd(
         pt(v), pt(lambda_v), pt(k), pt(q), pt(a), pt(p), pt(lam0), pt(eta0), pt(y), pt(y_var),
         pt(lam_fin), pt(eta_fin), pt(ck_lam) if save else None, pt(ck_eta) if save else None,
         int(decode_from_prior), B, L, M, S, stream))
+    return y, y_var, lam_fin, eta_fin
+
+
+@torch.library.custom_op("kla_hip::kla_scan_fused", mutates_args=())
+def _fused_fwd_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
+                  p: torch.Tensor, lam0: Optional[torch.Tensor], eta0: Optional[torch.Tensor],
+                  decode_from_prior: bool, save: bool
+                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Returns (y, y_var, lam_fin, eta_fin, ck_lam, ck_eta); the checkpoints are
+    empty unless ``save``. d_state above MAX_STATE runs as state_groups(S)."""
+    dev = _require_device(v, lambda_v, k, q, a, p, lam0, eta0)
+    B, L, M, S = _check(v, lambda_v, k, q, a, p, lam0, eta0, max_state=None)
+    n_ck = int(_lib.lib().kla_fused_checkpoints(L))
+    ck_lam = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
+    ck_eta = v.new_empty(B, n_ck, M, S) if save else v.new_empty(0)
+    if S <= MAX_STATE:
+        return (*_fwd_one(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save, dev, ck_lam, ck_eta),
+                ck_lam, ck_eta)
+    y = y_var = None
+    lam_fin, eta_fin = v.new_empty(B, M, S), v.new_empty(B, M, S)
+    for s0, n in state_groups(S):
+        cl = _ck_group(ck_lam, B, n_ck, M, s0, n) if save else ck_lam
+        ce = _ck_group(ck_eta, B, n_ck, M, s0, n) if save else ck_eta
+        yg, yvg, lf, ef = _fwd_one(v, lambda_v, _lanes(k, s0, n), _lanes(q, s0, n), _lanes(a, s0, n),
+                                   _lanes(p, s0, n), _lanes(lam0, s0, n), _lanes(eta0, s0, n), decode_from_prior,
+                                   save, dev, cl, ce)
+        y, y_var = (yg, yvg) if y is None else (y.add_(yg), y_var.add_(yvg))
+        lam_fin[..., s0:s0 + n] = lf
+        eta_fin[..., s0:s0 + n] = ef
     return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
 
 
@@ -215,18 +260,11 @@ def _(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save):
             torch.empty_like(ck))
 
 
-@torch.library.custom_op("kla_hip::kla_scan_fused_backward", mutates_args=())
-def _fused_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: Optional[torch.Tensor],
-                  deta_fin: Optional[torch.Tensor],
-                  v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
-                  p: torch.Tensor, ck_lam: torch.Tensor, ck_eta: torch.Tensor, decode_from_prior: bool
-                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-                             torch.Tensor, torch.Tensor]:
-    """Returns (dv, dlambda_v, dk, dq, da, dp, dlam0, deta0). dy_var, dlam_fin,
-    deta_fin None: zero (without dy_var the kernel skips the variance read-out's
-    adjoint)."""
-    dev = _require_device(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta)
-    B, L, M, S = _check(v, lambda_v, k, q, a, p, None, None)
+def _bwd_one(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta, decode_from_prior, dev):
+    """One fused backward over d_state <= MAX_STATE; returns (dv, dlambda_v, dk,
+    dq, da, dp, dlam0, deta0)."""
+    B, L, M = v.shape
+    S = k.shape[2]
     dv, dlv = torch.empty_like(v), torch.empty_like(lambda_v)
     dk, dq = torch.empty_like(k), torch.empty_like(q)
     da, dp = torch.empty_like(a), torch.empty_like(p)
@@ -250,6 +288,37 @@ def _fused_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: Op
     nbytes = int(_lib.lib().kla_fused_workspace_bytes(B, L, M, S))
     ws, _ = _lib.scratch(nbytes, dev)
     bwd(B, L, dlam_fin, deta_fin, dlam0, deta0, ws, ws.numel())
+    return dv, dlv, dk, dq, da, dp, dlam0, deta0
+
+
+@torch.library.custom_op("kla_hip::kla_scan_fused_backward", mutates_args=())
+def _fused_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: Optional[torch.Tensor],
+                  deta_fin: Optional[torch.Tensor],
+                  v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
+                  p: torch.Tensor, ck_lam: torch.Tensor, ck_eta: torch.Tensor, decode_from_prior: bool
+                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                             torch.Tensor, torch.Tensor]:
+    """Returns (dv, dlambda_v, dk, dq, da, dp, dlam0, deta0). dy_var, dlam_fin,
+    deta_fin None: zero (without dy_var the kernel skips the variance read-out's
+    adjoint). d_state above MAX_STATE runs as the forward's state_groups(S)."""
+    dev = _require_device(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta)
+    B, L, M, S = _check(v, lambda_v, k, q, a, p, None, None, max_state=None)
+    if S <= MAX_STATE:
+        return _bwd_one(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck_eta,
+                        decode_from_prior, dev)
+    n_ck = int(_lib.lib().kla_fused_checkpoints(L))
+    dv = dlv = None
+    dk, dq = torch.empty_like(k), torch.empty_like(q)
+    da, dp = torch.empty_like(a), torch.empty_like(p)
+    dlam0, deta0 = v.new_empty(B, M, S), v.new_empty(B, M, S)
+    for s0, n in state_groups(S):
+        g = _bwd_one(dy, dy_var, _lanes(dlam_fin, s0, n), _lanes(deta_fin, s0, n), v, lambda_v,
+                     _lanes(k, s0, n), _lanes(q, s0, n), _lanes(a, s0, n), _lanes(p, s0, n),
+                     _ck_group(ck_lam, B, n_ck, M, s0, n), _ck_group(ck_eta, B, n_ck, M, s0, n),
+                     decode_from_prior, dev)
+        dv, dlv = (g[0], g[1]) if dv is None else (dv.add_(g[0]), dlv.add_(g[1]))
+        for out, part in zip((dk, dq, da, dp, dlam0, deta0), g[2:]):
+            out[..., s0:s0 + n] = part
     return dv, dlv, dk, dq, da, dp, dlam0, deta0
 
 

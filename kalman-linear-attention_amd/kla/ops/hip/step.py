@@ -18,7 +18,8 @@ _F32 = torch.float32
 def _step_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
              p: torch.Tensor, lam: torch.Tensor, eta: torch.Tensor, decode_from_prior: bool
              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(y [B, M], y_var [B, M], lam [B, M, S], eta [B, M, S]) after one step."""
+    """(y [B, M], y_var [B, M], lam [B, M, S], eta [B, M, S]) after one step; a
+    d_state above 256 runs as the fused scan's state groups."""
     dev = _require_device(v, lambda_v, k, q, a, p, lam, eta)
     B, M = v.shape
     S = k.shape[1]
@@ -26,10 +27,26 @@ def _step_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.
                            ("p", p, (M, S)), ("lam", lam, (B, M, S)), ("eta", eta, (B, M, S))):
         if tuple(t.shape) != shape:
             raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {shape}")
-    from kla.ops.hip.fused import MAX_STATE
+    from kla.ops.hip.fused import MAX_STATE, state_groups
 
     if S > MAX_STATE:
-        raise NotImplementedError(f"the hip decode step supports d_state <= {MAX_STATE}")
+        # The scan's state groups: each a step of its own lanes, the read-outs summed in group order.
+        y = y_var = None
+        lam_out, eta_out = torch.empty_like(lam), torch.empty_like(eta)
+        for s0, n in state_groups(S):
+            part = [t[..., s0:s0 + n].contiguous() for t in (k, q, a, p, lam, eta)]
+            yg, yvg, lg, eg = _step_one(v, lambda_v, *part, decode_from_prior, dev)
+            y, y_var = (yg, yvg) if y is None else (y.add_(yg), y_var.add_(yvg))
+            lam_out[..., s0:s0 + n] = lg
+            eta_out[..., s0:s0 + n] = eg
+        return y, y_var, lam_out, eta_out
+    return _step_one(v, lambda_v, k, q, a, p, lam, eta, decode_from_prior, dev)
+
+
+def _step_one(v, lambda_v, k, q, a, p, lam, eta, decode_from_prior, dev):
+    """One kla_step_fwd launch (d_state <= 256)."""
+    B, M = v.shape
+    S = k.shape[1]
     y, y_var = v.new_empty(B, M), v.new_empty(B, M)
     lam_out, eta_out = torch.empty_like(lam), torch.empty_like(eta)
     if B * M * S == 0:

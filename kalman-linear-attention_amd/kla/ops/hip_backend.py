@@ -1,8 +1,9 @@
 """The ``"hip"`` KLA backend: the KLA scan on MI355X kernels.
 
-Fused path (``kernel="fused"``, the default for d_state <= 256): the whole
-filter in one kernel per direction (:mod:`kla.ops.hip.fused`); nothing of shape
-[B, L, M, S] is materialised, and the backward is the exact adjoint.
+Fused path (``kernel="fused"``, the default): the whole filter in one kernel
+per direction (:mod:`kla.ops.hip.fused`); nothing of shape [B, L, M, S] is
+materialised, and the backward is the exact adjoint. A d_state above 256 runs as
+consecutive groups of at most 256 state lanes whose read-outs are summed.
 
 Composed path (``kernel="composed"``): the per-(b, l, m, s) glue -- sufficient
 statistics, Moebius leaves, the gain alpha, posterior and read-out -- is torch
@@ -42,13 +43,13 @@ def kla_scan_hip(
 ):
     """KLA scan on the MI355X kernels. ``kernel``: "auto", "fused" or "composed"."""
     from kla.ops.hip import affine_scan, mobius_scan
-    from kla.ops.hip.fused import MAX_STATE, kla_scan_fused
+    from kla.ops.hip.fused import kla_scan_fused
 
     if kernel not in ("auto", "fused", "composed"):
         raise ValueError(f"Unknown hip kernel {kernel!r}; expected 'auto', 'fused' or 'composed'")
     if not v.is_cuda:
         raise NotImplementedError("The hip KLA backend requires tensors on a ROCm GPU; use backend='torch'.")
-    if kernel == "fused" or (kernel == "auto" and k.shape[-1] <= MAX_STATE):
+    if kernel in ("auto", "fused"):
         lam0 = eta0 = None
         if initial_state is not None:
             lam0, eta0 = initial_state.lam, initial_state.eta

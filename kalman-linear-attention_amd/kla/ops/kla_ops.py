@@ -18,7 +18,7 @@ leaf A = (1 + p phi)/a^2, B = phi, C = p/a^2, D = 1, scanned as trace-normalised
 Backends (``kla_scan(..., backend=...)``):
   torch          this module's pure-torch path (CPU or GPU)
   hip            MI355X kernels (see :mod:`kla.ops.hip_backend`): the fused scan
-  hip_fused      pinned to the fused kernels (d_state <= 256)
+  hip_fused      pinned to the fused kernels (any d_state: groups of <= 256 lanes)
   hip_composed   pinned to the composed path (HIP scans + torch glue)
   triton*, cuda*, mps*  names kept from the reference registry for config
                  compatibility; their kernels are not part of this build and
@@ -232,7 +232,7 @@ def kla_step(
     MI355X step when no gradient is required; every other case is the torch
     formula below.
     """
-    if backend != "torch" and _step_on_hip(backend, v) and k.shape[-1] <= _hip_max_state() and not (
+    if backend != "torch" and _step_on_hip(backend, v) and not (
             torch.is_grad_enabled() and any(t.requires_grad for t in (v, lambda_v, k, q, a, p, *state))):
         from kla.ops.hip.step import kla_step_hip
 
@@ -274,13 +274,6 @@ def _step_on_hip(backend: str, x: torch.Tensor) -> bool:
 
     _lib.lib()   # RuntimeError when libkla_hip.so is missing or built for another ABI
     return True
-
-
-def _hip_max_state() -> int:
-    """Largest d_state the fused scan and the decode-step kernels take."""
-    from kla.ops.hip.fused import MAX_STATE
-
-    return MAX_STATE
 
 
 def kla_scan_reference(v, lambda_v, k, q, a, p, initial_state: Optional[KLAState] = None,

@@ -445,6 +445,28 @@ def test_time_chunks_plan():
         assert L % nc == 0 and (nc == 1 or L // nc >= MIN_CHUNK)
 
 
+def test_state_groups_plan():
+    """d_state above 256 runs as groups of 256 state lanes with the remainder last;
+    each group's checkpoints are one contiguous block of the [B, n_ck, M, S] buffer,
+    in group order, so the blocks tile the buffer exactly."""
+    import torch
+
+    from kla.ops.hip.fused import MAX_STATE, _ck_group, state_groups
+
+    assert MAX_STATE == 256
+    assert state_groups(16) == [(0, 16)]
+    assert state_groups(256) == [(0, 256)]
+    assert state_groups(257) == [(0, 256), (256, 1)]
+    assert state_groups(300) == [(0, 256), (256, 44)]
+    assert state_groups(520) == [(0, 256), (256, 256), (512, 8)]
+    B, n_ck, M, S = 2, 3, 5, 300
+    ck = torch.arange(B * n_ck * M * S, dtype=torch.float32).view(B, n_ck, M, S)
+    blocks = [_ck_group(ck, B, n_ck, M, s0, n) for s0, n in state_groups(S)]
+    assert [tuple(b.shape) for b in blocks] == [(B, n_ck, M, 256), (B, n_ck, M, 44)]
+    assert all(b.is_contiguous() and b.data_ptr() >= ck.data_ptr() for b in blocks)
+    assert torch.equal(torch.cat([b.reshape(-1) for b in blocks]), ck.view(-1))
+
+
 def test_sensor_row_layouts():
     """Which [B, L, M] views the fused-sensor kernels read in place: rows of one
     stride ld >= M with element (b, t, m) at (b * L + t) * ld + m."""

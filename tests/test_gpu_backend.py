@@ -140,7 +140,9 @@ def test_forward_and_state_match_oracle(cuda, backend, decode_from_prior, with_s
 @pytest.mark.parametrize("backend", BACKENDS)
 @pytest.mark.parametrize("shape", [(1, 1, 3, 2), (3, 257, 5, 16), (2, 1000, 8, 8), (1, 40, 70, 3), (2, 33, 9, 64),
                                    (1, 17, 300, 1), (2, 64, 3, 40), (2, 50, 7, 24), (1, 45, 20, 12),
-                                   (2, 300, 3, 128), (1, 70, 2, 256), (2, 45, 5, 65)])
+                                   (2, 300, 3, 128), (1, 70, 2, 256), (2, 45, 5, 65),
+                                   # d_state above 256: state groups of 256 lanes, remainder last
+                                   (1, 40, 3, 300), (2, 30, 2, 520)])
 def test_forward_ragged_shapes(cuda, backend, shape):
     B, L, M, S = shape
     ins = make_inputs(B, L, M, S, seed=7)
@@ -172,7 +174,9 @@ def test_chunked_state_carry(cuda, backend):
                                    # renumbering applies) with a ragged last channel group
                                    (2, 150, 120, 16), (8, 40, 9, 32),
                                    # d_state above 64: a channel spans 2 or 4 waves (ragged S too)
-                                   (2, 40, 5, 128), (1, 37, 3, 100), (1, 21, 2, 256), (2, 19, 3, 200)])
+                                   (2, 40, 5, 128), (1, 37, 3, 100), (1, 21, 2, 256), (2, 19, 3, 200),
+                                   # d_state above 256: two and three state groups
+                                   (1, 19, 2, 300), (1, 17, 2, 520)])
 def test_gradients_match_float64_autograd(cuda, backend, decode_from_prior, shape):
     """Every input gradient, the initial-state gradients, and gradients flowing in
     through the returned state, against float64 autograd of the reference's
@@ -397,7 +401,7 @@ def test_sequence_model_prefill_and_decode_on_hip(cuda):
 
 @pytest.mark.parametrize("decode_from_prior", [False, True])
 @pytest.mark.parametrize("shape", [(2, 16, 8), (3, 70, 5), (1, 9, 64), (4, 33, 1), (2, 5, 128), (3, 4, 256),
-                                   (2, 3, 150)])
+                                   (2, 3, 150), (2, 3, 300), (1, 4, 520)])
 def test_step_kernel_matches_reference_step(cuda, decode_from_prior, shape):
     """kla_step(backend="hip") (one HIP kernel) against the reference's step
     formula evaluated in float64 (kla_ops.py:293-331, phi floored)."""
@@ -1698,3 +1702,71 @@ def test_layer_with_wide_state_runs_the_fused_kernels(cuda, monkeypatch, autocas
     tol = dict(rtol=2e-2, atol=1e-2) if autocast else dict(rtol=2e-5, atol=2e-6)
     for i, (a, b) in enumerate(zip(*outs)):
         check(f"t{i}", a.float(), b.float().cpu().numpy(), **tol)
+
+
+@pytest.mark.parametrize("decode_from_prior", [False, True])
+def test_wide_state_groups_with_time_split_match_float64_autograd(cuda, monkeypatch, decode_from_prior):
+    """d_state 300 on "hip": two state groups (256 + 44 lanes), each on the
+    time-split training pair (L = 512 cut into 4 chunks of 128 steps: the grid is
+    3 and 1 workgroups), and never the composed path; forward, final state and every
+    gradient (inputs, initial state, and through the returned state) against
+    float64 autograd of the reference's torch algorithm."""
+    from kla.ops import hip_backend
+    from kla.ops.hip import fused
+
+    def no_composed(*args, **kwargs):
+        raise AssertionError("the composed path ran")
+
+    monkeypatch.setattr(hip_backend, "_sufficient_stats", no_composed)
+    B, L, M, S = 1, 512, 3, 300
+    cus = fused._cus(0)
+    assert [fused.train_chunks(B, L, M, n, cus) for _, n in fused.state_groups(S)] == [4, 4]
+    ins = make_inputs(B, L, M, S, seed=11)
+    st = random_state(B, M, S)
+    g = torch.Generator().manual_seed(5)
+    w = [torch.randn(B, L, M, generator=g), torch.randn(B, L, M, generator=g),
+         torch.randn(B, M, S, generator=g), torch.randn(B, M, S, generator=g)]
+
+    def loss(y, y_var, lam, eta):
+        ww = [t.to(device=y.device, dtype=y.dtype) for t in w]
+        return (ww[0] * y).sum() + (ww[1] * y_var).sum() + (ww[2] * lam).sum() + (ww[3] * eta).sum()
+
+    xs = [t.double().requires_grad_(True) for t in ins + (st.lam, st.eta)]
+    ref = torch_ref.kla_scan_torch(*xs, decode_from_prior=decode_from_prior)
+    loss(*ref).backward()
+    gs = [t.to(cuda).requires_grad_(True) for t in ins + (st.lam, st.eta)]
+    y, y_var, fin = kla_scan(*gs[:6], backend="hip", initial_state=KLAState(gs[6], gs[7]),
+                             decode_from_prior=decode_from_prior)
+    for name, got, want in (("y", y, ref[0]), ("y_var", y_var, ref[1]), ("lam", fin.lam, ref[2]),
+                            ("eta", fin.eta, ref[3])):
+        check_scan(name, got.detach(), want.detach().numpy())
+    loss(y, y_var, fin.lam, fin.eta).backward()
+    for name, got, want in zip(("v", "lambda_v", "k", "q", "a", "p", "lam0", "eta0"), gs, xs):
+        check_scan("d" + name, got.grad, want.grad.numpy())
+
+
+def test_layer_with_state_above_256_runs_the_fused_kernels(cuda, monkeypatch):
+    """KLALayer(d_state=300) on "hip": the scan runs as fused state groups (the
+    composed path is never called) and a forward + backward matches the same
+    layer on the torch backend."""
+    import copy
+
+    from kla.ops import hip_backend
+
+    def no_composed(*args, **kwargs):
+        raise AssertionError("the composed path ran")
+
+    torch.manual_seed(0)
+    hip = KLALayer(32, KLAConfig(d_state=300, backend="hip")).to(cuda)
+    ref = copy.deepcopy(hip)
+    ref.config = KLAConfig(d_state=300, backend="torch")
+    x = torch.randn(2, 40, 32, generator=torch.Generator().manual_seed(1)).to(cuda)
+    monkeypatch.setattr(hip_backend, "_sufficient_stats", no_composed)
+    outs = []
+    for layer in (hip, ref):
+        xx = x.clone().requires_grad_(True)
+        y = _first(layer(xx))
+        (y * torch.linspace(-1, 1, y.shape[-1], device=cuda)).sum().backward()
+        outs.append([y.detach(), xx.grad] + [p.grad for p in layer.parameters()])
+    for i, (a, b) in enumerate(zip(*outs)):
+        check(f"t{i}", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
