@@ -69,7 +69,10 @@ def time_chunks(B: int, L: int, M: int, S: int, cus: int) -> int:
 
 def _grid(B: int, M: int, S: int) -> tuple[int, int]:
     """(SP, workgroups) of the fused kernels' plain grid: SP = S rounded up to a
-    power of two (at least 4), 256 / SP channels a workgroup, B x channel groups."""
+    power of two (at least 4), 256 / SP channels a workgroup, B x channel groups.
+    One launch's plan: S is at most MAX_STATE (a wider state plans per group)."""
+    if S > MAX_STATE:
+        raise ValueError(f"one fused launch takes d_state <= {MAX_STATE} (got {S}); plan each of state_groups(S)")
     sp = 4
     while sp < S:
         sp *= 2

@@ -451,9 +451,12 @@ def test_state_groups_plan():
     in group order, so the blocks tile the buffer exactly."""
     import torch
 
-    from kla.ops.hip.fused import MAX_STATE, _ck_group, state_groups
+    from kla.ops.hip.fused import MAX_STATE, _ck_group, state_groups, time_chunks, train_chunks
 
     assert MAX_STATE == 256
+    for plan in (train_chunks, time_chunks):   # the planners plan one launch
+        with pytest.raises(ValueError, match="state_groups"):
+            plan(1, 1024, 4, 300, 256)
     assert state_groups(16) == [(0, 16)]
     assert state_groups(256) == [(0, 256)]
     assert state_groups(257) == [(0, 256), (256, 1)]

@@ -1745,10 +1745,12 @@ def test_wide_state_groups_with_time_split_match_float64_autograd(cuda, monkeypa
         check_scan("d" + name, got.grad, want.grad.numpy())
 
 
-def test_layer_with_state_above_256_runs_the_fused_kernels(cuda, monkeypatch):
+@pytest.mark.parametrize("autocast", [False, True])
+def test_layer_with_state_above_256_runs_the_fused_kernels(cuda, monkeypatch, autocast):
     """KLALayer(d_state=300) on "hip": the scan runs as fused state groups (the
     composed path is never called) and a forward + backward matches the same
-    layer on the torch backend."""
+    layer on the torch backend, in fp32 and under bf16 autocast (bf16
+    tolerance)."""
     import copy
 
     from kla.ops import hip_backend
@@ -1765,8 +1767,10 @@ def test_layer_with_state_above_256_runs_the_fused_kernels(cuda, monkeypatch):
     outs = []
     for layer in (hip, ref):
         xx = x.clone().requires_grad_(True)
-        y = _first(layer(xx))
-        (y * torch.linspace(-1, 1, y.shape[-1], device=cuda)).sum().backward()
-        outs.append([y.detach(), xx.grad] + [p.grad for p in layer.parameters()])
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+            y = _first(layer(xx))
+        (y.float() * torch.linspace(-1, 1, y.shape[-1], device=cuda)).sum().backward()
+        outs.append([y.detach().float(), xx.grad] + [p.grad for p in layer.parameters()])
+    tol = dict(rtol=2e-2, atol=1e-2) if autocast else dict(rtol=2e-5, atol=2e-6)
     for i, (a, b) in enumerate(zip(*outs)):
-        check(f"t{i}", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
+        check(f"t{i}", a.float(), b.float().cpu().numpy(), **tol)

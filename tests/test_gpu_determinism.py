@@ -34,18 +34,20 @@ def _inputs(B, L, M, S, seed):
 
 
 @pytest.mark.parametrize("shape", [(4, 4096, 2048, 16), (2, 150, 120, 16), (8, 40, 9, 32), (3, 100, 50, 64),
-                                   (2, 300, 40, 128), (2, 100, 9, 256), (1, 2048, 512, 16), (2, 1024, 256, 64)])
+                                   (2, 300, 40, 128), (2, 100, 9, 256), (1, 2048, 512, 16), (2, 1024, 256, 64),
+                                   (2, 100, 5, 300)])
 def test_fused_backward_is_bitwise_repeatable(cuda, shape):
     """The fused scan's forward and every gradient are bit-identical over three runs
     (C4's shape with 128 channel groups per batch row, ragged multi-group shapes
     whose grids take the XCD renumbering, and two small grids that the training
-    planner splits in time: 8 and 4 chunks, with the adjoint maps and the chunk
-    walks)."""
+    planner splits in time: 16 and 4 chunks, with the adjoint maps and the chunk
+    walks; and d_state 300, two state groups whose sums are added in group
+    order)."""
     from kla.ops.hip import fused
 
     B, L, M, S = shape
-    print(f"[determinism] fused shape={shape} train chunks={fused.train_chunks(B, L, M, S, fused._cus(0))}",
-          flush=True)
+    chunks = [fused.train_chunks(B, L, M, n, fused._cus(0)) for _, n in fused.state_groups(S)]
+    print(f"[determinism] fused shape={shape} train chunks per state group={chunks}", flush=True)
     ins = [t.to(cuda) for t in _inputs(B, L, M, S, seed=7)]
     dy, dyv = ins[6], ins[7]
     runs = []
