@@ -818,30 +818,58 @@ struct AffineBwd {
     r = raw;
   }
 
+  // Aggregate of the thread's steps j < nvalid: leaves (g, g dh), composed in
+  // order (affine_reduce's arithmetic; g is read once per step, which for bf16
+  // is one widening instead of two). A whole chunk runs without the per-step
+  // bound, whose branches made the compiler copy the running sum at every step.
   template <int S, int V>
   __device__ __forceinline__ static Agg<2> reduce(const Regs<S, V> &r, int v, int nvalid) {
-    return affine_reduce<S>([&](int j) { return r.g[j][v]; },
-                            [&](int j) { return r.g[j][v] * r.dh[j][v]; }, nvalid);
+    Agg<2> acc{{1.0f, 0.0f}};
+    auto step = [&](int j) __attribute__((always_inline)) {
+      const float gj = r.g[j][v];
+      const Agg<2> f{{gj, gj * r.dh[j][v]}};
+      acc = (j == 0) ? f : affine_compose(f, acc);
+    };
+    if (nvalid == S) {
+#pragma unroll
+      for (int j = 0; j < S; ++j) step(j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < S; ++j)
+        if (j < nvalid) step(j);
+    }
+    return acc;
   }
 
   __device__ __forceinline__ static Agg<2> compose(const Agg<2> &L, const Agg<2> &M) { return affine_compose(L, M); }
   __device__ __forceinline__ static float apply(const Agg<2> &a, float x) { return affine_apply(a, x); }
   __device__ __forceinline__ static float initial(const Params &, const Geom &, const Pos &, int) { return 0.0f; }
 
+  // Scan position s0 + j is time t = T-1-s0-j; the step at time 0 (bf16) takes
+  // h_{-1} = h0 from h_init. jz, the position of time 0 within the thread's
+  // steps (S when they do not reach it), is a wave-uniform 32-bit value, so the
+  // test is a scalar compare: written as s0 + j + 1 >= T it was a 64-bit
+  // less-than, which has no scalar form, and cost vector compares, a select and
+  // moves at every step (C3 bf16 backward 274 -> 261 us with the reduce above).
+  // (A second, unguarded copy of the walk for whole chunks spilled 30 VGPRs
+  // instead of 10 in the bf16 tile and ran slower.)
   template <int S, int V>
   __device__ __forceinline__ static void walk(const Params &p, const Geom &gm, const Regs<S, V> &r, const Pos &q,
                               int64_t s0, int nvalid, float (&x)[V]) {
     const int64_t row = row_index(gm, q, gm.steps - 1 - s0);
+    const int64_t left = gm.steps - 1 - s0;
+    const int jz = __builtin_amdgcn_readfirstlane(left < S ? static_cast<int>(left) : S);
 #pragma unroll
     for (int j = 0; j < S; ++j) {
       if (j < nvalid) {
         const int64_t rj = row - j * gm.lanes;
-        const bool first = SPLIT_H0 && s0 + j + 1 >= gm.steps;   // bf16: time 0 takes h0 apart
+        const bool first = SPLIT_H0 && j == jz;
         float dg[V], mu[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           mu[v] = r.dh[j][v] + x[v];
-          dg[v] = mu[v] * (first ? r.h_init[SPLIT_H0 ? v : 0] : r.hp[j][v]);
+          const float hp = r.hp[j][v];
+          dg[v] = mu[v] * (first ? r.h_init[SPLIT_H0 ? v : 0] : hp);
           x[v] = r.g[j][v] * mu[v];
         }
         if (q.ok) {
