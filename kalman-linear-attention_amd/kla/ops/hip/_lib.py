@@ -174,6 +174,39 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+# ------------------------------------------------------------ op dispatch
+#
+# Each kernel entry point is a torch.library custom op (autograd, fake tensors
+# for torch.compile). Going through the dispatcher costs ~13 us of host time a
+# call against ~2 us for a plain Python call, more than several of these kernels
+# take on the GPU, so calls that need none of what it adds run the op's function
+# directly.
+
+
+def hip_op(name: str):
+    """Decorator: ``torch.library.custom_op(name, mutates_args=())`` that keeps the
+    undecorated function as ``op.direct``."""
+    def wrap(fn):
+        op = torch.library.custom_op(name, mutates_args=())(fn)
+        op.direct = fn
+        return op
+    return wrap
+
+
+def call(op, *args):
+    """``op(*args)``, run without the dispatcher where it adds nothing: outside
+    torch.compile / export tracing, every tensor argument a plain tensor (no fake
+    or other subclass), and no autograd to record (grad mode off, or no tensor
+    argument requires grad). The same function runs either way."""
+    if torch.compiler.is_compiling():
+        return op(*args)
+    grad = torch.is_grad_enabled()
+    for a in args:
+        if isinstance(a, torch.Tensor) and (type(a) is not torch.Tensor or (grad and a.requires_grad)):
+            return op(*args)
+    return op.direct(*args)
+
+
 # ----------------------------------------------------------------- workspace
 #
 # One zero-filled workspace per (device, stream): the kernels keep it valid from

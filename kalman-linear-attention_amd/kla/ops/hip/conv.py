@@ -39,7 +39,7 @@ def _strides(x: torch.Tensor) -> tuple[int, int]:
     return x.stride(1), x.stride(0)
 
 
-@torch.library.custom_op("kla_hip::causal_conv", mutates_args=())
+@_lib.hip_op("kla_hip::causal_conv")
 def _conv_op(x: torch.Tensor, state: Optional[torch.Tensor], weight: torch.Tensor, bias: Optional[torch.Tensor],
              activation: int) -> tuple[torch.Tensor, torch.Tensor]:
     """(y [B, L, D], new_state [B, D, K-1]); weight [D, K] fp32."""
@@ -64,7 +64,7 @@ def _(x, state, weight, bias, activation):
     return x.new_empty(B, L, D), x.new_empty(B, D, weight.shape[1] - 1)
 
 
-@torch.library.custom_op("kla_hip::causal_conv_backward", mutates_args=())
+@_lib.hip_op("kla_hip::causal_conv_backward")
 def _conv_bwd_op(dy: torch.Tensor, dstate_out: Optional[torch.Tensor], x: torch.Tensor, state: Optional[torch.Tensor],
                  weight: torch.Tensor, bias: Optional[torch.Tensor], activation: int,
                  need_dstate: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -110,7 +110,7 @@ def _setup(ctx, inputs, output):
 def _backward(ctx, dy, dstate_out):
     x, state, weight, bias = ctx.saved_tensors
     need_dstate = ctx.has_state and ctx.needs_input_grad[1]
-    dx, dstate, dweight, dbias = _conv_bwd_op(
+    dx, dstate, dweight, dbias = _lib.call(_conv_bwd_op,
         dy.contiguous(), dstate_out.contiguous() if dstate_out is not None else None, x,
         state if ctx.has_state else None, weight, bias if ctx.has_bias else None, ctx.activation, need_dstate)
     return (dx, dstate if need_dstate else None, dweight.to(weight.dtype),
@@ -132,4 +132,4 @@ def causal_conv_hip(x: torch.Tensor, state: Optional[torch.Tensor], weight: torc
         state = state.to(x.dtype).contiguous()
     w = weight.float()
     b = bias.float() if bias is not None else None
-    return _conv_op(x, state, w, b, ACTIVATIONS[activation])
+    return _lib.call(_conv_op, x, state, w, b, ACTIVATIONS[activation])

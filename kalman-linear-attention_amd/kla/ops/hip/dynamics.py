@@ -22,7 +22,7 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-@torch.library.custom_op("kla_hip::discretize", mutates_args=())
+@_lib.hip_op("kla_hip::discretize")
 def _disc_op(delta: torch.Tensor, lambda_log: torch.Tensor, pnoise: torch.Tensor, ou: bool, zero_pn: bool,
              has_clip: bool, clip: float) -> tuple[torch.Tensor, torch.Tensor]:
     _require_device(delta, lambda_log, pnoise)
@@ -38,7 +38,7 @@ def _(delta, lambda_log, pnoise, ou, zero_pn, has_clip, clip):
     return torch.empty_like(delta), torch.empty_like(delta)
 
 
-@torch.library.custom_op("kla_hip::discretize_backward", mutates_args=())
+@_lib.hip_op("kla_hip::discretize_backward")
 def _disc_bwd_op(delta: torch.Tensor, lambda_log: torch.Tensor, pnoise: torch.Tensor, g_a: torch.Tensor,
                  g_p: torch.Tensor, ou: bool, zero_pn: bool, has_clip: bool,
                  clip: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -66,7 +66,7 @@ def _backward(ctx, g_a, g_p):
     delta, lambda_log, pnoise = ctx.saved_tensors
     g_a = torch.zeros_like(delta) if g_a is None else g_a.float().contiguous()
     g_p = torch.zeros_like(delta) if g_p is None else g_p.float().contiguous()
-    d_delta, d_ll, d_pn = _disc_bwd_op(delta, lambda_log, pnoise, g_a, g_p, *ctx.cfg)
+    d_delta, d_ll, d_pn = _lib.call(_disc_bwd_op, delta, lambda_log, pnoise, g_a, g_p, *ctx.cfg)
     return d_delta, d_ll, d_pn, None, None, None, None
 
 
@@ -84,6 +84,6 @@ def discretize_hip(delta: torch.Tensor, lambda_log: torch.Tensor, process_noise:
             raise ValueError(f"discretize_hip: {name} has shape {tuple(t.shape)}, expected {tuple(delta.shape)}")
     if discretization not in ("ou", "zoh"):
         raise ValueError(f"discretize_hip: unknown discretization {discretization!r}")
-    return _disc_op(delta.contiguous(), lambda_log.contiguous(), process_noise.contiguous(),
-                    discretization == "ou", bool(zero_process_noise), clip_value is not None,
-                    float(clip_value) if clip_value is not None else 0.0)
+    return _lib.call(_disc_op, delta.contiguous(), lambda_log.contiguous(), process_noise.contiguous(),
+                     discretization == "ou", bool(zero_process_noise), clip_value is not None,
+                     float(clip_value) if clip_value is not None else 0.0)

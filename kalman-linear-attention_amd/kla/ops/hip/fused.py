@@ -224,7 +224,7 @@ def _fwd_one(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save, dev, 
     return y, y_var, lam_fin, eta_fin
 
 
-@torch.library.custom_op("kla_hip::kla_scan_fused", mutates_args=())
+@_lib.hip_op("kla_hip::kla_scan_fused")
 def _fused_fwd_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
                   p: torch.Tensor, lam0: Optional[torch.Tensor], eta0: Optional[torch.Tensor],
                   decode_from_prior: bool, save: bool
@@ -294,7 +294,7 @@ def _bwd_one(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck
     return dv, dlv, dk, dq, da, dp, dlam0, deta0
 
 
-@torch.library.custom_op("kla_hip::kla_scan_fused_backward", mutates_args=())
+@_lib.hip_op("kla_hip::kla_scan_fused_backward")
 def _fused_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: Optional[torch.Tensor],
                   deta_fin: Optional[torch.Tensor],
                   v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
@@ -352,7 +352,7 @@ def _backward(ctx, dy, dy_var, dlam_fin, deta_fin, _dck_lam, _dck_eta):
     def f32(t):
         return None if t is None else t.to(_F32).contiguous()
 
-    dv, dlv, dk, dq, da, dp, dlam0, deta0 = _fused_bwd_op(
+    dv, dlv, dk, dq, da, dp, dlam0, deta0 = _lib.call(_fused_bwd_op,
         torch.zeros_like(v) if dy is None else f32(dy), f32(dy_var), f32(dlam_fin), f32(deta_fin), v, lambda_v,
         k, q, a, p, ck_lam, ck_eta, ctx.prior)
     return (dv, dlv, dk, dq, da, dp, dlam0 if ctx.has_lam0 else None, deta0 if ctx.has_eta0 else None,
@@ -372,8 +372,8 @@ def kla_scan_fused(v, lambda_v, k, q, a, p, lam0=None, eta0=None, decode_from_pr
     v, lambda_v, k, q, a, p, lam0, eta0 = (_f32(t) for t in (v, lambda_v, k, q, a, p, lam0, eta0))
     save = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (v, lambda_v, k, q, a, p, lam0, eta0))
-    y, y_var, lam_fin, eta_fin, _, _ = _fused_fwd_op(v, lambda_v, k, q, a, p, lam0, eta0,
-                                                     bool(decode_from_prior), save)
+    y, y_var, lam_fin, eta_fin, _, _ = _lib.call(_fused_fwd_op, v, lambda_v, k, q, a, p, lam0, eta0,
+                                                  bool(decode_from_prior), save)
     return y, y_var, lam_fin, eta_fin
 
 
@@ -417,7 +417,7 @@ def _check_sensors(v, obs):
         raise ValueError("sensor operands must be [B, L, M] rows with a contiguous last dimension")
 
 
-@torch.library.custom_op("kla_hip::kla_scan_fused_sensors", mutates_args=())
+@_lib.hip_op("kla_hip::kla_scan_fused_sensors")
 def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
                     p: torch.Tensor, lam0: Optional[torch.Tensor], eta0: Optional[torch.Tensor], log_var: bool,
                     obs_var_min: float, obs_var_max: float, decode_from_prior: bool, save: bool, with_var: bool
@@ -466,7 +466,7 @@ def _(v, obs, k, q, a, p, lam0, eta0, log_var, obs_var_min, obs_var_max, decode_
             torch.empty_like(ck))
 
 
-@torch.library.custom_op("kla_hip::kla_scan_fused_sensors_backward", mutates_args=())
+@_lib.hip_op("kla_hip::kla_scan_fused_sensors_backward")
 def _sensors_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: Optional[torch.Tensor],
                     deta_fin: Optional[torch.Tensor],
                     v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
@@ -536,7 +536,7 @@ def _sensors_backward(ctx, dy, dy_var, dlam_fin, deta_fin, _dck_lam, _dck_eta):
 
     B, L, M = v.shape
     dy = k.new_zeros(B, L, M) if dy is None else f32(dy)
-    dv, dobs, dk, dq, da, dp, dlam0, deta0 = _sensors_bwd_op(
+    dv, dobs, dk, dq, da, dp, dlam0, deta0 = _lib.call(_sensors_bwd_op,
         dy, f32(dy_var), f32(dlam_fin), f32(deta_fin), v, obs, k, q, a, p, ck_lam, ck_eta, *ctx.opts)
     return (dv, dobs, dk, dq, da, dp, dlam0 if ctx.has_lam0 else None, deta0 if ctx.has_eta0 else None,
             None, None, None, None, None, None)
@@ -569,7 +569,7 @@ def kla_scan_fused_sensors(v, obs, k, q, a, p, lam0=None, eta0=None, *, log_var:
     save = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (v, obs, k, q, a, p, lam0, eta0))
     ov_max = math.inf if obs_var_max is None else float(obs_var_max)
-    y, y_var, lam_fin, eta_fin, _, _ = _sensors_fwd_op(v, obs, k, q, a, p, lam0, eta0, bool(log_var),
-                                                       float(obs_var_min), ov_max, bool(decode_from_prior), save,
-                                                       bool(with_var))
+    y, y_var, lam_fin, eta_fin, _, _ = _lib.call(_sensors_fwd_op, v, obs, k, q, a, p, lam0, eta0, bool(log_var),
+                                                  float(obs_var_min), ov_max, bool(decode_from_prior), save,
+                                                  bool(with_var))
     return y, (y_var if with_var else None), lam_fin, eta_fin

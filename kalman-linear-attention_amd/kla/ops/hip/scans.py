@@ -77,7 +77,7 @@ def _check_seq(ts, like: torch.Tensor, dtype: torch.dtype) -> None:
 # ================================================================== Moebius
 
 
-@torch.library.custom_op("kla_hip::mobius_scan", mutates_args=())
+@_lib.hip_op("kla_hip::mobius_scan")
 def _mobius_scan_op(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, D: Optional[torch.Tensor],
                     lam0: Optional[torch.Tensor]) -> torch.Tensor:
     dev = _require_device(A, B, C, D, lam0)
@@ -99,7 +99,7 @@ def _(A, B, C, D, lam0):
     return torch.empty_like(A)
 
 
-@torch.library.custom_op("kla_hip::mobius_scan_backward", mutates_args=())
+@_lib.hip_op("kla_hip::mobius_scan_backward")
 def _mobius_scan_bwd_op(dlam: torch.Tensor, A: torch.Tensor, B: torch.Tensor, C: torch.Tensor,
                         D: Optional[torch.Tensor], lam0: Optional[torch.Tensor], lam: torch.Tensor
                         ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -139,7 +139,7 @@ def _mobius_setup(ctx, inputs, output):
 
 def _mobius_backward(ctx, dlam):
     A, B, C, D, lam0, lam = ctx.saved_tensors
-    dA, dB, dC, dD, dlam0 = _mobius_scan_bwd_op(dlam.contiguous(), A, B, C, D, lam0, lam)
+    dA, dB, dC, dD, dlam0 = _lib.call(_mobius_scan_bwd_op, dlam.contiguous(), A, B, C, D, lam0, lam)
     return dA, dB, dC, (dD if ctx.has_d else None), (dlam0 if ctx.has_l0 else None)
 
 
@@ -156,7 +156,7 @@ def mobius_scan(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, D: Optional[t
     A, B, C = (t.to(_F32).contiguous() for t in (A, B, C))
     D = None if D is None else D.to(_F32).contiguous()
     lam0 = None if lam0 is None else lam0.to(_F32).contiguous()
-    return _mobius_scan_op(A, B, C, D, lam0)
+    return _lib.call(_mobius_scan_op, A, B, C, D, lam0)
 
 
 # =================================================================== affine
@@ -170,7 +170,7 @@ def _io_dtype(t: torch.Tensor) -> int:
     raise TypeError(f"affine scan I/O must be float32 or bfloat16, got {t.dtype}")
 
 
-@torch.library.custom_op("kla_hip::affine_scan", mutates_args=())
+@_lib.hip_op("kla_hip::affine_scan")
 def _affine_scan_op(g: torch.Tensor, u: torch.Tensor, h0: Optional[torch.Tensor]) -> torch.Tensor:
     dev = _require_device(g, u, h0)
     _check_seq((("g", g), ("u", u)), g, g.dtype)
@@ -192,7 +192,7 @@ def _(g, u, h0):
     return torch.empty_like(g)
 
 
-@torch.library.custom_op("kla_hip::affine_scan_backward", mutates_args=())
+@_lib.hip_op("kla_hip::affine_scan_backward")
 def _affine_scan_bwd_op(dh: torch.Tensor, g: torch.Tensor, h: torch.Tensor, h0: Optional[torch.Tensor]
                         ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Returns (dg, du, dh0); dh0 is empty when h0 is None."""
@@ -227,7 +227,7 @@ def _affine_setup(ctx, inputs, output):
 
 def _affine_backward(ctx, dh):
     g, h0, h = ctx.saved_tensors
-    dg, du, dh0 = _affine_scan_bwd_op(dh.to(g.dtype).contiguous(), g, h, h0)
+    dg, du, dh0 = _lib.call(_affine_scan_bwd_op, dh.to(g.dtype).contiguous(), g, h, h0)
     return dg, du, (dh0 if ctx.has_h0 else None)
 
 
@@ -245,4 +245,4 @@ def affine_scan(g: torch.Tensor, u: torch.Tensor, h0: Optional[torch.Tensor] = N
         g, u = g.to(_F32), u.to(_F32)
     g, u = g.contiguous(), u.contiguous()
     h0 = None if h0 is None else h0.to(_F32).contiguous()
-    return _affine_scan_op(g, u, h0)
+    return _lib.call(_affine_scan_op, g, u, h0)

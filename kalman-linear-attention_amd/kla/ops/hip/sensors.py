@@ -23,7 +23,7 @@ def _code(t: torch.Tensor) -> int:
     return _lib.KLA_DTYPE_BF16 if t.dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32
 
 
-@torch.library.custom_op("kla_hip::qk_sensors", mutates_args=())
+@_lib.hip_op("kla_hip::qk_sensors")
 def _qk_op(k: torch.Tensor, q: torch.Tensor, norm: bool, has_clip: bool,
            clip: float) -> tuple[torch.Tensor, torch.Tensor]:
     _require_device(k, q)
@@ -41,7 +41,7 @@ def _(k, q, norm, has_clip, clip):
     return k.new_empty(k.shape, dtype=torch.float32), q.new_empty(q.shape, dtype=torch.float32)
 
 
-@torch.library.custom_op("kla_hip::qk_sensors_backward", mutates_args=())
+@_lib.hip_op("kla_hip::qk_sensors_backward")
 def _qk_bwd_op(k: torch.Tensor, q: torch.Tensor, dyk: torch.Tensor, dyq: torch.Tensor, norm: bool, has_clip: bool,
                clip: float) -> tuple[torch.Tensor, torch.Tensor]:
     _require_device(k, q, dyk, dyq)
@@ -70,7 +70,7 @@ def _backward(ctx, dyk, dyq):
     k, q = ctx.saved_tensors
     dyk = torch.zeros(k.shape, dtype=torch.float32, device=k.device) if dyk is None else dyk.float().contiguous()
     dyq = torch.zeros(q.shape, dtype=torch.float32, device=q.device) if dyq is None else dyq.float().contiguous()
-    dk, dq = _qk_bwd_op(k, q, dyk, dyq, *ctx.cfg)
+    dk, dq = _lib.call(_qk_bwd_op, k, q, dyk, dyq, *ctx.cfg)
     return dk, dq, None, None, None
 
 
@@ -90,4 +90,4 @@ def qk_sensors_hip(k: torch.Tensor, q: torch.Tensor, *, norm: bool, clip: float 
         k = k.contiguous()
     if _sensor_rows(q) is None:
         q = q.contiguous()
-    return _qk_op(k, q, bool(norm), clip is not None, float(clip) if clip is not None else 0.0)
+    return _lib.call(_qk_op, k, q, bool(norm), clip is not None, float(clip) if clip is not None else 0.0)

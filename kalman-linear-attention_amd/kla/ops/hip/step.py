@@ -14,7 +14,7 @@ from kla.ops.hip.scans import _require_device
 _F32 = torch.float32
 
 
-@torch.library.custom_op("kla_hip::kla_step", mutates_args=())
+@_lib.hip_op("kla_hip::kla_step")
 def _step_op(v: torch.Tensor, lambda_v: torch.Tensor, k: torch.Tensor, q: torch.Tensor, a: torch.Tensor,
              p: torch.Tensor, lam: torch.Tensor, eta: torch.Tensor, decode_from_prior: bool
              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -65,4 +65,4 @@ def _(v, lambda_v, k, q, a, p, lam, eta, decode_from_prior):
 
 def kla_step_hip(v, lambda_v, k, q, a, p, lam, eta, decode_from_prior: bool = False):
     v, lambda_v, k, q, a, p, lam, eta = (t.to(_F32).contiguous() for t in (v, lambda_v, k, q, a, p, lam, eta))
-    return _step_op(v, lambda_v, k, q, a, p, lam, eta, bool(decode_from_prior))
+    return _lib.call(_step_op, v, lambda_v, k, q, a, p, lam, eta, bool(decode_from_prior))

@@ -35,7 +35,7 @@ def _code(dtype: torch.dtype) -> int:
     return _lib.KLA_DTYPE_BF16 if dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32
 
 
-@torch.library.custom_op("kla_hip::gate_skip", mutates_args=())
+@_lib.hip_op("kla_hip::gate_skip")
 def _tail_op(y: torch.Tensor, residual: Optional[torch.Tensor], gate: Optional[torch.Tensor],
              lambda_skip: Optional[torch.Tensor], activation: int, out_bf16: bool) -> torch.Tensor:
     """out [B, L, M] = (y + lambda_skip * residual) * act(gate), fp32 or (out_bf16) bf16."""
@@ -55,7 +55,7 @@ def _(y, residual, gate, lambda_skip, activation, out_bf16):
     return torch.empty_like(y, dtype=torch.bfloat16 if out_bf16 else torch.float32)
 
 
-@torch.library.custom_op("kla_hip::gate_skip_backward", mutates_args=())
+@_lib.hip_op("kla_hip::gate_skip_backward")
 def _tail_bwd_op(dout: torch.Tensor, y: torch.Tensor, residual: Optional[torch.Tensor], gate: Optional[torch.Tensor],
                  lambda_skip: Optional[torch.Tensor], activation: int, need_res: bool, need_gate: bool
                  ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -105,8 +105,8 @@ def _backward(ctx, dout):
     need_gate = has_gate and ctx.needs_input_grad[2]
     if dout.dtype not in (torch.float32, torch.bfloat16):
         dout = dout.float()
-    dy, dres, dgate, dlam = _tail_bwd_op(dout.contiguous(), y, residual, gate, lambda_skip, ctx.activation,
-                                         need_res, need_gate)
+    dy, dres, dgate, dlam = _lib.call(_tail_bwd_op, dout.contiguous(), y, residual, gate, lambda_skip,
+                                      ctx.activation, need_res, need_gate)
     return (dy, dres if need_res else None, dgate if need_gate else None,
             dlam if has_res and ctx.needs_input_grad[3] else None, None, None)
 
@@ -139,5 +139,5 @@ def gate_skip_hip(y: torch.Tensor, residual: Optional[torch.Tensor], gate: Optio
         lam = lam.float().contiguous()
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise TypeError(f"out_dtype must be float32 or bfloat16, got {out_dtype}")
-    return _tail_op(y.float().contiguous(), residual, gate, lam, ACTIVATIONS[activation],
-                    out_dtype == torch.bfloat16)
+    return _lib.call(_tail_op, y.float().contiguous(), residual, gate, lam, ACTIVATIONS[activation],
+                     out_dtype == torch.bfloat16)
