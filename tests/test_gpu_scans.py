@@ -140,25 +140,39 @@ def test_affine_fwd_bwd_matches_oracle(cuda, shape, with_h0):
         _close("dh0", hh0.grad, dh0)
 
 
-@pytest.mark.parametrize("shape", [(2, 65, 63), (2, 1000, 130), (1, 4096, 64)])
-def test_affine_bf16_io(cuda, shape):
+@pytest.mark.parametrize("with_h0", [False, True])
+@pytest.mark.parametrize("shape", [(2, 65, 63), (2, 1000, 130), (1, 4096, 64), (2, 1000, 128), (1, 4096, 256),
+                                   (3, 300, 2048)])
+def test_affine_bf16_io(cuda, shape, with_h0):
     """bf16 sequence I/O, fp32 accumulation: within rtol 2e-2 of the fp64 oracle run
     on the same (bf16-exact) inputs (atol 1e-5 for values that cancel to near
-    zero); outputs come back in bf16."""
+    zero); outputs come back in bf16. With an fp32 initial state h0 the backward's
+    step at time 0 takes h_{-1} = h0 unrounded (dg_0 = mu_0 h0) and dh0 comes back
+    fp32. Lanes that are a multiple of 4 run the 4-lanes-per-thread tile (time 0 in
+    a partial chunk at T = 300 and 1000, in a whole one at T = 4096), the others
+    the 1-lane tile."""
     from kla.ops.hip import affine_scan
 
     B, T, N = shape
+    _log(f"[affine bf16] shape={shape} h0={with_h0}")
     g, u, dh = affine_inputs(B, T, N, seed=7, dtype=torch.bfloat16)
+    h0 = torch.randn(B, N, generator=torch.Generator().manual_seed(8)) if with_h0 else None
     gg, uu = g.to(cuda).requires_grad_(True), u.to(cuda).requires_grad_(True)
-    h = affine_scan(gg, uu)
+    hh0 = h0.to(cuda).requires_grad_(True) if with_h0 else None
+    h = affine_scan(gg, uu, hh0)
     assert h.dtype == torch.bfloat16
     torch.autograd.backward(h, dh.to(cuda))
     assert gg.grad.dtype == torch.bfloat16 and uu.grad.dtype == torch.bfloat16
-    want = ref.affine_scan_fwd(g.float(), u.float())
+    want = ref.affine_scan_fwd(g.float(), u.float(), h0)
     _close("h", h, want, rtol=2e-2, atol=1e-5)
-    dg, du, _ = ref.affine_scan_bwd(dh.float(), g.float(), want)
+    dg, du, dh0 = ref.affine_scan_bwd(dh.float(), g.float(), want, h0)
     _close("dg", gg.grad, dg, rtol=2e-2, atol=1e-5)
     _close("du", uu.grad, du, rtol=2e-2, atol=1e-5)
+    if with_h0:
+        assert hh0.grad.dtype == torch.float32
+        _close("dh0", hh0.grad, dh0, rtol=2e-2, atol=1e-5)
+        # The step at time 0 multiplies by h0 itself: dg_0 / mu_0 = h0 to bf16 rounding.
+        _close("dg_0", gg.grad[:, 0], (uu.grad[:, 0].double().cpu() * h0.double()).numpy(), rtol=1e-2, atol=1e-5)
 
 
 @pytest.mark.parametrize("lanes", [64, 130, 2048])
