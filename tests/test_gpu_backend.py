@@ -401,7 +401,7 @@ def test_sequence_model_prefill_and_decode_on_hip(cuda):
 
 @pytest.mark.parametrize("decode_from_prior", [False, True])
 @pytest.mark.parametrize("shape", [(2, 16, 8), (3, 70, 5), (1, 9, 64), (4, 33, 1), (2, 5, 128), (3, 4, 256),
-                                   (2, 3, 150), (2, 3, 300), (1, 4, 520)])
+                                   (2, 3, 150), (2, 3, 300), (1, 4, 520), (2, 7, 16), (1, 5, 32), (2, 3, 24)])
 def test_step_kernel_matches_reference_step(cuda, decode_from_prior, shape):
     """kla_step(backend="hip") (one HIP kernel) against the reference's step
     formula evaluated in float64 (kla_ops.py:293-331, phi floored)."""
@@ -659,6 +659,13 @@ DECODE_CASES = {
     "no_gate_k2": (32, dict(d_state=16, use_gating=False, conv_kernel_size=2)),
     "wide_state_128": (24, dict(d_state=128)),
     "wide_state_200_prior": (16, dict(d_state=200, decode_from_prior=True, return_variance=True, qk_norm=True)),
+    # the remaining compiled (lanes, prior) pairs of the one-token kernel
+    "prior_16": (32, dict(d_state=16, decode_from_prior=True)),
+    "state_32": (24, dict(d_state=32)),
+    "prior_state_32": (24, dict(d_state=27, decode_from_prior=True, return_variance=True)),
+    "prior_state_64": (16, dict(d_state=64, decode_from_prior=True)),
+    "prior_state_128": (16, dict(d_state=100, decode_from_prior=True)),
+    "state_256": (16, dict(d_state=256)),
 }
 
 
@@ -760,7 +767,7 @@ def _conv_reference(x, state, weight, bias, act):
     return get_activation(act)(y).transpose(1, 2), pad[..., pad.shape[-1] - (K - 1):]
 
 
-@pytest.mark.parametrize("K", [1, 2, 4, 7])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("L", [1, 3, 64, 65, 200])
 @pytest.mark.parametrize("act", ["silu", "gelu", "relu"])
 def test_causal_conv_matches_float64_autograd(cuda, K, L, act):
@@ -791,10 +798,14 @@ def test_causal_conv_matches_float64_autograd(cuda, K, L, act):
             check(name, got.grad, want.grad.numpy())
 
 
-def test_causal_conv_without_state_or_bias_and_bf16(cuda):
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 6, 7, 8])
+def test_causal_conv_without_state_or_bias_and_bf16(cuda, K):
+    """No state, no bias: fp32 against float64, and bf16 I/O (every compiled
+    width) within bf16 rounding of the float64 reference, with a finite bf16
+    input gradient."""
     from kla.ops.hip.conv import causal_conv_hip
 
-    B, L, D, K = 3, 130, 64, 4
+    B, L, D = 3, 130, 64
     g = torch.Generator().manual_seed(9)
     x = torch.randn(B, L, D, generator=g)
     weight = torch.randn(D, K, generator=g) * 0.5
@@ -802,7 +813,9 @@ def test_causal_conv_without_state_or_bias_and_bf16(cuda):
                                    "silu")
     y, s_new = causal_conv_hip(x.to(cuda), None, weight.to(cuda), None, "silu")
     check("y", y, y_ref.numpy())
-    check("new_state", s_new, s_ref.numpy())
+    assert s_new.shape == (B, D, K - 1)
+    if K > 1:
+        check("new_state", s_new, s_ref.numpy())
     # bf16 I/O against the float64 reference of the same (bf16-exact) inputs: rtol 2e-2.
     xb = x.to(torch.bfloat16)
     wb = weight.to(torch.bfloat16).float()
@@ -813,6 +826,60 @@ def test_causal_conv_without_state_or_bias_and_bf16(cuda):
     check("y_bf16", y, y_ref.numpy(), rtol=2e-2, atol=1e-2)
     y.float().sum().backward()
     assert xg.grad.dtype == torch.bfloat16 and torch.isfinite(xg.grad.float()).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_causal_conv_empty_sequence(cuda, dtype):
+    """L = 0 (a prefill chunk with no tokens): y is empty, the state passes
+    through unchanged, and the backward hands the new state's gradient to the
+    old state with zero weight and bias gradients."""
+    from kla.ops.hip.conv import causal_conv_hip
+
+    B, D, K = 2, 40, 4
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(B, 0, D, generator=g).to(dtype).to(cuda).requires_grad_(True)
+    st = torch.randn(B, D, K - 1, generator=g).to(dtype).to(cuda).requires_grad_(True)
+    w = torch.randn(D, K, generator=g).to(cuda).requires_grad_(True)
+    b = torch.randn(D, generator=g).to(cuda).requires_grad_(True)
+    y, new_state = causal_conv_hip(x, st, w, b, "silu")
+    assert y.shape == (B, 0, D) and y.dtype == dtype
+    assert torch.equal(new_state, st.detach())
+    r = torch.randn(B, D, K - 1, generator=g).to(dtype).to(cuda)
+    (new_state.float() * r.float()).sum().backward()
+    assert torch.equal(st.grad, r)
+    assert not w.grad.any() and not b.grad.any()
+    assert x.grad is None or x.grad.numel() == 0
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("aligned", [True, False])
+@pytest.mark.parametrize("k", [96, 2000])
+def test_rows_linear_conv_variants(cuda, norm, aligned, k):
+    """The conv epilogue with and without the RMSNorm prologue, 16-byte aligned and
+    unaligned input rows, and a k range one pass covers (96) or not (2000):
+    against the product alone (rows_linear_hip of the same operands) followed
+    by the conv step kernel."""
+    from kla.ops.hip.decode import conv_step_hip
+    from kla.ops.hip.model_ops import rows_linear_conv_hip, rows_linear_hip
+
+    g = torch.Generator().manual_seed(k + 3 * norm + aligned)
+    rows, D, K = 5, 40, 4
+    ld = (k + 3) // 4 * 4 + 4
+    xb = torch.randn(rows, ld, generator=g).to(cuda)
+    off = 0 if aligned else 1
+    x = xb[:, off:off + k]
+    w = (torch.randn(2 * D, k, generator=g) / k ** 0.5).to(cuda)
+    gw = (torch.rand(k, generator=g) + 0.5).to(cuda) if norm else None
+    cw = torch.randn(D, K, generator=g).to(cuda)
+    cb = torch.randn(D, generator=g).to(cuda)
+    win = torch.randn(rows, D, K - 1, generator=g).to(cuda)
+    y, new_win = rows_linear_conv_hip(x, w, None, norm_weight=gw, eps=1e-5, conv_weight=cw, conv_bias=cb,
+                                      window=win, activation="silu")
+    a = rows_linear_hip(x, w, norm_weight=gw, eps=1e-5)
+    zs, want_win = conv_step_hip(a[:, :D], win.clone(), cw, cb, "silu")
+    check(f"conv k={k} norm={norm} aligned={aligned}", y[:, :D], zs.cpu().numpy(), rtol=2e-6, atol=2e-6)
+    assert torch.equal(y[:, D:], a[:, D:])
+    assert torch.equal(new_win, want_win)
 
 
 def test_layer_conv_on_hip_matches_torch_conv(cuda):
@@ -1205,6 +1272,7 @@ def test_sequence_model_inference_kernels_match_torch(cuda):
 @pytest.mark.parametrize("epilogue", ["plain", "residual", "swiglu"])
 @pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("rows,k,n", [(16, 512, 2048), (5, 1365, 512), (17, 64, 50), (1, 7, 3), (40, 1024, 1056),
+                                      (3, 500, 16500),
                                       (3, 2048, 33)])
 @pytest.mark.parametrize("aligned_x", [True, False])
 def test_rows_linear_matches_float64(cuda, epilogue, norm, rows, k, n, aligned_x):
@@ -1430,7 +1498,7 @@ def test_discretize_matches_float64_autograd(cuda, discretization, zero_pn, clip
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("S", [16, 7, 64])
+@pytest.mark.parametrize("S", [16, 7, 64, 32, 24])
 @pytest.mark.parametrize("norm,clip", [(True, None), (True, 0.3), (False, 0.5)])
 def test_qk_sensors_match_torch(cuda, dtype, S, norm, clip):
     """qk_sensors_hip (l2 norm over S, clip, .float()) on column views of a wider

@@ -63,11 +63,12 @@ def test_fused_backward_is_bitwise_repeatable(cuda, shape):
             assert torch.equal(a, b), name
 
 
-@pytest.mark.parametrize("S", [4, 16, 64, 128, 256])
+@pytest.mark.parametrize("S", [1, 2, 4, 8, 16, 32, 64, 128, 256])
 def test_reduce_kernels_give_identical_sums(cuda, S):
     """dk and dq through the wave reduce (16-byte aligned outputs) and through the
     LDS reduce (outputs at a 4-byte offset) are bit-identical, with B * L >= 256
-    rows and several channel groups."""
+    rows and several channel groups (1 and 2 lanes take the LDS reduce either
+    way: every compiled width runs)."""
     from kla.ops.hip import _lib
     from kla.ops.hip.fused import _fused_fwd_op
 
