@@ -193,16 +193,19 @@ def hip_op(name: str):
     return wrap
 
 
+_PLAIN = (torch.Tensor, torch.nn.Parameter)
+
+
 def call(op, *args):
     """``op(*args)``, run without the dispatcher where it adds nothing: outside
-    torch.compile / export tracing, every tensor argument a plain tensor (no fake
-    or other subclass), and no autograd to record (grad mode off, or no tensor
-    argument requires grad). The same function runs either way."""
+    torch.compile / export tracing, every tensor argument a plain tensor or
+    parameter (no fake or other subclass), and no autograd to record (grad mode
+    off, or no tensor argument requires grad). The same function runs either way."""
     if torch.compiler.is_compiling():
         return op(*args)
     grad = torch.is_grad_enabled()
     for a in args:
-        if isinstance(a, torch.Tensor) and (type(a) is not torch.Tensor or (grad and a.requires_grad)):
+        if isinstance(a, torch.Tensor) and (type(a) not in _PLAIN or (grad and a.requires_grad)):
             return op(*args)
     return op.direct(*args)
 

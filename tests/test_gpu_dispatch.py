@@ -65,6 +65,20 @@ def test_direct_call_equals_dispatched_call(cuda):
     xx = x.clone().requires_grad_(True)
     y, _ = _lib.call(conv._conv_op, xx, None, w, bias, 1)
     assert y.grad_fn is not None
+    # Parameters count as plain tensors: under no_grad a module's weights take the
+    # direct path too (no autograd node, the same values).
+    pw = torch.nn.Parameter(w.clone())
+    calls = []
+    direct = conv._conv_op.direct
+    conv._conv_op.direct = lambda *a: calls.append(1) or direct(*a)
+    try:
+        with torch.no_grad():
+            y2, _ = _lib.call(conv._conv_op, x, None, pw, bias, 1)
+    finally:
+        conv._conv_op.direct = direct
+    assert calls == [1] and y2.grad_fn is None
+    with torch.no_grad():
+        _same(y2, conv._conv_op(x, None, w, bias, 1)[0])
 
 
 def test_ops_trace_under_torch_compile(cuda):
