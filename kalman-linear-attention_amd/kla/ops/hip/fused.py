@@ -207,7 +207,8 @@ def _fwd_one(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save, dev, 
     lam_fin = v.new_empty(B, M, S)
     eta_fin = v.new_empty(B, M, S)
     if B * M * S == 0:
-        return y, y_var, lam_fin, eta_fin
+        # No lanes: the read-outs sum over no state lanes (zero where B, L, M leave entries).
+        return y.zero_(), y_var.zero_(), lam_fin, eta_fin
     cus = _cus(dev.index or 0)
     nc = train_chunks(B, L, M, S, cus) if save else time_chunks(B, L, M, S, cus)
     if nc > 1:
@@ -272,7 +273,10 @@ def _bwd_one(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck
     dk, dq = torch.empty_like(k), torch.empty_like(q)
     da, dp = torch.empty_like(a), torch.empty_like(p)
     dlam0, deta0 = v.new_empty(B, M, S), v.new_empty(B, M, S)
-    if M * S == 0:
+    if B * M * S == 0:
+        # No lanes: every gradient with entries (dk, dq over no channels, da, dp over no batch rows) is zero.
+        for t in (dv, dlv, dk, dq, da, dp):
+            t.zero_()
         return dv, dlv, dk, dq, da, dp, dlam0, deta0
     pt = _lib.ptr
 
@@ -436,7 +440,8 @@ def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torc
     ck_lam = torch.empty(B, n_ck, M, S, **f32) if save else torch.empty(0, **f32)
     ck_eta = torch.empty(B, n_ck, M, S, **f32) if save else torch.empty(0, **f32)
     if B * M * S == 0:
-        return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
+        # No lanes: the read-outs sum over no state lanes (zero where B, L, M leave entries).
+        return y.zero_(), y_var.zero_(), lam_fin, eta_fin, ck_lam, ck_eta
     sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
     cus = _cus(dev.index or 0)
     nc = train_chunks(B, L, M, S, cus) if save else time_chunks(B, L, M, S, cus)
@@ -485,7 +490,10 @@ def _sensors_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: 
     dk, dq = torch.empty_like(k), torch.empty_like(q)
     da, dp = torch.empty_like(a), torch.empty_like(p)
     dlam0, deta0 = k.new_empty(B, M, S), k.new_empty(B, M, S)
-    if M * S == 0:
+    if B * M * S == 0:
+        # No lanes: every gradient with entries (dk, dq over no channels, da, dp over no batch rows) is zero.
+        for t in (dv, dobs, dk, dq, da, dp):
+            t.zero_()
         return dv, dobs, dk, dq, da, dp, dlam0, deta0
     sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
     pt = _lib.ptr

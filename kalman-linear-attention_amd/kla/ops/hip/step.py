@@ -50,7 +50,7 @@ def _step_one(v, lambda_v, k, q, a, p, lam, eta, decode_from_prior, dev):
     y, y_var = v.new_empty(B, M), v.new_empty(B, M)
     lam_out, eta_out = torch.empty_like(lam), torch.empty_like(eta)
     if B * M * S == 0:
-        return y, y_var, lam_out, eta_out
+        return y.zero_(), y_var.zero_(), lam_out, eta_out   # sums over no state lanes
     pt = _lib.ptr
     _lib.check("kla_step_fwd", _lib.lib().kla_step_fwd(
         pt(v), pt(lambda_v), pt(k), pt(q), pt(a), pt(p), pt(lam), pt(eta), pt(y), pt(y_var), pt(lam_out),

@@ -63,6 +63,10 @@ def kla_scan_hip(
         initial_state = init_state(Bn, M, S, device=v.device)
     lam0 = initial_state.lam.float().contiguous()
     eta0 = initial_state.eta.float().contiguous()
+    if L == 0:
+        # No steps: empty read-outs, and the state leaves as it came in.
+        empty = v.new_zeros(Bn, 0, M)
+        return empty, empty.clone(), KLAState(lam=lam0, eta=eta0)
 
     phi, r = _sufficient_stats(v, lambda_v, k)
     a_, p_ = _broadcast_ap(a.float(), p.float(), phi)
@@ -84,6 +88,4 @@ def kla_scan_hip(
         mean = a_ * mean
         var = a2 * var + p_
     y, y_var = _readout(mean, var, q)
-    if L == 0:
-        return y, y_var, KLAState(lam=lam0, eta=eta0)
     return y, y_var, KLAState(lam=lam[:, -1], eta=eta[:, -1])

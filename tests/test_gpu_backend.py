@@ -155,6 +155,35 @@ def test_forward_ragged_shapes(cuda, backend, shape):
 
 
 @pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("shape", [(2, 0, 3, 4), (0, 5, 3, 4), (2, 5, 0, 4), (2, 0, 3, 300), (1, 0, 2, 16),
+                                   (2, 5, 3, 0)])
+def test_empty_inputs(cuda, backend, shape):
+    """An empty batch, sequence or channel dimension: empty y and y_var, the final
+    state equal to the initial state (no steps taken), its gradient passed
+    straight back to the initial state, and zero gradients for every input a
+    gradient has entries for (dk, dq over no channels; da, dp over no batch rows
+    or steps). The reference's torch path raises here under autograd (its
+    associative scan rejects a zero-length dimension), so the expectation is
+    written out."""
+    B, L, M, S = shape
+    ins = make_inputs(B, L, M, S, seed=4)
+    st = random_state(B, M, S)
+    g = torch.Generator().manual_seed(6)
+    wl, we = torch.randn(B, M, S, generator=g), torch.randn(B, M, S, generator=g)
+    xs = [t.to(cuda).requires_grad_(True) for t in ins + (st.lam, st.eta)]
+    y, y_var, fin = kla_scan(*xs[:6], backend=backend, initial_state=KLAState(xs[6], xs[7]))
+    assert y.shape == y_var.shape == (B, L, M) and fin.lam.shape == fin.eta.shape == (B, M, S)
+    assert not y.any() and not y_var.any()   # empty, or sums over no state lanes (S = 0)
+    assert torch.equal(fin.lam, xs[6].detach()) and torch.equal(fin.eta, xs[7].detach())
+    loss = y.sum() + y_var.sum() + (wl.to(cuda) * fin.lam).sum() + (we.to(cuda) * fin.eta).sum()
+    loss.backward()
+    grads = [torch.zeros_like(x) if x.grad is None else x.grad for x in xs]
+    for name, got, x in zip(("dv", "dlambda_v", "dk", "dq", "da", "dp"), grads[:6], xs[:6]):
+        assert got.shape == x.shape and not got.any(), name   # also with S = 0: y does not depend on v
+    assert torch.equal(grads[6], wl.to(cuda)) and torch.equal(grads[7], we.to(cuda))
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
 def test_chunked_state_carry(cuda, backend):
     """Reference tests/test_backends.py:269-288: two halves with the carried state = one scan."""
     v, lv, k, q, a, p = (t.to(cuda) for t in make_inputs())
