@@ -160,6 +160,15 @@ def _f32(t: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
     return None if t is None else t.to(_F32).contiguous()
 
 
+def _dynamics(a: torch.Tensor, p: torch.Tensor, M: int, S: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """a, p as dense fp32 [M, S]: the reference's torch path takes any shape that
+    broadcasts to [M, S] (kla_ops.py:181-185 views them as [1, 1, *shape]); the
+    gradient flows back through the expansion."""
+    if a.dim() > 2 or p.dim() > 2:
+        raise ValueError(f"a and p must broadcast to [M, S] = [{M}, {S}]; got {tuple(a.shape)}, {tuple(p.shape)}")
+    return _f32(a.expand(M, S)), _f32(p.expand(M, S))
+
+
 def _check(v, lambda_v, k, q, a, p, lam0, eta0, max_state: Optional[int] = MAX_STATE):
     if v.dim() != 3 or k.dim() != 3:
         raise ValueError(f"v must be [B, L, M] and k [B, L, S]; got {tuple(v.shape)} and {tuple(k.shape)}")
@@ -373,7 +382,8 @@ def kla_scan_fused(v, lambda_v, k, q, a, p, lam0=None, eta0=None, decode_from_pr
     compute in float32 too). Checkpoints for the backward are kept only when a
     gradient can be required.
     """
-    v, lambda_v, k, q, a, p, lam0, eta0 = (_f32(t) for t in (v, lambda_v, k, q, a, p, lam0, eta0))
+    a, p = _dynamics(a, p, v.shape[-1], k.shape[-1])
+    v, lambda_v, k, q, lam0, eta0 = (_f32(t) for t in (v, lambda_v, k, q, lam0, eta0))
     save = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (v, lambda_v, k, q, a, p, lam0, eta0))
     y, y_var, lam_fin, eta_fin, _, _ = _lib.call(_fused_fwd_op, v, lambda_v, k, q, a, p, lam0, eta0,
@@ -573,7 +583,8 @@ def kla_scan_fused_sensors(v, obs, k, q, a, p, lam0=None, eta0=None, *, log_var:
         v = v.contiguous()
     if _sensor_rows(obs) is None:
         obs = obs.contiguous()
-    k, q, a, p, lam0, eta0 = (_f32(t) for t in (k, q, a, p, lam0, eta0))
+    a, p = _dynamics(a, p, v.shape[-1], k.shape[-1])
+    k, q, lam0, eta0 = (_f32(t) for t in (k, q, lam0, eta0))
     save = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (v, obs, k, q, a, p, lam0, eta0))
     ov_max = math.inf if obs_var_max is None else float(obs_var_max)

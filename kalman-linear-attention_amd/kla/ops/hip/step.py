@@ -64,5 +64,7 @@ def _(v, lambda_v, k, q, a, p, lam, eta, decode_from_prior):
 
 
 def kla_step_hip(v, lambda_v, k, q, a, p, lam, eta, decode_from_prior: bool = False):
+    # a, p: any shape that broadcasts to [M, S], as the torch formula takes them.
+    a, p = a.expand(v.shape[-1], k.shape[-1]), p.expand(v.shape[-1], k.shape[-1])
     v, lambda_v, k, q, a, p, lam, eta = (t.to(_F32).contiguous() for t in (v, lambda_v, k, q, a, p, lam, eta))
     return _lib.call(_step_op, v, lambda_v, k, q, a, p, lam, eta, bool(decode_from_prior))

@@ -184,6 +184,44 @@ def test_empty_inputs(cuda, backend, shape):
 
 
 @pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("a_shape,p_shape", [((1, 8), (16, 1)), ((8,), (1, 1)), ((16, 1), (8,))])
+def test_dynamics_broadcast_like_the_torch_path(cuda, backend, a_shape, p_shape):
+    """a and p of any shape that broadcasts to [M, S] (the reference's torch path
+    views them as [1, 1, *shape]): the same outputs as with a, p expanded to
+    [M, S], and their gradients are the expanded gradients summed over the
+    broadcast dimensions; kla_step on hip takes them the same way."""
+    from kla.ops import kla_step
+
+    B, L, M, S = 2, 30, 16, 8
+    v, lv, k, q, _, _ = make_inputs(B, L, M, S, seed=12)
+    g = torch.Generator().manual_seed(13)
+    a_small = torch.rand(*a_shape, generator=g) * 0.5 + 0.45
+    p_small = torch.rand(*p_shape, generator=g) * 0.05 + 0.01
+    st = random_state(B, M, S)
+    outs = []
+    for expanded in (False, True):
+        a = (a_small.expand(M, S).contiguous() if expanded else a_small).to(cuda).requires_grad_(True)
+        p = (p_small.expand(M, S).contiguous() if expanded else p_small).to(cuda).requires_grad_(True)
+        y, y_var, fin = kla_scan(*(t.to(cuda) for t in (v, lv, k, q)), a, p, backend=backend,
+                                 initial_state=KLAState(st.lam.to(cuda), st.eta.to(cuda)))
+        (y.sum() + y_var.square().sum() + fin.lam.sum()).backward()
+        outs.append((y.detach(), y_var.detach(), fin.lam, fin.eta, a.grad, p.grad))
+    for name, x, e in zip(("y", "y_var", "lam", "eta"), outs[0][:4], outs[1][:4]):
+        torch.testing.assert_close(x, e, rtol=1e-6, atol=1e-7, msg=name)
+    da, dp = outs[0][4], outs[0][5]
+    assert da.shape == a_small.shape and dp.shape == p_small.shape
+    torch.testing.assert_close(da, outs[1][4].sum_to_size(a_small.shape), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(dp, outs[1][5].sum_to_size(p_small.shape), rtol=1e-5, atol=1e-5)
+    with torch.no_grad():
+        args = [t[:, 0].to(cuda) for t in (v, lv, k, q)]
+        state = KLAState(st.lam.to(cuda), st.eta.to(cuda))
+        got = kla_step(*args, a_small.to(cuda), p_small.to(cuda), state, backend="hip")
+        want = kla_step(*args, a_small.expand(M, S).to(cuda), p_small.expand(M, S).to(cuda), state, backend="hip")
+    for x, e in zip((got[0], got[1], got[2].lam, got[2].eta), (want[0], want[1], want[2].lam, want[2].eta)):
+        assert torch.equal(x, e)
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
 def test_chunked_state_carry(cuda, backend):
     """Reference tests/test_backends.py:269-288: two halves with the carried state = one scan."""
     v, lv, k, q, a, p = (t.to(cuda) for t in make_inputs())
