@@ -222,6 +222,36 @@ def test_dynamics_broadcast_like_the_torch_path(cuda, backend, a_shape, p_shape)
 
 
 @pytest.mark.parametrize("backend", BACKENDS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float64])
+def test_input_dtypes_and_strided_views(cuda, backend, dtype):
+    """Inputs of another float dtype, passed as non-contiguous views: the scan
+    computes in float32 on the values the inputs hold (the reference's GPU
+    backends are float32-only) and returns float32 outputs equal to a run on those
+    values as contiguous float32; each input's gradient comes back in its own
+    dtype and equals the float32 run's gradient cast to it."""
+    B, L, M, S = 2, 40, 12, 8
+    ins = [t.to(dtype) for t in make_inputs(B, L, M, S, seed=14)]
+    # Non-contiguous views of the same values: v, lambda_v via a transpose, k, q via a slice.
+    views = [ins[0].transpose(1, 2).contiguous().transpose(1, 2), ins[1].transpose(1, 2).contiguous().transpose(1, 2),
+             torch.cat([ins[2], ins[2]], -1)[..., :S], torch.cat([ins[3], ins[3]], -1)[..., S:], ins[4].t().contiguous().t(),
+             ins[5]]
+    assert not views[0].is_contiguous() and not views[2].is_contiguous()
+    runs = []
+    for xs in ([t.to(cuda) for t in views], [t.float().contiguous().to(cuda) for t in ins]):
+        xs = [t.detach().requires_grad_(True) for t in xs]
+        y, y_var, fin = kla_scan(*xs, backend=backend)
+        assert y.dtype == y_var.dtype == fin.lam.dtype == torch.float32
+        (y.sum() + y_var.sum() + fin.lam.sum() + fin.eta.sum()).backward()
+        runs.append([y.detach(), y_var.detach(), fin.lam.detach(), fin.eta.detach()] + [x.grad for x in xs])
+    for i, (got, want) in enumerate(zip(*runs)):
+        if i < 4:
+            torch.testing.assert_close(got, want, rtol=1e-6, atol=1e-7)
+        else:
+            assert got.dtype == dtype
+            torch.testing.assert_close(got, want.to(dtype), rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("backend", BACKENDS)
 def test_chunked_state_carry(cuda, backend):
     """Reference tests/test_backends.py:269-288: two halves with the carried state = one scan."""
     v, lv, k, q, a, p = (t.to(cuda) for t in make_inputs())
