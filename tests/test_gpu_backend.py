@@ -79,7 +79,7 @@ def check_scan(name, got, want):
     want = np.asarray(want, dtype=np.float64).reshape(got.shape)
     assert np.isfinite(got).all(), f"{name}: non-finite values"
     err = np.abs(got - want)
-    atol = ATOL * max(float(np.abs(want).max()), 1e-30) if name in CONTRACTIONS else ATOL
+    atol = ATOL * max(float(np.abs(want).max()) if want.size else 0.0, 1e-30) if name in CONTRACTIONS else ATOL
     worst = float((err / (atol + RTOL * np.abs(want))).max()) if err.size else 0.0
     lit, share = literal_ratio(got, want)
     kind = "atol 1e-6*max|ref|" if name in CONTRACTIONS else "atol 1e-6"
@@ -92,15 +92,21 @@ def check_scan(name, got, want):
     assert worst <= 1.0, f"{name}: outside rtol={RTOL}, {kind} (ratio {worst:.3f})"
 
 
+def scaled_ratio(got, want, rtol, atol):
+    """max |got - want| / (atol * max|want| + rtol * |want|): at most 1 within the bar."""
+    got = got.detach().double().cpu().numpy() if isinstance(got, torch.Tensor) else np.asarray(got, np.float64)
+    want = np.asarray(want, dtype=np.float64).reshape(got.shape)
+    assert np.isfinite(got).all(), "non-finite values"
+    if not want.size:
+        return 0.0
+    scale = max(float(np.abs(want).max()), 1e-30)
+    return float((np.abs(got - want) / (atol * scale + rtol * np.abs(want))).max())
+
+
 def check(name, got, want, rtol=RTOL, atol=ATOL):
     """Tolerance relative to the tensor's scale (atol * max|want|), for the layer
     kernels checked against torch's own operations at their own tolerances."""
-    got = got.detach().double().cpu().numpy()
-    want = np.asarray(want, dtype=np.float64).reshape(got.shape)
-    assert np.isfinite(got).all(), f"{name}: non-finite values"
-    scale = max(float(np.abs(want).max()), 1e-30)
-    err = np.abs(got - want)
-    worst = float((err / (atol * scale + rtol * np.abs(want))).max()) if err.size else 0.0
+    worst = scaled_ratio(got, want, rtol, atol)
     print(f"  {name:10s} worst |d|/(atol*scale + rtol|ref|) = {worst:.3f}", flush=True)
     assert worst <= 1.0, f"{name}: outside rtol={rtol} atol={atol} (ratio {worst:.3f})"
 
@@ -421,6 +427,76 @@ GOLDEN_CASES = {
 
 def _first(y):
     return y[0] if isinstance(y, tuple) else y
+
+
+def _random_layer(seed):
+    """(d_model, KLAConfig kwargs) drawn over the layer's option space."""
+    import random
+
+    r = random.Random(seed)
+    value_rank = r.choice(["full", "dt", "conv", 3])
+    kw = dict(d_state=r.choice([1, 3, 5, 8, 16, 24, 33, 64, 100]), expand=r.choice([1.0, 1.5, 2.0]),
+              discretization=r.choice(["ou", "zoh"]), zero_process_noise=r.random() < 0.2,
+              obs_var_max=r.choice([None, 2.0]), value_rank=value_rank, var_rank=r.choice(["full", "dt", 4]),
+              qk_norm=r.random() < 0.7, bias=r.random() < 0.5,
+              use_conv=value_rank == "conv" or r.random() < 0.8, conv_kernel_size=r.randint(1, 8),
+              conv_activation=r.choice(["silu", "relu", "gelu"]), use_gating=r.random() < 0.7,
+              gating_activation=r.choice(["silu", "gelu", "relu"]), use_lambda_skip=r.random() < 0.7,
+              lambda_skip_mode=r.choice(["scalar", "vector"]), return_variance=r.random() < 0.4,
+              decode_from_prior=r.random() < 0.3, clip_value=r.choice([None, 0.5]))
+    return r.choice([17, 24, 32, 45]), kw
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_layer_configs_match_torch_backend(cuda, seed):
+    """A KLALayer with a randomly drawn configuration (odd widths, every sensor
+    rank, conv width and activation, gate, skip, variance and prior option) on hip
+    against the same weights evaluated in float64 on the CPU (backend torch): the
+    forward output (and y_var) and the input gradient at rtol 2e-5 / atol 2e-6 of
+    each tensor's scale, every parameter gradient at atol 1e-5 (sums over all
+    tokens: on the draw with d_state 1 and a full-rank variance projection the
+    torch backend's own fp32 run misses float64 by 1.5e-5 of scale there); then a
+    stateful prefill split in two chunks on hip against one chunk."""
+    import copy
+
+    d_model, kw = _random_layer(seed)
+    print(f"[layer config] d_model={d_model} {kw}", flush=True)
+    torch.manual_seed(seed)
+    hip = KLALayer(d_model, KLAConfig(**kw, backend="hip")).to(cuda)
+    ref = copy.deepcopy(hip).double().cpu()
+    ref.config = KLAConfig(**kw, backend="torch")
+    x = torch.randn(2, 29, d_model, generator=torch.Generator().manual_seed(seed + 100))
+    outs = []
+    for layer, xin in ((hip, x.to(cuda)), (ref, x.double())):
+        xx = xin.clone().requires_grad_(True)
+        out = layer(xx)
+        y, y_var = out if isinstance(out, tuple) else (out, None)
+        loss = (y * torch.linspace(-1, 1, y.shape[-1], device=y.device, dtype=y.dtype)).sum()
+        if y_var is not None:
+            loss = loss + 0.1 * y_var.sum()
+        loss.backward()
+        outs.append([y.detach(), xx.grad] + ([y_var.detach()] if y_var is not None else [])
+                    + [p.grad if p.grad is not None else torch.zeros_like(p) for p in layer.parameters()])
+    names = ["y", "dx"] + (["y_var"] if kw["return_variance"] else []) + [n for n, _ in hip.named_parameters()]
+    n_params = len(list(hip.parameters()))
+    assert len(outs[0]) == len(outs[1]) == len(names)
+    for i, (name, a, b) in enumerate(zip(names, *outs)):
+        assert a is not None and b is not None, f"{name}: no gradient (hip {a is None}, float64 {b is None})"
+        check(name, a, b.numpy(), rtol=2e-5, atol=2e-6 if i < len(names) - n_params else 1e-5)
+    xc = x.to(cuda)
+    with torch.no_grad():
+        hip.eval()
+        whole, st_whole = hip(xc, return_state=True)
+        first, st = hip(xc[:, :13], return_state=True)
+        second, st2 = hip(xc[:, 13:], state=st, return_state=True)
+    w = whole[0] if isinstance(whole, tuple) else whole
+    f = torch.cat([(first[0] if isinstance(first, tuple) else first),
+                   (second[0] if isinstance(second, tuple) else second)], dim=1)
+    check("chunked", f, w.cpu().numpy(), rtol=2e-5, atol=2e-6)
+    for a, b in zip(torch.utils._pytree.tree_leaves(st2), torch.utils._pytree.tree_leaves(st_whole)):
+        assert (a is None) == (b is None)   # parts a config does not carry (no conv: no window)
+        if a is not None:
+            check("state", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
 
 
 @pytest.mark.parametrize("tag", sorted(GOLDEN_CASES))
