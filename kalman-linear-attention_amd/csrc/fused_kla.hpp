@@ -679,17 +679,30 @@ __global__ void __launch_bounds__(kFusedThreads)
           prm.ck_eta[ck_off + (th / kCkpt) * ck_stride] = eta;
         }
         if (th + kCkpt <= L) {
-          // The whole half lies inside the sequence: no per-step bound.
+          // The whole half lies inside the sequence: no per-step bound. Four-step
+          // LDS reads are issued two steps ahead of their first step.
+          float4 nl4{}, nv4{}, nk4{}, nk24{}, nq4{};
+          auto read4 = [&](int jb, float4 &l, float4 &v, float4 &k, float4 &k2, float4 &q) {
+            asm volatile("" ::: "memory");
+            l = lds4(s_l[cur][c], jb);
+            v = lds4(s_sv[cur][c], jb);
+            k = lds4(s_k[KQB == 1 ? 0 : cur][ln.s], jb);
+            if constexpr (kK2) k2 = lds4(s_k2[kK2 && KQB == 2 ? cur : 0][kK2 ? ln.s : 0], jb);
+            q = lds4(s_q[KQB == 1 ? 0 : cur][ln.s], jb);
+            asm volatile("" ::: "memory");
+          };
+          if (kVecLds) read4(h * kCkpt, l4, v4, k4, k24, q4);
 #pragma unroll
           for (int j = 0; j < kCkpt; ++j) {
             const int jb = h * kCkpt + j;
-            if (kVecLds && jb % 4 == 0) {
-              l4 = lds4(s_l[cur][c], jb);
-              v4 = lds4(s_sv[cur][c], jb);
-              k4 = lds4(s_k[KQB == 1 ? 0 : cur][ln.s], jb);
-              if constexpr (kK2) k24 = lds4(s_k2[kK2 && KQB == 2 ? cur : 0][kK2 ? ln.s : 0], jb);
-              q4 = lds4(s_q[KQB == 1 ? 0 : cur][ln.s], jb);
+            if (kVecLds && j % 4 == 0 && j > 0) {
+              l4 = nl4;
+              v4 = nv4;
+              k4 = nk4;
+              k24 = nk24;
+              q4 = nq4;
             }
+            if (kVecLds && j % 4 == 2 && j + 2 < kCkpt) read4(jb + 2, nl4, nv4, nk4, nk24, nq4);
             step(jb, j, kVecLds);
           }
         } else {
@@ -827,13 +840,17 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
     constexpr int64_t el = BF16 ? 2 : 4;
     void *dvb = static_cast<char *>(prm.dv) + (offM + t0 * M) * el;
     void *dlb = static_cast<char *>(prm.dlv) + (offM + t0 * M) * el;
-    lds_to_global_sensor<TB, CH, WPC, BF16, false>(s_dv[buf], s_l[buf], s_v[buf], nullptr, dvb, M, L - t0, cols_m);
+    // Every pointer argument is an LDS tile, also where a call does not read it:
+    // the two dLv calls share code after inlining, and a null among the pointers
+    // there would turn the LDS reads into flat loads, whose wait would cover the
+    // next block's tile loads still in flight.
+    lds_to_global_sensor<TB, CH, WPC, BF16, false>(s_dv[buf], s_l[buf], s_v[buf], s_lf[buf], dvb, M, L - t0, cols_m);
     if (sn.log_var)
       lds_to_global_sensor<TB, CH, WPC, BF16, true>(s_dl[buf], s_l[buf], s_v[buf], s_lf[buf], dlb, M, L - t0,
                                                     cols_m, s_dv[buf]);
     else
-      lds_to_global_sensor<TB, CH, WPC, BF16, false>(s_dl[buf], nullptr, s_v[buf], nullptr, dlb, M, L - t0, cols_m,
-                                                     s_dv[buf]);
+      lds_to_global_sensor<TB, CH, WPC, BF16, false>(s_dl[buf], s_l[buf], s_v[buf], s_lf[buf], dlb, M, L - t0,
+                                                     cols_m, s_dv[buf]);
     for (int i = tid; i < 2 * TB * SP; i += kFusedThreads) {
       const int which = i / (TB * SP);
       const int j = (i / SP) % TB;
@@ -850,8 +867,21 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
   };
 
   const int64_t n_ck = g.n_ck;
+  // The checkpoint entering a block is read one block ahead, with the block's
+  // tiles: a load issued just before the replay would make the replay wait for
+  // every load still in flight (memory counters retire in order), the next
+  // block's tiles included.
+  float ck_l = 1.0f, ck_e = 0.0f;
+  auto load_ck = [&](int64_t blk) {
+    if (ln.active) {
+      const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
+      ck_l = prm.ck_lam[ci];
+      ck_e = prm.ck_eta[ci];
+    }
+  };
   if (n_ck > 0) {
     load((n_ck - 1) * TB);
+    load_ck(n_ck - 1);
     stage(0);
   }
   __syncthreads();
@@ -859,7 +889,11 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
     const int cur = static_cast<int>(i & 1);
     const int64_t blk = n_ck - 1 - i;
     const int64_t t0 = blk * TB;
-    if (i + 1 < n_ck) load(t0 - TB);
+    const float lam_ck = ck_l, eta_ck = ck_e;
+    if (i + 1 < n_ck) {
+      load(t0 - TB);
+      load_ck(blk - 1);
+    }
     if (i > 0) {
       flush(blk + 1, cur ^ 1);
       if constexpr (RB == 1) __syncthreads();   // the flush has read s_red before the walk refills it
@@ -886,28 +920,38 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
     // and each step's lam_t) >= EPS. Then var = 1/lam_t has its plain derivative,
     // and lam' >= 0 makes a2 + p' lam' >= a2 >= EPS, so alpha's clamp is idle too.
     bool unclamped = true;
-    const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
     // The replay from the block's checkpoint. FULL: every step of the block lies
     // inside the sequence (all blocks but the sequence's last partial one), so
     // the steps need no bound and the block is one straight run of code.
     auto replay = [&](auto full_c) __attribute__((always_inline)) {
       constexpr bool FULL = decltype(full_c)::value;
-      float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
-      float eta = ln.active ? prm.ck_eta[ci] : 0.0f;
+      float lam = lam_ck;
+      float eta = eta_ck;
       unclamped = lam >= kEps;
-      float4 l4{}, v4{}, k4{}, k24{};
+      // Tile values of four steps per LDS read, issued two steps before the
+      // first of them (the last two values of the group in use are dead by
+      // then), so that less of the reads' latency is waited for. (Compiler
+      // barriers around the reads: hoisted further, they would hold more
+      // registers than two waves per SIMD allow.)
+      float4 l4{}, v4{}, k4{}, k24{}, nl4{}, nv4{}, nk4{}, nk24{};
+      auto read4 = [&](int j, float4 &l, float4 &v, float4 &k, float4 &k2) {
+        asm volatile("" ::: "memory");
+        l = lds4(s_l[cur][c], j);
+        v = lds4(s_sv[cur][c], j);
+        k = lds4(s_k[kb][ln.s], j);
+        if constexpr (kK2) k2 = lds4(s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0], j);
+        asm volatile("" ::: "memory");
+      };
+      if (kVecLds) read4(0, l4, v4, k4, k24);
 #pragma unroll
       for (int j = 0; j < TB; ++j) {
-        if (kVecLds && j % 4 == 0) {
-          // (A compiler barrier: the next four steps' LDS reads are not hoisted
-          // into earlier steps, which would hold more registers than two waves
-          // per SIMD allow.)
-          asm volatile("" ::: "memory");
-          l4 = lds4(s_l[cur][c], j);
-          v4 = lds4(s_sv[cur][c], j);
-          k4 = lds4(s_k[kb][ln.s], j);
-          if constexpr (kK2) k24 = lds4(s_k2[kK2 ? kb : 0][kK2 ? ln.s : 0], j);
+        if (kVecLds && j % 4 == 0 && j > 0) {
+          l4 = nl4;
+          v4 = nv4;
+          k4 = nk4;
+          k24 = nk24;
         }
+        if (kVecLds && j % 4 == 2 && j + 2 < TB) read4(j + 2, nl4, nv4, nk4, nk24);
         lh[j] = lam;
         eh[j] = eta;
         if (!FULL) idn[j] = 0.0f;
@@ -941,17 +985,28 @@ __global__ void __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per
 #pragma clang fp contract(off)
       constexpr bool CLAMPS = decltype(clamps_c)::value;
       constexpr bool FULL = decltype(full_c)::value;
-      float4 sv4{}, s24{}, dy4{}, k4{}, q4{};
+      // (Four-step LDS reads issued two steps ahead, as in the replay.)
+      float4 sv4{}, s24{}, dy4{}, k4{}, q4{}, nsv4{}, ns24{}, ndy4{}, nk4{}, nq4{};
+      auto read4 = [&](int j0, float4 &sv, float4 &s2, float4 &dy, float4 &k, float4 &q) {
+        asm volatile("" ::: "memory");
+        sv = lds4(s_sv[cur][c], j0);
+        if constexpr (kS2) s2 = lds4(s_s2[kS2 ? cur : 0][kS2 ? c : 0], j0);
+        dy = lds4(s_dy[cur][c], j0);
+        k = lds4(s_k[kb][ln.s], j0);
+        q = lds4(s_q[kb][ln.s], j0);
+        asm volatile("" ::: "memory");
+      };
+      if (kVecLds) read4(TB - 4, sv4, s24, dy4, k4, q4);
 #pragma unroll
       for (int j = TB - 1; j >= 0; --j) {
-        if (kVecLds && j % 4 == 3) {
-          asm volatile("" ::: "memory");   // (as in the replay)
-          sv4 = lds4(s_sv[cur][c], j - 3);
-          if constexpr (kS2) s24 = lds4(s_s2[kS2 ? cur : 0][kS2 ? c : 0], j - 3);
-          dy4 = lds4(s_dy[cur][c], j - 3);
-          k4 = lds4(s_k[kb][ln.s], j - 3);
-          q4 = lds4(s_q[kb][ln.s], j - 3);
+        if (kVecLds && j % 4 == 3 && j < TB - 1) {
+          sv4 = nsv4;
+          s24 = ns24;
+          dy4 = ndy4;
+          k4 = nk4;
+          q4 = nq4;
         }
+        if (kVecLds && j % 4 == 1 && j >= 4) read4(j - 5, nsv4, ns24, ndy4, nk4, nq4);
         float dk_c = 0.0f, dq_c = 0.0f;
         if constexpr (!FULL) {
           dv_w[j] = 0.0f;
@@ -1447,8 +1502,19 @@ __global__ void __launch_bounds__(kFusedThreads) fused_adjoint_map_kernel(Adjoin
   // right, x, becomes [[P, Q], [0, A]] x + (ul, ue) before the steps walked.
   float P = 1.0f, Q = 0.0f, A = 1.0f, ul = 0.0f, ue = 0.0f;
   const int64_t n_ck = g.n_ck;
+  // Checkpoints are read one block ahead, with the block's tiles (as in
+  // fused_kla_bwd_kernel: a load just before the replay waits for all in flight).
+  float ck_l = 1.0f, ck_e = 0.0f;
+  auto load_ck = [&](int64_t blk) {
+    if (ln.active) {
+      const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
+      ck_l = prm.ck_lam[ci];
+      ck_e = prm.ck_eta[ci];
+    }
+  };
   if (n_ck > 0) {
     load((n_ck - 1) * TB);
+    load_ck(n_ck - 1);
     stage(0);
   }
   __syncthreads();
@@ -1457,9 +1523,12 @@ __global__ void __launch_bounds__(kFusedThreads) fused_adjoint_map_kernel(Adjoin
     const int kb = KQB == 1 ? 0 : cur;
     const int64_t blk = n_ck - 1 - i;
     const int64_t t0 = blk * TB;
-    if (i + 1 < n_ck) load(t0 - TB);
+    const float lam_ck = ck_l, eta_ck = ck_e;
+    if (i + 1 < n_ck) {
+      load(t0 - TB);
+      load_ck(blk - 1);
+    }
     const int nv = static_cast<int>(L - t0 < TB ? L - t0 : TB);
-    const int64_t ci = ((ln.b * n_ck + blk) * M + ln.m) * S + ln.s;
     // The block's replay and its steps composed in reverse, as the backward's
     // replay and walk (FULL: every step of the block lies inside the sequence;
     // tile values four steps per LDS read from 16 lanes per channel on).
@@ -1468,8 +1537,8 @@ __global__ void __launch_bounds__(kFusedThreads) fused_adjoint_map_kernel(Adjoin
       constexpr bool X4 = SP >= 16;
       float lh[TB + 1], eh[TB + 1], idn[TB];
       {
-        float lam = ln.active ? prm.ck_lam[ci] : 1.0f;
-        float eta = ln.active ? prm.ck_eta[ci] : 0.0f;
+        float lam = lam_ck;
+        float eta = eta_ck;
         float4 l4{}, v4{}, k4{}, k24{};
 #pragma unroll
         for (int j = 0; j < TB; ++j) {
