@@ -249,13 +249,17 @@ class KLALayer(nn.Module):
 
     def _linear_split(self, mod: nn.Linear, x: torch.Tensor, sizes: list[int]):
         """self._split(mod(x), sizes); on a hip-family backend with a gradient to
-        carry, the projection and the split as one (kla.ops.hip.linear)."""
+        carry, the projection and the split as one (kla.ops.hip.linear), and
+        otherwise the product in row blocks where the pieces allow it
+        (kla.ops.hip.linear.split_blocks)."""
         from kla.ops.kla_ops import _step_on_hip
 
-        if torch.is_grad_enabled() and _step_on_hip(self.config.backend, x):
-            from kla.ops.hip.linear import linear_split
+        if _step_on_hip(self.config.backend, x):
+            from kla.ops.hip.linear import linear_split, split_blocks
 
-            pieces = linear_split(mod, x, sizes)
+            pieces = linear_split(mod, x, sizes) if torch.is_grad_enabled() else None
+            if pieces is None and not (torch.is_grad_enabled() and x.requires_grad):
+                pieces = split_blocks(mod, x, sizes)
             if pieces is not None:
                 return pieces
         return self._split(mod(x), sizes)

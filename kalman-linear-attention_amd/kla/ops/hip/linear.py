@@ -139,20 +139,11 @@ class _SplitLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, sizes):
         n = w.shape[0]
-        blocks = row_blocks(n)
-        cuts = {sum(sizes[:i]) for i in range(len(sizes) + 1)}
-        if any(r0 not in cuts for r0, _ in blocks):
-            blocks = [(0, n)]   # a piece would straddle two blocks
+        blocks = _blocks_for(n, sizes) or [(0, n)]   # one block where a piece would straddle two
         ctx.save_for_backward(x, w)
         ctx.blocks, ctx.sizes = blocks, list(sizes)
         outs = [F.linear(x, w[r0:r1]) for r0, r1 in blocks]
-        pieces, c0 = [], 0
-        for size in sizes:
-            b = max(i for i, (r0, _) in enumerate(blocks) if r0 <= c0)
-            r0 = blocks[b][0]
-            pieces.append(outs[b][..., c0 - r0:c0 - r0 + size])
-            c0 += size
-        return tuple(pieces)
+        return _pieces(outs, blocks, sizes)
 
     @staticmethod
     def backward(ctx, *grads):
@@ -210,6 +201,51 @@ def linear(mod: torch.nn.Linear, x: torch.Tensor) -> torch.Tensor:
         return mod(x)
     with torch.autocast("cuda", enabled=False):
         return _Linear.apply(*ops)
+
+
+def _blocks_for(n: int, sizes: list[int]):
+    """row_blocks(n) when each piece of ``sizes`` lies within one block (and there
+    is more than one block), else None."""
+    blocks = row_blocks(n)
+    cuts = {sum(sizes[:i]) for i in range(len(sizes) + 1)}
+    if len(blocks) == 1 or any(r0 not in cuts for r0, _ in blocks):
+        return None
+    return blocks
+
+
+def _pieces(outs, blocks, sizes):
+    """The pieces of ``sizes`` as column views of the blocks' outputs."""
+    pieces, c0 = [], 0
+    for size in sizes:
+        b = max(i for i, (r0, _) in enumerate(blocks) if r0 <= c0)
+        r0 = blocks[b][0]
+        pieces.append(outs[b][..., c0 - r0:c0 - r0 + size])
+        c0 += size
+    return tuple(pieces)
+
+
+# Fewest tokens for split_blocks: below, the second product's host cost (one
+# more library call and the weight slices, ~20 us) outweighs what it saves on the
+# GPU, and a layer of that size is bound by host time (C1, 2048 tokens).
+_MIN_BLOCK_TOKENS = 8192
+
+
+def split_blocks(mod: torch.nn.Linear, x: torch.Tensor, sizes: list[int]):
+    """``torch.split(mod(x), sizes, dim=-1)`` as one product per row block of the
+    weight (whole 256-row tiles, then the rest) where every piece lies within one
+    block: hipBLASLt otherwise runs the ragged last tile row's kernel over the
+    whole product (``sensor_proj`` [2080, 1024] in fp32 at 32768 tokens 1091 ->
+    982 us on MI355X). Autograd goes through the weight slices. None where that
+    does not apply (the caller splits ``mod(x)`` itself), including inputs of
+    fewer than ``_MIN_BLOCK_TOKENS`` tokens."""
+    w, b = mod.weight, mod.bias
+    if not x.is_cuda or sum(sizes) != w.shape[0] or x.numel() < _MIN_BLOCK_TOKENS * w.shape[1]:
+        return None
+    blocks = _blocks_for(w.shape[0], sizes)
+    if blocks is None:
+        return None
+    outs = [F.linear(x, w[r0:r1], None if b is None else b[r0:r1]) for r0, r1 in blocks]
+    return _pieces(outs, blocks, sizes)
 
 
 def linear_split(mod: torch.nn.Linear, x: torch.Tensor, sizes: list[int]):

@@ -1873,6 +1873,41 @@ def test_linear_split_matches_torch(cuda, x_grad):
         assert err <= 1e-3 * float(b.abs().max()), name
 
 
+def test_split_blocks_match_one_product(cuda):
+    """split_blocks (inference: one fp32 product per row block, bias sliced with
+    the weight) against torch.split(F.linear(...)) at 8192 tokens: the pieces within
+    fp32 GEMM rounding, each a view of its block; None below 8192 tokens, where a
+    piece would straddle two blocks, or for a weight of whole tiles; and with a
+    gradient to carry, autograd through the weight slices gives torch's dx, dw."""
+    from kla.ops.hip.linear import split_blocks
+
+    g = torch.Generator().manual_seed(98)
+    mod = torch.nn.Linear(256, 1056, bias=True).to(cuda)
+    x = torch.randn(2, 4096, 256, generator=g).to(cuda)
+    sizes = [512, 512, 16, 16]
+    with torch.no_grad():
+        got = split_blocks(mod, x, sizes)
+        want = torch.split(mod(x), sizes, dim=-1)
+        assert got is not None and [p.shape for p in got] == [p.shape for p in want]
+        assert got[0].untyped_storage().data_ptr() == got[1].untyped_storage().data_ptr()
+        assert got[2].untyped_storage().data_ptr() != got[0].untyped_storage().data_ptr()
+        for i, (a, b) in enumerate(zip(got, want)):
+            check(f"piece{i}", a, b.cpu().numpy(), rtol=1e-5, atol=1e-6)
+        assert split_blocks(mod, x[:, :4095], sizes) is None            # fewer than 8192 tokens
+        assert split_blocks(mod, x, [500, 540, 8, 8]) is None           # a piece across the 1024 cut
+        whole = torch.nn.Linear(256, 1024, bias=False).to(cuda)
+        assert split_blocks(whole, x, [512, 512]) is None               # whole tiles: one product
+    res = []
+    for blocks in (True, False):
+        xx = x.clone().requires_grad_(True)
+        mod.zero_grad(set_to_none=True)
+        pieces = split_blocks(mod, xx, sizes) if blocks else torch.split(mod(xx), sizes, dim=-1)
+        (pieces[0].square().sum() + pieces[3].sum()).backward()
+        res.append((xx.grad, mod.weight.grad, mod.bias.grad))
+    for name, a, b in zip(("dx", "dw", "db"), *res):
+        check(name, a, b.cpu().numpy(), rtol=1e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("d_model,B,L", [(256, 2, 4096), (1024, 4, 4096)])
 def test_layer_split_linear_matches_torch_linear(cuda, monkeypatch, d_model, B, L):
     """A KLALayer training step under bf16 autocast with its projections on
