@@ -74,6 +74,52 @@ def test_mobius_fwd_bwd_matches_oracle(cuda, shape, with_lam0):
         _close("dlam0", l0.grad, dl0)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shapes_match_oracle(cuda, seed):
+    """Randomly drawn (B, T, lanes) -- T up to 5000, so several chunks of every
+    kernel's tile, lanes from 1 to 300, ragged against the 64-lane tiles -- with or
+    without the initial states and an explicit D: the Moebius and affine scans,
+    forward and backward, against the float64 oracle at rtol 1e-5 / atol 1e-6."""
+    import random
+
+    from kla.ops.hip import affine_scan, mobius_scan
+
+    r = random.Random(seed)
+    B, T, N = r.randint(1, 3), r.randint(1, 5000), r.randint(1, 300)
+    with_init, with_D = r.random() < 0.6, r.random() < 0.3
+    _log(f"[random scans] seed={seed} shape={(B, T, N)} init={with_init} D={with_D}")
+    A, Bm, C, lam0, dlam = mobius_inputs(B, T, N, seed=100 + seed)
+    D = (torch.rand(B, T, N, generator=torch.Generator().manual_seed(200 + seed)) + 0.5) if with_D else None
+    lam0 = lam0 if with_init else None
+    leaves = [t.to(cuda).requires_grad_(True) for t in (A, Bm, C) + ((D,) if with_D else ())]
+    l0 = lam0.to(cuda).requires_grad_(True) if lam0 is not None else None
+    lam = mobius_scan(*leaves[:3], leaves[3] if with_D else None, l0)
+    torch.autograd.backward(lam, dlam.to(cuda))
+    want = ref.mobius_scan_fwd(A, Bm, C, D, lam0)
+    _close("lam", lam, want)
+    grads = ref.mobius_scan_bwd(dlam, A, Bm, C, D, lam0, want)
+    for name, got, w in zip(("dA", "dB", "dC"), leaves, grads[:3]):
+        _close(name, got.grad, w)
+    if with_D:
+        _close("dD", leaves[3].grad, grads[3])
+    if l0 is not None:
+        _close("dlam0", l0.grad, grads[4])
+
+    g, u, dh = affine_inputs(B, T, N, seed=300 + seed)
+    h0 = torch.randn(B, N, generator=torch.Generator().manual_seed(400 + seed)) if with_init else None
+    gg, uu = g.to(cuda).requires_grad_(True), u.to(cuda).requires_grad_(True)
+    hh0 = h0.to(cuda).requires_grad_(True) if h0 is not None else None
+    h = affine_scan(gg, uu, hh0)
+    torch.autograd.backward(h, dh.to(cuda))
+    want = ref.affine_scan_fwd(g, u, h0)
+    _close("h", h, want)
+    dg, du, dh0 = ref.affine_scan_bwd(dh, g, want, h0)
+    _close("dg", gg.grad, dg)
+    _close("du", uu.grad, du)
+    if hh0 is not None:
+        _close("dh0", hh0.grad, dh0)
+
+
 @pytest.mark.parametrize("shape", [(2, 130, 65), (1, 300, 128)])
 def test_mobius_explicit_D(cuda, shape):
     """A general D tensor (the reference passes ones_like(phi)) and its gradient dD."""
