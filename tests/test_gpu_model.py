@@ -253,3 +253,73 @@ def test_c5_prefill_logits_against_float64(cuda, monkeypatch):
     print(f"  last-position logits vs float64: max |d| {float(err.max()):.3e} (scale {scale:.3e}); "
           f"literal rtol 1e-5 / atol 1e-6 ratio {lit:.3f}, rtol 1e-5 / atol 1e-5 max ratio {bar:.3f}", flush=True)
     assert bar <= 1.0
+
+
+def _random_model(seed):
+    """(ModelConfig, KLAConfig kwargs) drawn over the model's and the layer's options."""
+    import random
+
+    from test_gpu_backend import _random_layer
+
+    r = random.Random(seed)
+    _, kw = _random_layer(seed + 500)
+    kw["return_variance"] = False   # the model reads out the mean only
+    cfg = ModelConfig(vocab_size=r.choice([97, 256, 1000]), d_model=r.choice([24, 32, 48]),
+                      n_layers=r.randint(1, 3), mlp=r.choice(["none", "swiglu", "gelu"]),
+                      mlp_ratio=r.choice([2.0, 8.0 / 3.0, 4.0]), tie_embeddings=r.random() < 0.3,
+                      logit_softcap=r.choice([None, 30.0]))
+    return cfg, kw
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_models_match_float64(cuda, seed):
+    """A SequenceModel with a randomly drawn model and layer configuration on hip
+    against the same weights in float64 on the CPU (backend torch everywhere): the
+    prefill logits of every position, the prefill state, and four decode steps
+    (both models fed the float64 model's greedy tokens, so a near tie cannot make
+    them diverge) at rtol 1e-5 / atol 1e-5 of each tensor's scale (fp32 products
+    over the blocks round at ~1e-6 of their terms); the same steps replayed by a
+    DecodeGraph from the prefill state give the eager hip logits bit for bit."""
+    cfg, kw = _random_model(seed)
+    print(f"[random model] seed={seed} {cfg} {kw}", flush=True)
+    torch.manual_seed(seed)
+    model = SequenceModel(cfg, KLAConfig(**kw, backend="hip")).to(cuda).eval()
+    ref = copy.deepcopy(model).double().cpu()
+    for m in ref.modules():
+        if isinstance(m, KLALayer):
+            m.config = KLAConfig(**kw, backend="torch")
+        if hasattr(m, "backend"):
+            m.backend = "torch"
+    B, L = 2, 23
+    ids = torch.randint(0, cfg.vocab_size, (B, L), generator=torch.Generator().manual_seed(seed + 7))
+
+    def close(name, got, want):
+        assert (got is None) == (want is None), name   # parts a configuration does not carry
+        if want is None:
+            return
+        got = got.detach().double().cpu()
+        assert got.shape == want.shape, name
+        if not want.numel():   # e.g. the conv window of a width-1 conv
+            return
+        scale = max(float(want.abs().max()), 1e-30)
+        ratio = float(((got - want).abs() / (1e-5 * scale + 1e-5 * want.abs())).max()) if want.numel() else 0.0
+        print(f"  {name:14s} ratio {ratio:.3f}", flush=True)
+        assert torch.isfinite(got).all() and ratio <= 1.0, f"{name}: ratio {ratio:.3f}"
+
+    from kla.models.decode_graph import DecodeGraph
+
+    with torch.no_grad():
+        got, st = model(ids.to(cuda), state=model.init_state(B))
+        want, st_ref = ref(ids, state=ref.init_state(B))
+        close("prefill logits", got, want)
+        for i, (a, b) in enumerate(zip(torch.utils._pytree.tree_leaves(st), torch.utils._pytree.tree_leaves(st_ref))):
+            close(f"state[{i}]", a, b)
+        graph = DecodeGraph(model, st)
+        tok = want[:, -1:].argmax(-1)
+        for step in range(4):
+            got, st = model(tok.to(cuda), state=st)
+            want, st_ref = ref(tok, state=st_ref)
+            close(f"decode {step}", got, want)
+            # The graph replays the same one-token step: the same bits.
+            assert torch.equal(graph.step(tok.to(cuda)), got), f"graph decode {step}"
+            tok = want[:, -1:].argmax(-1)
