@@ -499,6 +499,46 @@ def test_random_layer_configs_match_torch_backend(cuda, seed):
             check("state", a, b.cpu().numpy(), rtol=2e-5, atol=2e-6)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_layer_configs_bf16_training_match_torch_backend(cuda, seed):
+    """A randomly drawn KLALayer configuration trained one step under bf16 autocast
+    on hip (bf16 sensors into the fused kernels, the split projections and weight
+    gradients, the HIP conv and tail) against the same weights on the torch
+    backend on the same GPU under the same autocast: the output and every
+    parameter gradient within the bf16 bar, rtol 2e-2 / atol 1e-2 of each
+    tensor's scale. x (2, 512, d_model): 1024 tokens, so the weight gradients
+    split over the tokens. The draws leave out the layer's two discontinuities,
+    which the paths' different bf16 roundings of the same values can straddle
+    (the fp32 test above keeps them): the k, q clip, and the l2 norm over a single
+    state (the sign of k)."""
+    import copy
+
+    d_model, kw = _random_layer(seed + 900)
+    kw["clip_value"] = None
+    if kw["qk_norm"] and kw["d_state"] == 1:
+        kw["d_state"] = 4
+    print(f"[bf16 layer config] d_model={d_model} {kw}", flush=True)
+    torch.manual_seed(seed)
+    hip = KLALayer(d_model, KLAConfig(**kw, backend="hip")).to(cuda)
+    ref = copy.deepcopy(hip)
+    ref.config = KLAConfig(**kw, backend="torch")
+    x = torch.randn(2, 512, d_model, generator=torch.Generator().manual_seed(seed + 950)).to(cuda)
+    res = []
+    for layer in (hip, ref):
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = layer(x)
+        y = out[0] if isinstance(out, tuple) else out
+        y.float().square().mean().backward()
+        res.append([y.detach().float()] + [p.grad.float() if p.grad is not None else torch.zeros_like(p)
+                                           for p in layer.parameters()])
+    names = ["out"] + [n for n, _ in hip.named_parameters()]
+    for name, a, b in zip(names, *res):
+        scale = max(float(b.abs().max()), 1e-30)
+        ratio = float(((a - b).abs() / (1e-2 * scale + 2e-2 * b.abs())).max()) if b.numel() else 0.0
+        print(f"  {name:18s} ratio {ratio:.3f}", flush=True)
+        assert torch.isfinite(a).all() and ratio <= 1.0, f"{name}: ratio {ratio:.3f}"
+
+
 @pytest.mark.parametrize("tag", sorted(GOLDEN_CASES))
 def test_layer_on_hip_reproduces_reference_vectors(cuda, tag):
     """A seeded KLALayer(backend="hip") on the GPU reproduces the outputs the
