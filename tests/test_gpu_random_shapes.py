@@ -71,6 +71,6 @@ def test_random_problem_matches_float64_autograd(cuda, monkeypatch, seed):
     for name, got, want in zip(("y", "y_var", "lam", "eta"), out, ref):
         check_scan(name, got, want.detach().numpy())
     loss(*out).backward()
-    names = ["v", "lv", "k", "q", "a", "p", "lam0", "eta0"]
+    names = ["v", "lambda_v", "k", "q", "a", "p", "lam0", "eta0"]
     for name, got, want in zip(names, gs, xs):
         check_scan("d" + name, got.grad, want.grad.numpy())
