@@ -1,13 +1,15 @@
-"""Randomly drawn problems through the public kla_scan on the fused hip path.
+"""Randomly drawn problems through the public kla_scan on both hip paths (the
+fused kernels, and the composed HIP scans with torch glue).
 
 Each seed draws a shape (batch, a ragged sequence length, channels, and a state
 width from 1 to past 256, where the state runs as consecutive groups), whether an
 initial state is given, the prior read-out, whether the loss uses y_var (without
 it the kernels skip the variance read-out and its adjoint), and a forced time
-split of 1, 2 or 4 chunks (the chunk maps, their adjoints and both walks). The
-outputs, the final state and the gradients of every input and of the initial
-state are checked against float64 autograd of the reference's torch algorithm
-(oracle.torch_ref, reference kla_ops.py:188-290) at the scan's bars.
+split of 1, 2 or 4 chunks (the fused path's chunk maps, their adjoints and both
+walks; the composed path has no split). The outputs, the final state and the
+gradients of every input and of the initial state are checked against float64
+autograd of the reference's torch algorithm (oracle.torch_ref, reference
+kla_ops.py:188-290) at the scan's bars.
 """
 
 import random
@@ -39,13 +41,14 @@ def _draw(seed):
                 with_state=r.random() < 0.6)
 
 
+@pytest.mark.parametrize("backend", ["hip_fused", "hip_composed"])
 @pytest.mark.parametrize("seed", range(24))
-def test_random_problem_matches_float64_autograd(cuda, monkeypatch, seed):
+def test_random_problem_matches_float64_autograd(cuda, monkeypatch, seed, backend):
     from kla.ops.hip import fused
 
     d = _draw(seed)
     B, L, M, S = d["B"], d["L"], d["M"], d["S"]
-    print(f"[random scan] seed={seed} {d}", flush=True)
+    print(f"[random scan] {backend} seed={seed} {d}", flush=True)
     monkeypatch.setattr(fused, "train_chunks", lambda *a: d["split"])
     monkeypatch.setattr(fused, "time_chunks", lambda *a: d["split"])
     v, lv, k, q, a, p = make_inputs(B, L, M, S, seed=1000 + seed)
@@ -66,7 +69,7 @@ def test_random_problem_matches_float64_autograd(cuda, monkeypatch, seed):
 
     gs = [t.to(cuda).requires_grad_(True) for t in leaves]
     init = KLAState(lam=gs[6], eta=gs[7]) if st is not None else None
-    y, y_var, state = kla_scan(*gs[:6], initial_state=init, backend="hip_fused", decode_from_prior=d["prior"])
+    y, y_var, state = kla_scan(*gs[:6], initial_state=init, backend=backend, decode_from_prior=d["prior"])
     out = (y, y_var, state.lam, state.eta)
     for name, got, want in zip(("y", "y_var", "lam", "eta"), out, ref):
         check_scan(name, got, want.detach().numpy())
