@@ -24,6 +24,7 @@ import torch.nn.functional as F
 from kla.configs import KLAConfig
 from kla.layers.common import CausalConv1d, get_activation, inv_softplus_dt_init, l2_norm
 from kla.ops import KLAState, init_state, kla_scan, kla_step
+from kla.ops.kla_ops import _resolve_auto, _step_on_hip
 
 
 class KLALayerState(NamedTuple):
@@ -228,8 +229,6 @@ class KLALayer(nn.Module):
     def _split(self, t: torch.Tensor, sizes: list[int]):
         """torch.split(t, sizes, dim=-1); on a hip-family backend with a gradient to
         carry, the split whose backward concatenates on the MI355X."""
-        from kla.ops.kla_ops import _step_on_hip
-
         if t.requires_grad and torch.is_grad_enabled() and _step_on_hip(self.config.backend, t):
             from kla.ops.hip.split import split_last
 
@@ -239,8 +238,6 @@ class KLALayer(nn.Module):
     def _linear(self, mod: nn.Linear, x: torch.Tensor) -> torch.Tensor:
         """mod(x); on a hip-family backend with a gradient to carry, the projection
         whose weight gradient is split over the tokens (kla.ops.hip.linear)."""
-        from kla.ops.kla_ops import _step_on_hip
-
         if torch.is_grad_enabled() and _step_on_hip(self.config.backend, x):
             from kla.ops.hip.linear import linear
 
@@ -252,8 +249,6 @@ class KLALayer(nn.Module):
         carry, the projection and the split as one (kla.ops.hip.linear), and
         otherwise the product in row blocks where the pieces allow it
         (kla.ops.hip.linear.split_blocks)."""
-        from kla.ops.kla_ops import _step_on_hip
-
         if _step_on_hip(self.config.backend, x):
             from kla.ops.hip.linear import linear_split, split_blocks
 
@@ -268,8 +263,6 @@ class KLALayer(nn.Module):
         """Whether the k, q sensors come from the MI355X kernels: a hip-family backend
         on a ROCm GPU, fp32 or bf16 projection, d_state <= 64, and a norm or a clip
         to apply."""
-        from kla.ops.kla_ops import _step_on_hip
-
         cfg = self.config
         return ((cfg.qk_norm or cfg.clip_value is not None) and k.dtype in (torch.float32, torch.bfloat16)
                 and self.d_state <= 64 and k.dim() == 3 and _step_on_hip(cfg.backend, k))
@@ -277,8 +270,6 @@ class KLALayer(nn.Module):
     def _aq_on_hip(self) -> bool:
         """Whether (a_bar, p_bar) come from the MI355X kernels: fp32 parameters on a
         ROCm GPU and a hip-family backend."""
-        from kla.ops.kla_ops import _step_on_hip
-
         params = (self.delta, self.lambda_log, self.process_noise)
         return (all(t.dtype == torch.float32 for t in params)
                 and _step_on_hip(self.config.backend, self.delta))
@@ -288,7 +279,6 @@ class KLALayer(nn.Module):
         read-out inside it: a backend that picks the fused scan ("hip", "hip_fused"
         or "auto" on a ROCm GPU), d_state <= 256, a ROCm GPU."""
         from kla.ops.hip.fused import MAX_STATE
-        from kla.ops.kla_ops import _resolve_auto, _step_on_hip
 
         backend = self.config.backend
         if backend == "auto":
@@ -302,8 +292,6 @@ class KLALayer(nn.Module):
         (fp32 or bf16), and a skip or a gate to apply. Not with return_variance
         and a gate: act(gate) then also scales y_var, and torch adds the two
         bf16 gradients of act(gate) before the activation's backward."""
-        from kla.ops.kla_ops import _step_on_hip
-
         skip = self.lambda_skip is not None
         if not (skip or gate is not None) or y.dtype != torch.float32:
             return False
@@ -318,15 +306,11 @@ class KLALayer(nn.Module):
         (no gradient), fp32 activations on a ROCm GPU, a hip-family backend,
         d_state <= 256."""
         from kla.ops.hip.fused import MAX_STATE
-        from kla.ops.kla_ops import _step_on_hip
-
         return (not torch.is_grad_enabled() and projected.dtype == torch.float32 and self.d_state <= MAX_STATE
                 and _step_on_hip(self.config.backend, projected))
 
     def _conv_on_hip(self, z: torch.Tensor) -> bool:
         """Whether the causal conv runs on the MI355X kernels (with autograd)."""
-        from kla.ops.kla_ops import _step_on_hip
-
         return (z.dtype in (torch.float32, torch.bfloat16) and self.conv.kernel_size <= 8
                 and _step_on_hip(self.config.backend, z))
 

@@ -174,6 +174,15 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def stream(device: torch.device) -> int:
+    """Handle of the current HIP stream of ``device``: the value of
+    ``torch.cuda.current_stream(device).cuda_stream`` (the capture stream under
+    graph capture) without building the Stream object, ~0.1 us of host time a call
+    against ~2 us."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
+
+
 # ------------------------------------------------------------ op dispatch
 #
 # Each kernel entry point is a torch.library custom op (autograd, fake tensors
@@ -224,18 +233,18 @@ def workspace(kind: int, batch: int, steps: int, lanes: int, device: torch.devic
     need = int(lib().kla_scan_workspace_bytes(kind, batch, steps, lanes))
     if need == 0:
         raise ValueError(f"kla_scan_workspace_bytes: {last_error()}")
-    stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
+    handle = stream(device)
+    key = (device.index, handle)
     with _WS_LOCK:
         ws = _WORKSPACES.get(key)
         if ws is None or ws.numel() < need:
             size = max(need, 2 * ws.numel() if ws is not None else 0)
-            with torch.cuda.stream(stream):
+            with torch.cuda.stream(torch.cuda.current_stream(device)):
                 ws = torch.zeros(size, dtype=torch.uint8, device=device)
             if ws.data_ptr() % 256:
                 raise RuntimeError("workspace allocation is not 256-byte aligned")
             _WORKSPACES[key] = ws
-    return ws, stream.cuda_stream
+    return ws, handle
 
 
 _SCRATCH: dict = {}
@@ -245,15 +254,15 @@ def scratch(nbytes: int, device: torch.device) -> tuple[torch.Tensor, int]:
     """(uninitialised buffer of at least ``nbytes``, stream handle) for the current
     stream of ``device``: scratch whose contents no call relies on between calls
     (the fused backward's partial sums). Reused while large enough."""
-    stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
+    handle = stream(device)
+    key = (device.index, handle)
     with _WS_LOCK:
         buf = _SCRATCH.get(key)
         if buf is None or buf.numel() < nbytes:
-            with torch.cuda.stream(stream):
+            with torch.cuda.stream(torch.cuda.current_stream(device)):
                 buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
             _SCRATCH[key] = buf
-    return buf, stream.cuda_stream
+    return buf, handle
 
 
 def workspace_failures(device: torch.device) -> int:

@@ -54,7 +54,7 @@ def _conv_op(x: torch.Tensor, state: Optional[torch.Tensor], weight: torch.Tenso
     pt = _lib.ptr
     _lib.check("kla_causal_conv_fwd", _lib.lib().kla_causal_conv_fwd(
         _dtype_code(x), pt(x), ld_t, ld_b, pt(state), pt(weight), pt(bias), activation, pt(y), pt(new_state),
-        B, L, D, K, torch.cuda.current_stream(dev).cuda_stream))
+        B, L, D, K, _lib.stream(dev)))
     return y, new_state
 
 

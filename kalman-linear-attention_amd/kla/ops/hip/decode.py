@@ -96,7 +96,7 @@ def decode_step_hip(v, log_var, k, q, delta, lambda_log, process_noise, lam, eta
         pt(residual), _row_stride(residual) if residual is not None else 0, pt(lambda_skip),
         pt(gate), _row_stride(gate) if gate is not None else 0,
         pt(delta), pt(lambda_log), pt(process_noise), pt(lam), pt(eta), pt(lam_out), pt(eta_out), pt(y), pt(y_var),
-        ctypes.byref(cfg), B, M, S, torch.cuda.current_stream(dev).cuda_stream))
+        ctypes.byref(cfg), B, M, S, _lib.stream(dev)))
     return y, y_var, lam_out, eta_out
 
 
@@ -113,5 +113,5 @@ def conv_step_hip(x, state, weight, bias, activation="silu", in_place=False):
     pt = _lib.ptr
     _lib.check("kla_conv_step_fwd", _lib.lib().kla_conv_step_fwd(
         pt(x), _row_stride(x), pt(state), pt(state_out), pt(weight), pt(bias), ACTIVATIONS.get(activation, 0),
-        pt(y), B, D, K, torch.cuda.current_stream(x.device).cuda_stream))
+        pt(y), B, D, K, _lib.stream(x.device)))
     return y, state_out

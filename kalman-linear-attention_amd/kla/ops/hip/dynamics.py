@@ -19,7 +19,7 @@ from kla.ops.hip.scans import _require_device
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _lib.stream(t.device)
 
 
 @_lib.hip_op("kla_hip::discretize")

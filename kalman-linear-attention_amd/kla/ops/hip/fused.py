@@ -97,31 +97,29 @@ def train_chunks(B: int, L: int, M: int, S: int, cus: int) -> int:
     return nc
 
 
-def _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, decode_from_prior, B, L, M, S, nc, dev,
-                   ck_lam=None, ck_eta=None):
+def _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin, decode_from_prior, B, L, M, S, nc,
+                   dev, ck_lam=None, ck_eta=None):
     """The time-split forward: kla_fused_chunk_maps on the [B * nc, L / nc] view,
     kla_chunk_starts, then the fused forward on the view from those starts (with
     the checkpoints when given: [B, n_ck, M, S] is the view's [B * nc, n_ck / nc,
-    M, S] when L / nc is a multiple of 16). Returns (lam_fin, eta_fin), the state
-    after each sequence's last chunk (from the chunk maps, written [B, M, S] by
-    kla_chunk_starts)."""
+    M, S] when L / nc is a multiple of 16). Writes lam_fin, eta_fin [B, M, S], the
+    state after each sequence's last chunk (from the chunk maps, by
+    kla_chunk_starts). The maps and the chunk starts share one buffer; every
+    chunk's final state (unused) then lands in the maps' part, no longer read."""
     lib, pt = _lib.lib(), _lib.ptr
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _lib.stream(dev)
     Bp, Lc = B * nc, L // nc
-    f32 = dict(dtype=_F32, device=dev)
-    maps = torch.empty(Bp, M, S, 8, **f32)
-    lam_st, eta_st = torch.empty(Bp, M, S, **f32), torch.empty(Bp, M, S, **f32)
-    lam_fin, eta_fin = torch.empty(B, M, S, **f32), torch.empty(B, M, S, **f32)
+    lanes = Bp * M * S
+    buf = torch.empty(10 * lanes, dtype=_F32, device=dev)   # maps [Bp, M, S, 8], then two [Bp, M, S]
+    maps = pt(buf)
+    lam_st, eta_st = maps + 32 * lanes, maps + 36 * lanes
     _lib.check("kla_fused_chunk_maps", lib.kla_fused_chunk_maps(
-        ctypes.byref(sn), pt(k), pt(a), pt(p), pt(maps), Bp, Lc, M, S, stream))
+        ctypes.byref(sn), pt(k), pt(a), pt(p), maps, Bp, Lc, M, S, stream))
     _lib.check("kla_chunk_starts", lib.kla_chunk_starts(
-        pt(maps), pt(lam0), pt(eta0), pt(lam_st), pt(eta_st), pt(lam_fin), pt(eta_fin), B, nc, M, S, stream))
-    # Every chunk's final state (unused) lands in the maps' buffer, no longer read.
-    scratch = maps.view(-1)
+        maps, pt(lam0), pt(eta0), lam_st, eta_st, pt(lam_fin), pt(eta_fin), B, nc, M, S, stream))
     _lib.check("kla_fused_scan_sensors_fwd", lib.kla_fused_scan_sensors_fwd(
-        ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam_st), pt(eta_st), pt(y), pt(y_var), pt(scratch),
-        pt(scratch[Bp * M * S:]), pt(ck_lam), pt(ck_eta), int(decode_from_prior), Bp, Lc, M, S, stream))
-    return lam_fin, eta_fin
+        ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), lam_st, eta_st, pt(y), pt(y_var), maps, maps + 4 * lanes,
+        pt(ck_lam), pt(ck_eta), int(decode_from_prior), Bp, Lc, M, S, stream))
 
 
 def _split_backward(bwd, dy, dy_var, dlam_fin, deta_fin, sn, k, q, a, p, ck_lam, ck_eta, decode_from_prior,
@@ -132,7 +130,7 @@ def _split_backward(bwd, dy, dy_var, dlam_fin, deta_fin, sn, k, q, a, p, ck_lam,
     chunk's adjoint entering from its end. Returns (dlam0, deta0) [B, M, S], the
     first chunks' initial-state gradients."""
     lib, pt = _lib.lib(), _lib.ptr
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _lib.stream(dev)
     Bp, Lc = B * nc, L // nc
     f32 = dict(dtype=_F32, device=dev)
     maps = torch.empty(Bp, M, S, 8, **f32)
@@ -221,11 +219,11 @@ def _fwd_one(v, lambda_v, k, q, a, p, lam0, eta0, decode_from_prior, save, dev, 
     cus = _cus(dev.index or 0)
     nc = train_chunks(B, L, M, S, cus) if save else time_chunks(B, L, M, S, cus)
     if nc > 1:
-        lam_fin, eta_fin = _split_forward(_dense_sensors(v, lambda_v), k, q, a, p, lam0, eta0, y, y_var,
-                                          decode_from_prior, B, L, M, S, nc, dev,
-                                          ck_lam=ck_lam if save else None, ck_eta=ck_eta if save else None)
+        _split_forward(_dense_sensors(v, lambda_v), k, q, a, p, lam0, eta0, y, y_var, lam_fin, eta_fin,
+                       decode_from_prior, B, L, M, S, nc, dev,
+                       ck_lam=ck_lam if save else None, ck_eta=ck_eta if save else None)
         return y, y_var, lam_fin, eta_fin
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _lib.stream(dev)
     pt = _lib.ptr
     _lib.check("kla_fused_scan_fwd", _lib.lib().kla_fused_scan_fwd(
         pt(v), pt(lambda_v), pt(k), pt(q), pt(a), pt(p), pt(lam0), pt(eta0), pt(y), pt(y_var),
@@ -290,7 +288,7 @@ def _bwd_one(dy, dy_var, dlam_fin, deta_fin, v, lambda_v, k, q, a, p, ck_lam, ck
     pt = _lib.ptr
 
     def bwd(batch, steps, lam_fin_grad, eta_fin_grad, lam0_grad, eta0_grad, ws, nbytes):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+        stream = _lib.stream(dev)
         _lib.check("kla_fused_scan_bwd", _lib.lib().kla_fused_scan_bwd(
             pt(dy), pt(dy_var), pt(lam_fin_grad), pt(eta_fin_grad), pt(v), pt(lambda_v), pt(k), pt(q), pt(a),
             pt(p), pt(ck_lam), pt(ck_eta), pt(dv), pt(dlv), pt(dk), pt(dq), pt(da), pt(dp), pt(lam0_grad),
@@ -416,19 +414,23 @@ def _sensor_rows(t: torch.Tensor) -> Optional[int]:
     return ld if ld >= M else None
 
 
-def _sensor_desc(v: torch.Tensor, obs: torch.Tensor, log_var: bool, obs_var_min: float,
+def _sensor_desc(v: torch.Tensor, obs: torch.Tensor, lds: tuple[int, int], log_var: bool, obs_var_min: float,
                  obs_var_max: float) -> "_lib.Sensors":
-    return _lib.Sensors(v=_lib.ptr(v), ld_v=_sensor_rows(v), obs=_lib.ptr(obs), ld_obs=_sensor_rows(obs),
+    return _lib.Sensors(v=_lib.ptr(v), ld_v=lds[0], obs=_lib.ptr(obs), ld_obs=lds[1],
                         dtype=_lib.KLA_DTYPE_BF16 if v.dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32,
                         log_var=int(log_var), obs_var_min=obs_var_min, obs_var_max=obs_var_max)
 
 
-def _check_sensors(v, obs):
+def _check_sensors(v, obs) -> tuple[int, int]:
+    """(ld_v, ld_obs), the row strides of the two sensor operands; raises if
+    their dtypes or layouts are not ones the kernels read."""
     if v.dtype != obs.dtype or v.dtype not in (torch.float32, torch.bfloat16):
         raise TypeError(f"v and the precision operand must both be float32 or both bfloat16; "
                         f"got {v.dtype} and {obs.dtype}")
-    if _sensor_rows(v) is None or _sensor_rows(obs) is None:
+    lds = _sensor_rows(v), _sensor_rows(obs)
+    if None in lds:
         raise ValueError("sensor operands must be [B, L, M] rows with a contiguous last dimension")
+    return lds
 
 
 @_lib.hip_op("kla_hip::kla_scan_fused_sensors")
@@ -441,7 +443,7 @@ def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torc
     y_var is empty (and not computed) unless ``with_var``."""
     dev = _require_device(v, obs, k, q, a, p, lam0, eta0)
     B, L, M, S = _check(v, obs, k, q, a, p, lam0, eta0)
-    _check_sensors(v, obs)
+    lds = _check_sensors(v, obs)
     f32 = dict(dtype=_F32, device=dev)
     y = torch.empty(B, L, M, **f32)
     y_var = torch.empty(B, L, M, **f32) if with_var else torch.empty(0, **f32)
@@ -452,20 +454,20 @@ def _sensors_fwd_op(v: torch.Tensor, obs: torch.Tensor, k: torch.Tensor, q: torc
     if B * M * S == 0:
         # No lanes: the read-outs sum over no state lanes (zero where B, L, M leave entries).
         return y.zero_(), y_var.zero_(), lam_fin, eta_fin, ck_lam, ck_eta
-    sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
+    sn = _sensor_desc(v, obs, lds, log_var, obs_var_min, obs_var_max)
     cus = _cus(dev.index or 0)
     nc = train_chunks(B, L, M, S, cus) if save else time_chunks(B, L, M, S, cus)
     if nc > 1:
-        lam_fin, eta_fin = _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var if with_var else None,
-                                          decode_from_prior, B, L, M, S, nc, dev,
-                                          ck_lam=ck_lam if save else None, ck_eta=ck_eta if save else None)
+        _split_forward(sn, k, q, a, p, lam0, eta0, y, y_var if with_var else None, lam_fin, eta_fin,
+                       decode_from_prior, B, L, M, S, nc, dev,
+                       ck_lam=ck_lam if save else None, ck_eta=ck_eta if save else None)
         return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
     pt = _lib.ptr
     _lib.check("kla_fused_scan_sensors_fwd", _lib.lib().kla_fused_scan_sensors_fwd(
         ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p), pt(lam0), pt(eta0), pt(y), pt(y_var) if with_var else None,
         pt(lam_fin),
         pt(eta_fin), pt(ck_lam) if save else None, pt(ck_eta) if save else None, int(decode_from_prior),
-        B, L, M, S, torch.cuda.current_stream(dev).cuda_stream))
+        B, L, M, S, _lib.stream(dev)))
     return y, y_var, lam_fin, eta_fin, ck_lam, ck_eta
 
 
@@ -494,7 +496,7 @@ def _sensors_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: 
     adjoint is skipped)."""
     dev = _require_device(dy, dy_var, dlam_fin, deta_fin, v, obs, k, q, a, p, ck_lam, ck_eta)
     B, L, M, S = _check(v, obs, k, q, a, p, None, None)
-    _check_sensors(v, obs)
+    lds = _check_sensors(v, obs)
     dv = torch.empty(B, L, M, dtype=v.dtype, device=dev)
     dobs = torch.empty(B, L, M, dtype=v.dtype, device=dev)
     dk, dq = torch.empty_like(k), torch.empty_like(q)
@@ -505,11 +507,11 @@ def _sensors_bwd_op(dy: torch.Tensor, dy_var: Optional[torch.Tensor], dlam_fin: 
         for t in (dv, dobs, dk, dq, da, dp):
             t.zero_()
         return dv, dobs, dk, dq, da, dp, dlam0, deta0
-    sn = _sensor_desc(v, obs, log_var, obs_var_min, obs_var_max)
+    sn = _sensor_desc(v, obs, lds, log_var, obs_var_min, obs_var_max)
     pt = _lib.ptr
 
     def bwd(batch, steps, lam_fin_grad, eta_fin_grad, lam0_grad, eta0_grad, ws, nbytes):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+        stream = _lib.stream(dev)
         _lib.check("kla_fused_scan_sensors_bwd", _lib.lib().kla_fused_scan_sensors_bwd(
             pt(dy), pt(dy_var), pt(lam_fin_grad), pt(eta_fin_grad), ctypes.byref(sn), pt(k), pt(q), pt(a), pt(p),
             pt(ck_lam), pt(ck_eta), pt(dv), pt(dobs), pt(dk), pt(dq), pt(da), pt(dp), pt(lam0_grad),

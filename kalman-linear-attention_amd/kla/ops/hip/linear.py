@@ -87,7 +87,7 @@ def _weight_grad_into(out: torch.Tensor, dy: torch.Tensor, r0: int, r1: int, x: 
     p = torch.bmm(gt, x.view(parts, c, k), out_dtype=torch.float32)
     code = _lib.KLA_DTYPE_BF16 if dy.dtype == torch.bfloat16 else _lib.KLA_DTYPE_F32
     _lib.check("kla_sum_parts", _lib.lib().kla_sum_parts(
-        code, p.data_ptr(), parts, (r1 - r0) * k, out.data_ptr(), torch.cuda.current_stream(dy.device).cuda_stream))
+        code, p.data_ptr(), parts, (r1 - r0) * k, out.data_ptr(), _lib.stream(dy.device)))
 
 
 def weight_grad_hip(dy: torch.Tensor, x: torch.Tensor, parts: int) -> torch.Tensor:

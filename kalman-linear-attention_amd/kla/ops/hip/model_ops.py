@@ -42,7 +42,7 @@ def rms_norm_hip(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Ten
     rows = xc.numel() // dim if dim else 0
     _lib.check("kla_rms_norm_fwd", _lib.lib().kla_rms_norm_fwd(
         _code(xc), xc.data_ptr(), w.data_ptr(), float(eps), y.data_ptr(), rows, dim,
-        torch.cuda.current_stream(x.device).cuda_stream))
+        _lib.stream(x.device)))
     return y
 
 
@@ -56,7 +56,7 @@ def swiglu_hip(h: torch.Tensor) -> torch.Tensor:
     out = torch.empty(*lead, hidden, dtype=h.dtype, device=h.device)
     _lib.check("kla_swiglu_fwd", _lib.lib().kla_swiglu_fwd(
         _code(h), h2.data_ptr(), h2.stride(0), out.data_ptr(), h2.shape[0], hidden,
-        torch.cuda.current_stream(h.device).cuda_stream))
+        _lib.stream(h.device)))
     return out
 
 
@@ -132,7 +132,7 @@ def rows_linear_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | 
     _lib.check("kla_rows_linear_fwd", _lib.lib().kla_rows_linear_fwd(
         epi, p(x), x.stride(0), p(w), w.stride(0), p(b), p(g), float(eps),
         p(residual), residual.stride(0) if residual is not None else 0, p(y), y.stride(0),
-        rows, n, k, glu_off, torch.cuda.current_stream(x.device).cuda_stream))
+        rows, n, k, glu_off, _lib.stream(x.device)))
     return y
 
 
@@ -148,7 +148,7 @@ def gather_rows_hip(weight: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
     out = torch.empty(flat.numel(), dim, dtype=weight.dtype, device=weight.device)
     _lib.check("kla_gather_rows", _lib.lib().kla_gather_rows(
         _code(weight), weight.data_ptr(), weight.stride(0), weight.shape[0], flat.data_ptr(), out.data_ptr(),
-        out.stride(0), flat.numel(), dim, torch.cuda.current_stream(weight.device).cuda_stream))
+        out.stride(0), flat.numel(), dim, _lib.stream(weight.device)))
     return out.view(*ids.shape, dim)
 
 
@@ -165,7 +165,7 @@ def argmax_rows_hip(x: torch.Tensor) -> torch.Tensor:
     ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
     _lib.check("kla_argmax_rows", _lib.lib().kla_argmax_rows(
         x2.data_ptr(), x2.stride(0), x2.shape[0], x2.shape[1], out.data_ptr(), 1,
-        ws.data_ptr() if ws is not None else None, nbytes, torch.cuda.current_stream(x.device).cuda_stream))
+        ws.data_ptr() if ws is not None else None, nbytes, _lib.stream(x.device)))
     return out.view(*x.shape[:-1], 1)
 
 
@@ -197,5 +197,5 @@ def rows_linear_conv_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tens
     _lib.check("kla_rows_linear_conv_fwd", _lib.lib().kla_rows_linear_conv_fwd(
         p(x), x.stride(0), p(w), w.stride(0), p(bias.contiguous() if bias is not None else None), p(g), float(eps),
         p(y), y.stride(0), rows, n, k, p(cw), p(conv_bias.contiguous() if conv_bias is not None else None),
-        p(window), p(win_out), D, K, _CONV_ACT[activation], torch.cuda.current_stream(x.device).cuda_stream))
+        p(window), p(win_out), D, K, _CONV_ACT[activation], _lib.stream(x.device)))
     return y, win_out

@@ -32,7 +32,7 @@ def _qk_op(k: torch.Tensor, q: torch.Tensor, norm: bool, has_clip: bool,
     yq = torch.empty_like(yk)
     _lib.check("kla_qk_sensors_fwd", _lib.lib().kla_qk_sensors_fwd(
         _code(k), k.data_ptr(), _sensor_rows(k), q.data_ptr(), _sensor_rows(q), yk.data_ptr(), yq.data_ptr(),
-        B * L, S, int(norm), int(has_clip), float(clip), torch.cuda.current_stream(k.device).cuda_stream))
+        B * L, S, int(norm), int(has_clip), float(clip), _lib.stream(k.device)))
     return yk, yq
 
 
@@ -51,7 +51,7 @@ def _qk_bwd_op(k: torch.Tensor, q: torch.Tensor, dyk: torch.Tensor, dyq: torch.T
     _lib.check("kla_qk_sensors_bwd", _lib.lib().kla_qk_sensors_bwd(
         _code(k), k.data_ptr(), _sensor_rows(k), q.data_ptr(), _sensor_rows(q), dyk.data_ptr(), dyq.data_ptr(),
         dk.data_ptr(), dq.data_ptr(), B * L, S, int(norm), int(has_clip), float(clip),
-        torch.cuda.current_stream(k.device).cuda_stream))
+        _lib.stream(k.device)))
     return dk, dq
 
 

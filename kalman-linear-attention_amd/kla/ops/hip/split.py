@@ -46,7 +46,7 @@ def cat_cols_hip(pieces: list, widths: list[int], like: torch.Tensor) -> torch.T
     vp = ctypes.c_void_p
     _lib.check("kla_cat_cols", _lib.lib().kla_cat_cols(
         _code(like), n, ctypes.cast(ptrs, vp), ctypes.cast(lds, vp), ctypes.cast(ws, vp), out.data_ptr(), rows,
-        torch.cuda.current_stream(like.device).cuda_stream))
+        _lib.stream(like.device)))
     return out
 
 

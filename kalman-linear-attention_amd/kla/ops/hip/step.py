@@ -54,7 +54,7 @@ def _step_one(v, lambda_v, k, q, a, p, lam, eta, decode_from_prior, dev):
     pt = _lib.ptr
     _lib.check("kla_step_fwd", _lib.lib().kla_step_fwd(
         pt(v), pt(lambda_v), pt(k), pt(q), pt(a), pt(p), pt(lam), pt(eta), pt(y), pt(y_var), pt(lam_out),
-        pt(eta_out), int(decode_from_prior), B, M, S, torch.cuda.current_stream(dev).cuda_stream))
+        pt(eta_out), int(decode_from_prior), B, M, S, _lib.stream(dev)))
     return y, y_var, lam_out, eta_out
 
 

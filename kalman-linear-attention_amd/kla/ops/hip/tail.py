@@ -46,7 +46,7 @@ def _tail_op(y: torch.Tensor, residual: Optional[torch.Tensor], gate: Optional[t
     _lib.check("kla_gate_skip_fwd", _lib.lib().kla_gate_skip_fwd(
         _io(residual, gate), _code(out.dtype), pt(y), pt(residual), _ld(residual), pt(gate), _ld(gate),
         pt(lambda_skip), int(lambda_skip is not None and lambda_skip.dim() == 1), activation, pt(out), B * L, M,
-        torch.cuda.current_stream(dev).cuda_stream))
+        _lib.stream(dev)))
     return out
 
 

@@ -270,10 +270,16 @@ def _step_on_hip(backend: str, x: torch.Tensor) -> bool:
         backend = _resolve_auto(x)
     if backend.split("_", 1)[0] != "hip":
         return False
-    from kla.ops.hip import _lib
+    if not _HIP_LIB_LOADED:
+        from kla.ops.hip import _lib
 
-    _lib.lib()   # RuntimeError when libkla_hip.so is missing or built for another ABI
+        _lib.lib()   # RuntimeError when libkla_hip.so is missing or built for another ABI
+        _HIP_LIB_LOADED.append(True)
     return True
+
+
+# Non-empty once _step_on_hip has loaded libkla_hip.so (the load is then skipped).
+_HIP_LIB_LOADED: list = []
 
 
 def kla_scan_reference(v, lambda_v, k, q, a, p, initial_state: Optional[KLAState] = None,
