@@ -287,11 +287,16 @@ def time_kernels_in_step(kernels, steps, stream):
 
 
 class _NoGC:
-    """Python's cyclic garbage collector off for a timed region (collected just before).
+    """Python's cyclic garbage collector off for the warmup and the timed region
+    (collected just before the warmup).
 
     A generation-2 collection is a host-side pause of tens of milliseconds (81 ms
     measured in the C4 step's process) during which no kernel is launched and the
-    GPU runs dry; the step's kernels are the same either way."""
+    GPU runs dry; the step's kernels are the same either way. The collection comes
+    before the warmup, not between the warmup's synchronize and the first timed
+    launch: after such a pause the steps that follow run slower while the GPU
+    comes back from idle (C1's forward over 20 steps: 0.236-0.247 ms with no
+    gap, 0.25-0.27 after a 50 ms sleep, 0.268-0.276 after gc.collect())."""
 
     def __enter__(self):
         gc.collect()
@@ -304,11 +309,11 @@ class _NoGC:
 
 
 def _timed(fn, steps, warmup, stream):
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with _NoGC():
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
         start.record(stream)
         for _ in range(steps):
             fn()
@@ -822,11 +827,11 @@ def main(argv=None) -> int:
               flush=True)
         return 0
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with _NoGC():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record(stream)
         for _ in range(args.steps):
