@@ -502,6 +502,7 @@ def config_c4(device, stream, steps, warmup, backend="hip", cpu=True) -> dict:
     committed rocprofv3 counter run) and on their compulsory HBM bytes."""
     from kla import KLAConfig, KLALayer
 
+    torch.cuda.reset_peak_memory_stats(device)   # peak_mem_GiB: this config's own
     torch.manual_seed(0)
     layer = KLALayer(1024, KLAConfig(d_state=16, backend=backend))
     out = {}
@@ -592,6 +593,7 @@ def config_c5(device, stream, steps, backend="hip", nb=16, phases=("prefill", "d
     prefill of (nb, 2048) random ids, then 256 greedy one-token decode steps."""
     from kla import KLAConfig, ModelConfig, SequenceModel
 
+    torch.cuda.reset_peak_memory_stats(device)   # peak_mem_GiB: this config's own
     torch.manual_seed(0)
     model = SequenceModel(ModelConfig(vocab_size=50304, d_model=512, n_layers=6),
                           KLAConfig(backend=backend)).eval()
