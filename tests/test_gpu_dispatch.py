@@ -111,3 +111,28 @@ def test_ops_trace_under_torch_compile(cuda):
         outs.append((out.detach(), y_var.detach(), xx.grad))
     for name, e, c in zip(("out", "y_var", "dx"), *outs):
         torch.testing.assert_close(c, e, rtol=1e-6, atol=1e-6, msg=name)
+
+
+def test_stream_handle_is_torchs_current_stream(cuda):
+    """_lib.stream (the handle every launch passes) is the value of
+    torch.cuda.current_stream(device).cuda_stream: on the default stream, on a
+    side stream, and under graph capture (the capture stream)."""
+    assert _lib.stream(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+    side = torch.cuda.Stream(cuda)
+    with torch.cuda.stream(side):
+        assert _lib.stream(cuda) == side.cuda_stream
+        assert _lib.stream(torch.device("cuda")) == side.cuda_stream
+    assert _lib.stream(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+    x = torch.ones(4, device=cuda)
+    g = torch.cuda.CUDAGraph()
+    seen = []
+    side.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g):
+            seen.append((_lib.stream(cuda), torch.cuda.current_stream(cuda).cuda_stream))
+            y = x * 2
+    torch.cuda.current_stream(cuda).wait_stream(side)
+    g.replay()
+    torch.cuda.synchronize()
+    assert seen[0][0] == seen[0][1]
+    assert torch.equal(y, torch.full_like(x, 2.0))
