@@ -566,6 +566,19 @@ int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *
                         int64_t rows, int64_t n, int64_t k, int64_t glu_off, hipStream_t stream);
 
 /*
+ * The k and q sensors of a sequence from the sensor projection's last 2 S rows
+ * w [2 S, k] (row stride ldw), bias [2 S] or NULL, for fp32 x [rows, k] (row
+ * stride ldx): a = x w^T + bias, k_out[r, :] = a[r, :S], q_out[r, :] = a[r, S:],
+ * each row divided by max(||row||_2, 1e-12) when norm, then clamped to
+ * [-clip, clip] when has_clip; k_out and q_out [rows, S] dense fp32. S is a power
+ * of two in [1, 16]. Replaces the k, q columns of sensor_proj followed by
+ * l2_norm and clamp (reference src/kla/layers/kla_layer.py:205-222).
+ */
+int kla_rows_linear_qk_fwd(const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
+                           float *k_out, float *q_out, int64_t rows, int64_t k, int64_t S, int norm, int has_clip,
+                           float clip, hipStream_t stream);
+
+/*
  * kla_rows_linear_fwd's plain product (same x, w, bias, norm_w, eps, y, rows, n,
  * k) with one token of the depthwise causal conv applied to output columns
  * j < conv_n (in_proj's z half in one-token decode):

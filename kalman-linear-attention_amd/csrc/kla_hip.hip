@@ -28,7 +28,7 @@ namespace {
 
 using namespace kla;
 
-constexpr int kAbiVersion = 16;
+constexpr int kAbiVersion = 17;
 
 // Tile shapes: W waves x S steps per wave (chunk = W*S steps), V lanes per
 // thread (tile = 64 V lanes), each chosen by timing the kernel inside the
@@ -1443,7 +1443,9 @@ int rows_linear_launch(const char *fn, int epi, RowsLinearParams &p, hipStream_t
   if (epi == kEpiSwiglu && p.glu_off < n)
     return fail(KLA_ERR_INVALID_ARG, "%s: glu_off %lld below n %lld (the halves overlap)", fn,
                 (long long)p.glu_off, (long long)n);
-  if (p.ldx < k || p.ldw < k || p.ldy < n || (epi == kEpiResidual && p.ldres < n))
+  const bool qk = epi == kEpiQk;
+  if (p.ldx < k || p.ldw < k || (!qk && p.ldy < n) || (qk && (p.ldy < p.qk_seg || p.ldy2 < p.qk_seg)) ||
+      (epi == kEpiResidual && p.ldres < n))
     return fail(KLA_ERR_INVALID_ARG, "%s: a row stride is below its row length", fn);
   if (p.norm_w && k == 0) return fail(KLA_ERR_INVALID_ARG, "%s: RMSNorm over zero columns", fn);
   if (misaligned(p.x) || misaligned(p.w) || misaligned(p.bias) || misaligned(p.norm_w) || misaligned(p.res) ||
@@ -1508,6 +1510,9 @@ int rows_linear_launch(const char *fn, int epi, RowsLinearParams &p, hipStream_t
     case kEpiSwiglu:
       by_norm(std::integral_constant<int, kEpiSwiglu>{});
       break;
+    case kEpiQk:
+      by_vec(std::integral_constant<int, kEpiQk>{}, F{});
+      break;
     default:
       by_norm(std::integral_constant<int, kEpiConv>{});
       break;
@@ -1564,6 +1569,24 @@ int kla_rows_linear_fwd(int epilogue, const float *x, int64_t ldx, const float *
   p.glu_off = glu_off;
   const int epi = epilogue == KLA_ROWS_PLAIN ? kEpiPlain : epilogue == KLA_ROWS_RESIDUAL ? kEpiResidual : kEpiSwiglu;
   return rows_linear_launch(fn, epi, p, stream);
+}
+
+int kla_rows_linear_qk_fwd(const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,
+                           float *k_out, float *q_out, int64_t rows, int64_t k, int64_t S, int norm, int has_clip,
+                           float clip, hipStream_t stream) {
+  const char *fn = "kla_rows_linear_qk_fwd";
+  if (S < 1 || S > 16 || (S & (S - 1)) != 0)
+    return fail(KLA_ERR_INVALID_ARG, "%s: S must be a power of two in [1, 16], got %lld", fn, (long long)S);
+  if (rows > 0 && !q_out) return fail(KLA_ERR_INVALID_ARG, "%s: q_out must not be NULL", fn);
+  if (misaligned(q_out)) return fail(KLA_ERR_ALIGN, "%s: fp32 operand not 4-byte aligned", fn);
+  RowsLinearParams p = rows_params(x, ldx, w, ldw, bias, nullptr, 0.0f, k_out, S, rows, 2 * S, k);
+  p.y2 = q_out;
+  p.ldy2 = S;
+  p.qk_seg = static_cast<int>(S);
+  p.qk_norm = norm ? 1 : 0;
+  p.qk_has_clip = has_clip ? 1 : 0;
+  p.qk_clip = clip;
+  return rows_linear_launch(fn, kEpiQk, p, stream);
 }
 
 int kla_rows_linear_conv_fwd(const float *x, int64_t ldx, const float *w, int64_t ldw, const float *bias,

@@ -43,7 +43,7 @@ constexpr int kRowsLinWaves = 16;
 constexpr int kRowsLinThreads = kRowsLinWaves * kWave;
 constexpr int kRowsLinTile = 16;    // rows and columns per workgroup
 
-enum RowsLinEpilogue { kEpiPlain = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiConv = 3 };
+enum RowsLinEpilogue { kEpiPlain = 0, kEpiResidual = 1, kEpiSwiglu = 2, kEpiConv = 3, kEpiQk = 4 };
 
 constexpr int kRowsLinMaxConvK = 8;   // conv taps the kEpiConv epilogue supports
 
@@ -73,6 +73,15 @@ struct RowsLinearParams {
   float *window_out;
   int64_t conv_n;
   int conv_k, conv_act;
+  // kEpiQk: the k, q sensors. Output columns [0, qk_seg) are k (y, row stride
+  // ldy), [qk_seg, 2 qk_seg) q (y2, row stride ldy2); each row of each is
+  // l2-normalised over its qk_seg columns when qk_norm, then clipped to
+  // [-qk_clip, qk_clip] when qk_has_clip. qk_seg is a power of two <= 16, so a
+  // segment lies within one 16-column tile.
+  float *y2;
+  int64_t ldy2;
+  int qk_seg, qk_norm, qk_has_clip;
+  float qk_clip;
 };
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -260,7 +269,32 @@ __global__ void __launch_bounds__(kRowsLinThreads) rows_linear_kernel(RowsLinear
       for (int u = 0; u < kRowsLinWaves; ++u) tot += s_ss[u][om - m0];
       rs = rsqrtf(tot / static_cast<float>(p.k) + p.eps);
     }
-    if (out_ok) {
+    if constexpr (EPI == kEpiQk) {
+      // The 16 columns of a row lie 4 lanes apart in one wave (lane = 4 col +
+      // row % 4): its segment's sum of squares is a butterfly over lane bits
+      // 2 .. 2 + log2(qk_seg) - 1, run by every lane (masked columns add 0).
+      float val = 0.0f;
+      if (out_ok) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kRowsLinWaves; ++u) sum += s_part[buf][0][u][e_lane][e_i];
+        val = sum + b0;
+      }
+      float out = val;
+      if (p.qk_norm) {
+        float ss = val * val;
+        for (int off = 4; off < 4 * p.qk_seg; off <<= 1) ss += __shfl_xor(ss, off);
+        out = val / fmaxf(sqrtf(ss), 1e-12f);
+      }
+      if (p.qk_has_clip) out = fminf(fmaxf(out, -p.qk_clip), p.qk_clip);
+      if (out_ok) {
+        if (on < p.qk_seg)
+          p.y[om * p.ldy + on] = out;
+        else
+          p.y2[om * p.ldy2 + (on - p.qk_seg)] = out;
+      }
+    }
+    if (EPI != kEpiQk && out_ok) {
       float v[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {

@@ -153,6 +153,26 @@ class KLALayer(nn.Module):
         [B, L, S] float32 after the norm and the clip)."""
         cfg = self.config
         S = self.d_state
+        if self._qk_project_on_hip(z):
+            # Inference at few tokens: value and variance columns as one hipBLASLt
+            # product, k and q with their norm and clip as one HIP kernel (a 2S-row
+            # tail would otherwise set hipBLASLt's tile for the whole product).
+            from kla.ops.hip.sensors import qk_project_hip
+
+            w, b = self.sensor_proj.weight, self.sensor_proj.bias
+            n1 = self._w_value + self._w_var
+            B, L, _ = z.shape
+            k, q = qk_project_hip(z.reshape(B * L, z.shape[-1]), w[n1:], None if b is None else b[n1:], S,
+                                  norm=cfg.qk_norm, clip=cfg.clip_value)
+            v, log_var = torch.split(F.linear(z, w[:n1], None if b is None else b[:n1]),
+                                     [self._w_value, self._w_var], dim=-1)
+            if self._value_rank == "conv":
+                v = z
+            elif self.value_expand is not None:
+                v = self.value_expand(v)
+            if self.var_expand is not None:
+                log_var = self.var_expand(log_var)
+            return v, log_var, k.view(B, L, S), q.view(B, L, S)
         v, log_var, k, q = self._linear_split(self.sensor_proj, z, [self._w_value, self._w_var, S, S])
         if self._value_rank == "conv":
             v = z
@@ -258,6 +278,21 @@ class KLALayer(nn.Module):
             if pieces is not None:
                 return pieces
         return self._split(mod(x), sizes)
+
+    def _qk_project_on_hip(self, z: torch.Tensor) -> bool:
+        """Whether the k, q columns of the sensor projection, their norm and clip run
+        as one HIP kernel (kla.ops.hip.sensors.qk_project_hip): inference (no
+        gradient, no autocast), fp32 dense z on a ROCm GPU with a hip-family
+        backend, d_state a power of two <= 16, value or variance columns beside
+        them, and fewer than QK_PROJECT_MAX_TOKENS tokens."""
+        from kla.ops.hip.sensors import QK_PROJECT_MAX_TOKENS
+
+        S = self.d_state
+        return (not torch.is_grad_enabled() and z.dtype == torch.float32 and z.dim() == 3 and z.is_cuda
+                and self.sensor_proj.weight.dtype == torch.float32
+                and S <= 16 and S & (S - 1) == 0 and self._w_value + self._w_var > 0
+                and 0 < z.shape[0] * z.shape[1] < QK_PROJECT_MAX_TOKENS and z.is_contiguous()
+                and not torch.is_autocast_enabled(z.device.type) and _step_on_hip(self.config.backend, z))
 
     def _qk_on_hip(self, k: torch.Tensor) -> bool:
         """Whether the k, q sensors come from the MI355X kernels: a hip-family backend

@@ -19,7 +19,7 @@ import torch
 # one the ABI tests run against); by default the in-tree libkla_hip.so.
 LIB_PATH = os.environ.get("KLA_HIP_LIB") or os.path.join(
     os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))), "lib", "libkla_hip.so")
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 KLA_OK = 0
 KLA_ERR_INVALID_ARG = 1
@@ -79,6 +79,8 @@ _SIGNATURES = {
     "kla_gate_skip_workspace_bytes": (ctypes.c_size_t, [_i64] * 2),
     "kla_rms_norm_fwd": (ctypes.c_int, [ctypes.c_int, _p, _p, ctypes.c_float, _p, _i64, _i64, _p]),
     "kla_swiglu_fwd": (ctypes.c_int, [ctypes.c_int, _p, _i64, _p, _i64, _i64, _p]),
+    "kla_rows_linear_qk_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i64, _i64, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_float, _p]),
     "kla_rows_linear_conv_fwd": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, ctypes.c_float, _p, _i64, _i64, _i64,
                                                 _i64, _p, _p, _p, _p, _i64, ctypes.c_int, ctypes.c_int, _p]),
     "kla_discretize_fwd": (ctypes.c_int, [_p] * 3 + [_i64] + [ctypes.c_int] * 3 + [ctypes.c_float] + [_p] * 3),

@@ -91,3 +91,40 @@ def qk_sensors_hip(k: torch.Tensor, q: torch.Tensor, *, norm: bool, clip: float 
     if _sensor_rows(q) is None:
         q = q.contiguous()
     return _lib.call(_qk_op, k, q, bool(norm), clip is not None, float(clip) if clip is not None else 0.0)
+
+
+# Token counts below which the k, q columns of the sensor projection run as
+# kla_rows_linear_qk_fwd: at 2048 tokens (k = 1024, S = 16) its product, norm and
+# clip take ~9 us against ~19 us for hipBLASLt's 32-row product alone (plus the
+# qk sensor kernel); at 32768 tokens hipBLASLt's product is the faster (23
+# against 68 us).
+QK_PROJECT_MAX_TOKENS = 8192
+
+
+def qk_project_hip(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, S: int, *, norm: bool,
+                   clip: float | None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(k, q) [rows, S] fp32 from fp32 x [rows, K] (last dim contiguous) and the
+    sensor projection's last 2 S rows ``weight`` [2 S, K], ``bias`` [2 S]: the k
+    and q columns of ``sensor_proj(x)``, each l2-normalised over S when ``norm``
+    and clamped to +-clip when given (reference
+    ``src/kla/layers/kla_layer.py:205-222``), in one HIP kernel. Inference only
+    (no autograd); S a power of two <= 16."""
+    if x.dtype != torch.float32 or weight.dtype != torch.float32 or x.dim() != 2 or x.stride(-1) != 1:
+        raise TypeError("qk_project_hip: x must be fp32 [rows, K] with a contiguous last dimension, weight fp32")
+    if S < 1 or S > 16 or S & (S - 1) or weight.shape[0] != 2 * S or weight.shape[1] != x.shape[1]:
+        raise ValueError(f"qk_project_hip: S must be a power of two <= 16 and weight [2 S, K]; got S = {S}, "
+                         f"weight {tuple(weight.shape)}, x {tuple(x.shape)}")
+    _require_device(x, weight, bias)
+    if weight.stride(-1) != 1:
+        weight = weight.contiguous()
+    if bias is not None:
+        bias = bias.float().contiguous()
+    rows = x.shape[0]
+    k = torch.empty(rows, S, dtype=torch.float32, device=x.device)
+    q = torch.empty(rows, S, dtype=torch.float32, device=x.device)
+    _lib.check("kla_rows_linear_qk_fwd", _lib.lib().kla_rows_linear_qk_fwd(
+        x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), _lib.ptr(bias), k.data_ptr(), q.data_ptr(),
+        rows, x.shape[1], S, int(bool(norm)), int(clip is not None), float(clip) if clip is not None else 0.0,
+        _lib.stream(x.device)))
+    return k, q
+
