@@ -65,3 +65,21 @@ def test_layer_inference_takes_the_kernel_and_matches_torch(cuda, monkeypatch):
     assert calls, "the inference path did not run qk_project_hip"
     err = ((got - want).abs().max() / want.abs().max()).item()
     assert err < 1e-5, err
+
+
+def test_training_and_autocast_forwards_keep_the_differentiable_path(cuda, monkeypatch):
+    """The kernel has no backward and computes in fp32: a forward that records a
+    gradient, or one under bf16 autocast, keeps the split product and the qk
+    sensor op, and its gradients still flow to the sensor projection's k, q rows."""
+    torch.manual_seed(0)
+    layer = KLALayer(512, KLAConfig(d_state=16, backend="hip")).to(cuda)
+    x = torch.randn(2, 64, 512, device=cuda)
+    calls = []
+    orig = sensors.qk_project_hip
+    monkeypatch.setattr(sensors, "qk_project_hip", lambda *a, **k: calls.append(1) or orig(*a, **k))
+    layer(x).square().mean().backward()
+    g = layer.sensor_proj.weight.grad
+    assert g is not None and g[-32:].abs().sum().item() > 0
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        layer(x)
+    assert not calls
